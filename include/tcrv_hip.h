@@ -1,0 +1,150 @@
+/*
+ * tcrv_hip.h -- C-ABI of libtcrv_hip.so, the MI355X (gfx950) runtime library
+ * for the kernels TianChen-RV compiles: elementwise add, ggml Q8_0 dequant,
+ * the Q8_0.Q8_0 and Q4_0.Q8_0 block dots, and the quantized GEMV/GEMM.
+ *
+ * Every entry point keeps the parameter roles and order of the reference's
+ * emitted kernel `extern "C" void tcrv_emitc_<kernel>_<variant>(...)`
+ * (lib/Conversion/RVV/RVVToEmitC.cpp:167-172, :258-268: parameters appear in
+ * tcrv_rvv.runtime_abi_value declaration order) and appends one `stream`
+ * argument.  Differences from the emitted C, all deliberate:
+ *   - pointers are DEVICE pointers owned by the caller (the reference's
+ *     "target-export-abi-owned" ownership, include/TianChenRV/Support/
+ *     RuntimeABI.h:57-60: the library never allocates, frees or retains them);
+ *   - the call is asynchronous on `stream` (a hipStream_t; NULL = the null
+ *     stream) and returns an int status instead of void;
+ *   - like the reference, nb = n / 32 and a trailing partial block is ignored
+ *     (RVVToEmitCBlockQuantLinear.cpp:7340, RVVOps.td:8395).
+ *
+ * Status: 0 = success; negative = an argument error detected before launch
+ * (nothing was launched); positive = the hipError_t reported by the launch.
+ * Entry points are reentrant and thread-safe; calls on one stream execute in
+ * order, calls on different streams may overlap.
+ */
+#ifndef TCRV_HIP_H
+#define TCRV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define TCRV_HIP_API __attribute__((visibility("default")))
+#else
+#define TCRV_HIP_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TCRV_HIP_QK 32
+#define TCRV_HIP_Q8_0_BLOCK_BYTES 34
+#define TCRV_HIP_Q4_0_BLOCK_BYTES 18
+#define TCRV_HIP_Q4_0X16_BLOCK_BYTES 288
+
+enum {
+  TCRV_HIP_OK = 0,
+  TCRV_HIP_ERR_NULL_POINTER = -1,   /* a required pointer is NULL */
+  TCRV_HIP_ERR_BAD_SIZE = -2,       /* a size/stride violates the kernel's contract */
+  TCRV_HIP_ERR_MISALIGNED = -3,     /* a pointer/stride is not aligned as documented */
+  TCRV_HIP_ERR_TOO_LARGE = -4,      /* a size exceeds the kernel's index range */
+  TCRV_HIP_ERR_UNSUPPORTED = -5     /* argument combination not implemented */
+};
+
+/* Human-readable name of a status value (static storage, never NULL). */
+TCRV_HIP_API const char *tcrv_hip_status_string(int status);
+
+/* Library version string, e.g. "tcrv_hip 0.1.0 gfx950". */
+TCRV_HIP_API const char *tcrv_hip_version(void);
+
+/* Blocks until all work on `stream` is complete; returns a hipError_t. */
+TCRV_HIP_API int tcrv_hip_stream_synchronize(void *stream);
+
+/* ---- a1: elementwise add -------------------------------------------------
+ * Replaces tcrv_emitc_<kernel>_<variant>(const T *lhs, const T *rhs, T *out,
+ * size_t n) for T = float (test/Conversion/RVV/rvv-to-emitc-add-cpp-golden.mlir:
+ * 15-18,33; emitBinary lib/Conversion/RVV/RVVToEmitC.cpp:1873-1911).
+ * out[i] = lhs[i] + rhs[i], i < n.  Any 4-byte alignment; 16-byte aligned
+ * pointers take the 128-bit path.  out may alias lhs or rhs exactly. */
+TCRV_HIP_API int tcrv_hip_add_f32(const float *lhs, const float *rhs, float *out, size_t n, void *stream);
+
+/* ---- a3: Q8_0 dequantize --------------------------------------------------
+ * ggml dequantize_row_q8_0(const block_q8_0 *x, float *y, int64_t k) (no
+ * reference op; block layout RVVDialectWideningOps.cpp:3358-3372).
+ * y[32b+j] = qs_b[j] * d_b for b < n/32.  vx and y must be 16-byte aligned. */
+TCRV_HIP_API int tcrv_hip_dequantize_row_q8_0(const uint8_t *vx, float *y, size_t n, void *stream);
+
+/* ---- a10: f32 -> Q8_0 activation quantizer --------------------------------
+ * Replaces tcrv_emitc_..._quantize_row_q8_0(size_t n, const float *x,
+ * uint8_t *vy) (test/Conversion/RVV/rvv-to-emitc-ggml-quantize-row-q8-0.mlir:
+ * 25-27; RVVOps.td:8345-8431).  x must be 16-byte aligned. */
+TCRV_HIP_API int tcrv_hip_quantize_row_q8_0(size_t n, const float *x, uint8_t *vy, void *stream);
+
+/* ---- a5: Q8_0 . Q8_0 block dot ---------------------------------------------
+ * Replaces tcrv_emitc_..._q8_0_q8_0_block_dot(size_t n, float *s,
+ * const uint8_t *vx, const uint8_t *vy)
+ * (test/Conversion/RVV/rvv-to-emitc-q8-0-q8-0-block-dot.mlir:16-19).
+ * *s = sum_b fma((float)sumi_b, d_x*d_y, .) in ascending b.
+ * vx, vy 16-byte aligned. */
+TCRV_HIP_API int tcrv_hip_q8_0_q8_0_block_dot(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
+                                 void *stream);
+
+/* Batched form: s[r] = block_dot(vx + r*bx, vy + r*by) for r < nrows.
+ * vx, vy 16-byte aligned; bx, by multiples of 16. */
+TCRV_HIP_API int tcrv_hip_q8_0_q8_0_block_dot_rows(size_t n, float *s, const uint8_t *vx, size_t bx,
+                                      const uint8_t *vy, size_t by, size_t nrows,
+                                      void *stream);
+
+/* ---- a6: Q4_0 . Q8_0 block dot ---------------------------------------------
+ * Replaces tcrv_emitc_..._q4_0_q8_0_block_dot(size_t n, float *s, size_t bs,
+ * const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by, int32_t nrc),
+ * the ggml vec_dot ABI (test/Conversion/RVV/rvv-to-emitc-q4-0-q8-0-block-dot.
+ * mlir:24-31).  As in the reference only n, s, vx, vy are read
+ * (RVVToEmitCBlockQuantLinear.cpp:30-46); *s = sum_b fma(fl(sumi_b*d_x), d_y, .).
+ * vx, vy 16-byte aligned. */
+TCRV_HIP_API int tcrv_hip_q4_0_q8_0_block_dot(size_t n, float *s, size_t bs, const uint8_t *vx,
+                                 size_t bx, const uint8_t *vy, size_t by, int32_t nrc,
+                                 void *stream);
+
+/* Batched form: s[r] = block_dot(vx + r*bx, vy + r*by) for r < nrows. */
+TCRV_HIP_API int tcrv_hip_q4_0_q8_0_block_dot_rows(size_t n, float *s, const uint8_t *vx, size_t bx,
+                                      const uint8_t *vy, size_t by, size_t nrows,
+                                      void *stream);
+
+/* Per-block int32 sums (the integer core of a4/a5/a6, bit-exact) for nrows
+ * row pairs: sumi[r*(n/32) + b].  Same alignment rules as the _rows forms. */
+TCRV_HIP_API int tcrv_hip_q8_0_q8_0_block_sums(size_t n, int32_t *sumi, const uint8_t *vx, size_t bx,
+                                  const uint8_t *vy, size_t by, size_t nrows, void *stream);
+TCRV_HIP_API int tcrv_hip_q4_0_q8_0_block_sums(size_t n, int32_t *sumi, const uint8_t *vx, size_t bx,
+                                  const uint8_t *vy, size_t by, size_t nrows, void *stream);
+
+/* ---- a7: Q4_0 x Q8_0 GEMM / decode GEMV -----------------------------------
+ * Replaces tcrv_emitc_..._q4_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx,
+ * const uint8_t *vy, size_t by, size_t nr, size_t nc, size_t bx, size_t bs)
+ * (test/Conversion/RVV/rvv-to-emitc-q4-0-q8-0-gemm.mlir:23-31;
+ * RVVToEmitCBlockQuantLinear.cpp:1691-2121).
+ * s[ir*bs + col] = q4_0 block_dot(vx + ir*bx, vy + col*by), ir < nr, col < nc.
+ * vx, vy 16-byte aligned; bx, by multiples of 16; bs >= nc when nc > 1. */
+TCRV_HIP_API int tcrv_hip_q4_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
+                            size_t by, size_t nr, size_t nc, size_t bx, size_t bs,
+                            void *stream);
+
+/* The decode GEMV (the q4_0 GEMM with nc = 1): s[ir] for ir < nr. */
+TCRV_HIP_API int tcrv_hip_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx, size_t bx,
+                            const uint8_t *vy, size_t nr, void *stream);
+
+/* ---- a9: Q8_0 x Q8_0 GEMM (prefill) ---------------------------------------
+ * Same ABI as the q4_0 GEMM above; elements are the a5 block dot:
+ * s[ir*bs + col] = q8_0 block_dot(vx + ir*bx, vy + col*by).
+ * Runs on v_mfma_i32_32x32x32_i8 with one MFMA per 32-element block and the
+ * per-block fp32 fold in ascending block order.
+ * vx, vy 16-byte aligned; bx, by multiples of 16; bs >= nc. */
+TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
+                            size_t by, size_t nr, size_t nc, size_t bx, size_t bs,
+                            void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TCRV_HIP_H */

@@ -1,0 +1,107 @@
+/*
+ * tcrv_oracle.h -- scalar CPU restatement of TianChen-RV's quantized hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP library
+ * (libtcrv_hip.so).  Only tests/, __graft_entry__.smoke() and the cpu_baseline
+ * leg of bench.py may load it; no product code path calls it, and the product
+ * fails loudly when its HIP extension is missing instead of falling back here.
+ *
+ * Every function restates one emitter of the reference compiler (paths are
+ * relative to the TianChen-RV tree) in plain C with the reference's exact
+ * per-block fold order, written with explicit fmaf() so that the build's
+ * -ffp-contract setting cannot change a rounding.
+ *
+ * Block formats (ggml, pinned by the reference verifiers):
+ *   block_q8_0    34 B : fp16 d @0, int8  qs[32] @2
+ *   block_q4_0    18 B : fp16 d @0, uint8 qs[16] @2; element j = (qs[j]&15)-8,
+ *                        element j+16 = (qs[j]>>4)-8
+ *   block_q4_0x16 288 B: fp16 d[16] @0, uint8 qs[256] @32 (interleaved, ^0x88)
+ *   (lib/Dialect/RVV/IR/RVVDialectWideningOps.cpp:3358-3372;
+ *    include/TianChenRV/Dialect/RVV/IR/RVVOps.td:3893-3897, :4569-4577)
+ */
+#ifndef TCRV_ORACLE_H
+#define TCRV_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TCRV_QK 32
+#define TCRV_Q8_0_BLOCK_BYTES 34
+#define TCRV_Q4_0_BLOCK_BYTES 18
+#define TCRV_Q4_0X16_BLOCK_BYTES 288
+
+/* IEEE binary16 <-> binary32 (the reference reads d as (float)*(const _Float16*),
+ * RVVToEmitCBlockQuantLinear.cpp:117,140, and stores it as (_Float16)d, RNE). */
+float tcrv_oracle_fp16_to_f32(uint16_t h);
+uint16_t tcrv_oracle_f32_to_fp16(float f);
+
+/* a1: tcrv_rvv.binary{kind="add"}; emitBinary RVVToEmitC.cpp:1873-1911. */
+void tcrv_oracle_add_f32(const float *lhs, const float *rhs, float *out, size_t n);
+void tcrv_oracle_add_i32(const int32_t *lhs, const int32_t *rhs, int32_t *out, size_t n);
+
+/* a3: y[32b+j] = qs_b[j] * fp16->f32(d_b) (ggml dequantize_row_q8_0). */
+void tcrv_oracle_dequantize_row_q8_0(size_t n, float *y, const uint8_t *vx);
+
+/* a4: the packed-i4 offset-binary x i8 integer core for one Q4_0 block against
+ * one Q8_0 block (RVVToEmitC.cpp:2524-2589). */
+int32_t tcrv_oracle_q4_0_q8_0_block_sumi(const uint8_t *xb, const uint8_t *yb);
+/* a5's integer core for one block pair. */
+int32_t tcrv_oracle_q8_0_q8_0_block_sumi(const uint8_t *xb, const uint8_t *yb);
+
+/* Per-block integer sums of a whole row pair (nb = n/32 values). */
+void tcrv_oracle_block_sums_q8_0_q8_0(size_t n, int32_t *sumi, const uint8_t *vx,
+                                      const uint8_t *vy);
+void tcrv_oracle_block_sums_q4_0_q8_0(size_t n, int32_t *sumi, const uint8_t *vx,
+                                      const uint8_t *vy);
+
+/* a5: ggml_vec_dot_q8_0_q8_0; fold sumf = fma((float)sumi, d_x*d_y, sumf)
+ * (RVVToEmitCBlockQuantLinear.cpp:7538-7575). */
+void tcrv_oracle_vec_dot_q8_0_q8_0(size_t n, float *s, const uint8_t *vx,
+                                   const uint8_t *vy);
+/* a6: ggml_vec_dot_q4_0_q8_0 with the ggml vec_dot ABI; fold
+ * sumf = fma((float)sumi*d_x, d_y, sumf) (RVVToEmitCBlockQuantLinear.cpp:322-356). */
+void tcrv_oracle_vec_dot_q4_0_q8_0(size_t n, float *s, size_t bs, const uint8_t *vx,
+                                   size_t bx, const uint8_t *vy, size_t by, int32_t nrc);
+
+/* Batched independent row pairs: s[r] = vec_dot(vx + r*bx, vy + r*by).
+ * nthreads <= 1 runs serially; otherwise OpenMP over rows (each row's fold stays
+ * serial, so the result is identical for every thread count). */
+void tcrv_oracle_vec_dot_q8_0_q8_0_rows(size_t n, float *s, const uint8_t *vx, size_t bx,
+                                        const uint8_t *vy, size_t by, size_t nrows,
+                                        int nthreads);
+void tcrv_oracle_vec_dot_q4_0_q8_0_rows(size_t n, float *s, const uint8_t *vx, size_t bx,
+                                        const uint8_t *vy, size_t by, size_t nrows,
+                                        int nthreads);
+
+/* a7: tcrv_rvv.q4_0_q8_0_gemm, s[ir*bs + col] = a6(vx + ir*bx, vy + col*by)
+ * (RVVToEmitCBlockQuantLinear.cpp:1691-2121). nc = 1 is the decode GEMV. */
+void tcrv_oracle_gemm_q4_0_q8_0(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
+                                size_t by, size_t nr, size_t nc, size_t bx, size_t bs,
+                                int nthreads);
+/* a9: the Q8_0 x Q8_0 GEMM with the same loop nest and ABI, elements = a5. */
+void tcrv_oracle_gemm_q8_0_q8_0(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
+                                size_t by, size_t nr, size_t nc, size_t bx, size_t bs,
+                                int nthreads);
+
+/* a10: tcrv_rvv.quantize_row_q8_0 (RVVOps.td:8345-8431). */
+void tcrv_oracle_quantize_row_q8_0(size_t n, const float *x, uint8_t *vy);
+/* a11: ggml quantize_row_q4_0_ref (d = max/-8, q = min(15, (int8)(x*id + 8.5f))). */
+void tcrv_oracle_quantize_row_q4_0(size_t n, const float *x, uint8_t *vy);
+
+/* a8: make_block_q4_0x16 (RVVOps.td:4551-4626) over nblocks output blocks, each
+ * built from 16 consecutive source blocks. */
+void tcrv_oracle_pack_q4_0_to_q4_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst);
+/* a8: repack GEMV over x16 weights; fold fma((float)sumi, d_w*d_a, acc)
+ * (RVVToEmitCBlockQuantLinear.cpp:3245-3290). s[x*16 + r] for x < nc/16. */
+void tcrv_oracle_repack_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx,
+                                       const uint8_t *vy, size_t nc);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TCRV_ORACLE_H */

@@ -1,0 +1,34 @@
+"""Small helpers for the GPU parity tests (device copies, bit comparisons)."""
+import numpy as np
+
+
+def to_dev(a: np.ndarray, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def empty_dev(shape, dtype, dev):
+    import torch
+    return torch.empty(shape, dtype=dtype, device=dev)
+
+
+def from_dev(t) -> np.ndarray:
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def assert_f32_parity(got: np.ndarray, want: np.ndarray, rtol: float = 1e-5, what: str = ""):
+    """The bar: within rtol AND bit-identical, since
+    every kernel reproduces the reference fold order with the same fmaf."""
+    got = np.asarray(got, dtype=np.float32).reshape(-1)
+    want = np.asarray(want, dtype=np.float32).reshape(-1)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    denom = np.maximum(np.abs(want), np.float32(1e-30))
+    rel = np.abs(got.astype(np.float64) - want) / denom
+    bad = np.flatnonzero(rel > rtol)
+    assert bad.size == 0, (f"{what}: {bad.size} elements beyond rtol {rtol}; first at "
+                           f"{bad[0]}: got {got[bad[0]]!r} want {want[bad[0]]!r}")
+    diff = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+    assert diff.size == 0, (f"{what}: {diff.size} elements not bit-identical; first at "
+                            f"{diff[0]}: got {got[diff[0]]!r} want {want[diff[0]]!r}")

@@ -1,0 +1,76 @@
+"""CPU checks of the C-ABI boundary: libtcrv_hip.so loads without a GPU,
+exports exactly the symbols include/tcrv_hip.h declares, and rejects bad
+arguments before any launch (host logic only; no kernel runs here)."""
+import os
+import re
+import subprocess
+
+import pytest
+
+import tcrv_hip
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tcrv_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"TCRV_HIP_API\s+[\w\s\*]*?\b(tcrv_hip_\w+)\s*\(", text)))
+
+
+def exported_symbols():
+    out = subprocess.run(["nm", "-D", "--defined-only", tcrv_hip.LIB_PATH],
+                         capture_output=True, text=True, check=True).stdout
+    return sorted({line.split()[-1] for line in out.splitlines()
+                   if line.split() and line.split()[-1].startswith("tcrv_")})
+
+
+def test_library_is_built():
+    assert os.path.exists(tcrv_hip.LIB_PATH), "run __graft_entry__.build()"
+
+
+def test_exports_exactly_the_header():
+    decl = declared_symbols()
+    assert len(decl) >= 15
+    assert exported_symbols() == decl
+
+
+def test_binding_covers_the_header():
+    bound = set(tcrv_hip.SIGNATURES) | set(tcrv_hip.STRING_FUNCS)
+    assert bound == set(declared_symbols())
+
+
+def test_loads_and_reports_version_without_gpu():
+    tcrv_hip.load()
+    assert tcrv_hip.version().startswith("tcrv_hip")
+    assert tcrv_hip.status_string(0) == "ok"
+    assert "aligned" in tcrv_hip.status_string(tcrv_hip.ERR_MISALIGNED)
+
+
+@pytest.mark.parametrize("name,args,want", [
+    # null pointers
+    ("tcrv_hip_add_f32", (0, 16, 32, 8, 0), tcrv_hip.ERR_NULL_POINTER),
+    ("tcrv_hip_q8_0_q8_0_gemm", (64, 0, 256, 512, 80, 2, 2, 80, 2, 0), tcrv_hip.ERR_NULL_POINTER),
+    # misalignment (fake device addresses: rejected before any launch)
+    ("tcrv_hip_add_f32", (2, 16, 32, 8, 0), tcrv_hip.ERR_MISALIGNED),
+    ("tcrv_hip_dequantize_row_q8_0", (8, 256, 64, 0), tcrv_hip.ERR_MISALIGNED),
+    ("tcrv_hip_q8_0_q8_0_gemm", (64, 256, 264, 512, 80, 2, 2, 80, 2, 0), tcrv_hip.ERR_MISALIGNED),
+    # bad strides / output row stride
+    ("tcrv_hip_q8_0_q8_0_gemm", (64, 256, 256, 512, 70, 2, 2, 80, 2, 0), tcrv_hip.ERR_BAD_SIZE),
+    ("tcrv_hip_q8_0_q8_0_gemm", (64, 256, 256, 512, 80, 2, 2, 80, 1, 0), tcrv_hip.ERR_BAD_SIZE),
+    ("tcrv_hip_q4_0_q8_0_block_dot_rows", (64, 256, 256, 24, 512, 80, 3, 0),
+     tcrv_hip.ERR_BAD_SIZE),
+    ("tcrv_hip_gemv_q4_0_q8_0", (64, 256, 512, 40, 1024, 3, 0), tcrv_hip.ERR_BAD_SIZE),
+])
+def test_argument_errors_before_launch(name, args, want):
+    assert tcrv_hip.call(name, *args, check=False) == want
+
+
+@pytest.mark.parametrize("name,args", [
+    ("tcrv_hip_q8_0_q8_0_gemm", (64, 256, 256, 512, 80, 0, 2, 80, 2, 0)),
+    ("tcrv_hip_q8_0_q8_0_gemm", (64, 256, 256, 512, 80, 2, 0, 80, 2, 0)),
+    ("tcrv_hip_q4_0_q8_0_block_sums", (16, 256, 256, 18, 512, 34, 4, 0)),
+    ("tcrv_hip_add_f32", (256, 256, 256, 0, 0)),
+])
+def test_empty_problems_are_no_ops(name, args):
+    assert tcrv_hip.call(name, *args, check=False) == tcrv_hip.OK

@@ -1,0 +1,425 @@
+"""Pins the CPU oracle (oracle/libtcrv_oracle.so) before it is trusted.
+
+Each test checks one oracle function against something fixed independently of
+it: the reference's own add harness vector, IEEE conversions done by numpy,
+exhaustive or brute-force integer sums, exact rational folds (tests/exact.py),
+closed forms, and planted mistakes that must be caught.
+"""
+import numpy as np
+import pytest
+
+import exact
+import synth
+
+pytestmark = []
+
+RNG = np.random.default_rng(12345)
+
+
+def rand_q8_blocks(nb, rng=RNG, dmin=-14, dmax=-4):
+    """Random block_q8_0 bytes: fp16 d = +-2^k * m, random int8 quants."""
+    out = np.zeros((nb, 34), dtype=np.uint8)
+    d = (rng.uniform(0.5, 1.0, nb) * 2.0 ** rng.integers(dmin, dmax, nb)).astype(np.float16)
+    out[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    out[:, 2:] = rng.integers(0, 256, (nb, 32), dtype=np.uint8)
+    return out.reshape(-1)
+
+
+def rand_q4_blocks(nb, rng=RNG):
+    out = np.zeros((nb, 18), dtype=np.uint8)
+    d = (rng.uniform(0.5, 1.0, nb) * 2.0 ** rng.integers(-12, -2, nb)).astype(np.float16)
+    out[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    out[:, 2:] = rng.integers(0, 256, (nb, 16), dtype=np.uint8)
+    return out.reshape(-1)
+
+
+def q8_fields(blocks):
+    b = blocks.reshape(-1, 34)
+    d = b[:, 0:2].copy().view(np.float16).reshape(-1).astype(np.float32)
+    q = b[:, 2:].view(np.int8).astype(np.int64)
+    return d, q
+
+
+def q4_fields(blocks):
+    b = blocks.reshape(-1, 18)
+    d = b[:, 0:2].copy().view(np.float16).reshape(-1).astype(np.float32)
+    qs = b[:, 2:].astype(np.int64)
+    vals = np.concatenate([(qs & 15) - 8, (qs >> 4) - 8], axis=1)  # element j, j+16
+    return d, vals
+
+
+# ---------------------------------------------------------------- formats ---
+
+def test_block_format_sizes():
+    # verifier constants: qk 32, strides 34 / 18 / 288 (RVVDialectWideningOps.cpp:3358-3372,
+    # RVVOps.td:3893-3897, :4569-4576)
+    assert synth.Q8_0_BLOCK_BYTES == 2 + 32
+    assert synth.Q4_0_BLOCK_BYTES == 2 + 16
+    assert 16 * 2 + 16 * 16 == 288
+
+
+def test_fp16_to_f32_exhaustive(oracle):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([oracle.fp16_to_f32(int(v)) for v in h], dtype=np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_fp16_round_nearest_even(oracle):
+    rng = np.random.default_rng(7)
+    bits = rng.integers(0, 2 ** 32, 60000, dtype=np.uint64).astype(np.uint32)
+    # concentrate on the fp16 range, subnormals and exact ties
+    f = bits.view(np.float32)
+    f = np.concatenate([
+        f[np.isfinite(f)][:20000],
+        rng.normal(0, 1, 20000).astype(np.float32),
+        (rng.uniform(-1, 1, 5000) * 2.0 ** -20).astype(np.float32),
+        np.array([65504, 65519.996, 65520, 65536, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -25,
+                  2.0 ** -26, 1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, -0.0, 0.0,
+                  np.inf, -np.inf], dtype=np.float32),
+    ])
+    ties = (np.arange(-2000, 2000) * 2.0 + 1) * 2.0 ** -11  # halfway between fp16 values
+    f = np.concatenate([f, ties.astype(np.float32)])
+    want = f.astype(np.float16).view(np.uint16)
+    got = np.array([oracle.f32_to_fp16(float(v)) for v in f], dtype=np.uint16)
+    assert np.array_equal(got, want)
+
+
+# -------------------------------------------------------------------- a1 ---
+
+def test_add_i32_harness_vector(oracle):
+    # examples/qemu/harness_add.cpp:14-21: lhs = 3i-17, rhs = 41-2i, n = 1031,
+    # scalar oracle lhs+rhs.  The closed form is i + 24.
+    n = 1031
+    i = np.arange(n, dtype=np.int64)
+    lhs = (3 * i - 17).astype(np.int32)
+    rhs = (41 - 2 * i).astype(np.int32)
+    out = oracle.add_i32(lhs, rhs)
+    assert np.array_equal(out, (i + 24).astype(np.int32))
+
+
+def test_add_f32_closed_form(oracle):
+    a = synth.uniform_f32(1001, 4099)
+    b = synth.uniform_f32(1002, 4099)
+    out = oracle.add_f32(a, b)
+    assert np.array_equal(out.view(np.uint32), (a + b).view(np.uint32))
+
+
+# -------------------------------------------------------------------- a3 ---
+
+def test_dequant_closed_form(oracle):
+    blocks = rand_q8_blocks(300)
+    # special blocks: d = 0, subnormal d, full int8 range
+    b = blocks.reshape(-1, 34)
+    b[0, 0:2] = 0
+    b[1, 0:2] = np.array([1], dtype=np.uint16).view(np.uint8)  # smallest subnormal
+    b[2, 2:] = np.arange(-128, 128, 8, dtype=np.int8).view(np.uint8)
+    n = 300 * 32
+    y = oracle.dequantize_row_q8_0(blocks, n)
+    d, q = q8_fields(blocks)
+    want = (q.astype(np.float32) * d[:, None]).reshape(-1)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+    assert not np.any(y[:32])
+
+
+# -------------------------------------------------------------------- a4 ---
+
+def test_q4_integer_core_exhaustive_weight_bytes(oracle):
+    rng = np.random.default_rng(3)
+    for w in range(256):
+        xb = np.zeros(18, dtype=np.uint8)
+        xb[2:] = w
+        lo, hi = (w & 15) - 8, (w >> 4) - 8
+        for _ in range(4):
+            yb = rand_q8_blocks(1, rng)
+            q = yb[2:].view(np.int8).astype(np.int64)
+            want = int(lo * q[:16].sum() + hi * q[16:].sum())
+            assert oracle.q4_block_sumi(xb, yb) == want
+
+
+def test_q4_integer_core_bounds(oracle):
+    xb = np.zeros(18, dtype=np.uint8)  # every nibble 0 -> value -8
+    yb = np.zeros(34, dtype=np.uint8)
+    yb[2:] = np.uint8(0x80)  # -128
+    assert oracle.q4_block_sumi(xb, yb) == 32 * 8 * 128
+
+
+def test_q4_block_sums_bruteforce(oracle):
+    nb = 64
+    vx, vy = rand_q4_blocks(nb), rand_q8_blocks(nb)
+    _, xv = q4_fields(vx)
+    _, yq = q8_fields(vy)
+    want = (xv * yq).sum(axis=1)
+    assert np.array_equal(oracle.block_sums_q4_0(nb * 32, vx, vy), want.astype(np.int32))
+
+
+# -------------------------------------------------------------------- a5 ---
+
+def test_q8_block_sums_bruteforce_and_bounds(oracle):
+    nb = 96
+    vx, vy = rand_q8_blocks(nb), rand_q8_blocks(nb)
+    vx.reshape(-1, 34)[0, 2:] = 0x80
+    vy.reshape(-1, 34)[0, 2:] = 0x80
+    _, xq = q8_fields(vx)
+    _, yq = q8_fields(vy)
+    want = (xq * yq).sum(axis=1)
+    got = oracle.block_sums_q8_0(nb * 32, vx, vy)
+    assert np.array_equal(got, want.astype(np.int32))
+    assert got[0] == 524288
+
+
+def exact_fold_q8(vx, vy, nb):
+    dx, xq = q8_fields(vx)
+    dy, yq = q8_fields(vy)
+    acc = np.float32(0.0)
+    for b in range(nb):
+        s = int((xq[b] * yq[b]).sum())
+        acc = exact.fma32(np.float32(s), exact.mul32(dx[b], dy[b]), acc)
+    return acc
+
+
+def exact_fold_q4(vx, vy, nb):
+    dx, xv = q4_fields(vx)
+    dy, yq = q8_fields(vy)
+    acc = np.float32(0.0)
+    for b in range(nb):
+        s = int((xv[b] * yq[b]).sum())
+        acc = exact.fma32(exact.mul32(np.float32(s), dx[b]), dy[b], acc)
+    return acc
+
+
+def test_exact_helper_matches_ieee():
+    rng = np.random.default_rng(11)
+    a = rng.normal(size=500).astype(np.float32)
+    b = rng.normal(size=500).astype(np.float32)
+    for x, y in zip(a, b):
+        assert exact.mul32(x, y) == np.float32(x * y)  # numpy float32 mul is IEEE
+        assert exact.fma32(x, np.float32(1.0), y) == np.float32(x + y)
+
+
+def test_q8_fold_single_block_closed_form(oracle):
+    for seed in range(20):
+        rng = np.random.default_rng(seed)
+        vx, vy = rand_q8_blocks(1, rng), rand_q8_blocks(1, rng)
+        dx, xq = q8_fields(vx)
+        dy, yq = q8_fields(vy)
+        s = int((xq * yq).sum())
+        # one block: round(S * (dx*dy)), dx*dy exact in binary32 and S*dx*dy exact in binary64
+        want = np.float32(float(s) * (float(dx[0]) * float(dy[0])))
+        assert oracle.vec_dot_q8_0(32, vx, vy) == want
+    assert oracle.vec_dot_q8_0(0, vx, vy) == 0.0
+    assert oracle.vec_dot_q8_0(31, vx, vy) == 0.0  # nb = n/32 drops the remainder
+
+
+def test_q8_fold_matches_exact_and_catches_mistakes(oracle):
+    nb = 8
+    mism_rev = mism_q4order = mism_unfused = 0
+    for seed in range(40):
+        rng = np.random.default_rng(100 + seed)
+        vx, vy = rand_q8_blocks(nb, rng, -3, 2), rand_q8_blocks(nb, rng, -3, 2)
+        want = exact_fold_q8(vx, vy, nb)
+        got = oracle.vec_dot_q8_0(nb * 32, vx, vy)
+        assert got.view(np.uint32) == np.float32(want).view(np.uint32)
+        # planted mistakes (CPU-only variants of the fold) must change some results
+        dx, xq = q8_fields(vx)
+        dy, yq = q8_fields(vy)
+        sums = [(xq[b] * yq[b]).sum() for b in range(nb)]
+        acc = np.float32(0)
+        for b in reversed(range(nb)):
+            acc = exact.fma32(np.float32(sums[b]), exact.mul32(dx[b], dy[b]), acc)
+        mism_rev += acc != want
+        acc = np.float32(0)
+        for b in range(nb):
+            acc = exact.fma32(exact.mul32(np.float32(sums[b]), dx[b]), dy[b], acc)
+        mism_q4order += acc != want
+        acc = np.float32(0)
+        for b in range(nb):
+            acc = np.float32(acc + exact.mul32(np.float32(sums[b]), exact.mul32(dx[b], dy[b])))
+        mism_unfused += acc != want
+    assert mism_rev > 0 and mism_q4order > 0 and mism_unfused > 0
+
+
+def test_q8_fold_fp64_error_bound(oracle):
+    n, rows = 4096, 16
+    vx = synth.q8_0_matrix(rows, n, 1004, 1.0)
+    vy = synth.q8_0_matrix(rows, n, 1005, 1.0)
+    got = oracle.vec_dot_q8_0_rows(n, vx, vx.shape[1], vy, vy.shape[1], rows)
+    nb = n // 32
+    for r in range(rows):
+        dx, xq = q8_fields(vx[r])
+        dy, yq = q8_fields(vy[r])
+        terms = (xq * yq).sum(axis=1).astype(np.float64) * (dx.astype(np.float64) * dy)
+        exact_sum = terms.sum()
+        bound = np.abs(terms).sum() * nb * 2.0 ** -24
+        assert abs(float(got[r]) - exact_sum) <= bound
+
+
+# -------------------------------------------------------------------- a6 ---
+
+def test_q4_fold_matches_exact_and_catches_mistakes(oracle):
+    nb = 8
+    mism_q8order = 0
+    for seed in range(40):
+        rng = np.random.default_rng(200 + seed)
+        vx, vy = rand_q4_blocks(nb, rng), rand_q8_blocks(nb, rng, -3, 2)
+        if seed % 2:
+            # correlated signs give |sumi| ~ 2^14, so fl(sumi*d_x) really rounds
+            _, xv = q4_fields(vx)
+            mag = rng.integers(100, 128, xv.shape)
+            yb = vy.reshape(nb, 34)
+            yb[:, 2:] = (np.where(xv < 0, -mag, mag)).astype(np.int8).view(np.uint8)
+        want = exact_fold_q4(vx, vy, nb)
+        got = oracle.vec_dot_q4_0(nb * 32, vx, vy)
+        assert got.view(np.uint32) == np.float32(want).view(np.uint32)
+        dx, xv = q4_fields(vx)
+        dy, yq = q8_fields(vy)
+        acc = np.float32(0)
+        for b in range(nb):
+            s = (xv[b] * yq[b]).sum()
+            acc = exact.fma32(np.float32(s), exact.mul32(dx[b], dy[b]), acc)
+        mism_q8order += acc != want
+    assert mism_q8order > 0
+
+
+def test_q4_fold_single_block(oracle):
+    rng = np.random.default_rng(5)
+    vx, vy = rand_q4_blocks(1, rng), rand_q8_blocks(1, rng)
+    dx, xv = q4_fields(vx)
+    dy, yq = q8_fields(vy)
+    s = int((xv * yq).sum())
+    want = exact.fma32(exact.mul32(np.float32(s), dx[0]), dy[0], np.float32(0))
+    assert oracle.vec_dot_q4_0(32, vx, vy) == want
+
+
+def test_rows_thread_count_invariant(oracle):
+    n, rows = 1024, 64
+    vx = synth.q4_0_matrix(rows, n, 21, 0.02)
+    vy = synth.q8_0_matrix(rows, n, 22, 1.0)
+    a = oracle.vec_dot_q4_0_rows(n, vx, vx.shape[1], vy, vy.shape[1], rows, 1)
+    b = oracle.vec_dot_q4_0_rows(n, vx, vx.shape[1], vy, vy.shape[1], rows, 4)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ----------------------------------------------------------------- a7/a9 ---
+
+@pytest.mark.parametrize("fmt", ["q4", "q8"])
+def test_gemm_elements_are_independent_block_dots(oracle, fmt):
+    n, nr, nc = 96, 5, 3
+    bx_pad, by_pad, bs = 16 if fmt == "q8" else 8, 32, 7
+    xbytes = (n // 32) * (18 if fmt == "q4" else 34)
+    bx = xbytes + bx_pad
+    by = (n // 32) * 34 + by_pad
+    rng = np.random.default_rng(9)
+    vx = rng.integers(0, 256, nr * bx, dtype=np.uint8)
+    vy = rng.integers(0, 256, nc * by, dtype=np.uint8)
+    for r in range(nr):  # sane fp16 scales
+        for b in range(n // 32):
+            o = r * bx + b * (18 if fmt == "q4" else 34)
+            vx[o:o + 2] = np.array([rng.uniform(0.01, 0.1)], np.float16).view(np.uint8)
+    for c in range(nc):
+        for b in range(n // 32):
+            o = c * by + b * 34
+            vy[o:o + 2] = np.array([rng.uniform(0.01, 0.1)], np.float16).view(np.uint8)
+    gemm = oracle.gemm_q4_0 if fmt == "q4" else oracle.gemm_q8_0
+    dot = oracle.vec_dot_q4_0 if fmt == "q4" else oracle.vec_dot_q8_0
+    s = gemm(n, vx, vy, by, nr, nc, bx, bs)
+    for r in range(nr):
+        for c in range(nc):
+            x = np.ascontiguousarray(vx[r * bx:r * bx + xbytes])
+            y = np.ascontiguousarray(vy[c * by:c * by + (n // 32) * 34])
+            assert s[r * bs + c] == dot(n, x, y)
+
+
+def test_gemm_q8_tiny_bruteforce(oracle):
+    n, nr, nc = 64, 6, 4
+    vx = synth.q8_0_matrix(nr, n, 31, 0.02)
+    vy = synth.q8_0_matrix(nc, n, 32, 1.0)
+    s = oracle.gemm_q8_0(n, vx, vy, vy.shape[1], nr, nc, vx.shape[1], nc)
+    for r in range(nr):
+        for c in range(nc):
+            assert s[r * nc + c] == np.float32(exact_fold_q8(vx[r], vy[c], n // 32))
+
+
+# ---------------------------------------------------------------- a10/a11 ---
+
+def test_quantize_q8_0_closed_form_and_special_cases(oracle):
+    x = synth.normal_f32(77, 32 * 200, 0.0, 1.0)
+    x[:32] = 0.0                      # all-zero block: d = 0, id = 0, q = 0
+    x[32:64] = np.arange(32) - 15.5   # halves: x*id ties for some lanes
+    x[64:96] = 1e-30                  # tiny: d underflows to fp16 zero, q = 127
+    got = oracle.quantize_q8_0(x)
+    assert np.array_equal(got, synth.quantize_q8_0(x))
+    blocks = got.reshape(-1, 34)
+    assert not blocks[0].any()
+    amax_lane = np.abs(x.reshape(-1, 32)).argmax(axis=1)
+    q = blocks[:, 2:].view(np.int8)
+    assert np.all(np.abs(q[np.arange(200), amax_lane][1:]) == 127)
+    # round trip: |dequant(quant(x)) - x| <= d/2 + fp16 rounding of d
+    d = blocks[:, 0:2].copy().view(np.float16).reshape(-1).astype(np.float32)
+    deq = oracle.dequantize_row_q8_0(got, x.size).reshape(-1, 32)
+    err = np.abs(deq - x.reshape(-1, 32))[3:]
+    assert np.all(err <= d[3:, None] * 0.5 + np.abs(x.reshape(-1, 32)[3:]) * 2e-3)
+
+
+def test_quantize_q8_0_rne_ties(oracle):
+    # amax = 127 -> d = 1, id = 1, so q = rne(x): 0.5 -> 0, 1.5 -> 2, 2.5 -> 2, -0.5 -> -0
+    x = np.zeros(32, dtype=np.float32)
+    x[0] = 127.0
+    x[1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 3.5, 126.5]
+    q = oracle.quantize_q8_0(x)[2:].view(np.int8)
+    assert list(q[:9]) == [127, 0, 2, 2, 0, -2, -2, 4, 126]
+
+
+def test_quantize_q4_0_matches_host_quantizer(oracle):
+    x = synth.normal_f32(1006, 32 * 500, 0.0, 0.02)
+    x[:32] = 0.0
+    got = oracle.quantize_q4_0(x)
+    assert np.array_equal(got, synth.quantize_q4_0(x))
+    # the element of largest magnitude maps to nibble 0 (value -8): x = max = -8*d
+    b = got.reshape(-1, 18)
+    idx = np.abs(x.reshape(-1, 32)).argmax(axis=1)
+    nib = np.where(idx < 16, b[np.arange(500), 2 + idx % 16] & 15,
+                   b[np.arange(500), 2 + idx % 16] >> 4)
+    assert np.all(nib[1:] == 0)
+
+
+# -------------------------------------------------------------------- a8 ---
+
+def unpack_q4_0x16(packed, nblocks):
+    out = np.zeros((nblocks * 16, 18), dtype=np.uint8)
+    p = packed.reshape(nblocks, 288)
+    for o in range(nblocks):
+        for i in range(16):
+            out[o * 16 + i, 0:2] = p[o, 2 * i:2 * i + 2]
+        qs = p[o, 32:] ^ 0x88
+        for i in range(256):
+            out[o * 16 + i % 16, 2 + i // 16] = qs[i]
+    return out.reshape(-1)
+
+
+def test_pack_q4_0x16_round_trip(oracle):
+    src = rand_q4_blocks(64)
+    packed = oracle.pack_q4_0x16(src, 4)
+    assert np.array_equal(unpack_q4_0x16(packed, 4), src)
+
+
+def test_repack_gemv_alternate_fold(oracle):
+    n, nc = 128, 32
+    nb = n // 32
+    w = synth.q4_0_matrix(nc, n, 41, 0.02)      # nc rows x nb blocks
+    y = synth.q8_0_matrix(1, n, 42, 1.0).reshape(-1)
+    # group x, block b gathers block b of rows 16x..16x+15
+    src = np.concatenate([w[16 * x + r, 18 * b:18 * b + 18]
+                          for x in range(nc // 16) for b in range(nb) for r in range(16)])
+    packed = oracle.pack_q4_0x16(src, (nc // 16) * nb)
+    got = oracle.repack_gemv_q4_0(n, packed, y, nc)
+    dy, yq = q8_fields(y)
+    for row in range(nc):
+        dx, xv = q4_fields(w[row])
+        acc = np.float32(0)
+        for b in range(nb):
+            s = int((xv[b] * yq[b]).sum())
+            acc = exact.fma32(np.float32(s), exact.mul32(dx[b], dy[b]), acc)
+        assert got[row] == acc

@@ -1,0 +1,334 @@
+// block_dot.hip -- the ggml block dots of libtcrv_hip:
+//   a4  packed-i4 offset-binary x i8 integer core (Q4_0 . Q8_0 per block)
+//   a5  tcrv_rvv.q8_0_q8_0_block_dot  (ggml_vec_dot_q8_0_q8_0)
+//   a6  tcrv_rvv.q4_0_q8_0_block_dot  (ggml_vec_dot_q4_0_q8_0)
+// as one wavefront per (x row, y row) pair, plus the per-block int32 sums.
+//
+// Per pair, the wave stages up to 128 blocks of each row through LDS with
+// 128-bit loads, lane l computes the integer sums of blocks 2l and 2l+1
+// (v_dot4_i32_i8), and the fp32 fold runs serially in ascending block order
+// exactly as the reference emits it:
+//   Q8_0: sumf = fma((float)sumi, d_x*d_y, sumf)
+//         (lib/Conversion/RVV/RVVToEmitCBlockQuantLinear.cpp:7538-7575)
+//   Q4_0: sumf = fma(fl((float)sumi*d_x), d_y, sumf)   (same file, :322-356)
+// The kernels are built with -ffp-contract=off and use explicit fmaf, so the
+// compiler cannot re-associate or re-fuse either fold.
+#include "tcrv_hip_internal.h"
+
+namespace tcrv {
+
+enum class DotFmt { kQ8Q8, kQ4Q8 };
+
+constexpr int kChunkBlocks = 128;  // blocks per LDS chunk: 128*34 = 4352 B (16-B multiple)
+
+// One Q8_0 block at block index b of an LDS chunk, read as 9 aligned dwords.
+// Even b starts on a dword (34*b % 4 == 0): the quants sit 2 bytes into the
+// dword run.  Odd b starts 2 bytes into a dword: the quants are dword aligned.
+template <int kParity>
+__device__ __forceinline__ void read_q8_block(const uint8_t *chunk, int b, uint32_t q[8],
+                                              uint32_t &d_bits) {
+  const uint32_t *w = reinterpret_cast<const uint32_t *>(chunk) + ((b * kQ8Bytes) >> 2);
+  uint32_t r[9];
+#pragma unroll
+  for (int k = 0; k < 9; ++k)
+    r[k] = w[k];
+  if constexpr (kParity == 0) {
+    d_bits = r[0] & 0xffffu;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      q[k] = funnel16(r[k], r[k + 1]);
+  } else {
+    d_bits = r[0] >> 16;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      q[k] = r[k + 1];
+  }
+}
+
+// One Q4_0 block (18 B) at block index b of an LDS chunk, read as 5 dwords.
+template <int kParity>
+__device__ __forceinline__ void read_q4_block(const uint8_t *chunk, int b, uint32_t q[4],
+                                              uint32_t &d_bits) {
+  const uint32_t *w = reinterpret_cast<const uint32_t *>(chunk) + ((b * kQ4Bytes) >> 2);
+  uint32_t r[5];
+#pragma unroll
+  for (int k = 0; k < 5; ++k)
+    r[k] = w[k];
+  if constexpr (kParity == 0) {
+    d_bits = r[0] & 0xffffu;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      q[k] = funnel16(r[k], r[k + 1]);
+  } else {
+    d_bits = r[0] >> 16;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      q[k] = r[k + 1];
+  }
+}
+
+// a5 integer core: sum of the 32 int8 products (order-free, exact).
+__device__ __forceinline__ int q8_q8_sumi(const uint32_t qx[8], const uint32_t qy[8]) {
+  int acc = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    acc = sdot4(qx[k], qy[k], acc);
+  return acc;
+}
+
+// a4 integer core: byte j of the Q4_0 quants holds element j (low nibble) and
+// element j+16 (high nibble), each offset-binary (value = nibble - 8); they
+// pair with Q8_0 quants j and j+16 (RVVToEmitC.cpp:2524-2589).
+__device__ __forceinline__ int q4_q8_sumi(const uint32_t qx[4], const uint32_t qy[8]) {
+  int acc = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    acc = sdot4(nibbles_to_i8x4(qx[k]), qy[k], acc);
+    acc = sdot4(nibbles_to_i8x4(qx[k] >> 4), qy[k + 4], acc);
+  }
+  return acc;
+}
+
+// Integer sum + fold operands of block b for this lane.  The fold is
+// fmaf(t.x, t.y, sumf) for both formats:
+//   Q8_0: t = { (float)sumi, d_x*d_y }   (d_x*d_y is exact: two 11-bit significands)
+//   Q4_0: t = { fl((float)sumi*d_x), d_y }
+template <DotFmt F, int kParity>
+__device__ __forceinline__ float2 block_terms(const uint8_t *xc, const uint8_t *yc, int b,
+                                              int &sumi) {
+  uint32_t qy[8], dy_bits;
+  read_q8_block<kParity>(yc, b, qy, dy_bits);
+  const float dy = fp16_bits_to_f32(dy_bits);
+  if constexpr (F == DotFmt::kQ8Q8) {
+    uint32_t qx[8], dx_bits;
+    read_q8_block<kParity>(xc, b, qx, dx_bits);
+    sumi = q8_q8_sumi(qx, qy);
+    const float dx = fp16_bits_to_f32(dx_bits);
+    return make_float2(static_cast<float>(sumi), dx * dy);
+  } else {
+    uint32_t qx[4], dx_bits;
+    read_q4_block<kParity>(xc, b, qx, dx_bits);
+    sumi = q4_q8_sumi(qx, qy);
+    const float dx = fp16_bits_to_f32(dx_bits);
+    return make_float2(static_cast<float>(sumi) * dx, dy);
+  }
+}
+
+// One wave (64 threads) per pair p.  ncols == 0: x row p, y row p, output
+// s[p].  ncols > 0: x row p / ncols, y row p % ncols, output
+// s[(p / ncols) * bs + p % ncols] (the reference GEMM's loop nest).
+// kSums: write sumi[p*nb + b] instead of the fold.
+template <DotFmt F, bool kSums>
+__global__ __launch_bounds__(64) void block_dot_pairs(size_t nb, float *s, int32_t *sums,
+                                                      const uint8_t *vx, size_t bx,
+                                                      const uint8_t *vy, size_t by,
+                                                      size_t ncols, size_t bs) {
+  constexpr int kXBytes = F == DotFmt::kQ8Q8 ? kQ8Bytes : kQ4Bytes;
+  // +16: the last even block's 9th dword (or 5th) reads 2 bytes past its end.
+  __shared__ __align__(16) uint8_t xl[kChunkBlocks * kXBytes + 16];
+  __shared__ __align__(16) uint8_t yl[kChunkBlocks * kQ8Bytes + 16];
+  __shared__ float2 terms[kChunkBlocks];
+
+  const size_t p = blockIdx.x;
+  size_t xr = p, yr = p, oi = p;
+  if (ncols != 0) {
+    xr = p / ncols;
+    yr = p - xr * ncols;
+    oi = xr * bs + yr;
+  }
+  const uint8_t *xrow = vx + xr * bx;
+  const uint8_t *yrow = vy + yr * by;
+  const int l = threadIdx.x;
+  float sumf = 0.0f;
+
+  for (size_t c0 = 0; c0 < nb; c0 += kChunkBlocks) {
+    const int nbc = static_cast<int>(min(static_cast<size_t>(kChunkBlocks), nb - c0));
+    copy_span_to_lds(xl, xrow + c0 * kXBytes, nbc * kXBytes, l, 64);
+    copy_span_to_lds(yl, yrow + c0 * kQ8Bytes, nbc * kQ8Bytes, l, 64);
+    __syncthreads();
+    {
+      int sumi;
+      const int b0 = 2 * l;
+      if (b0 < nbc) {
+        const float2 t = block_terms<F, 0>(xl, yl, b0, sumi);
+        if constexpr (kSums)
+          sums[p * nb + c0 + b0] = sumi;
+        else
+          terms[b0] = t;
+      }
+      const int b1 = 2 * l + 1;
+      if (b1 < nbc) {
+        const float2 t = block_terms<F, 1>(xl, yl, b1, sumi);
+        if constexpr (kSums)
+          sums[p * nb + c0 + b1] = sumi;
+        else
+          terms[b1] = t;
+      }
+    }
+    __syncthreads();
+    if constexpr (!kSums) {
+      // Serial ascending fold; every lane computes it (LDS broadcast reads).
+#pragma unroll 8
+      for (int b = 0; b < nbc; ++b) {
+        const float2 t = terms[b];
+        sumf = fmaf(t.x, t.y, sumf);
+      }
+      __syncthreads();
+    }
+  }
+  if constexpr (!kSums) {
+    if (l == 0)
+      s[oi] = sumf;
+  }
+}
+
+}  // namespace tcrv
+
+namespace tcrv_host {
+
+using tcrv::DotFmt;
+
+template <DotFmt F>
+int launch_pairs(size_t n, float *s, int32_t *sums, const uint8_t *vx, size_t bx,
+                 const uint8_t *vy, size_t by, size_t npairs, size_t ncols, size_t bs,
+                 void *stream) {
+  const size_t nb = n / tcrv::kQK;
+  if (nb == 0 || npairs == 0)
+    return TCRV_HIP_OK;  // the reference writes sumf = 0 for nb == 0; see callers
+  if (!vx || !vy || (!s && !sums))
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned16(vx) || !aligned16(vy))
+    return TCRV_HIP_ERR_MISALIGNED;
+  const size_t xrows = ncols ? npairs / ncols : npairs;
+  const size_t yrows = ncols ? ncols : npairs;
+  const size_t xbytes = nb * (F == DotFmt::kQ8Q8 ? tcrv::kQ8Bytes : tcrv::kQ4Bytes);
+  if ((xrows > 1 && (bx % 16 != 0 || bx < xbytes)) ||
+      (yrows > 1 && (by % 16 != 0 || by < nb * tcrv::kQ8Bytes)))
+    return TCRV_HIP_ERR_BAD_SIZE;
+  if (npairs > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  hipStream_t st = as_stream(stream);
+  if (sums)
+    tcrv::block_dot_pairs<F, true><<<dim3(static_cast<unsigned>(npairs)), dim3(64), 0, st>>>(
+        nb, s, sums, vx, bx, vy, by, ncols, bs);
+  else
+    tcrv::block_dot_pairs<F, false><<<dim3(static_cast<unsigned>(npairs)), dim3(64), 0, st>>>(
+        nb, s, sums, vx, bx, vy, by, ncols, bs);
+  return launch_status();
+}
+
+}  // namespace tcrv_host
+
+// Zero-block calls: the reference still stores sumf = 0.0f (nb = 0 skips the
+// loop, then *s = sumf).  A tiny kernel keeps that observable behaviour.
+namespace {
+__global__ void store_zeros(float *s, size_t count, size_t stride, size_t ncols) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < count) {
+    const size_t r = ncols ? i / ncols : i;
+    const size_t c = ncols ? i - r * ncols : 0;
+    s[ncols ? r * stride + c : i] = 0.0f;
+  }
+}
+
+}  // namespace
+
+namespace tcrv_host {
+
+int zero_outputs(float *s, size_t count, size_t stride, size_t ncols, void *stream) {
+  if (count == 0)
+    return TCRV_HIP_OK;
+  if (!s)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  const size_t grid = (count + 255) / 256;
+  if (grid > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  store_zeros<<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, as_stream(stream)>>>(
+      s, count, stride, ncols);
+  return launch_status();
+}
+
+int q4_0_grid(size_t n, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by,
+              size_t nr, size_t nc, size_t bs, void *stream) {
+  if (n / tcrv::kQK == 0)
+    return zero_outputs(s, nr * nc, bs, nc, stream);
+  if (!s)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  return launch_pairs<tcrv::DotFmt::kQ4Q8>(n, s, nullptr, vx, bx, vy, by, nr * nc, nc, bs,
+                                           stream);
+}
+
+}  // namespace tcrv_host
+
+using tcrv_host::zero_outputs;
+
+extern "C" {
+
+int tcrv_hip_q8_0_q8_0_block_dot(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
+                                 void *stream) {
+  if (n / tcrv::kQK == 0)
+    return zero_outputs(s, 1, 0, 0, stream);
+  if (!s)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  return tcrv_host::launch_pairs<tcrv::DotFmt::kQ8Q8>(n, s, nullptr, vx, 0, vy, 0, 1, 0, 0,
+                                                      stream);
+}
+
+int tcrv_hip_q8_0_q8_0_block_dot_rows(size_t n, float *s, const uint8_t *vx, size_t bx,
+                                      const uint8_t *vy, size_t by, size_t nrows,
+                                      void *stream) {
+  if (n / tcrv::kQK == 0)
+    return zero_outputs(s, nrows, 0, 0, stream);
+  if (!s)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  return tcrv_host::launch_pairs<tcrv::DotFmt::kQ8Q8>(n, s, nullptr, vx, bx, vy, by, nrows,
+                                                      0, 0, stream);
+}
+
+int tcrv_hip_q4_0_q8_0_block_dot(size_t n, float *s, size_t bs, const uint8_t *vx,
+                                 size_t bx, const uint8_t *vy, size_t by, int32_t nrc,
+                                 void *stream) {
+  (void)bs;
+  (void)bx;
+  (void)by;
+  (void)nrc;  // read by neither the reference emitter nor this entry
+  if (n / tcrv::kQK == 0)
+    return zero_outputs(s, 1, 0, 0, stream);
+  if (!s)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  return tcrv_host::launch_pairs<tcrv::DotFmt::kQ4Q8>(n, s, nullptr, vx, 0, vy, 0, 1, 0, 0,
+                                                      stream);
+}
+
+int tcrv_hip_q4_0_q8_0_block_dot_rows(size_t n, float *s, const uint8_t *vx, size_t bx,
+                                      const uint8_t *vy, size_t by, size_t nrows,
+                                      void *stream) {
+  if (n / tcrv::kQK == 0)
+    return zero_outputs(s, nrows, 0, 0, stream);
+  if (!s)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  return tcrv_host::launch_pairs<tcrv::DotFmt::kQ4Q8>(n, s, nullptr, vx, bx, vy, by, nrows,
+                                                      0, 0, stream);
+}
+
+int tcrv_hip_q8_0_q8_0_block_sums(size_t n, int32_t *sumi, const uint8_t *vx, size_t bx,
+                                  const uint8_t *vy, size_t by, size_t nrows, void *stream) {
+  if (n / tcrv::kQK == 0 || nrows == 0)
+    return TCRV_HIP_OK;
+  if (!sumi)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  return tcrv_host::launch_pairs<tcrv::DotFmt::kQ8Q8>(n, nullptr, sumi, vx, bx, vy, by, nrows,
+                                                      0, 0, stream);
+}
+
+int tcrv_hip_q4_0_q8_0_block_sums(size_t n, int32_t *sumi, const uint8_t *vx, size_t bx,
+                                  const uint8_t *vy, size_t by, size_t nrows, void *stream) {
+  if (n / tcrv::kQK == 0 || nrows == 0)
+    return TCRV_HIP_OK;
+  if (!sumi)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  return tcrv_host::launch_pairs<tcrv::DotFmt::kQ4Q8>(n, nullptr, sumi, vx, bx, vy, by, nrows,
+                                                      0, 0, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,268 @@
+// elementwise.hip -- the HBM-streaming kernels of libtcrv_hip:
+//   a1  add_f32                (tcrv_rvv.binary{kind="add"})
+//   a3  dequantize_row_q8_0    (ggml block dequant)
+//   a10 quantize_row_q8_0      (tcrv_rvv.quantize_row_q8_0)
+// plus the library's status/version/synchronize entry points.
+#include "tcrv_hip_internal.h"
+
+namespace {
+
+using namespace tcrv;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 128-bit streaming store (the output is not re-read by this kernel).
+__device__ __forceinline__ void store_stream(float4 v, float4 *p) {
+  const f32x4 x = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(x, reinterpret_cast<f32x4 *>(p));
+}
+
+// ---------------------------------------------------------------------------
+// a1: out[i] = lhs[i] + rhs[i].  The reference emits a VL strip loop of
+// vle32/vfadd/vse32 (lib/Conversion/RVV/RVVToEmitC.cpp:605, :1873-1911); here
+// each thread moves kAddUnroll 128-bit vectors per operand, all loads issued
+// before the adds.  IEEE binary32 addition is correctly rounded, so the result
+// is bit-identical to the scalar loop.
+// ---------------------------------------------------------------------------
+constexpr int kAddThreads = 256;
+constexpr int kAddUnroll = 4;
+
+__global__ __launch_bounds__(kAddThreads) void add_f32_vec4(const float4 *lhs,
+                                                            const float4 *rhs, float4 *out,
+                                                            size_t n4) {
+  const size_t base =
+      static_cast<size_t>(blockIdx.x) * (kAddThreads * kAddUnroll) + threadIdx.x;
+  float4 a[kAddUnroll], b[kAddUnroll];
+#pragma unroll
+  for (int u = 0; u < kAddUnroll; ++u) {
+    const size_t i = base + static_cast<size_t>(u) * kAddThreads;
+    if (i < n4) {
+      a[u] = lhs[i];
+      b[u] = rhs[i];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kAddUnroll; ++u) {
+    const size_t i = base + static_cast<size_t>(u) * kAddThreads;
+    if (i < n4) {
+      float4 r;
+      r.x = a[u].x + b[u].x;
+      r.y = a[u].y + b[u].y;
+      r.z = a[u].z + b[u].z;
+      r.w = a[u].w + b[u].w;
+      store_stream(r, &out[i]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kAddThreads) void add_f32_scalar(const float *lhs, const float *rhs,
+                                                              float *out, size_t begin,
+                                                              size_t n) {
+  const size_t i = begin + static_cast<size_t>(blockIdx.x) * kAddThreads + threadIdx.x;
+  if (i < n)
+    out[i] = lhs[i] + rhs[i];
+}
+
+// ---------------------------------------------------------------------------
+// a3: y[32b+j] = qs_b[j] * d_b.  A work-group stages kDqBlocks contiguous
+// 34-byte blocks (a 16-byte multiple: 128*34 = 4352) through LDS with 128-bit
+// loads, then writes 128-bit float4 rows of the output.  int8 * fp16-valued
+// float is exact in binary32, so the result is bit-exact.
+// ---------------------------------------------------------------------------
+constexpr int kDqThreads = 256;
+constexpr int kDqBlocks = 128;
+
+__global__ __launch_bounds__(kDqThreads) void dequantize_q8_0(const uint8_t *vx, float *y,
+                                                              size_t nb) {
+  __shared__ __align__(16) uint8_t lds[kDqBlocks * kQ8Bytes];
+  const size_t blk0 = static_cast<size_t>(blockIdx.x) * kDqBlocks;
+  const int nblk = static_cast<int>(min(static_cast<size_t>(kDqBlocks), nb - blk0));
+  copy_span_to_lds(lds, vx + blk0 * kQ8Bytes, nblk * kQ8Bytes, threadIdx.x, kDqThreads);
+  __syncthreads();
+  const uint16_t *l16 = reinterpret_cast<const uint16_t *>(lds);
+  float4 *dst = reinterpret_cast<float4 *>(y + blk0 * kQK);
+  const int nf4 = nblk * (kQK / 4);
+  for (int f = threadIdx.x; f < nf4; f += kDqThreads) {
+    const int b = f >> 3;
+    const int j = (f & 7) * 4;
+    const int h = (b * kQ8Bytes) >> 1;  // block start in halfwords
+    const float d = fp16_bits_to_f32(l16[h]);
+    const uint32_t q01 = l16[h + 1 + (j >> 1)];
+    const uint32_t q23 = l16[h + 2 + (j >> 1)];
+    float4 r;
+    r.x = static_cast<float>(static_cast<int8_t>(q01 & 0xffu)) * d;
+    r.y = static_cast<float>(static_cast<int8_t>(q01 >> 8)) * d;
+    r.z = static_cast<float>(static_cast<int8_t>(q23 & 0xffu)) * d;
+    r.w = static_cast<float>(static_cast<int8_t>(q23 >> 8)) * d;
+    store_stream(r, &dst[f]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// a10: f32 -> block_q8_0 (RVVOps.td:8345-8431; ggml riscv/quants.c RVV path).
+// Eight lanes own one 32-float block (one float4 each):
+//   amax = max|x|; d = amax/127.0f; id = d ? 1/d : 0; y.d = (_Float16)d (RNE);
+//   q = (int8)(int16)sat_rne(x*id)   (vfncvt_x_f_w_i16 then vncvt_x_x_w_i8).
+// Division and reciprocal are the correctly rounded IEEE operations, as the
+// reference's scalar `amax / 127.0f` and `1.0f/d` are.  A work-group stages
+// its kQzBlocks output blocks (32*34 = 1088 bytes, a 16-byte multiple) in LDS
+// and writes them with 128-bit stores.
+// ---------------------------------------------------------------------------
+constexpr int kQzThreads = 256;
+constexpr int kQzBlocks = kQzThreads / 8;
+
+__device__ __forceinline__ uint32_t quant_byte(float x, float id) {
+  const float v = x * id;
+  float r = __builtin_rintf(v);  // v_rndne_f32: nearest-even
+  int w;
+  if (v != v)
+    w = 32767;  // RVV float->int conversion of NaN gives the largest value
+  else if (r >= 32767.0f)
+    w = 32767;
+  else if (r <= -32768.0f)
+    w = -32768;
+  else
+    w = static_cast<int>(r);
+  return static_cast<uint32_t>(w) & 0xffu;  // narrowing keeps the low byte
+}
+
+__global__ __launch_bounds__(kQzThreads) void quantize_q8_0(const float *x, uint8_t *vy,
+                                                            size_t nb) {
+  __shared__ __align__(16) uint8_t lds[kQzBlocks * kQ8Bytes];
+  const size_t blk0 = static_cast<size_t>(blockIdx.x) * kQzBlocks;
+  const int nblk = static_cast<int>(min(static_cast<size_t>(kQzBlocks), nb - blk0));
+  const int lb = threadIdx.x >> 3;  // block within the work-group
+  const int part = threadIdx.x & 7; // float4 within the block
+  const bool active = lb < nblk;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (active)
+    v = reinterpret_cast<const float4 *>(x + (blk0 + lb) * kQK)[part];
+  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  // max over the 8 lanes of the block (exact, order-free)
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+  amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+  const float d = __fdiv_rn(amax, 127.0f);
+  const float id = d != 0.0f ? __frcp_rn(d) : 0.0f;
+  if (active) {
+    uint16_t *l16 = reinterpret_cast<uint16_t *>(lds + lb * kQ8Bytes);
+    const uint32_t b0 = quant_byte(v.x, id), b1 = quant_byte(v.y, id);
+    const uint32_t b2 = quant_byte(v.z, id), b3 = quant_byte(v.w, id);
+    l16[1 + part * 2] = static_cast<uint16_t>(b0 | (b1 << 8));
+    l16[2 + part * 2] = static_cast<uint16_t>(b2 | (b3 << 8));
+    if (part == 0)
+      l16[0] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(d));
+  }
+  __syncthreads();
+  const int nbytes = nblk * kQ8Bytes;
+  uint8_t *dst = vy + blk0 * kQ8Bytes;
+  const int nchunks = nbytes >> 4;
+  for (int c = threadIdx.x; c < nchunks; c += kQzThreads)
+    reinterpret_cast<uint4 *>(dst)[c] = reinterpret_cast<const uint4 *>(lds)[c];
+  const int tail = (nbytes - (nchunks << 4)) >> 1;
+  if (static_cast<int>(threadIdx.x) < tail)
+    reinterpret_cast<uint16_t *>(dst + (nchunks << 4))[threadIdx.x] =
+        reinterpret_cast<const uint16_t *>(lds + (nchunks << 4))[threadIdx.x];
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *tcrv_hip_status_string(int status) {
+  switch (status) {
+  case TCRV_HIP_OK:
+    return "ok";
+  case TCRV_HIP_ERR_NULL_POINTER:
+    return "null pointer argument";
+  case TCRV_HIP_ERR_BAD_SIZE:
+    return "size or stride violates the kernel contract";
+  case TCRV_HIP_ERR_MISALIGNED:
+    return "pointer or stride is not aligned as required";
+  case TCRV_HIP_ERR_TOO_LARGE:
+    return "size exceeds the kernel's index range";
+  case TCRV_HIP_ERR_UNSUPPORTED:
+    return "argument combination not supported";
+  default:
+    break;
+  }
+  if (status > 0)
+    return hipGetErrorString(static_cast<hipError_t>(status));
+  return "unknown status";
+}
+
+const char *tcrv_hip_version(void) { return "tcrv_hip 0.1.0 gfx950"; }
+
+int tcrv_hip_stream_synchronize(void *stream) {
+  return static_cast<int>(hipStreamSynchronize(tcrv_host::as_stream(stream)));
+}
+
+int tcrv_hip_add_f32(const float *lhs, const float *rhs, float *out, size_t n, void *stream) {
+  using namespace tcrv_host;
+  if (n == 0)
+    return TCRV_HIP_OK;
+  if (!lhs || !rhs || !out)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned4(lhs) || !aligned4(rhs) || !aligned4(out))
+    return TCRV_HIP_ERR_MISALIGNED;
+  hipStream_t st = as_stream(stream);
+  size_t done = 0;
+  if (aligned16(lhs) && aligned16(rhs) && aligned16(out)) {
+    const size_t n4 = n / 4;
+    if (n4 > 0) {
+      const size_t per = static_cast<size_t>(kAddThreads) * kAddUnroll;
+      const size_t grid = (n4 + per - 1) / per;
+      if (grid > 0x7fffffffu)
+        return TCRV_HIP_ERR_TOO_LARGE;
+      add_f32_vec4<<<dim3(static_cast<unsigned>(grid)), dim3(kAddThreads), 0, st>>>(
+          reinterpret_cast<const float4 *>(lhs), reinterpret_cast<const float4 *>(rhs),
+          reinterpret_cast<float4 *>(out), n4);
+      done = n4 * 4;
+    }
+  }
+  if (done < n) {
+    const size_t rest = n - done;
+    const size_t grid = (rest + kAddThreads - 1) / kAddThreads;
+    if (grid > 0x7fffffffu)
+      return TCRV_HIP_ERR_TOO_LARGE;
+    add_f32_scalar<<<dim3(static_cast<unsigned>(grid)), dim3(kAddThreads), 0, st>>>(
+        lhs, rhs, out, done, n);
+  }
+  return launch_status();
+}
+
+int tcrv_hip_dequantize_row_q8_0(const uint8_t *vx, float *y, size_t n, void *stream) {
+  using namespace tcrv_host;
+  const size_t nb = n / kQK;
+  if (nb == 0)
+    return TCRV_HIP_OK;
+  if (!vx || !y)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned16(vx) || !aligned16(y))
+    return TCRV_HIP_ERR_MISALIGNED;
+  const size_t grid = (nb + kDqBlocks - 1) / kDqBlocks;
+  if (grid > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  dequantize_q8_0<<<dim3(static_cast<unsigned>(grid)), dim3(kDqThreads), 0, as_stream(stream)>>>(
+      vx, y, nb);
+  return launch_status();
+}
+
+int tcrv_hip_quantize_row_q8_0(size_t n, const float *x, uint8_t *vy, void *stream) {
+  using namespace tcrv_host;
+  const size_t nb = n / kQK;
+  if (nb == 0)
+    return TCRV_HIP_OK;
+  if (!x || !vy)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned16(x) || !aligned16(vy))
+    return TCRV_HIP_ERR_MISALIGNED;
+  const size_t grid = (nb + kQzBlocks - 1) / kQzBlocks;
+  if (grid > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  quantize_q8_0<<<dim3(static_cast<unsigned>(grid)), dim3(kQzThreads), 0, as_stream(stream)>>>(
+      x, vy, nb);
+  return launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,86 @@
+// tcrv_hip_internal.h -- device helpers shared by the gfx950 kernels of
+// libtcrv_hip.  Block formats are ggml's (pinned by the reference verifiers,
+// lib/Dialect/RVV/IR/RVVDialectWideningOps.cpp:3358-3372, RVVOps.td:3893-3897):
+//   block_q8_0  34 B : fp16 d @0, int8  qs[32] @2
+//   block_q4_0  18 B : fp16 d @0, uint8 qs[16] @2 (element j = lo nibble - 8,
+//                      element j+16 = hi nibble - 8)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "tcrv_hip.h"
+
+namespace tcrv {
+
+constexpr int kQK = 32;
+constexpr int kQ8Bytes = 34;
+constexpr int kQ4Bytes = 18;
+
+// Exact widening of an fp16 bit pattern (the reference's
+// (float)*(const _Float16 *) read, RVVToEmitCBlockQuantLinear.cpp:117,140).
+__device__ __forceinline__ float fp16_bits_to_f32(uint32_t bits) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+}
+
+// v_dot4_i32_i8: c + sum of the four signed byte products (exact in int32).
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+// Four packed offset-binary nibbles (raw value n in 0..15, meaning n - 8, held
+// in the low nibble of each byte of u after masking) -> four signed bytes.
+// (n + 0x78) ^ 0x80 == (n - 8) as a byte and never carries into the next byte.
+__device__ __forceinline__ uint32_t nibbles_to_i8x4(uint32_t u) {
+  return ((u & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+}
+
+// Bytes 2..5 of the 8-byte little-endian value hi:lo (v_alignbyte_b32).
+__device__ __forceinline__ uint32_t funnel16(uint32_t lo, uint32_t hi) {
+  return __builtin_amdgcn_alignbyte(hi, lo, 2);
+}
+
+// Copies `nbytes` (even) bytes from global `src` (16-byte aligned) into LDS
+// `dst` (16-byte aligned) with 128-bit loads plus a 16-bit tail; every thread
+// of the work-group (nthreads of them) takes part.  Reads stay inside
+// [src, src + nbytes).
+__device__ __forceinline__ void copy_span_to_lds(uint8_t *dst, const uint8_t *src,
+                                                 int nbytes, int tid, int nthreads) {
+  const int nchunks = nbytes >> 4;
+  const uint4 *s4 = reinterpret_cast<const uint4 *>(src);
+  uint4 *d4 = reinterpret_cast<uint4 *>(dst);
+  for (int c = tid; c < nchunks; c += nthreads)
+    d4[c] = s4[c];
+  const int tail_halves = (nbytes - (nchunks << 4)) >> 1;
+  if (tid < tail_halves) {
+    const uint16_t *s2 = reinterpret_cast<const uint16_t *>(src + (nchunks << 4));
+    uint16_t *d2 = reinterpret_cast<uint16_t *>(dst + (nchunks << 4));
+    d2[tid] = s2[tid];
+  }
+}
+
+}  // namespace tcrv
+
+// Host-side helpers shared by the entry points.
+namespace tcrv_host {
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TCRV_HIP_OK : static_cast<int>(e);
+}
+
+inline hipStream_t as_stream(void *stream) { return reinterpret_cast<hipStream_t>(stream); }
+
+// Stores 0.0f to `count` outputs: s[i] when ncols == 0, else
+// s[(i / ncols) * stride + i % ncols] (what the reference writes when nb == 0).
+int zero_outputs(float *s, size_t count, size_t stride, size_t ncols, void *stream);
+
+// Q4_0 x Q8_0 GEMM for nc > 1 as one wave per output element (block_dot.hip).
+int q4_0_grid(size_t n, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by,
+              size_t nr, size_t nc, size_t bs, void *stream);
+
+}  // namespace tcrv_host

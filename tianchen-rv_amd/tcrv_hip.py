@@ -1,0 +1,196 @@
+"""ctypes binding of libtcrv_hip.so, the gfx950 runtime library.
+
+The entry points keep the reference's emitted-kernel ABI (parameter roles and
+order of ``tcrv_emitc_<kernel>_<variant>``, lib/Conversion/RVV/RVVToEmitC.cpp:
+134-145, :258-268) and take caller-owned DEVICE pointers plus a HIP stream.
+PyTorch is used only as the device-memory and stream allocator: tensors are
+passed by ``data_ptr()``.
+
+Loading fails loudly (``TcrvHipError``) when the library is missing: there is
+no CPU fallback anywhere in this module.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtcrv_hip.so")
+
+QK = 32
+Q8_0_BLOCK_BYTES = 34
+Q4_0_BLOCK_BYTES = 18
+Q4_0X16_BLOCK_BYTES = 288
+
+OK = 0
+ERR_NULL_POINTER = -1
+ERR_BAD_SIZE = -2
+ERR_MISALIGNED = -3
+ERR_TOO_LARGE = -4
+ERR_UNSUPPORTED = -5
+
+
+class TcrvHipError(RuntimeError):
+    """A libtcrv_hip call returned a non-zero status, or the library is absent."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+_sz = ctypes.c_size_t
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_int = ctypes.c_int
+
+# name -> argtypes (all return int status, except the string getters)
+SIGNATURES = {
+    "tcrv_hip_stream_synchronize": [_p],
+    "tcrv_hip_add_f32": [_p, _p, _p, _sz, _p],
+    "tcrv_hip_dequantize_row_q8_0": [_p, _p, _sz, _p],
+    "tcrv_hip_quantize_row_q8_0": [_sz, _p, _p, _p],
+    "tcrv_hip_q8_0_q8_0_block_dot": [_sz, _p, _p, _p, _p],
+    "tcrv_hip_q8_0_q8_0_block_dot_rows": [_sz, _p, _p, _sz, _p, _sz, _sz, _p],
+    "tcrv_hip_q4_0_q8_0_block_dot": [_sz, _p, _sz, _p, _sz, _p, _sz, _i32, _p],
+    "tcrv_hip_q4_0_q8_0_block_dot_rows": [_sz, _p, _p, _sz, _p, _sz, _sz, _p],
+    "tcrv_hip_q8_0_q8_0_block_sums": [_sz, _p, _p, _sz, _p, _sz, _sz, _p],
+    "tcrv_hip_q4_0_q8_0_block_sums": [_sz, _p, _p, _sz, _p, _sz, _sz, _p],
+    "tcrv_hip_q4_0_q8_0_gemm": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p],
+    "tcrv_hip_gemv_q4_0_q8_0": [_sz, _p, _p, _sz, _p, _sz, _p],
+    "tcrv_hip_q8_0_q8_0_gemm": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p],
+}
+STRING_FUNCS = {"tcrv_hip_status_string": [_int], "tcrv_hip_version": []}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Loads libtcrv_hip.so once; raises TcrvHipError if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise TcrvHipError(
+            ERR_UNSUPPORTED,
+            f"libtcrv_hip.so not found at {path}: run __graft_entry__.build() "
+            "(make -C tianchen-rv_amd); there is no CPU fallback")
+    lib = ctypes.CDLL(path)
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = _int
+    for name, argtypes in STRING_FUNCS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def status_string(status: int) -> str:
+    return load().tcrv_hip_status_string(status).decode()
+
+
+def version() -> str:
+    return load().tcrv_hip_version().decode()
+
+
+def _check(name: str, status: int) -> int:
+    if status != OK:
+        raise TcrvHipError(status, f"{name} failed: {status} ({status_string(status)})")
+    return status
+
+
+def _ptr(t) -> int:
+    """Device address of a torch tensor (or an int address / None)."""
+    if t is None:
+        return 0
+    if isinstance(t, int):
+        return t
+    if not t.is_cuda:
+        raise TcrvHipError(ERR_UNSUPPORTED, "libtcrv_hip takes device tensors only")
+    return t.data_ptr()
+
+
+def _stream(stream) -> int:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def call(name: str, *args, check: bool = True) -> int:
+    """Raw call by symbol name; tensor arguments are passed as device addresses."""
+    fn = getattr(load(), name)
+    conv = []
+    for a, t in zip(args, fn.argtypes):
+        conv.append(_ptr(a) if t is _p else a)
+    status = fn(*conv)
+    return _check(name, status) if check else status
+
+
+# ---------------------------------------------------------------------------
+# Typed wrappers in the reference's parameter order (plus a stream).
+# ---------------------------------------------------------------------------
+
+def add_f32(lhs, rhs, out, n: Optional[int] = None, stream=None):
+    n = lhs.numel() if n is None else n
+    return call("tcrv_hip_add_f32", lhs, rhs, out, n, _stream(stream))
+
+
+def dequantize_row_q8_0(vx, y, n: int, stream=None):
+    return call("tcrv_hip_dequantize_row_q8_0", vx, y, n, _stream(stream))
+
+
+def quantize_row_q8_0(n: int, x, vy, stream=None):
+    return call("tcrv_hip_quantize_row_q8_0", n, x, vy, _stream(stream))
+
+
+def q8_0_q8_0_block_dot(n: int, s, vx, vy, stream=None):
+    return call("tcrv_hip_q8_0_q8_0_block_dot", n, s, vx, vy, _stream(stream))
+
+
+def q8_0_q8_0_block_dot_rows(n: int, s, vx, bx: int, vy, by: int, nrows: int, stream=None):
+    return call("tcrv_hip_q8_0_q8_0_block_dot_rows", n, s, vx, bx, vy, by, nrows,
+                _stream(stream))
+
+
+def q4_0_q8_0_block_dot(n: int, s, bs: int, vx, bx: int, vy, by: int, nrc: int, stream=None):
+    return call("tcrv_hip_q4_0_q8_0_block_dot", n, s, bs, vx, bx, vy, by, nrc,
+                _stream(stream))
+
+
+def q4_0_q8_0_block_dot_rows(n: int, s, vx, bx: int, vy, by: int, nrows: int, stream=None):
+    return call("tcrv_hip_q4_0_q8_0_block_dot_rows", n, s, vx, bx, vy, by, nrows,
+                _stream(stream))
+
+
+def q8_0_q8_0_block_sums(n: int, sumi, vx, bx: int, vy, by: int, nrows: int, stream=None):
+    return call("tcrv_hip_q8_0_q8_0_block_sums", n, sumi, vx, bx, vy, by, nrows,
+                _stream(stream))
+
+
+def q4_0_q8_0_block_sums(n: int, sumi, vx, bx: int, vy, by: int, nrows: int, stream=None):
+    return call("tcrv_hip_q4_0_q8_0_block_sums", n, sumi, vx, bx, vy, by, nrows,
+                _stream(stream))
+
+
+def q4_0_q8_0_gemm(n: int, s, vx, vy, by: int, nr: int, nc: int, bx: int, bs: int,
+                   stream=None):
+    return call("tcrv_hip_q4_0_q8_0_gemm", n, s, vx, vy, by, nr, nc, bx, bs, _stream(stream))
+
+
+def gemv_q4_0_q8_0(n: int, s, vx, bx: int, vy, nr: int, stream=None):
+    return call("tcrv_hip_gemv_q4_0_q8_0", n, s, vx, bx, vy, nr, _stream(stream))
+
+
+def q8_0_q8_0_gemm(n: int, s, vx, vy, by: int, nr: int, nc: int, bx: int, bs: int,
+                   stream=None):
+    return call("tcrv_hip_q8_0_q8_0_gemm", n, s, vx, vy, by, nr, nc, bx, bs, _stream(stream))
+
+
+def synchronize(stream=None):
+    return call("tcrv_hip_stream_synchronize", _stream(stream))
