@@ -14,7 +14,11 @@
  *   - the call is asynchronous on `stream` (a hipStream_t; NULL = the null
  *     stream) and returns an int status instead of void;
  *   - like the reference, nb = n / 32 and a trailing partial block is ignored
- *     (RVVToEmitCBlockQuantLinear.cpp:7340, RVVOps.td:8395).
+ *     (RVVToEmitCBlockQuantLinear.cpp:7340, RVVOps.td:8395);
+ *   - block pointers and row strides need only the 2-byte alignment every
+ *     ggml block already has (fp16 d at offset 0); 16-byte aligned rows (every
+ *     row of a 4096-wide matrix) take the 128-bit load path.  An odd address or
+ *     stride returns TCRV_HIP_ERR_MISALIGNED.
  *
  * Status: 0 = success; negative = an argument error detected before launch
  * (nothing was launched); positive = the hipError_t reported by the launch.
@@ -71,26 +75,25 @@ TCRV_HIP_API int tcrv_hip_add_f32(const float *lhs, const float *rhs, float *out
 /* ---- a3: Q8_0 dequantize --------------------------------------------------
  * ggml dequantize_row_q8_0(const block_q8_0 *x, float *y, int64_t k) (no
  * reference op; block layout RVVDialectWideningOps.cpp:3358-3372).
- * y[32b+j] = qs_b[j] * d_b for b < n/32.  vx and y must be 16-byte aligned. */
+ * y[32b+j] = qs_b[j] * d_b for b < n/32.  y 4-byte aligned. */
 TCRV_HIP_API int tcrv_hip_dequantize_row_q8_0(const uint8_t *vx, float *y, size_t n, void *stream);
 
 /* ---- a10: f32 -> Q8_0 activation quantizer --------------------------------
  * Replaces tcrv_emitc_..._quantize_row_q8_0(size_t n, const float *x,
  * uint8_t *vy) (test/Conversion/RVV/rvv-to-emitc-ggml-quantize-row-q8-0.mlir:
- * 25-27; RVVOps.td:8345-8431).  x must be 16-byte aligned. */
+ * 25-27; RVVOps.td:8345-8431).  x 4-byte aligned. */
 TCRV_HIP_API int tcrv_hip_quantize_row_q8_0(size_t n, const float *x, uint8_t *vy, void *stream);
 
 /* ---- a5: Q8_0 . Q8_0 block dot ---------------------------------------------
  * Replaces tcrv_emitc_..._q8_0_q8_0_block_dot(size_t n, float *s,
  * const uint8_t *vx, const uint8_t *vy)
  * (test/Conversion/RVV/rvv-to-emitc-q8-0-q8-0-block-dot.mlir:16-19).
- * *s = sum_b fma((float)sumi_b, d_x*d_y, .) in ascending b.
- * vx, vy 16-byte aligned. */
+ * *s = sum_b fma((float)sumi_b, d_x*d_y, .) in ascending b. */
 TCRV_HIP_API int tcrv_hip_q8_0_q8_0_block_dot(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
                                  void *stream);
 
-/* Batched form: s[r] = block_dot(vx + r*bx, vy + r*by) for r < nrows.
- * vx, vy 16-byte aligned; bx, by multiples of 16. */
+/* Batched form: s[r] = block_dot(vx + r*bx, vy + r*by) for r < nrows;
+ * bx, by >= the row bytes when nrows > 1. */
 TCRV_HIP_API int tcrv_hip_q8_0_q8_0_block_dot_rows(size_t n, float *s, const uint8_t *vx, size_t bx,
                                       const uint8_t *vy, size_t by, size_t nrows,
                                       void *stream);
@@ -100,8 +103,7 @@ TCRV_HIP_API int tcrv_hip_q8_0_q8_0_block_dot_rows(size_t n, float *s, const uin
  * const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by, int32_t nrc),
  * the ggml vec_dot ABI (test/Conversion/RVV/rvv-to-emitc-q4-0-q8-0-block-dot.
  * mlir:24-31).  As in the reference only n, s, vx, vy are read
- * (RVVToEmitCBlockQuantLinear.cpp:30-46); *s = sum_b fma(fl(sumi_b*d_x), d_y, .).
- * vx, vy 16-byte aligned. */
+ * (RVVToEmitCBlockQuantLinear.cpp:30-46); *s = sum_b fma(fl(sumi_b*d_x), d_y, .). */
 TCRV_HIP_API int tcrv_hip_q4_0_q8_0_block_dot(size_t n, float *s, size_t bs, const uint8_t *vx,
                                  size_t bx, const uint8_t *vy, size_t by, int32_t nrc,
                                  void *stream);
@@ -124,7 +126,7 @@ TCRV_HIP_API int tcrv_hip_q4_0_q8_0_block_sums(size_t n, int32_t *sumi, const ui
  * (test/Conversion/RVV/rvv-to-emitc-q4-0-q8-0-gemm.mlir:23-31;
  * RVVToEmitCBlockQuantLinear.cpp:1691-2121).
  * s[ir*bs + col] = q4_0 block_dot(vx + ir*bx, vy + col*by), ir < nr, col < nc.
- * vx, vy 16-byte aligned; bx, by multiples of 16; bs >= nc when nc > 1. */
+ * bx, by >= the row bytes when nr, nc > 1; bs >= nc when nr > 1. */
 TCRV_HIP_API int tcrv_hip_q4_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
                             size_t by, size_t nr, size_t nc, size_t bx, size_t bs,
                             void *stream);
@@ -138,7 +140,7 @@ TCRV_HIP_API int tcrv_hip_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx, 
  * s[ir*bs + col] = q8_0 block_dot(vx + ir*bx, vy + col*by).
  * Runs on v_mfma_i32_32x32x32_i8 with one MFMA per 32-element block and the
  * per-block fp32 fold in ascending block order.
- * vx, vy 16-byte aligned; bx, by multiples of 16; bs >= nc. */
+ * bx, by >= the row bytes when nr, nc > 1; bs >= nc when nr > 1. */
 TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
                             size_t by, size_t nr, size_t nc, size_t bx, size_t bs,
                             void *stream);

@@ -258,8 +258,50 @@ def test_argument_errors_launch_nothing(hip, dev):
     st = hip.call
     assert st("tcrv_hip_q8_0_q8_0_gemm", 64, f, t[1:], t, 34 * 2, 2, 2, 34 * 2, 2,
               0, check=False) == hip.ERR_MISALIGNED
-    assert st("tcrv_hip_q8_0_q8_0_gemm", 64, f, t, t, 70, 2, 2, 68, 2,
-              0, check=False) == hip.ERR_BAD_SIZE
+    assert st("tcrv_hip_q8_0_q8_0_gemm", 64, f, t, t, 66, 2, 2, 68, 2,
+              0, check=False) == hip.ERR_BAD_SIZE    # by < row bytes (68)
+    assert st("tcrv_hip_q8_0_q8_0_gemm", 64, f, t, t, 69, 2, 2, 68, 2,
+              0, check=False) == hip.ERR_MISALIGNED  # odd stride
+    assert st("tcrv_hip_q8_0_q8_0_gemm", 64, f, t, t, 68, 3, 2, 68, 1,
+              0, check=False) == hip.ERR_BAD_SIZE    # bs < nc
     assert st("tcrv_hip_gemv_q4_0_q8_0", 64, 0, t, 48, t, 2, 0,
               check=False) == hip.ERR_NULL_POINTER
     torch.cuda.synchronize()
+
+
+# ------------------------------------------ 2-byte aligned (non-16) layouts ---
+
+def test_unaligned_rows_all_entries(hip, oracle, dev):
+    """Rows that start 2 bytes past a 16-byte boundary and odd-block strides
+    (34*nb, 18*nb with nb odd) take the narrow-load staging path; results must
+    be identical to the oracle."""
+    nb, rows = 37, 11
+    n = nb * 32
+    x8 = synth.q8_0_matrix(rows, n, 21, 1.0)
+    y8 = synth.q8_0_matrix(rows, n, 22, 1.0)
+    x4 = synth.q4_0_matrix(rows, n, 23, 0.02)
+    rb8, rb4 = x8.shape[1], x4.shape[1]
+
+    def shifted(a):  # device copy whose first byte sits 2 bytes past a 16-byte boundary
+        buf = empty_dev(a.size + 16, torch.uint8, dev)
+        buf[2:2 + a.size] = to_dev(a.reshape(-1), dev)
+        return buf[2:2 + a.size]
+
+    dx8, dy8, dx4 = shifted(x8), shifted(y8), shifted(x4)
+    s = empty_dev(rows, torch.float32, dev)
+    hip.q8_0_q8_0_block_dot_rows(n, s, dx8, rb8, dy8, rb8, rows)
+    assert_f32_parity(from_dev(s), oracle.vec_dot_q8_0_rows(n, x8, rb8, y8, rb8, rows))
+    hip.q4_0_q8_0_block_dot_rows(n, s, dx4, rb4, dy8, rb8, rows)
+    assert_f32_parity(from_dev(s), oracle.vec_dot_q4_0_rows(n, x4, rb4, y8, rb8, rows))
+    hip.gemv_q4_0_q8_0(n, s, dx4, rb4, dy8, rows)
+    assert_f32_parity(from_dev(s), oracle.gemm_q4_0(n, x4, y8[0].copy(), 0, rows, 1, rb4, 1))
+    g = empty_dev(rows * rows, torch.float32, dev)
+    hip.q8_0_q8_0_gemm(n, g, dx8, dy8, rb8, rows, rows, rb8, rows)
+    assert_f32_parity(from_dev(g), oracle.gemm_q8_0(n, x8, y8, rb8, rows, rows, rb8, rows))
+    y = empty_dev(n + 1, torch.float32, dev)
+    hip.dequantize_row_q8_0(dx8, y[1:], n)  # 4-byte aligned output: scalar stores
+    assert_f32_parity(from_dev(y)[1:], oracle.dequantize_row_q8_0(x8[0].copy(), n))
+    xf = synth.normal_f32(24, n + 1)
+    dq = empty_dev(nb * 34 + 16, torch.uint8, dev)
+    hip.quantize_row_q8_0(n, to_dev(xf, dev)[1:], dq[2:])
+    assert np.array_equal(from_dev(dq)[2:2 + nb * 34], oracle.quantize_q8_0(xf[1:].copy()))

@@ -53,14 +53,18 @@ def test_loads_and_reports_version_without_gpu():
     ("tcrv_hip_q8_0_q8_0_gemm", (64, 0, 256, 512, 80, 2, 2, 80, 2, 0), tcrv_hip.ERR_NULL_POINTER),
     # misalignment (fake device addresses: rejected before any launch)
     ("tcrv_hip_add_f32", (2, 16, 32, 8, 0), tcrv_hip.ERR_MISALIGNED),
-    ("tcrv_hip_dequantize_row_q8_0", (8, 256, 64, 0), tcrv_hip.ERR_MISALIGNED),
-    ("tcrv_hip_q8_0_q8_0_gemm", (64, 256, 264, 512, 80, 2, 2, 80, 2, 0), tcrv_hip.ERR_MISALIGNED),
+    ("tcrv_hip_dequantize_row_q8_0", (257, 256, 64, 0), tcrv_hip.ERR_MISALIGNED),
+    ("tcrv_hip_dequantize_row_q8_0", (256, 258, 64, 0), tcrv_hip.ERR_MISALIGNED),
+    ("tcrv_hip_q8_0_q8_0_gemm", (64, 256, 257, 512, 80, 2, 2, 80, 2, 0), tcrv_hip.ERR_MISALIGNED),
+    ("tcrv_hip_q8_0_q8_0_gemm", (64, 256, 256, 512, 81, 2, 2, 80, 2, 0), tcrv_hip.ERR_MISALIGNED),
+    ("tcrv_hip_q8_0_q8_0_block_dot_rows", (64, 256, 256, 69, 512, 68, 2, 0),
+     tcrv_hip.ERR_MISALIGNED),
     # bad strides / output row stride
-    ("tcrv_hip_q8_0_q8_0_gemm", (64, 256, 256, 512, 70, 2, 2, 80, 2, 0), tcrv_hip.ERR_BAD_SIZE),
+    ("tcrv_hip_q8_0_q8_0_gemm", (64, 256, 256, 512, 66, 2, 2, 80, 2, 0), tcrv_hip.ERR_BAD_SIZE),
     ("tcrv_hip_q8_0_q8_0_gemm", (64, 256, 256, 512, 80, 2, 2, 80, 1, 0), tcrv_hip.ERR_BAD_SIZE),
     ("tcrv_hip_q4_0_q8_0_block_dot_rows", (64, 256, 256, 24, 512, 80, 3, 0),
      tcrv_hip.ERR_BAD_SIZE),
-    ("tcrv_hip_gemv_q4_0_q8_0", (64, 256, 512, 40, 1024, 3, 0), tcrv_hip.ERR_BAD_SIZE),
+    ("tcrv_hip_gemv_q4_0_q8_0", (64, 256, 512, 34, 1024, 3, 0), tcrv_hip.ERR_BAD_SIZE),
 ])
 def test_argument_errors_before_launch(name, args, want):
     assert tcrv_hip.call(name, *args, check=False) == want

@@ -197,13 +197,12 @@ int launch_pairs(size_t n, float *s, int32_t *sums, const uint8_t *vx, size_t bx
     return TCRV_HIP_OK;  // the reference writes sumf = 0 for nb == 0; see callers
   if (!vx || !vy || (!s && !sums))
     return TCRV_HIP_ERR_NULL_POINTER;
-  if (!aligned16(vx) || !aligned16(vy))
-    return TCRV_HIP_ERR_MISALIGNED;
   const size_t xrows = ncols ? npairs / ncols : npairs;
   const size_t yrows = ncols ? ncols : npairs;
+  if (!aligned2(vx) || !aligned2(vy) || (xrows > 1 && (bx & 1u)) || (yrows > 1 && (by & 1u)))
+    return TCRV_HIP_ERR_MISALIGNED;
   const size_t xbytes = nb * (F == DotFmt::kQ8Q8 ? tcrv::kQ8Bytes : tcrv::kQ4Bytes);
-  if ((xrows > 1 && (bx % 16 != 0 || bx < xbytes)) ||
-      (yrows > 1 && (by % 16 != 0 || by < nb * tcrv::kQ8Bytes)))
+  if ((xrows > 1 && bx < xbytes) || (yrows > 1 && by < nb * tcrv::kQ8Bytes))
     return TCRV_HIP_ERR_BAD_SIZE;
   if (npairs > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;

@@ -72,6 +72,7 @@ __global__ __launch_bounds__(kAddThreads) void add_f32_scalar(const float *lhs, 
 constexpr int kDqThreads = 256;
 constexpr int kDqBlocks = 128;
 
+template <bool kVecOut>
 __global__ __launch_bounds__(kDqThreads) void dequantize_q8_0(const uint8_t *vx, float *y,
                                                               size_t nb) {
   __shared__ __align__(16) uint8_t lds[kDqBlocks * kQ8Bytes];
@@ -94,7 +95,15 @@ __global__ __launch_bounds__(kDqThreads) void dequantize_q8_0(const uint8_t *vx,
     r.y = static_cast<float>(static_cast<int8_t>(q01 >> 8)) * d;
     r.z = static_cast<float>(static_cast<int8_t>(q23 & 0xffu)) * d;
     r.w = static_cast<float>(static_cast<int8_t>(q23 >> 8)) * d;
-    store_stream(r, &dst[f]);
+    if constexpr (kVecOut) {
+      store_stream(r, &dst[f]);
+    } else {
+      float *d1 = y + blk0 * kQK + 4 * f;
+      d1[0] = r.x;
+      d1[1] = r.y;
+      d1[2] = r.z;
+      d1[3] = r.w;
+    }
   }
 }
 
@@ -135,8 +144,13 @@ __global__ __launch_bounds__(kQzThreads) void quantize_q8_0(const float *x, uint
   const int part = threadIdx.x & 7; // float4 within the block
   const bool active = lb < nblk;
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (active)
-    v = reinterpret_cast<const float4 *>(x + (blk0 + lb) * kQK)[part];
+  if (active) {
+    const float *xp = x + (blk0 + lb) * kQK + 4 * part;
+    if ((reinterpret_cast<uintptr_t>(x) & 15u) == 0)
+      v = *reinterpret_cast<const float4 *>(xp);
+    else
+      v = make_float4(xp[0], xp[1], xp[2], xp[3]);
+  }
   float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
   // max over the 8 lanes of the block (exact, order-free)
   amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
@@ -154,15 +168,7 @@ __global__ __launch_bounds__(kQzThreads) void quantize_q8_0(const float *x, uint
       l16[0] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(d));
   }
   __syncthreads();
-  const int nbytes = nblk * kQ8Bytes;
-  uint8_t *dst = vy + blk0 * kQ8Bytes;
-  const int nchunks = nbytes >> 4;
-  for (int c = threadIdx.x; c < nchunks; c += kQzThreads)
-    reinterpret_cast<uint4 *>(dst)[c] = reinterpret_cast<const uint4 *>(lds)[c];
-  const int tail = (nbytes - (nchunks << 4)) >> 1;
-  if (static_cast<int>(threadIdx.x) < tail)
-    reinterpret_cast<uint16_t *>(dst + (nchunks << 4))[threadIdx.x] =
-        reinterpret_cast<const uint16_t *>(lds + (nchunks << 4))[threadIdx.x];
+  copy_lds_to_span(vy + blk0 * kQ8Bytes, lds, nblk * kQ8Bytes, threadIdx.x, kQzThreads);
 }
 
 }  // namespace
@@ -238,13 +244,17 @@ int tcrv_hip_dequantize_row_q8_0(const uint8_t *vx, float *y, size_t n, void *st
     return TCRV_HIP_OK;
   if (!vx || !y)
     return TCRV_HIP_ERR_NULL_POINTER;
-  if (!aligned16(vx) || !aligned16(y))
+  if (!aligned2(vx) || !aligned4(y))
     return TCRV_HIP_ERR_MISALIGNED;
   const size_t grid = (nb + kDqBlocks - 1) / kDqBlocks;
   if (grid > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
-  dequantize_q8_0<<<dim3(static_cast<unsigned>(grid)), dim3(kDqThreads), 0, as_stream(stream)>>>(
-      vx, y, nb);
+  if (aligned16(y))
+    dequantize_q8_0<true><<<dim3(static_cast<unsigned>(grid)), dim3(kDqThreads), 0,
+                            as_stream(stream)>>>(vx, y, nb);
+  else
+    dequantize_q8_0<false><<<dim3(static_cast<unsigned>(grid)), dim3(kDqThreads), 0,
+                             as_stream(stream)>>>(vx, y, nb);
   return launch_status();
 }
 
@@ -255,7 +265,7 @@ int tcrv_hip_quantize_row_q8_0(size_t n, const float *x, uint8_t *vy, void *stre
     return TCRV_HIP_OK;
   if (!x || !vy)
     return TCRV_HIP_ERR_NULL_POINTER;
-  if (!aligned16(x) || !aligned16(vy))
+  if (!aligned4(x) || !aligned2(vy))
     return TCRV_HIP_ERR_MISALIGNED;
   const size_t grid = (nb + kQzBlocks - 1) / kQzBlocks;
   if (grid > 0x7fffffffu)

@@ -97,7 +97,7 @@ __device__ __forceinline__ void gm_block(GemmTileState &st, const uint8_t *la,
 
 __global__ __launch_bounds__(kGmThreads) void gemm_q8_0_q8_0_kernel(
     size_t nb, float *s, const uint8_t *vx, const uint8_t *vy, size_t by, size_t nr,
-    size_t nc, size_t bx, size_t bs) {
+    size_t nc, size_t bx, size_t bs, int rows16) {
   __shared__ __align__(16) uint8_t la[kGmBM * kGmRow + 16];
   __shared__ __align__(16) uint8_t lb[kGmBN * kGmRow + 16];
   __shared__ __align__(16) float da[kGmKB][kGmBM];
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(kGmThreads) void gemm_q8_0_q8_0_kernel(
   for (size_t c0 = 0; c0 < nb; c0 += kGmKB) {
     const int nbc = static_cast<int>(min(static_cast<size_t>(kGmKB), nb - c0));
     const size_t koff = c0 * kQ8Bytes;
-    if (nbc == kGmKB) {
+    if (nbc == kGmKB && rows16) {  // every staged row segment is 16-byte aligned
       for (int t = tid; t < kGmBM * kGmRowChunks; t += kGmThreads) {
         const int r = t / kGmRowChunks, c = t - r * kGmRowChunks;
         const size_t gr = min(m0 + r, nr - 1);  // rows past nr reuse row nr-1, unstored
@@ -194,17 +194,19 @@ extern "C" int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx,
     return zero_outputs(s, nr * nc, bs, nc, stream);
   if (!s || !vx || !vy)
     return TCRV_HIP_ERR_NULL_POINTER;
-  if (!aligned16(vx) || !aligned16(vy))
+  if (!aligned2(vx) || !aligned2(vy) || (nr > 1 && (bx & 1u)) || (nc > 1 && (by & 1u)))
     return TCRV_HIP_ERR_MISALIGNED;
   const size_t rowbytes = nb * tcrv::kQ8Bytes;
-  if ((nr > 1 && (bx % 16 != 0 || bx < rowbytes)) || (nc > 1 && (by % 16 != 0 || by < rowbytes)))
+  if ((nr > 1 && bx < rowbytes) || (nc > 1 && by < rowbytes))
     return TCRV_HIP_ERR_BAD_SIZE;
+  const int rows16 = aligned16(vx) && aligned16(vy) && (nr == 1 || bx % 16 == 0) &&
+                     (nc == 1 || by % 16 == 0);
   const size_t gx = (nc + tcrv::kGmBN - 1) / tcrv::kGmBN;
   const size_t gy = (nr + tcrv::kGmBM - 1) / tcrv::kGmBM;
   if (gx > 0x7fffffffu || gy > 65535u)
     return TCRV_HIP_ERR_TOO_LARGE;
   tcrv::gemm_q8_0_q8_0_kernel<<<dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)),
                                 dim3(tcrv::kGmThreads), 0, as_stream(stream)>>>(
-      nb, s, vx, vy, by, nr, nc, bx, bs);
+      nb, s, vx, vy, by, nr, nc, bx, bs, rows16);
   return launch_status();
 }

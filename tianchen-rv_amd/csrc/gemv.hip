@@ -138,11 +138,11 @@ int gemv_q4_0_q8_0(size_t n, float *s, size_t os, const uint8_t *vx, size_t bx,
     return TCRV_HIP_OK;
   if (!s || !vx || !vy)
     return TCRV_HIP_ERR_NULL_POINTER;
-  if (!aligned16(vx) || !aligned16(vy))
+  if (!aligned2(vx) || !aligned2(vy) || (nr > 1 && (bx & 1u)))
     return TCRV_HIP_ERR_MISALIGNED;
   if (nb == 0)
     return TCRV_HIP_ERR_BAD_SIZE;  // handled by the caller (zero fill)
-  if (nr > 1 && (bx % 16 != 0 || bx < nb * tcrv::kQ4Bytes))
+  if (nr > 1 && bx < nb * tcrv::kQ4Bytes)
     return TCRV_HIP_ERR_BAD_SIZE;
   const size_t rows_per_wg = static_cast<size_t>(tcrv::kGvWaves) * kGemvRows;
   const size_t grid = (nr + rows_per_wg - 1) / rows_per_wg;

@@ -41,22 +41,62 @@ __device__ __forceinline__ uint32_t funnel16(uint32_t lo, uint32_t hi) {
   return __builtin_amdgcn_alignbyte(hi, lo, 2);
 }
 
-// Copies `nbytes` (even) bytes from global `src` (16-byte aligned) into LDS
-// `dst` (16-byte aligned) with 128-bit loads plus a 16-bit tail; every thread
-// of the work-group (nthreads of them) takes part.  Reads stay inside
+// Copies `nbytes` (even) bytes from global `src` (2-byte aligned, as every
+// ggml block is) into LDS `dst` (16-byte aligned); every thread of the
+// work-group (nthreads of them) takes part.  A 16-byte aligned source (every
+// row of a 4096-wide matrix) moves with 128-bit loads plus a 16-bit tail; other
+// sources fall back to 32-bit or 16-bit loads.  Reads stay inside
 // [src, src + nbytes).
 __device__ __forceinline__ void copy_span_to_lds(uint8_t *dst, const uint8_t *src,
                                                  int nbytes, int tid, int nthreads) {
-  const int nchunks = nbytes >> 4;
-  const uint4 *s4 = reinterpret_cast<const uint4 *>(src);
-  uint4 *d4 = reinterpret_cast<uint4 *>(dst);
-  for (int c = tid; c < nchunks; c += nthreads)
-    d4[c] = s4[c];
-  const int tail_halves = (nbytes - (nchunks << 4)) >> 1;
-  if (tid < tail_halves) {
-    const uint16_t *s2 = reinterpret_cast<const uint16_t *>(src + (nchunks << 4));
-    uint16_t *d2 = reinterpret_cast<uint16_t *>(dst + (nchunks << 4));
-    d2[tid] = s2[tid];
+  const uintptr_t a = reinterpret_cast<uintptr_t>(src);
+  if ((a & 15u) == 0) {
+    const int nchunks = nbytes >> 4;
+    const uint4 *s4 = reinterpret_cast<const uint4 *>(src);
+    uint4 *d4 = reinterpret_cast<uint4 *>(dst);
+    for (int c = tid; c < nchunks; c += nthreads)
+      d4[c] = s4[c];
+    const int tail_halves = (nbytes - (nchunks << 4)) >> 1;
+    if (tid < tail_halves) {
+      const uint16_t *s2 = reinterpret_cast<const uint16_t *>(src + (nchunks << 4));
+      uint16_t *d2 = reinterpret_cast<uint16_t *>(dst + (nchunks << 4));
+      d2[tid] = s2[tid];
+    }
+  } else if ((a & 3u) == 0) {
+    const int nwords = nbytes >> 2;
+    const uint32_t *s1 = reinterpret_cast<const uint32_t *>(src);
+    uint32_t *d1 = reinterpret_cast<uint32_t *>(dst);
+    for (int c = tid; c < nwords; c += nthreads)
+      d1[c] = s1[c];
+    if ((nbytes & 2) && tid == 0)
+      reinterpret_cast<uint16_t *>(dst)[nwords * 2] =
+          reinterpret_cast<const uint16_t *>(src)[nwords * 2];
+  } else {
+    const int nhalves = nbytes >> 1;
+    const uint16_t *s2 = reinterpret_cast<const uint16_t *>(src);
+    uint16_t *d2 = reinterpret_cast<uint16_t *>(dst);
+    for (int c = tid; c < nhalves; c += nthreads)
+      d2[c] = s2[c];
+  }
+}
+
+// The reverse copy: `nbytes` (even) bytes from LDS `src` (16-byte aligned) to
+// global `dst` (2-byte aligned), widest stores the destination allows.
+__device__ __forceinline__ void copy_lds_to_span(uint8_t *dst, const uint8_t *src, int nbytes,
+                                                 int tid, int nthreads) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(dst);
+  if ((a & 15u) == 0) {
+    const int nchunks = nbytes >> 4;
+    for (int c = tid; c < nchunks; c += nthreads)
+      reinterpret_cast<uint4 *>(dst)[c] = reinterpret_cast<const uint4 *>(src)[c];
+    const int tail_halves = (nbytes - (nchunks << 4)) >> 1;
+    if (tid < tail_halves)
+      reinterpret_cast<uint16_t *>(dst + (nchunks << 4))[tid] =
+          reinterpret_cast<const uint16_t *>(src + (nchunks << 4))[tid];
+  } else {
+    const int nhalves = nbytes >> 1;
+    for (int c = tid; c < nhalves; c += nthreads)
+      reinterpret_cast<uint16_t *>(dst)[c] = reinterpret_cast<const uint16_t *>(src)[c];
   }
 }
 
@@ -67,6 +107,7 @@ namespace tcrv_host {
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+inline bool aligned2(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
 
 inline int launch_status() {
   hipError_t e = hipGetLastError();
