@@ -124,12 +124,206 @@ __global__ __launch_bounds__(kGvWaves * 64) void gemv_q4_0_q8_0_kernel(
     s[(row0 + l) * os] = sumf;
 }
 
+
+// ---------------------------------------------------------------------------
+// Register-direct decode GEMV (the fast path: nb even, rows 4-byte aligned).
+//
+// Lane l of a wave owns blocks 2l and 2l+1 of each 128-block chunk: 36
+// contiguous weight bytes per row (two 128-bit loads and one 32-bit load, all
+// issued for the wave's kR rows before the first use) and 68 contiguous
+// activation bytes, which stay in registers for every row of the wave.
+//
+// Integer core: with n the raw nibble (0..15) and y the Q8_0 quant,
+//   sumi = sum_j (n_j - 8) y_j = sum_j n_j y_j - 8 sum_j y_j,
+// so the decode is a mask (low nibbles) or a shift and a mask (high nibbles)
+// and the -8 offset enters once per activation block as the accumulator's
+// start value; both forms are exact int32 arithmetic, so sumi is bit-identical
+// to the reference's offset-binary decode (RVVToEmitC.cpp:2524-2589).
+//
+// Fold: t_b = fl((float)sumi_b * d_x) per block goes to LDS; after a barrier
+// lane r < kR of each wave runs sumf = fma(t_b, d_y, sumf) for b ascending --
+// the reference's per-row serial fold (RVVToEmitCBlockQuantLinear.cpp:322-356).
+// ---------------------------------------------------------------------------
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+__device__ __forceinline__ void load36(const uint8_t *p, uint32_t w[9]) {
+  const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
+  const u32x4a4 a = *reinterpret_cast<const u32x4a4 *>(q);
+  const u32x4a4 b = *reinterpret_cast<const u32x4a4 *>(q + 4);
+  w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+  w[8] = q[8];
+}
+
+// Activation blocks 2l, 2l+1 (68 bytes, dword aligned) -> quants of each block
+// as 8 aligned dwords, fp32 scales and the -8*sum(q) accumulator seeds.
+struct ActPair {
+  uint32_t q0[8], q1[8];
+  float d0, d1;
+  int c0, c1;
+};
+
+__device__ __forceinline__ void load_act_pair(const uint8_t *p, ActPair &a) {
+  const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
+  uint32_t r[17];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(q + 4 * k);
+    r[4 * k + 0] = v.x; r[4 * k + 1] = v.y; r[4 * k + 2] = v.z; r[4 * k + 3] = v.w;
+  }
+  r[16] = q[16];
+  // block 2l: d at bytes 0-1, quants at bytes 2..33; block 2l+1: d at 34-35,
+  // quants at 36..67 (dwords 9..16)
+  a.d0 = fp16_bits_to_f32(r[0] & 0xffffu);
+  a.d1 = fp16_bits_to_f32(r[8] >> 16);
+  int s0 = 0, s1 = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    a.q0[k] = funnel16(r[k], r[k + 1]);
+    a.q1[k] = r[k + 9];
+    s0 = sdot4(a.q0[k], 0x01010101u, s0);
+    s1 = sdot4(a.q1[k], 0x01010101u, s1);
+  }
+  a.c0 = -8 * s0;
+  a.c1 = -8 * s1;
+}
+
+// sum_j n_j y_j + seed over one block: quants q[0..3] (16 bytes = 32 nibbles).
+__device__ __forceinline__ int nibble_dot(const uint32_t q[4], const uint32_t y[8], int seed) {
+  int acc = seed;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    acc = sdot4(q[k] & 0x0F0F0F0Fu, y[k], acc);
+    acc = sdot4((q[k] >> 4) & 0x0F0F0F0Fu, y[k + 4], acc);
+  }
+  return acc;
+}
+
+// Serial fold of one row spread over the kLanes lanes of a lane group (a
+// 16-lane DPP row, or half of one): lane p of the group holds the terms t[k]
+// and activation scales dy[k] of kTerms consecutive blocks, p*kTerms + k.
+// Phase ph runs the kTerms fmas of lane ph from the running sum it received,
+// then hands the sum to lane ph+1 with one DPP row shift (v_mov_b32 row_shr:1)
+// and a select; every lane executes every phase, and what the other lanes
+// compute is discarded.  The sum therefore sees the terms in ascending block
+// order, one fmaf each, exactly as a single scalar loop would.  The group's
+// result ends in lane kLanes-1; `sumf` seeds lane 0.
+template <int kLanes, int kTerms>
+__device__ __forceinline__ float fold_chain(const float t[kTerms], const float dy[kTerms],
+                                           float sumf) {
+  const int p = threadIdx.x & (kLanes - 1);
+#pragma unroll
+  for (int ph = 0; ph < kLanes; ++ph) {
+#pragma unroll
+    for (int k = 0; k < kTerms; ++k)
+      sumf = fmaf(t[k], dy[k], sumf);
+    if (ph + 1 < kLanes) {
+      const float moved = __builtin_bit_cast(
+          float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sumf), 0x111 /* row_shr:1 */,
+                                             0xf, 0xf, false));
+      sumf = (p == ph + 1) ? moved : sumf;
+    }
+  }
+  return sumf;
+}
+
+// kOneChunk: nb == kGvChunk exactly (n = 4096), so every lane owns a whole
+// block pair, there is one chunk and no carry between chunks.
+template <int kWaves, int kR, bool kOneChunk>
+__global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
+    size_t nb_arg, float *s, size_t os, const uint8_t *vx, size_t bx, const uint8_t *vy,
+    size_t nr) {
+  const size_t nb = kOneChunk ? static_cast<size_t>(kGvChunk) : nb_arg;
+  constexpr int kLanes = 64 / kR;              // fold lanes per row
+  constexpr int kTerms = kGvChunk / kLanes;    // blocks per fold lane
+  static_assert(kLanes == 8 || kLanes == 16, "fold groups live inside one DPP row");
+  __shared__ __align__(16) float tl[kWaves][kR][kGvChunk + 4];
+  __shared__ __align__(16) float dyl[kWaves][kGvChunk];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+  const int l = tid & 63;
+  const size_t row0 = (static_cast<size_t>(blockIdx.x) * kWaves + w) * kR;
+  const int fr = l / kLanes;          // row of this lane in the fold
+  const int fp = l & (kLanes - 1);    // position of this lane in its row's chain
+  float sumf = 0.0f;
+
+  for (size_t c0 = 0; c0 < nb; c0 += kGvChunk) {
+    const int nbc = static_cast<int>(min(static_cast<size_t>(kGvChunk), nb - c0));
+    const int b0 = 2 * l;
+    if (kOneChunk || b0 < nbc) {  // nbc is even: the pair is whole or absent
+      uint32_t wr[kR][9];
+#pragma unroll
+      for (int r = 0; r < kR; ++r) {
+        const size_t row = min(row0 + r, nr - 1);  // rows past nr: computed, never stored
+        load36(vx + row * bx + (c0 + b0) * kQ4Bytes, wr[r]);
+      }
+      ActPair ap;
+      load_act_pair(vy + (c0 + b0) * kQ8Bytes, ap);
+      dyl[w][b0] = ap.d0;
+      dyl[w][b0 + 1] = ap.d1;
+#pragma unroll
+      for (int r = 0; r < kR; ++r) {
+        // block 2l: d = bytes 0-1, quants bytes 2..17 (shift by 2 bytes);
+        // block 2l+1: d = bytes 18-19, quants bytes 20..35 (dwords 5..8)
+        uint32_t qa[4], qb[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          qa[k] = funnel16(wr[r][k], wr[r][k + 1]);
+          qb[k] = wr[r][k + 5];
+        }
+        const float dx0 = fp16_bits_to_f32(wr[r][0] & 0xffffu);
+        const float dx1 = fp16_bits_to_f32(wr[r][4] >> 16);
+        float2 t;
+        t.x = static_cast<float>(nibble_dot(qa, ap.q0, ap.c0)) * dx0;
+        t.y = static_cast<float>(nibble_dot(qb, ap.q1, ap.c1)) * dx1;
+        *reinterpret_cast<float2 *>(&tl[w][r][b0]) = t;
+      }
+    } else {
+      // blocks past the chunk: t = dy = 0, and fma(0, 0, sumf) == sumf (sumf is never -0)
+      dyl[w][b0] = 0.0f;
+      dyl[w][b0 + 1] = 0.0f;
+#pragma unroll
+      for (int r = 0; r < kR; ++r)
+        *reinterpret_cast<float2 *>(&tl[w][r][b0]) = make_float2(0.0f, 0.0f);
+    }
+    __syncthreads();
+    float t[kTerms], dy[kTerms];
+#pragma unroll
+    for (int k = 0; k < kTerms; k += 4) {
+      const float4 tv = *reinterpret_cast<const float4 *>(&tl[w][fr][fp * kTerms + k]);
+      const float4 dv = *reinterpret_cast<const float4 *>(&dyl[w][fp * kTerms + k]);
+      t[k] = tv.x; t[k + 1] = tv.y; t[k + 2] = tv.z; t[k + 3] = tv.w;
+      dy[k] = dv.x; dy[k + 1] = dv.y; dy[k + 2] = dv.z; dy[k + 3] = dv.w;
+    }
+    if constexpr (kOneChunk) {
+      sumf = fold_chain<kLanes, kTerms>(t, dy, 0.0f);
+    } else {
+      // the previous chunk's sum sits in the last lane of the group: seed lane 0
+      const float carry = __shfl(sumf, (l & ~(kLanes - 1)) + kLanes - 1);
+      sumf = fold_chain<kLanes, kTerms>(t, dy, fp == 0 ? carry : 0.0f);
+      __syncthreads();
+    }
+  }
+  if (fp == kLanes - 1 && row0 + fr < nr)
+    s[(row0 + fr) * os] = sumf;
+}
+
 }  // namespace tcrv
 
 namespace tcrv_host {
 
-// Rows per wave of the decode GEMV.
+// Rows per wave of the LDS-staged decode GEMV (odd nb or 2-byte aligned rows).
 constexpr int kGemvRows = 2;
+// Shape of the register-direct GEMV: waves per work-group, rows per wave.
+#ifndef TCRV_GEMV_WAVES
+#define TCRV_GEMV_WAVES 4
+#endif
+#ifndef TCRV_GEMV_ROWS
+#define TCRV_GEMV_ROWS 4
+#endif
+constexpr int kDirectWaves = TCRV_GEMV_WAVES;
+constexpr int kDirectRows = TCRV_GEMV_ROWS;
 
 int gemv_q4_0_q8_0(size_t n, float *s, size_t os, const uint8_t *vx, size_t bx,
                    const uint8_t *vy, size_t nr, void *stream) {
@@ -144,12 +338,27 @@ int gemv_q4_0_q8_0(size_t n, float *s, size_t os, const uint8_t *vx, size_t bx,
     return TCRV_HIP_ERR_BAD_SIZE;  // handled by the caller (zero fill)
   if (nr > 1 && bx < nb * tcrv::kQ4Bytes)
     return TCRV_HIP_ERR_BAD_SIZE;
+  hipStream_t st = as_stream(stream);
+  if (nb % 2 == 0 && aligned4(vx) && aligned4(vy) && (nr == 1 || bx % 4 == 0)) {
+    constexpr int kW = kDirectWaves, kR = kDirectRows;
+    const size_t rows_per_wg = static_cast<size_t>(kW) * kR;
+    const size_t grid = (nr + rows_per_wg - 1) / rows_per_wg;
+    if (grid > 0x7fffffffu)
+      return TCRV_HIP_ERR_TOO_LARGE;
+    if (nb == static_cast<size_t>(tcrv::kGvChunk))
+      tcrv::gemv_q4_0_q8_0_direct<kW, kR, true>
+          <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(nb, s, os, vx, bx, vy, nr);
+    else
+      tcrv::gemv_q4_0_q8_0_direct<kW, kR, false>
+          <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(nb, s, os, vx, bx, vy, nr);
+    return launch_status();
+  }
   const size_t rows_per_wg = static_cast<size_t>(tcrv::kGvWaves) * kGemvRows;
   const size_t grid = (nr + rows_per_wg - 1) / rows_per_wg;
   if (grid > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
   tcrv::gemv_q4_0_q8_0_kernel<kGemvRows>
-      <<<dim3(static_cast<unsigned>(grid)), dim3(tcrv::kGvWaves * 64), 0, as_stream(stream)>>>(
+      <<<dim3(static_cast<unsigned>(grid)), dim3(tcrv::kGvWaves * 64), 0, st>>>(
           nb, s, os, vx, bx, vy, nr);
   return launch_status();
 }
