@@ -1,18 +1,23 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized hot path on one MI355X.
 
-Headline (BASELINE.json metric "Q4_0 GEMV GB/s (% HBM peak); Q8_0 GEMM int8 TOPS
-(% MFMA peak)"): one step = one Q4_0 x Q8_0 decode GEMV, W 4096 x 4096
-(configs[3]), through the C-ABI entry tcrv_hip_gemv_q4_0_q8_0.  The weight
-matrix rotates over enough distinct copies (> 256 MB) that every launch reads
-W from HBM, not from the 256 MB Infinity Cache.  The second half of the metric,
-the Q8_0 x Q8_0 GEMM 4096^3 in int8 TOPS, and the other configs
-are reported in the same JSON line.
+BASELINE.json metric: "Q4_0 GEMV GB/s (% HBM peak); Q8_0 GEMM int8 TOPS (% MFMA
+peak)".  `value` is the first half: one step = one Q4_0 x Q8_0 decode GEMV,
+W 4096 x 4096, through the C-ABI entry tcrv_hip_gemv_q4_0_q8_0.
+The second half, the Q8_0 x Q8_0 GEMM 4096^3, is timed in the
+same run and reported under "gemm"; configs[0..2] (add, dequant, block dot)
+are reported under "configs".
 
-Inputs are synthetic (tianchen-rv_amd/synth.py, seeds 1001-1009) and already
-resident in HBM when a timed region starts.  Timed regions are bracketed by
-torch.cuda.synchronize() and HIP events recorded on the launch stream.
-The cpu_baseline leg times the scalar C oracle (oracle/) on the host cores.
+Timing: inputs are synthetic (tianchen-rv_amd/synth.py seeds) and resident in
+HBM before a timed region starts.  A region is K launches captured in one HIP
+graph and replayed once, bracketed by torch.cuda.synchronize() and HIP events
+recorded on the launch stream; per-launch time = region / K.  Every
+bandwidth-bound config rotates through enough distinct input sets (> 256 MB,
+the Infinity Cache size) that each launch reads its inputs from HBM.
+
+cpu_baseline: the scalar C oracle (oracle/, the CPU restatement of the
+reference emitters) timed on the host cores over a bounded sample of the same
+GEMV workload.
 """
 from __future__ import annotations
 
@@ -25,9 +30,20 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "tianchen-rv_amd"))
 
-HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
-INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
+INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published
 N = 4096
+MALL_BYTES = 256 << 20       # Infinity Cache
+
+METRIC = "Q4_0 GEMV GB/s (% HBM peak); Q8_0 GEMM int8 TOPS (% MFMA peak)"
+
+# Algorithmic bytes per launch (the roofline's `achieved` numerators).
+GEMV_BYTES = N * (N // 32) * 18 + (N // 32) * 34 + N * 4        # 9 457 920
+ADD_BYTES = 12 * (1 << 24)                                      # 201 326 592
+DEQ_BYTES = (N * N // 32) * (34 + 128)                          # 84 934 656
+DOT_ROWS = 16384
+DOT_BYTES = DOT_ROWS * (2 * (N // 32) * 34 + 4)                 # 142 671 872
+GEMM_OPS = 2.0 * N * N * N                                      # 137 438 953 472
 
 
 def log(msg: str) -> None:
@@ -37,189 +53,262 @@ def log(msg: str) -> None:
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--gemm-steps", type=int, default=50)
-    ap.add_argument("--mode", choices=["graph", "eager"], default="graph",
-                    help="launch the timed steps from a captured HIP graph or eagerly")
+    ap.add_argument("--steps", type=int, default=2000, help="timed GEMV launches")
+    ap.add_argument("--warmup", type=int, default=200, help="untimed GEMV launches")
+    ap.add_argument("--gemm-steps", type=int, default=20)
+    ap.add_argument("--config-steps", type=int, default=50,
+                    help="timed launches for each of add / dequant / block dot")
     ap.add_argument("--copies", type=int, default=40,
-                    help="distinct weight copies rotated by the GEMV (>256 MB total)")
-    ap.add_argument("--cpu-seconds", type=float, default=4.0,
-                    help="wall time per CPU-baseline leg")
-    ap.add_argument("--only", choices=["all", "gemv", "gemm"], default="all")
+                    help="distinct GEMV weight copies rotated over (> 256 MB in total)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="wall time of the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--only", choices=["all", "gemv", "gemm", "configs", "calib"], default="all",
+                    help="calib: 10 launches of add_f32 over n = 2^24 (reads 128 MiB, writes "
+                         "64 MiB each), the known-size kernel the HBM byte counters are "
+                         "scaled against")
     return ap.parse_args()
 
 
-class Timer:
-    """Events on the launch stream around a region of `count` launches."""
+class Region:
+    """HIP events on the launch stream around one replay of a captured graph
+    of `steps` launches; ms = region time."""
 
-    def __init__(self, torch, stream):
-        self.torch = torch
-        self.stream = stream
-        self.start = torch.cuda.Event(enable_timing=True)
-        self.stop = torch.cuda.Event(enable_timing=True)
-
-    def __enter__(self):
-        self.torch.cuda.synchronize()
-        self.start.record(self.stream)
-        return self
-
-    def __exit__(self, *exc):
-        self.stop.record(self.stream)
-        self.torch.cuda.synchronize()
-        self.ms = self.start.elapsed_time(self.stop)
-
-
-def run_region(torch, stream, launch, steps, mode):
-    """Runs `steps` launches (launch(i) issues step i) and returns elapsed ms."""
-    if mode == "graph":
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            for i in range(steps):
-                launch(i)
+    def __init__(self, torch, stream, launch, steps):
+        self.torch, self.stream = torch, stream
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(self.graph, stream=stream):
+                for i in range(steps):
+                    launch(i)
         torch.cuda.synchronize()
-        g.replay()  # untimed first replay
-        with Timer(torch, stream) as t:
-            g.replay()
-        return t.ms
-    with Timer(torch, stream) as t:
-        for i in range(steps):
-            launch(i)
-    return t.ms
+
+    def run(self) -> float:
+        torch = self.torch
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        # replay() launches on torch's current stream: make it the launch stream
+        # so the graph runs between the two events.
+        with torch.cuda.stream(self.stream):
+            e0.record(self.stream)
+            self.graph.replay()
+            e1.record(self.stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)
 
 
-def main():
-    args = parse()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the sharding design is described in DESIGN.md); run with --gpus 1",
-              file=sys.stderr)
-        sys.exit(2)
-
-    import numpy as np
-    import torch
-
-    import synth
+def checked(fn, name):
     import tcrv_hip
 
-    tcrv_hip.load()
+    def call(*args):
+        st = fn(*args)
+        if st != 0:
+            raise tcrv_hip.TcrvHipError(st, f"{name}: {tcrv_hip.status_string(st)}")
+    return call
+
+
+def same_as_eager(torch, stream, graph_out, eager_launch, what):
+    """Guards the timing: the output a graph replay left behind must equal the
+    output of one eager launch of the same step (so the graph really ran)."""
+    ref = torch.empty_like(graph_out)
+    with torch.cuda.stream(stream):
+        eager_launch(ref.data_ptr())
+    torch.cuda.synchronize()
+    if not torch.equal(ref.view(torch.int32), graph_out.view(torch.int32)):
+        raise RuntimeError(f"{what}: graph replay output differs from an eager launch")
+
+
+def copies_for(nbytes: int, minimum: int = 2) -> int:
+    return max(minimum, -(-(MALL_BYTES + (MALL_BYTES >> 2)) // nbytes))
+
+
+def bench_gemv(torch, lib, stream, args):
+    import synth
+    log("GEMV inputs: W 4096x4096 Q4_0 (seed 1006, N(0,0.02)), x Q8_0 (seed 1007, N(0,1))")
+    w = synth.q4_0_matrix(N, N, synth.SEEDS["gemv_w"], 0.02)
+    x = synth.q8_0_matrix(1, N, synth.SEEDS["gemv_x"], 1.0).reshape(-1)
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    stream = torch.cuda.Stream()
-    sptr = stream.cuda_stream
-    result = {}
+    copies = max(args.copies, copies_for(w.size, 2))
+    wd = torch.empty((copies, w.size), dtype=torch.uint8, device=dev)
+    wd[:] = torch.from_numpy(w.reshape(-1)).to(dev)
+    xd = torch.from_numpy(x).to(dev)
+    yd = torch.empty((copies, N), dtype=torch.float32, device=dev)
+    fn = checked(lib.tcrv_hip_gemv_q4_0_q8_0, "gemv")
+    wp = [wd[i].data_ptr() for i in range(copies)]
+    yp = [yd[i].data_ptr() for i in range(copies)]
+    sp = stream.cuda_stream
+    bx = w.shape[1]
 
-    # ------------------------------------------------------------ GEMV ---
-    if args.only in ("all", "gemv"):
-        log("building GEMV inputs (W 4096x4096 Q4_0 seed 1006, x Q8_0 seed 1007)")
-        w = synth.q4_0_matrix(N, N, synth.SEEDS["gemv_w"], 0.02)
-        x = synth.q8_0_matrix(1, N, synth.SEEDS["gemv_x"], 1.0).reshape(-1)
-        bx = w.shape[1]
-        wbytes = w.size
-        w_dev = torch.from_numpy(w).to(dev).reshape(-1)
-        copies = torch.empty((args.copies, wbytes), dtype=torch.uint8, device=dev)
-        copies[:] = w_dev
-        del w_dev
-        x_dev = torch.from_numpy(x).to(dev)
-        y_dev = torch.empty((args.copies, N), dtype=torch.float32, device=dev)
-        lib = tcrv_hip.load()
-        fn = lib.tcrv_hip_gemv_q4_0_q8_0
-        wp = [copies[i].data_ptr() for i in range(args.copies)]
-        yp = [y_dev[i].data_ptr() for i in range(args.copies)]
-        xp = x_dev.data_ptr()
+    def launch(i):
+        k = i % copies
+        fn(N, yp[k], wp[k], bx, xd.data_ptr(), N, sp)
 
-        def gemv(i):
-            k = i % args.copies
-            st = fn(N, yp[k], wp[k], bx, xp, N, sptr)
-            if st != 0:
-                raise RuntimeError(tcrv_hip.status_string(st))
+    warm = Region(torch, stream, launch, max(args.warmup, 1))
+    warm.run()
+    del warm
+    yd.zero_()
+    timed = Region(torch, stream, launch, args.steps)
+    ms = timed.run()
+    same_as_eager(torch, stream, yd[0], lambda out: fn(N, out, wp[0], bx, xd.data_ptr(), N, sp),
+                  "GEMV")
+    us = ms * 1e3 / args.steps
+    gbs = GEMV_BYTES / (us * 1e-6) / 1e9
+    log(f"GEMV {us:.2f} us/launch over {args.steps} launches, {copies} weight copies: "
+        f"{gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+    return {"us": us, "gbs": gbs, "copies": copies, "ms_region": ms}
 
-        with torch.cuda.stream(stream):
-            log(f"GEMV warmup {args.warmup} ({args.mode})")
-            run_region(torch, stream, gemv, args.warmup, args.mode)
-            log(f"GEMV timed {args.steps} steps over {args.copies} weight copies")
-            ms = run_region(torch, stream, gemv, args.steps, args.mode)
-        ms_step = ms / args.steps
-        gemv_bytes = wbytes + x.size + N * 4  # 9 457 920 B at 4096 x 4096
-        gbs = gemv_bytes / (ms_step * 1e-3) / 1e9
-        result["gemv"] = {"ms_per_step": ms_step, "bytes": gemv_bytes, "gbs": gbs}
-        log(f"GEMV {ms_step * 1e3:.2f} us/step, {gbs:.0f} GB/s "
-            f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
-        del copies, y_dev
 
-    # ------------------------------------------------------------ GEMM ---
-    if args.only in ("all", "gemm"):
-        log("building GEMM inputs (A 4096 tokens Q8_0 seed 1008, B 4096x4096 Q8_0 seed 1009)")
-        a = synth.q8_0_matrix(N, N, synth.SEEDS["gemm_a"], 1.0)
-        b = synth.q8_0_matrix(N, N, synth.SEEDS["gemm_b"], 0.02)
-        a_dev = torch.from_numpy(a).to(dev)
-        b_dev = torch.from_numpy(b).to(dev)
-        c_dev = torch.empty(N * N, dtype=torch.float32, device=dev)
-        lib = tcrv_hip.load()
-        gfn = lib.tcrv_hip_q8_0_q8_0_gemm
-        ap_, bp_, cp_ = a_dev.data_ptr(), b_dev.data_ptr(), c_dev.data_ptr()
-        rb = a.shape[1]
+def bench_gemm(torch, lib, stream, args):
+    import synth
+    log("GEMM inputs: A 4096 tokens x 4096 Q8_0 (seed 1008, N(0,1)), "
+        "B 4096x4096 Q8_0 (seed 1009, N(0,0.02))")
+    a = synth.q8_0_matrix(N, N, synth.SEEDS["gemm_a"], 1.0)
+    b = synth.q8_0_matrix(N, N, synth.SEEDS["gemm_b"], 0.02)
+    dev = torch.device("cuda:0")
+    ad = torch.from_numpy(a).to(dev)
+    bd = torch.from_numpy(b).to(dev)
+    cd = torch.empty(N * N, dtype=torch.float32, device=dev)
+    fn = checked(lib.tcrv_hip_q8_0_q8_0_gemm, "gemm")
+    rb, sp = a.shape[1], stream.cuda_stream
 
-        def gemm(i):
-            st = gfn(N, cp_, bp_, ap_, rb, N, N, rb, N, sptr)
-            if st != 0:
-                raise RuntimeError(tcrv_hip.status_string(st))
+    def launch(i):
+        # s[ir*bs + col]: ir = weight row (B), col = token (A)
+        fn(N, cd.data_ptr(), bd.data_ptr(), ad.data_ptr(), rb, N, N, rb, N, sp)
 
-        with torch.cuda.stream(stream):
-            run_region(torch, stream, gemm, 5, "eager")
-            ms = run_region(torch, stream, gemm, args.gemm_steps, "eager")
-        ms_step = ms / args.gemm_steps
-        ops = 2.0 * N * N * N
-        tops = ops / (ms_step * 1e-3) / 1e12
-        result["gemm"] = {"ms_per_step": ms_step, "ops": ops, "tops": tops}
-        log(f"GEMM {ms_step * 1e3:.1f} us/step, {tops:.1f} TOPS "
-            f"({100 * tops / INT8_PEAK_TOPS:.1f}% of int8 peak)")
-        del a_dev, b_dev, c_dev
+    Region(torch, stream, launch, 2).run()
+    cd.zero_()
+    timed = Region(torch, stream, launch, args.gemm_steps)
+    ms = timed.run()
+    same_as_eager(torch, stream, cd,
+                  lambda out: fn(N, out, bd.data_ptr(), ad.data_ptr(), rb, N, N, rb, N, sp), "GEMM")
+    us = ms * 1e3 / args.gemm_steps
+    tops = GEMM_OPS / (us * 1e-6) / 1e12
+    log(f"GEMM {us:.1f} us/launch: {tops:.0f} TOPS ({100 * tops / INT8_PEAK_TOPS:.1f}% of "
+        f"dense int8 peak)")
+    return {"us": us, "tops": tops}
 
-    # ---------------------------------------------------- CPU baseline ---
-    cpu = cpu_baseline(args, result)
 
-    # --------------------------------------------------------- report ---
-    traffic = load_traffic()
-    line = {
-        "metric": "Q4_0 GEMV GB/s (% HBM peak); Q8_0 GEMM int8 TOPS (% MFMA peak)",
-        "higher_is_better": True,
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "q4_0/q8_0 blocks, int32 block sums, f32 fold",
-        "data": "synthetic: splitmix64 Box-Muller seeds 1006/1007 (GEMV), 1008/1009 (GEMM)",
-        "config": {"workload": "gemv_q4_0_q8_0 4096x4096 (configs[3])", "rows": N, "cols": N,
-                   "launch": args.mode, "weight_copies": args.copies},
+def bench_configs(torch, lib, stream, args):
+    """configs[0..2]: add f32 2^24, Q8_0 dequant 4096x4096, Q8_0.Q8_0 block dot
+    16384 x 4096 -- each over rotating input sets larger than the MALL."""
+    import synth
+    dev = torch.device("cuda:0")
+    sp = stream.cuda_stream
+    out = {}
+    steps = args.config_steps
+
+    # add
+    n = 1 << 24
+    sets = copies_for(12 * n, 2)
+    a = torch.from_numpy(synth.uniform_f32(synth.SEEDS["add_a"], n)).to(dev)
+    b = torch.from_numpy(synth.uniform_f32(synth.SEEDS["add_b"], n)).to(dev)
+    A = torch.empty((sets, n), device=dev); A[:] = a
+    B = torch.empty((sets, n), device=dev); B[:] = b
+    C = torch.empty((sets, n), device=dev)
+    fn = checked(lib.tcrv_hip_add_f32, "add")
+    ptrs = [(A[i].data_ptr(), B[i].data_ptr(), C[i].data_ptr()) for i in range(sets)]
+    reg = Region(torch, stream, lambda i: fn(*ptrs[i % sets], n, sp), steps)
+    reg.run()
+    us = reg.run() * 1e3 / steps
+    out["add_f32"] = {"workload": "configs[0] add f32 n=2^24", "us": round(us, 3),
+                      "GB/s": round(ADD_BYTES / us / 1e3, 1), "sets": sets}
+    del A, B, C, a, b, reg
+
+    # dequant
+    nb = N * N // 32
+    q = synth.quantize_q8_0(synth.normal_f32(synth.SEEDS["dequant_w"], N * N, 0.0, 0.02))
+    sets = copies_for(DEQ_BYTES, 2)
+    Q = torch.empty((sets, q.size), dtype=torch.uint8, device=dev)
+    Q[:] = torch.from_numpy(q).to(dev)
+    Y = torch.empty((sets, nb * 32), device=dev)
+    fn = checked(lib.tcrv_hip_dequantize_row_q8_0, "dequant")
+    ptrs = [(Q[i].data_ptr(), Y[i].data_ptr()) for i in range(sets)]
+    reg = Region(torch, stream, lambda i: fn(*ptrs[i % sets], N * N, sp), steps)
+    reg.run()
+    us = reg.run() * 1e3 / steps
+    out["dequant_q8_0"] = {"workload": "configs[1] Q8_0 dequant 4096x4096", "us": round(us, 3),
+                           "GB/s": round(DEQ_BYTES / us / 1e3, 1), "sets": sets}
+    del Q, Y, reg
+
+    # block dot
+    xq = synth.q8_0_matrix(DOT_ROWS, N, synth.SEEDS["dot_x"], 1.0)
+    yq = synth.q8_0_matrix(DOT_ROWS, N, synth.SEEDS["dot_y"], 1.0)
+    sets = copies_for(DOT_BYTES, 2)
+    X = torch.empty((sets, xq.size), dtype=torch.uint8, device=dev)
+    X[:] = torch.from_numpy(xq.reshape(-1)).to(dev)
+    Yd = torch.empty((sets, yq.size), dtype=torch.uint8, device=dev)
+    Yd[:] = torch.from_numpy(yq.reshape(-1)).to(dev)
+    S = torch.empty((sets, DOT_ROWS), device=dev)
+    fn = checked(lib.tcrv_hip_q8_0_q8_0_block_dot_rows, "block_dot_rows")
+    rb = xq.shape[1]
+    ptrs = [(S[i].data_ptr(), X[i].data_ptr(), Yd[i].data_ptr()) for i in range(sets)]
+
+    def dot(i):
+        s_, x_, y_ = ptrs[i % sets]
+        fn(N, s_, x_, rb, y_, rb, DOT_ROWS, sp)
+
+    reg = Region(torch, stream, dot, max(steps // 2, 1))
+    reg.run()
+    us = reg.run() * 1e3 / max(steps // 2, 1)
+    out["vec_dot_q8_0_q8_0"] = {"workload": "configs[2] Q8_0.Q8_0 block dot 16384 x 4096",
+                                "us": round(us, 3), "GB/s": round(DOT_BYTES / us / 1e3, 1),
+                                "sets": sets}
+    for k, v in out.items():
+        log(f"{k}: {v['us']:.1f} us, {v['GB/s']:.0f} GB/s "
+            f"({100 * v['GB/s'] / HBM_PEAK_GBS:.1f}% of HBM peak)")
+    return out
+
+
+def cpu_threads() -> int:
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit():
+        return max(1, int(env))
+    return max(1, min(os.cpu_count() or 1, 16))
+
+
+def cpu_baseline(seconds: float):
+    """The scalar C oracle (the CPU restatement of the reference's emitters) on
+    the host: whole 4096x4096 Q4_0 x Q8_0 GEMVs repeated for `seconds`, OpenMP
+    over rows (each row's fold stays serial, so results equal the 1-thread
+    run), plus a 1-thread figure over a quarter of the time."""
+    import synth
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_binding
+
+    ora = oracle_binding.load()
+    threads = cpu_threads()
+    w = synth.q4_0_matrix(N, N, synth.SEEDS["gemv_w"], 0.02)
+    x = synth.q8_0_matrix(1, N, synth.SEEDS["gemv_x"], 1.0).reshape(-1)
+
+    def rate(nt, budget):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            ora.gemm_q4_0(N, w, x, 0, N, 1, w.shape[1], 1, nt)
+            reps += 1
+            dt = time.perf_counter() - t0
+            if dt >= budget:
+                return GEMV_BYTES * reps / dt / 1e9, reps
+
+    one, reps1 = rate(1, seconds / 4)
+    many, reps = rate(threads, seconds)
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    log(f"CPU oracle GEMV: {many:.1f} GB/s on {threads} threads, {one:.2f} GB/s on 1 ({cpu})")
+    return {
+        "value": round(many, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "sample": (f"oracle/ scalar C (gcc -O3 -march=x86-64-v3, OpenMP over rows, serial "
+                   f"fmaf fold per row): {reps} whole 4096x4096 Q4_0xQ8_0 GEMVs in "
+                   f"{seconds:.0f} s on {threads} threads of {cpu}; 1 thread: "
+                   f"{one:.3f} GB/s ({reps1} GEMVs)"),
+        "value_1thread": round(one, 4),
     }
-    if "gemv" in result:
-        g = result["gemv"]
-        line.update({
-            "value": round(g["gbs"], 2), "unit": "GB/s",
-            "ms_per_step": g["ms_per_step"],
-            "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 2),
-                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
-                         "traffic": traffic.get("gemv_q4_0_q8_0")},
-        })
-    if "gemm" in result:
-        m = result["gemm"]
-        line["gemm"] = {
-            "workload": "q8_0_q8_0_gemm 4096x4096x4096 (configs[4])",
-            "value": round(m["tops"], 2), "unit": "TOPS", "ms_per_step": m["ms_per_step"],
-            "steps": args.gemm_steps,
-            "roofline": {"bound": "mfma", "achieved": round(m["tops"], 2),
-                         "peak": INT8_PEAK_TOPS, "unit": "TOPS",
-                         "frac": round(m["tops"] / INT8_PEAK_TOPS, 4),
-                         "traffic": traffic.get("q8_0_q8_0_gemm")},
-        }
-        if "gemv" not in result:
-            line.update({"value": line["gemm"]["value"], "unit": "TOPS",
-                         "ms_per_step": m["ms_per_step"]})
-    line["cpu_baseline"] = cpu
-    print(json.dumps(line), flush=True)
 
 
 def load_traffic():
@@ -230,59 +319,87 @@ def load_traffic():
     return {}
 
 
-def cpu_threads() -> int:
-    env = os.environ.get("OMP_NUM_THREADS")
-    if env and env.isdigit():
-        return max(1, int(env))
-    return max(1, min(os.cpu_count() or 1, 16))
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (each config "
+              "shards by rows with no exchange but an all-gather of the output; see the "
+              "sharding design in DESIGN.md).  Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
 
+    import torch
+    import tcrv_hip
 
-def cpu_baseline(args, result):
-    """Times the scalar C oracle on the host on a bounded sample of the same
-    workload.  The GEMV leg runs whole 4096x4096 GEMVs; the GEMM leg runs a
-    64-row slice of the 4096^3 GEMM and scales by rows."""
-    if args.cpu_seconds <= 0:
-        return None
-    import numpy as np
+    lib = tcrv_hip.load()
+    torch.cuda.set_device(0)
+    stream = torch.cuda.Stream()
+    if args.only == "calib":
+        n = 1 << 24
+        a = torch.rand(n, device="cuda:0")
+        b = torch.rand(n, device="cuda:0")
+        c = torch.empty(n, device="cuda:0")
+        fn = checked(lib.tcrv_hip_add_f32, "add")
+        for _ in range(10):
+            fn(a.data_ptr(), b.data_ptr(), c.data_ptr(), n, stream.cuda_stream)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib": "add_f32", "n": n, "read_bytes": 8 * n, "write_bytes": 4 * n}))
+        return
+    res = {}
+    if args.only in ("all", "gemv"):
+        res["gemv"] = bench_gemv(torch, lib, stream, args)
+    if args.only in ("all", "gemm"):
+        res["gemm"] = bench_gemm(torch, lib, stream, args)
+    if args.only in ("all", "configs"):
+        res["configs"] = bench_configs(torch, lib, stream, args)
+    cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+    traffic = load_traffic()
 
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import oracle_binding
-    import synth
-
-    ora = oracle_binding.load()
-    threads = cpu_threads()
-    out = {}
-    if "gemv" in result:
-        w = synth.q4_0_matrix(N, N, synth.SEEDS["gemv_w"], 0.02)
-        x = synth.q8_0_matrix(1, N, synth.SEEDS["gemv_x"], 1.0).reshape(-1)
-        reps, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < args.cpu_seconds:
-            ora.gemm_q4_0(N, w, x, 0, N, 1, w.shape[1], 1, threads)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        out["gemv_gbs"] = result["gemv"]["bytes"] / dt / 1e9
-        out["gemv_reps"] = reps
-        log(f"CPU GEMV oracle: {dt * 1e3:.2f} ms per 4096x4096 GEMV on {threads} threads")
-    if "gemm" in result:
-        rows = 64
-        b = synth.q8_0_matrix(rows, N, synth.SEEDS["gemm_b"], 0.02)
-        a = synth.q8_0_matrix(N, N, synth.SEEDS["gemm_a"], 1.0)
-        t0 = time.perf_counter()
-        ora.gemm_q8_0(N, b, a, a.shape[1], rows, N, b.shape[1], N, threads)
-        dt = (time.perf_counter() - t0) * (N / rows)
-        out["gemm_tops"] = 2.0 * N * N * N / dt / 1e12
-        log(f"CPU GEMM oracle: 64-row slice -> {out['gemm_tops']:.4f} TOPS scaled to 4096 rows")
-    primary = "gemv_gbs" if "gemv_gbs" in out else "gemm_tops"
-    return {
-        "value": round(out[primary], 4),
-        "unit": "GB/s" if primary == "gemv_gbs" else "TOPS",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"scalar C oracle (gcc -O3, OpenMP over rows, fold serial per row) on "
-                   f"{threads} host threads: whole 4096x4096 GEMVs repeated for "
-                   f"{args.cpu_seconds:.0f} s; GEMM = 64-row slice of 4096^3 scaled x64"),
-        "gemm_tops": round(out.get("gemm_tops", 0.0), 4) if "gemm_tops" in out else None,
+    line = {
+        "metric": METRIC,
+        "higher_is_better": True,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 (q4_0/q8_0 block quants) -> int32 block sums, fp32 fold",
+        "data": "synthetic: splitmix64 Box-Muller, seeds 1001-1009 (tianchen-rv_amd/synth.py)",
+        "config": {"workload": "gemv_q4_0_q8_0 W 4096x4096 Q4_0 x Q8_0 vector (configs[3])",
+                   "rows": N, "cols": N, "launch": "HIP graph of `steps` launches",
+                   "weight_copies": res.get("gemv", {}).get("copies")},
     }
+    if "gemv" in res:
+        g = res["gemv"]
+        line.update({
+            "value": round(g["gbs"], 2), "unit": "GB/s", "ms_per_step": g["us"] / 1e3,
+            "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
+                         "traffic": traffic.get("gemv_q4_0_q8_0", {}).get("bytes"),
+                         "kernel": "gemv_q4_0_q8_0_direct",
+                         "bytes_per_launch": GEMV_BYTES,
+                         "us_per_launch": round(g["us"], 4)},
+        })
+    if "gemm" in res:
+        m = res["gemm"]
+        line["gemm"] = {
+            "workload": "q8_0_q8_0_gemm 4096 weight rows x 4096 tokens x 4096 (configs[4])",
+            "value": round(m["tops"], 2), "unit": "TOPS", "ms_per_step": m["us"] / 1e3,
+            "steps": args.gemm_steps,
+            "roofline": {"bound": "mfma", "achieved": round(m["tops"], 2), "peak": INT8_PEAK_TOPS,
+                         "unit": "TOPS", "frac": round(m["tops"] / INT8_PEAK_TOPS, 4),
+                         "traffic": traffic.get("q8_0_q8_0_gemm", {}).get("bytes"),
+                         "kernel": "gemm_q8_0_q8_0_mfma", "ops_per_launch": GEMM_OPS},
+        }
+        if "gemv" not in res:
+            line.update({"value": line["gemm"]["value"], "unit": "TOPS",
+                         "ms_per_step": line["gemm"]["ms_per_step"]})
+    if "configs" in res:
+        line["configs"] = res["configs"]
+        if "value" not in line:
+            first = next(iter(res["configs"].values()))
+            line.update({"value": first["GB/s"], "unit": "GB/s", "ms_per_step": first["us"] / 1e3})
+    line["cpu_baseline"] = cpu
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

@@ -1,0 +1,92 @@
+#!/usr/bin/env python3
+"""Summaries of rocprofv3 output for the committed profiles.
+
+  rocprof_summary.py stats <run_kernel_stats.csv> [name-substring ...]
+      per-kernel call count and average / min / max duration (us)
+  rocprof_summary.py traffic <pmc-root>
+      HBM bytes per dispatch of the GEMV and GEMM kernels from the two
+      counter passes (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled by
+      what the same counter reads for the known-size calibration kernel
+      (add_f32 over n = 2^24: 128 MiB read, 64 MiB written per launch).
+      <pmc-root> holds pmc_<COUNTER>_<calib|gemv|gemm>/run_counter_collection.csv
+      as written by `rocprofv3 --pmc <COUNTER> -f csv -d <pmc-root>/pmc_<COUNTER>_<w>
+      -o run -- python3 bench.py --only <w> ...`.  Prints JSON.
+"""
+from __future__ import annotations
+
+import csv
+import json
+import os
+import statistics
+import sys
+
+KERNELS = {
+    "gemv_q4_0_q8_0": "gemv_q4_0_q8_0_direct",
+    "q8_0_q8_0_gemm": "gemm_q8_0_q8_0_mfma",
+    "calib": "add_f32_vec4",
+}
+CALIB_BYTES = {"FETCH_SIZE": 8 << 24, "WRITE_SIZE": 4 << 24}  # per add_f32 launch, n = 2^24
+
+
+def stats(path, needles):
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name = r["Name"]
+            if needles and not any(n in name for n in needles):
+                continue
+            rows.append((name, int(r["Calls"]), float(r["AverageNs"]) / 1e3,
+                         float(r["MinNs"]) / 1e3, float(r["MaxNs"]) / 1e3))
+    for name, calls, avg, mn, mx in rows:
+        short = name.split("(")[0]
+        print(f"| {short} | {calls} | {avg:.3f} | {mn:.3f} | {mx:.3f} |")
+
+
+def counter_per_dispatch(path, kernel):
+    vals = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            if kernel in r["Kernel_Name"]:
+                key = r["Dispatch_Id"]
+                vals[key] = vals.get(key, 0.0) + float(r["Counter_Value"])
+    if not vals:
+        raise SystemExit(f"{path}: no dispatch of {kernel}")
+    v = list(vals.values())
+    return statistics.median(v), len(v)
+
+
+def traffic(root):
+    out = {"method": "median KiB per dispatch x 1024, scaled by calib bytes / calib counter"}
+    scale = {}
+    for ctr, known in CALIB_BYTES.items():
+        kib, n = counter_per_dispatch(
+            os.path.join(root, f"pmc_{ctr}_calib", "run_counter_collection.csv"), KERNELS["calib"])
+        scale[ctr] = known / (kib * 1024.0)
+        out[f"calib_{ctr}"] = {"KiB_per_dispatch": kib, "dispatches": n, "known_bytes": known,
+                               "scale": scale[ctr]}
+    for key, tag in (("gemv_q4_0_q8_0", "gemv"), ("q8_0_q8_0_gemm", "gemm")):
+        total = 0.0
+        entry = {"kernel": KERNELS[key]}
+        for ctr in CALIB_BYTES:
+            kib, n = counter_per_dispatch(
+                os.path.join(root, f"pmc_{ctr}_{tag}", "run_counter_collection.csv"), KERNELS[key])
+            b = kib * 1024.0 * scale[ctr]
+            entry[ctr] = {"KiB_per_dispatch": kib, "dispatches": n, "bytes_scaled": round(b)}
+            total += b
+        entry["bytes"] = round(total)
+        out[key] = entry
+    print(json.dumps(out, indent=1))
+
+
+def main():
+    if len(sys.argv) >= 3 and sys.argv[1] == "stats":
+        stats(sys.argv[2], sys.argv[3:])
+    elif len(sys.argv) == 3 and sys.argv[1] == "traffic":
+        traffic(sys.argv[2])
+    else:
+        print(__doc__)
+        sys.exit(2)
+
+
+if __name__ == "__main__":
+    main()
