@@ -1,0 +1,81 @@
+#!/usr/bin/env python3
+"""Runs the hardware probes (hw_probes.hip, built by `make -C tianchen-rv_amd probes`)
+on cuda:0 and prints one line per measurement."""
+import ctypes
+import os
+import sys
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "libtcrv_probes.so")
+
+
+def graph_us(stream, launch, n=1000, reps=5):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(n):
+                launch()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / n)
+    return best
+
+
+def main():
+    if not os.path.exists(LIB):
+        sys.exit(f"{LIB} missing: run `make -C tianchen-rv_amd probes`")
+    lib = ctypes.CDLL(LIB)
+    lib.probe_mix.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                              ctypes.c_int, ctypes.c_void_p]
+    lib.probe_empty.argtypes = [ctypes.c_void_p]
+    lib.probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int,
+                               ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    sp = stream.cuda_stream
+    inp = torch.randint(-100, 100, (4096,), dtype=torch.int32, device=dev)
+    grid, iters = 256, 4000
+    out = torch.empty(grid * 512, device=dev)
+    names = ["MFMA only (2 x i8 32x32x32 per iteration)", "VALU only (64 x v_fma_f32)",
+             "both in every wave", "waves 0-3 MFMA, waves 4-7 VALU"]
+    for mode, name in enumerate(names):
+        assert lib.probe_mix(mode, inp.data_ptr(), out.data_ptr(), 10, grid, sp) == 0
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            assert lib.probe_mix(mode, inp.data_ptr(), out.data_ptr(), iters, grid, sp) == 0
+            e1.record(stream)
+        torch.cuda.synchronize()
+        print(f"mix mode {mode} ({name}): {e0.elapsed_time(e1):.3f} ms "
+              f"[{grid} x 512 threads, {iters} iterations]", flush=True)
+    print(f"empty kernel, graph of 1000: {graph_us(stream, lambda: lib.probe_empty(sp)):.2f} "
+          f"us per launch", flush=True)
+    nbytes = 9437184
+    copies = 40
+    bufs = torch.empty((copies, nbytes), dtype=torch.uint8, device=dev)
+    sink = torch.zeros(256, dtype=torch.int32, device=dev)
+    for grid in (576, 1024, 2304):
+        k = [0]
+
+        def launch():
+            lib.probe_read(bufs[k[0] % copies].data_ptr(), nbytes, sink.data_ptr(), grid, sp)
+            k[0] += 1
+        us = graph_us(stream, launch)
+        print(f"read-only {nbytes} B over {copies} rotating buffers, grid {grid} x 256: "
+              f"{us:.2f} us per launch ({nbytes / us / 1e3:.0f} GB/s)", flush=True)
+
+
+if __name__ == "__main__":
+    main()
