@@ -1,4 +1,4 @@
-// gemm.hip -- a9: Q8_0 x Q8_0 prefill GEMM on v_mfma_i32_32x32x32_i8.
+// gemm.hip -- a9: Q8_0 x Q8_0 prefill GEMM on MFMA.
 //
 // Semantics (the reference's GEMM loop nest, RVVToEmitCBlockQuantLinear.cpp:
 // 1691-2121, with the Q8_0 block dot of :7264-7671 as the element):
@@ -6,15 +6,15 @@
 //                    fma((float)sumi(ir,col,b), d_x(ir,b)*d_y(col,b), .)
 // where x = weight rows (vx, stride bx) and y = activation rows (vy, stride by).
 //
-// Mapping: K = 32 of the MFMA is exactly one Q8_0 block, so every MFMA yields
-// the int32 block sums of a 32x32 output tile for one block; the fp32 fold of
-// that block is applied to the tile right away, in ascending block order, so
-// every output element sees the reference's sequence of roundings.
-//   work-group: 128 weight rows x 128 activation rows, 4 waves as 2x2, each
-//               wave 2x2 MFMA tiles (64x64 outputs);
-//   K loop:     chunks of 8 blocks (272 B per row, 17 x 128-bit loads) staged
-//               through LDS; the fp16 scales are widened once per chunk into
-//               fp32 LDS arrays.
+// K = 32 of v_mfma_i32_32x32x32_i8 is exactly one Q8_0 block, so every MFMA
+// yields the int32 block sums of a 32x32 output tile for one block; the fp32
+// fold of that block is applied to the tile right away, in ascending block
+// order, so every output element sees the reference's sequence of roundings.
+//
+// Two kernels:
+//   gemm_q8_0_q8_0_occ     rows 4-byte aligned (the fast path, below);
+//   gemm_q8_0_q8_0_kernel  any 2-byte aligned rows: 4 waves, 2x2 tiles each,
+//                          raw block bytes through LDS, scalar scale epilogue.
 #include "tcrv_hip_internal.h"
 
 namespace tcrv {
@@ -181,68 +181,25 @@ __global__ __launch_bounds__(kGmThreads) void gemm_q8_0_q8_0_kernel(
 
 
 // ---------------------------------------------------------------------------
-// The fast path.  Per 32x32 output tile and Q8_0 block b:
-//   v_mfma_i32_32x32x32_i8   -> sumi(row, col, b) for the tile (K = one block)
-//   v_mfma_f32_32x32x16_f16  -> dx(row, b) * dy(col, b) for the tile: the A
-//                               operand carries dx in k-slot 0 only, the B
-//                               operand dy in k-slot 0 only, so the product is
-//                               a rank-1 outer product, exact in fp32 (two
-//                               11-bit significands)
+// Fast path.  Per 32x32 output tile and Q8_0 block b:
+//   v_mfma_i32_32x32x32_i8  -> sumi(row, col, b) for the tile
+//   v_mfma_f32_32x32x8f16   -> dx(row, b) * dy(col, b) for the tile: the A
+//                              operand carries dx in k-slot 0 only, the B
+//                              operand dy in k-slot 0 only, so the product is a
+//                              rank-1 outer product, exact in fp32 (two 11-bit
+//                              significands) -- no per-element VALU multiply
 //   VALU: acc = fma((float)sumi, dxy, acc)   -- the reference fold, in order.
-// Staging splits each 34-byte block into its 32 quants (row-major, 16-byte
-// aligned, row stride 272 bytes so 16-byte LDS reads of 32 consecutive rows hit
-// distinct banks) and its fp16 scale.
-// Work-group: 128 weight rows x 128 activation rows, 4 waves as 2x2, each wave
-// 2x2 tiles of 32x32; K chunk of kFbKB blocks, single-buffered, two
-// work-groups per CU overlap one's staging with the other's MFMAs.
 // ---------------------------------------------------------------------------
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 
-constexpr int kFbBM = 128;
-constexpr int kFbBN = 128;
-constexpr int kFbKB = 8;                      // blocks per K chunk
-constexpr int kFbQRow = kFbKB * kQK + 16;     // 272: quant bytes per staged row (+16 pad)
-constexpr int kFbThreads = 256;
-
-// Splits one staged block pair (68 bytes, dword aligned, at q) of one row into
-// LDS: quants of blocks 2m and 2m+1 at qrow[64m..64m+63], fp16 scales into
-// drow[2m*stride], drow[(2m+1)*stride].  `two` == false: only block 2m exists
-// (34 bytes are read).
-__device__ __forceinline__ void stage_pair(const uint8_t *q, bool two, int8_t *qrow,
-                                           uint16_t *d0, uint16_t *d1) {
-  const uint32_t *g = reinterpret_cast<const uint32_t *>(q);
-  uint32_t r[17];
-  if (two) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(g + 4 * k);
-      r[4 * k + 0] = v.x; r[4 * k + 1] = v.y; r[4 * k + 2] = v.z; r[4 * k + 3] = v.w;
-    }
-    r[16] = g[16];
-  } else {
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(g + 4 * k);
-      r[4 * k + 0] = v.x; r[4 * k + 1] = v.y; r[4 * k + 2] = v.z; r[4 * k + 3] = v.w;
-    }
-    r[8] = *reinterpret_cast<const uint16_t *>(q + 32);  // bytes 32-33: last two quants
-#pragma unroll
-    for (int k = 9; k < 17; ++k)
-      r[k] = 0;
-  }
-  uint4 *dst = reinterpret_cast<uint4 *>(qrow);
-  dst[0] = make_uint4(funnel16(r[0], r[1]), funnel16(r[1], r[2]), funnel16(r[2], r[3]),
-                      funnel16(r[3], r[4]));
-  dst[1] = make_uint4(funnel16(r[4], r[5]), funnel16(r[5], r[6]), funnel16(r[6], r[7]),
-                      funnel16(r[7], r[8]));
-  *d0 = static_cast<uint16_t>(r[0] & 0xffffu);
-  if (two) {
-    dst[2] = make_uint4(r[9], r[10], r[11], r[12]);
-    dst[3] = make_uint4(r[13], r[14], r[15], r[16]);
-    *d1 = static_cast<uint16_t>(r[8] >> 16);
-  }
-}
+constexpr int kFbBM = 128;                 // weight rows per work-group
+constexpr int kFbBN = 128;                 // tokens per work-group
+constexpr int kFbKB = 8;                   // blocks per K chunk
+constexpr int kFbQRow = kFbKB * kQK + 16;  // 272: quant bytes per staged row (+16 pad: 16-byte
+                                           // reads of 32 consecutive rows hit distinct banks)
 
 // XCD-aware tile order: work-groups are dispatched round-robin over the 8
 // XCDs (id % 8), so id is first remapped so that each XCD owns one contiguous
@@ -264,98 +221,64 @@ __device__ __forceinline__ void tile_of(unsigned id, unsigned tiles_m, unsigned 
   tn = in_group / gm;
 }
 
-// One block's MFMA operands for a wave's 2x2 tiles: int8 quants of the two
-// 32-row weight tiles and two 32-row activation tiles, and the fp16 scales as
-// k-slot 0 of 4-element f16 operands (every other k-slot, and every slot of
-// lanes 32..63, is zero), so the f16 MFMA yields the outer product dx*dy.
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-typedef int v2i __attribute__((ext_vector_type(2)));
+// Work-group: 16 waves, each owning one 32x32 tile of a 128x128 output tile
+// (four waves per SIMD hide LDS and MFMA latency; 90 VGPRs).  K chunks of 8
+// blocks are staged split -- each 34-byte block into its 32 quants (row-major,
+// 16-byte aligned) and its fp16 scale -- and double-buffered: each thread loads
+// its one 68-byte block pair of chunk c+1 into registers before computing chunk
+// c and writes it to the other LDS buffer afterwards.
+constexpr int kOcThreads = 1024;
+constexpr int kOcStage = (kFbBM + kFbBN) * kFbQRow;  // split quants of both panels
 
-struct Frags {
-  v4i a[2], b[2];
-  v2i ax[2], by[2];
+struct PairRegs {
+  uint32_t r[17];
 };
 
-struct TileOut {
-  v16i sumi;
-  v16f dxy;
-};
-
-__device__ __forceinline__ void read_frags(Frags &f, const int8_t *qa, const int8_t *qb,
-                                           const uint16_t (*da)[kFbBM],
-                                           const uint16_t (*db)[kFbBN], int b, int wm, int wn,
-                                           int li, int h) {
+// Loads one staged block pair task (68 bytes, or 34 when only block 2m exists).
+__device__ __forceinline__ void load_pair(PairRegs &p, const uint8_t *q, bool two) {
+  const uint32_t *g = reinterpret_cast<const uint32_t *>(q);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = wm * 64 + i * 32 + li;
-    f.a[i] = *reinterpret_cast<const v4i *>(qa + r * kFbQRow + b * kQK + 16 * h);
-    const uint32_t d = da[b][r];
-    f.ax[i] = v2i{h == 0 ? static_cast<int>(d) : 0, 0};
+  for (int k = 0; k < 2; ++k) {
+    const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(g + 4 * k);
+    p.r[4 * k + 0] = v.x; p.r[4 * k + 1] = v.y; p.r[4 * k + 2] = v.z; p.r[4 * k + 3] = v.w;
   }
+  if (two) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int c = wn * 64 + j * 32 + li;
-    f.b[j] = *reinterpret_cast<const v4i *>(qb + c * kFbQRow + b * kQK + 16 * h);
-    const uint32_t d = db[b][c];
-    f.by[j] = v2i{h == 0 ? static_cast<int>(d) : 0, 0};
+    for (int k = 2; k < 4; ++k) {
+      const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(g + 4 * k);
+      p.r[4 * k + 0] = v.x; p.r[4 * k + 1] = v.y; p.r[4 * k + 2] = v.z; p.r[4 * k + 3] = v.w;
+    }
+    p.r[16] = g[16];
+  } else {
+    p.r[8] = *reinterpret_cast<const uint16_t *>(q + 32);
   }
 }
 
-__device__ __forceinline__ void mfma_tile(TileOut &o, const Frags &f, int i, int j) {
-  const v16i izero = {};
-  const v16f fzero = {};
-  o.sumi = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[i], f.b[j], izero, 0, 0, 0);
-  o.dxy = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, f.ax[i]),
-                                               __builtin_bit_cast(v4h, f.by[j]), fzero, 0, 0, 0);
+__device__ __forceinline__ void store_pair(const PairRegs &p, bool two, int8_t *qrow,
+                                           uint16_t *d0, uint16_t *d1) {
+  const uint32_t *r = p.r;
+  uint4 *dst = reinterpret_cast<uint4 *>(qrow);
+  dst[0] = make_uint4(funnel16(r[0], r[1]), funnel16(r[1], r[2]), funnel16(r[2], r[3]),
+                      funnel16(r[3], r[4]));
+  dst[1] = make_uint4(funnel16(r[4], r[5]), funnel16(r[5], r[6]), funnel16(r[6], r[7]),
+                      funnel16(r[7], r[8]));
+  *d0 = static_cast<uint16_t>(r[0] & 0xffffu);
+  if (two) {
+    dst[2] = make_uint4(r[9], r[10], r[11], r[12]);
+    dst[3] = make_uint4(r[13], r[14], r[15], r[16]);
+    *d1 = static_cast<uint16_t>(r[8] >> 16);
+  }
 }
 
-// The reference fold for one block of one tile: acc = fma((float)sumi, dx*dy, acc).
-__device__ __forceinline__ void fold_tile(float acc[16], const TileOut &o) {
-#pragma unroll
-  for (int e = 0; e < 16; ++e)
-    acc[e] = fmaf(static_cast<float>(o.sumi[e]), o.dxy[e], acc[e]);
-}
-
-// Orders one pipeline step as: both MFMAs of the new tile, then the 32 VALU
-// ops (16 cvt + 16 fma) of the previous tile's fold, which no longer waits on
-// an MFMA issued in this step.
-__device__ __forceinline__ void step_order() {
-  __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // MFMA
-  __builtin_amdgcn_sched_group_barrier(0x002, 32, 0);  // VALU
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-// One block for the wave's four tiles; `pend` carries tile (1,1) between
-// blocks.  Each step issues a tile's MFMA pair and folds the tile issued one
-// step earlier.
-__device__ __forceinline__ void gemm_block(float (&acc)[2][2][16], TileOut &pend,
-                                           const Frags &f) {
-  TileOut t0, t1;
-  mfma_tile(t0, f, 0, 0);
-  fold_tile(acc[1][1], pend);
-  step_order();
-  mfma_tile(t1, f, 0, 1);
-  fold_tile(acc[0][0], t0);
-  step_order();
-  mfma_tile(t0, f, 1, 0);
-  fold_tile(acc[0][1], t1);
-  step_order();
-  mfma_tile(pend, f, 1, 1);
-  fold_tile(acc[1][0], t0);
-  step_order();
-}
-
-__global__ __launch_bounds__(kFbThreads, 2) void gemm_q8_0_q8_0_mfma(
+__global__ __launch_bounds__(kOcThreads, 1) void gemm_q8_0_q8_0_occ(
     size_t nb, float *s, const uint8_t *vx, const uint8_t *vy, size_t by, size_t nr,
     size_t nc, size_t bx, size_t bs) {
-  __shared__ __align__(16) int8_t qa[kFbBM * kFbQRow];
-  __shared__ __align__(16) int8_t qb[kFbBN * kFbQRow];
-  __shared__ __align__(16) uint16_t da[kFbKB][kFbBM];
-  __shared__ __align__(16) uint16_t db[kFbKB][kFbBN];
+  __shared__ __align__(16) int8_t q[2][kOcStage];
+  __shared__ __align__(16) uint16_t dsc[2][2][kFbKB][kFbBM];  // [stage][panel][block][row]
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;  // 4 x 4 waves, one 32x32 tile each
   const int li = lane & 31, h = lane >> 5;
   const unsigned tiles_m = static_cast<unsigned>((nr + kFbBM - 1) / kFbBM);
   const unsigned tiles_n = static_cast<unsigned>((nc + kFbBN - 1) / kFbBN);
@@ -364,75 +287,71 @@ __global__ __launch_bounds__(kFbThreads, 2) void gemm_q8_0_q8_0_mfma(
   const size_t m0 = static_cast<size_t>(tm) * kFbBM;
   const size_t n0 = static_cast<size_t>(tn) * kFbBN;
 
-  float acc[2][2][16];
+  // staging task of this thread: panel p (0 = weights, 1 = tokens), row r, pair m
+  const int sp = tid >> 9;
+  const int sr = (tid & 511) >> 2, sm = tid & 3;
+  const uint8_t *sbase = sp == 0 ? vx + min(m0 + sr, nr - 1) * bx : vy + min(n0 + sr, nc - 1) * by;
+
+  float acc[16];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
+  for (int e = 0; e < 16; ++e)
+    acc[e] = 0.0f;
+
+  const size_t nchunks = (nb + kFbKB - 1) / kFbKB;
+  PairRegs pr;
+  auto chunk_task = [&](size_t c, bool &active, bool &two) {
+    const int nbc = static_cast<int>(min(static_cast<size_t>(kFbKB), nb - c * kFbKB));
+    active = 2 * sm < nbc;
+    two = 2 * sm + 1 < nbc;
+  };
+  bool act, two;
+  chunk_task(0, act, two);
+  if (act)
+    load_pair(pr, sbase + 2 * sm * kQ8Bytes, two);
+  if (act)
+    store_pair(pr, two, q[0] + (sp * kFbBM + sr) * kFbQRow + 64 * sm, &dsc[0][sp][2 * sm][sr],
+               &dsc[0][sp][2 * sm + 1][sr]);
+  __syncthreads();
+
+  const int ra = wm * 32 + li, rb = kFbBM + wn * 32 + li;
+  for (size_t c = 0; c < nchunks; ++c) {
+    const int st = static_cast<int>(c & 1);
+    const int nbc = static_cast<int>(min(static_cast<size_t>(kFbKB), nb - c * kFbKB));
+    bool act1 = false, two1 = false;
+    if (c + 1 < nchunks) {
+      chunk_task(c + 1, act1, two1);
+      if (act1)
+        load_pair(pr, sbase + ((c + 1) * kFbKB + 2 * sm) * kQ8Bytes, two1);
+    }
+    const int8_t *qs = q[st];
+    for (int b = 0; b < nbc; ++b) {
+      const v4i a = *reinterpret_cast<const v4i *>(qs + ra * kFbQRow + b * kQK + 16 * h);
+      const v4i bq = *reinterpret_cast<const v4i *>(qs + rb * kFbQRow + b * kQK + 16 * h);
+      const uint32_t dxb = dsc[st][0][b][wm * 32 + li];
+      const uint32_t dyb = dsc[st][1][b][wn * 32 + li];
+      const v2i ax = v2i{h == 0 ? static_cast<int>(dxb) : 0, 0};
+      const v2i ay = v2i{h == 0 ? static_cast<int>(dyb) : 0, 0};
+      const v16i sumi = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, v16i{}, 0, 0, 0);
+      const v16f dxy = __builtin_amdgcn_mfma_f32_32x32x8f16(
+          __builtin_bit_cast(v4h, ax), __builtin_bit_cast(v4h, ay), v16f{}, 0, 0, 0);
 #pragma unroll
       for (int e = 0; e < 16; ++e)
-        acc[i][j][e] = 0.0f;
-
-  // Results of the last tile of the previous block, folded at the start of the
-  // next block; zero sums and zero scales make the first fold a no-op
-  // (fma(0, 0, acc) == acc, and acc is never -0).
-  TileOut pend;
-  pend.sumi = v16i{};
-  pend.dxy = v16f{};
-  for (size_t c0 = 0; c0 < nb; c0 += kFbKB) {
-    const int nbc = static_cast<int>(min(static_cast<size_t>(kFbKB), nb - c0));
-    const int npairs = (nbc + 1) >> 1;
-    __syncthreads();  // the previous chunk's fragments have been read
-    for (int t = tid; t < kFbBM * (kFbKB / 2); t += kFbThreads) {
-      const int r = t / (kFbKB / 2), m = t - r * (kFbKB / 2);
-      if (m < npairs) {
-        const size_t gr = min(m0 + r, nr - 1);  // rows past nr reuse row nr-1, never stored
-        stage_pair(vx + gr * bx + (c0 + 2 * m) * kQ8Bytes, 2 * m + 1 < nbc,
-                   qa + r * kFbQRow + 64 * m, &da[2 * m][r], &da[(2 * m + 1) & (kFbKB - 1)][r]);
-      }
+        acc[e] = fmaf(static_cast<float>(sumi[e]), dxy[e], acc[e]);
     }
-    for (int t = tid; t < kFbBN * (kFbKB / 2); t += kFbThreads) {
-      const int r = t / (kFbKB / 2), m = t - r * (kFbKB / 2);
-      if (m < npairs) {
-        const size_t gc = min(n0 + r, nc - 1);
-        stage_pair(vy + gc * by + (c0 + 2 * m) * kQ8Bytes, 2 * m + 1 < nbc,
-                   qb + r * kFbQRow + 64 * m, &db[2 * m][r], &db[(2 * m + 1) & (kFbKB - 1)][r]);
-      }
-    }
+    if (c + 1 < nchunks && act1)
+      store_pair(pr, two1, q[st ^ 1] + (sp * kFbBM + sr) * kFbQRow + 64 * sm,
+                 &dsc[st ^ 1][sp][2 * sm][sr], &dsc[st ^ 1][sp][2 * sm + 1][sr]);
     __syncthreads();
-    // Software pipeline: within a block each tile's MFMA pair is issued
-    // before the previous tile's fold, the last tile's fold is carried into
-    // the next block, and the next block's fragments are read from LDS while
-    // the current block computes (two fragment sets, loop unrolled by two).
-    Frags f0, f1;
-    read_frags(f0, qa, qb, da, db, 0, wm, wn, li, h);
-    for (int b = 0; b < nbc; b += 2) {
-      if (b + 1 < nbc)
-        read_frags(f1, qa, qb, da, db, b + 1, wm, wn, li, h);
-      gemm_block(acc, pend, f0);
-      if (b + 1 >= nbc)
-        break;
-      if (b + 2 < nbc)
-        read_frags(f0, qa, qb, da, db, b + 2, wm, wn, li, h);
-      gemm_block(acc, pend, f1);
-    }
   }
-  fold_tile(acc[1][1], pend);
 
+  const size_t col = n0 + wn * 32 + li;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const size_t col = n0 + wn * 64 + j * 32 + li;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const size_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (row < nr && col < nc)
-          s[row * bs + col] = acc[i][j][e];
-      }
-    }
+  for (int e = 0; e < 16; ++e) {
+    const size_t row = m0 + wm * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+    if (row < nr && col < nc)
+      s[row * bs + col] = acc[e];
+  }
 }
-
 }  // namespace tcrv
 
 extern "C" int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx,
@@ -453,16 +372,17 @@ extern "C" int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx,
   const size_t rowbytes = nb * tcrv::kQ8Bytes;
   if ((nr > 1 && bx < rowbytes) || (nc > 1 && by < rowbytes))
     return TCRV_HIP_ERR_BAD_SIZE;
-  const int rows16 = aligned16(vx) && aligned16(vy) && (nr == 1 || bx % 16 == 0) &&
-                     (nc == 1 || by % 16 == 0);
   if (aligned4(vx) && aligned4(vy) && (nr == 1 || bx % 4 == 0) && (nc == 1 || by % 4 == 0)) {
-    const size_t tiles = ((nr + tcrv::kFbBM - 1) / tcrv::kFbBM) * ((nc + tcrv::kFbBN - 1) / tcrv::kFbBN);
+    const size_t tiles =
+        ((nr + tcrv::kFbBM - 1) / tcrv::kFbBM) * ((nc + tcrv::kFbBN - 1) / tcrv::kFbBN);
     if (tiles > 0x7fffffffu)
       return TCRV_HIP_ERR_TOO_LARGE;
-    tcrv::gemm_q8_0_q8_0_mfma<<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kFbThreads), 0,
-                                as_stream(stream)>>>(nb, s, vx, vy, by, nr, nc, bx, bs);
+    tcrv::gemm_q8_0_q8_0_occ<<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kOcThreads), 0,
+                               as_stream(stream)>>>(nb, s, vx, vy, by, nr, nc, bx, bs);
     return launch_status();
   }
+  const int rows16 = aligned16(vx) && aligned16(vy) && (nr == 1 || bx % 16 == 0) &&
+                     (nc == 1 || by % 16 == 0);
   const size_t gx = (nc + tcrv::kGmBN - 1) / tcrv::kGmBN;
   const size_t gy = (nr + tcrv::kGmBM - 1) / tcrv::kGmBM;
   if (gx > 0x7fffffffu || gy > 65535u)

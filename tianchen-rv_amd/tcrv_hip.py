@@ -16,7 +16,8 @@ import os
 from typing import Optional
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libtcrv_hip.so")
+# TCRV_HIP_LIB selects another build of the library (same C-ABI).
+LIB_PATH = os.environ.get("TCRV_HIP_LIB") or os.path.join(HERE, "libtcrv_hip.so")
 
 QK = 32
 Q8_0_BLOCK_BYTES = 34
