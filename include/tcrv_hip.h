@@ -145,6 +145,38 @@ TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, 
                             size_t by, size_t nr, size_t nc, size_t bx, size_t bs,
                             void *stream);
 
+/* ---- a8: the x16 block-as-lane weight layout ---------------------------
+ * Replaces tcrv_emitc_..._pack_q4_0_to_q4_0x16(size_t nblocks, const uint8_t *src,
+ * uint8_t *dst) (test/Conversion/RVV/rvv-to-emitc-pack-q4-0-to-q4-0x16.mlir:
+ * 19-21; RVVOps.td:4551-4626, make_block_q4_0x16): for each of nblocks output
+ * blocks (288 B) built from 16 consecutive source blocks (18 B),
+ * d[i] = src[i].d and qs[i] = src[i % 16].qs[i / 16] ^ 0x88.
+ * src 2-byte aligned, dst 4-byte aligned. */
+TCRV_HIP_API int tcrv_hip_pack_q4_0_to_q4_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst,
+                                  void *stream);
+
+/* block_q8_0x16 (544 B: fp16 d[16], then qs[i*16 + r] = quant i of source block
+ * r), the layout tcrv_rvv.repack_gemv_q8_0_q8_0 reads (RVVOps.td:4846-4857).
+ * The reference has no op that produces it; this entry is the inverse of that
+ * consumer's addressing, so the Q8_0 repacked GEMV can be fed from plain rows. */
+TCRV_HIP_API int tcrv_hip_pack_q8_0_to_q8_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst,
+                                  void *stream);
+
+/* Replace tcrv_emitc_..._repack_gemv_{q4_0,q8_0}_q8_0(size_t n, float *s,
+ * const uint8_t *vx, const uint8_t *vy, size_t nc)
+ * (test/Conversion/RVV/rvv-to-emitc-repack-gemv-q4-0-q8-0.mlir:24-28 and the
+ * q8-0 fixture; emitters RVVToEmitCBlockQuantLinear.cpp:2853-3357, :3930-4379).
+ * vx holds nc/16 groups of 16 weight rows in the x16 layout (group x at
+ * vx + x*(n/32)*288, or *544 for Q8_0); vy is one plain Q8_0 activation row.
+ * s[x*16 + r] = fold_b fma((float)sumi_{r,b}, d_w[r]*d_a, .) in ascending b --
+ * for Q4_0 a different rounding from the plain block dot's fold.
+ * A trailing partial group (nc % 16) is not written, as in the reference.
+ * vx 4-byte aligned, vy 2-byte aligned. */
+TCRV_HIP_API int tcrv_hip_repack_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx,
+                                   const uint8_t *vy, size_t nc, void *stream);
+TCRV_HIP_API int tcrv_hip_repack_gemv_q8_0_q8_0(size_t n, float *s, const uint8_t *vx,
+                                   const uint8_t *vy, size_t nc, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -439,3 +439,75 @@ void tcrv_oracle_repack_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx,
       s[x * 16 + r] = acc[r];
   }
 }
+
+/* ------------------------------------------------------------------------ */
+/* block_q8_0x16 pack / unpack and the Q8_0 repacked GEMV                    */
+/* (emitRepackGemvQ8_0Q8_0 RVVToEmitCBlockQuantLinear.cpp:3930-4379: weight  */
+/* group x at vx + x*nb*544, block l at +l*544; position loop i < 32 reads   */
+/* byte 32 + i*16 + r of lane r; vwmul i8 x i8 -> i16, vwadd_wv into i32;    */
+/* fold vfmacc(acc, vfcvt(sumi), vfwmul(d_w[r], d_a)) (:4258-4330)).         */
+/* ------------------------------------------------------------------------ */
+
+void tcrv_oracle_pack_q8_0_to_q8_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst) {
+  for (size_t o = 0; o < nblocks; ++o) {
+    const uint8_t *in = src + o * 16 * TCRV_Q8_0_BLOCK_BYTES;
+    uint8_t *out = dst + o * TCRV_Q8_0X16_BLOCK_BYTES;
+    for (int r = 0; r < 16; ++r)
+      memcpy(out + 2 * r, in + r * TCRV_Q8_0_BLOCK_BYTES, 2);
+    for (int i = 0; i < 32; ++i)
+      for (int r = 0; r < 16; ++r)
+        out[32 + i * 16 + r] = in[r * TCRV_Q8_0_BLOCK_BYTES + 2 + i];
+  }
+}
+
+void tcrv_oracle_unpack_q4_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst) {
+  for (size_t o = 0; o < nblocks; ++o) {
+    const uint8_t *in = src + o * TCRV_Q4_0X16_BLOCK_BYTES;
+    uint8_t *out = dst + o * 16 * TCRV_Q4_0_BLOCK_BYTES;
+    for (int r = 0; r < 16; ++r)
+      memcpy(out + r * TCRV_Q4_0_BLOCK_BYTES, in + 2 * r, 2);
+    for (int i = 0; i < 256; ++i)
+      out[(i % 16) * TCRV_Q4_0_BLOCK_BYTES + 2 + i / 16] = (uint8_t)(in[32 + i] ^ 0x88u);
+  }
+}
+
+void tcrv_oracle_unpack_q8_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst) {
+  for (size_t o = 0; o < nblocks; ++o) {
+    const uint8_t *in = src + o * TCRV_Q8_0X16_BLOCK_BYTES;
+    uint8_t *out = dst + o * 16 * TCRV_Q8_0_BLOCK_BYTES;
+    for (int r = 0; r < 16; ++r)
+      memcpy(out + r * TCRV_Q8_0_BLOCK_BYTES, in + 2 * r, 2);
+    for (int i = 0; i < 32; ++i)
+      for (int r = 0; r < 16; ++r)
+        out[r * TCRV_Q8_0_BLOCK_BYTES + 2 + i] = in[32 + i * 16 + r];
+  }
+}
+
+void tcrv_oracle_repack_gemv_q8_0_q8_0(size_t n, float *s, const uint8_t *vx,
+                                       const uint8_t *vy, size_t nc) {
+  size_t nb = n / TCRV_QK;
+  size_t ngroups = nc / 16;
+  for (size_t x = 0; x < ngroups; ++x) {
+    float acc[16];
+    for (int r = 0; r < 16; ++r)
+      acc[r] = 0.0f;
+    for (size_t b = 0; b < nb; ++b) {
+      const uint8_t *bl = vx + (x * nb + b) * TCRV_Q8_0X16_BLOCK_BYTES;
+      const uint8_t *al = vy + b * TCRV_Q8_0_BLOCK_BYTES;
+      const int8_t *aqs = (const int8_t *)(al + 2);
+      float da = load_d(al);
+      for (int r = 0; r < 16; ++r) {
+        int32_t sumi = 0;
+        for (int i = 0; i < 32; ++i) {
+          int16_t prod = (int16_t)((int16_t)(int8_t)bl[32 + i * 16 + r] * (int16_t)aqs[i]);
+          sumi += prod; /* vwadd_wv: i32 += widened i16 */
+        }
+        float dw = load_d(bl + 2 * r);
+        float dc = dw * da; /* vfwmul f16 x f16 -> f32: exact */
+        acc[r] = fmaf((float)sumi, dc, acc[r]);
+      }
+    }
+    for (int r = 0; r < 16; ++r)
+      s[x * 16 + r] = acc[r];
+  }
+}

@@ -100,6 +100,23 @@ void tcrv_oracle_pack_q4_0_to_q4_0x16(size_t nblocks, const uint8_t *src, uint8_
 void tcrv_oracle_repack_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx,
                                        const uint8_t *vy, size_t nc);
 
+/* block_q8_0x16 (544 B: fp16 d[16] @0, int8 qs[512] @32, qs[i*16 + r] = quant i
+ * of block r; no bias) -- the layout tcrv_rvv.repack_gemv_q8_0_q8_0 reads
+ * (RVVOps.td:4846-4867; byte 32 + i*16 + r, RVVToEmitCBlockQuantLinear.cpp:
+ * 4204-4215).  The reference has no pack op for it; this is its inverse of the
+ * consumer's addressing. */
+#define TCRV_Q8_0X16_BLOCK_BYTES 544
+void tcrv_oracle_pack_q8_0_to_q8_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst);
+/* Inverse of both packs (test helper): x16 blocks back to 16 plain blocks each. */
+void tcrv_oracle_unpack_q4_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst);
+void tcrv_oracle_unpack_q8_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst);
+/* repack GEMV over q8_0x16 weights (emitRepackGemvQ8_0Q8_0,
+ * RVVToEmitCBlockQuantLinear.cpp:3930-4379): per row r of group x, sumi =
+ * sum_i w[r][i]*a[i] (i16 products widened into i32), fold
+ * acc = fma((float)sumi, d_w[r]*d_a, acc) in ascending block order. */
+void tcrv_oracle_repack_gemv_q8_0_q8_0(size_t n, float *s, const uint8_t *vx,
+                                       const uint8_t *vy, size_t nc);
+
 #ifdef __cplusplus
 }
 #endif

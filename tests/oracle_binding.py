@@ -40,6 +40,10 @@ _SIGS = {
     "tcrv_oracle_quantize_row_q4_0": ([_sz, _p, _p], None),
     "tcrv_oracle_pack_q4_0_to_q4_0x16": ([_sz, _p, _p], None),
     "tcrv_oracle_repack_gemv_q4_0_q8_0": ([_sz, _p, _p, _p, _sz], None),
+    "tcrv_oracle_pack_q8_0_to_q8_0x16": ([_sz, _p, _p], None),
+    "tcrv_oracle_unpack_q4_0x16": ([_sz, _p, _p], None),
+    "tcrv_oracle_unpack_q8_0x16": ([_sz, _p, _p], None),
+    "tcrv_oracle_repack_gemv_q8_0_q8_0": ([_sz, _p, _p, _p, _sz], None),
 }
 
 
@@ -152,6 +156,26 @@ class Oracle:
     def repack_gemv_q4_0(self, n: int, vx: np.ndarray, vy: np.ndarray, nc: int) -> np.ndarray:
         s = np.zeros(nc, dtype=np.float32)
         self.lib.tcrv_oracle_repack_gemv_q4_0_q8_0(n, _a(s), _a(vx), _a(vy), nc)
+        return s
+
+    def pack_q8_0x16(self, src: np.ndarray, nblocks: int) -> np.ndarray:
+        dst = np.zeros(nblocks * 544, dtype=np.uint8)
+        self.lib.tcrv_oracle_pack_q8_0_to_q8_0x16(nblocks, _a(src), _a(dst))
+        return dst
+
+    def unpack_q4_0x16(self, src: np.ndarray, nblocks: int) -> np.ndarray:
+        dst = np.zeros(nblocks * 16 * 18, dtype=np.uint8)
+        self.lib.tcrv_oracle_unpack_q4_0x16(nblocks, _a(src), _a(dst))
+        return dst
+
+    def unpack_q8_0x16(self, src: np.ndarray, nblocks: int) -> np.ndarray:
+        dst = np.zeros(nblocks * 16 * 34, dtype=np.uint8)
+        self.lib.tcrv_oracle_unpack_q8_0x16(nblocks, _a(src), _a(dst))
+        return dst
+
+    def repack_gemv_q8_0(self, n: int, vx: np.ndarray, vy: np.ndarray, nc: int) -> np.ndarray:
+        s = np.zeros(nc, dtype=np.float32)
+        self.lib.tcrv_oracle_repack_gemv_q8_0_q8_0(n, _a(s), _a(vx), _a(vy), nc)
         return s
 
 

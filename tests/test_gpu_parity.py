@@ -305,3 +305,64 @@ def test_unaligned_rows_all_entries(hip, oracle, dev):
     dq = empty_dev(nb * 34 + 16, torch.uint8, dev)
     hip.quantize_row_q8_0(n, to_dev(xf, dev)[1:], dq[2:])
     assert np.array_equal(from_dev(dq)[2:2 + nb * 34], oracle.quantize_q8_0(xf[1:].copy()))
+
+
+# ------------------------------------------------------- a8 x16 repack layout ---
+
+def x16_source(w, nb, k):
+    """Plain rows (nc x nb blocks of k bytes) in pack order: group x, block b
+    takes block b of rows 16x .. 16x+15."""
+    nc = w.shape[0]
+    return np.ascontiguousarray(np.concatenate(
+        [w[16 * x:16 * x + 16, k * b:k * b + k] for x in range(nc // 16) for b in range(nb)]
+    ).reshape(-1))
+
+
+@pytest.mark.parametrize("nblocks", [1, 7, 4096 * 128 // 16])
+def test_pack_q4_0x16(hip, oracle, dev, nblocks):
+    src = synth.q4_0_matrix(1, 16 * nblocks * 32, 61, 0.02).reshape(-1)
+    dst = empty_dev(nblocks * 288, torch.uint8, dev)
+    hip.pack_q4_0_to_q4_0x16(nblocks, to_dev(src, dev), dst)
+    assert np.array_equal(from_dev(dst), oracle.pack_q4_0x16(src, nblocks))
+
+
+@pytest.mark.parametrize("nblocks", [1, 9, 4096 * 128 // 16])
+def test_pack_q8_0x16(hip, oracle, dev, nblocks):
+    src = synth.q8_0_matrix(1, 16 * nblocks * 32, 62, 1.0).reshape(-1)
+    dst = empty_dev(nblocks * 544, torch.uint8, dev)
+    hip.pack_q8_0_to_q8_0x16(nblocks, to_dev(src, dev), dst)
+    assert np.array_equal(from_dev(dst), oracle.pack_q8_0x16(src, nblocks))
+
+
+@pytest.mark.parametrize("nc,nb", [(4096, 128), (48, 131), (40, 3), (16, 1), (32, 256)])
+def test_repack_gemv_q4_0(hip, oracle, dev, nc, nb):
+    n = nb * 32
+    w = synth.q4_0_matrix(nc, n, 1006, 0.02)
+    x = synth.q8_0_matrix(1, n, 1007, 1.0).reshape(-1)
+    groups = nc // 16
+    packed = oracle.pack_q4_0x16(x16_source(w[:16 * groups], nb, 18), groups * nb)
+    s = to_dev(np.full(nc, -7.0, np.float32), dev)
+    hip.repack_gemv_q4_0_q8_0(n, s, to_dev(packed, dev), to_dev(x, dev), nc)
+    got = from_dev(s)
+    assert_f32_parity(got[:16 * groups], oracle.repack_gemv_q4_0(n, packed, x, nc)[:16 * groups],
+                      what=f"repack q4 nc={nc} nb={nb}")
+    assert np.all(got[16 * groups:] == -7.0)  # trailing partial group untouched
+
+
+@pytest.mark.parametrize("nc,nb", [(4096, 128), (48, 131), (16, 1), (32, 256)])
+def test_repack_gemv_q8_0_equals_plain_gemv(hip, oracle, dev, nc, nb):
+    n = nb * 32
+    w = synth.q8_0_matrix(nc, n, 1009, 0.02)
+    x = synth.q8_0_matrix(1, n, 1008, 1.0).reshape(-1)
+    w[0, 2:34] = 0x80
+    x[2:34] = 0x80
+    dsrc = to_dev(x16_source(w, nb, 34), dev)
+    packed = empty_dev(nc // 16 * nb * 544, torch.uint8, dev)
+    hip.pack_q8_0_to_q8_0x16(nc // 16 * nb, dsrc, packed)
+    s = empty_dev(nc, torch.float32, dev)
+    hip.repack_gemv_q8_0_q8_0(n, s, packed, to_dev(x, dev), nc)
+    got = from_dev(s)
+    host_packed = from_dev(packed)
+    assert_f32_parity(got, oracle.repack_gemv_q8_0(n, host_packed, x, nc), what="repack q8")
+    assert_f32_parity(got, oracle.gemm_q8_0(n, w, x, 0, nc, 1, w.shape[1], 1, 8)[:nc],
+                      what="repack q8 vs plain")

@@ -423,3 +423,65 @@ def test_repack_gemv_alternate_fold(oracle):
             s = int((xv[b] * yq[b]).sum())
             acc = exact.fma32(np.float32(s), exact.mul32(dx[b], dy[b]), acc)
         assert got[row] == acc
+
+
+def unpack_q8_0x16_np(packed, nblocks):
+    """Independent numpy inverse of the block_q8_0x16 interleave
+    (qs[i*16 + r] = quant i of block r, scales d[r] at 2r)."""
+    p = packed.reshape(nblocks, 544)
+    out = np.zeros((nblocks, 16, 34), dtype=np.uint8)
+    out[:, :, 0:2] = p[:, 0:32].reshape(nblocks, 16, 2)
+    out[:, :, 2:] = p[:, 32:].reshape(nblocks, 32, 16).transpose(0, 2, 1)
+    return out.reshape(-1)
+
+
+def test_pack_q8_0x16_round_trip(oracle):
+    src = rand_q8_blocks(16 * 5)
+    packed = oracle.pack_q8_0x16(src, 5)
+    assert np.array_equal(unpack_q8_0x16_np(packed, 5), src)
+    assert np.array_equal(oracle.unpack_q8_0x16(packed, 5), src)
+    q4 = rand_q4_blocks(16 * 3)
+    assert np.array_equal(oracle.unpack_q4_0x16(oracle.pack_q4_0x16(q4, 3), 3), q4)
+
+
+def x16_gather(w, nb, row_bytes_per_block):
+    """Plain rows (nc x nb blocks) -> the source order of the x16 pack: group x,
+    block b takes block b of rows 16x .. 16x+15."""
+    nc = w.shape[0]
+    k = row_bytes_per_block
+    return np.concatenate([w[16 * x + r, k * b:k * b + k]
+                           for x in range(nc // 16) for b in range(nb) for r in range(16)])
+
+
+def test_repack_gemv_q8_equals_plain_gemm(oracle):
+    """The Q8_0 repacked GEMV folds fma((float)sumi, d_w*d_a, acc) -- the same
+    fold as the plain Q8_0 block dot -- so on the same bytes it must equal the
+    (separately pinned) plain GEMM bit for bit."""
+    n, nc = 4 * 32 * 9, 48
+    nb = n // 32
+    w = synth.q8_0_matrix(nc, n, 51, 0.02)
+    y = synth.q8_0_matrix(1, n, 52, 1.0).reshape(-1)
+    w[3, 2:34] = 0x80  # -128 x -128 block
+    y[2:34] = 0x80
+    packed = oracle.pack_q8_0x16(x16_gather(w, nb, 34), (nc // 16) * nb)
+    got = oracle.repack_gemv_q8_0(n, packed, y, nc)
+    want = oracle.gemm_q8_0(n, w, y, 0, nc, 1, w.shape[1], 1)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_repack_gemv_q8_exact_fold_and_trailing_columns(oracle):
+    n, nc = 96, 40           # nc % 16 != 0: the last 8 columns are not written
+    nb = n // 32
+    w = synth.q8_0_matrix(48, n, 53, 0.02)
+    y = synth.q8_0_matrix(1, n, 54, 1.0).reshape(-1)
+    packed = oracle.pack_q8_0x16(x16_gather(w[:32], nb, 34), 2 * nb)
+    got = oracle.repack_gemv_q8_0(n, packed, y, nc)
+    dy, yq = q8_fields(y)
+    for row in range(32):
+        dx, xq = q8_fields(w[row])
+        acc = np.float32(0)
+        for b in range(nb):
+            s = int((xq[b] * yq[b]).sum())
+            acc = exact.fma32(np.float32(s), exact.mul32(dx[b], dy[b]), acc)
+        assert got[row] == acc
+    assert np.all(got[32:] == 0)

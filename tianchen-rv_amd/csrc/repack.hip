@@ -1,0 +1,248 @@
+// repack.hip -- a8: the x16 block-as-lane weight layout.
+//   tcrv_hip_pack_q4_0_to_q4_0x16   make_block_q4_0x16 (tcrv_rvv.pack_q4_0_to_q4_0x16)
+//   tcrv_hip_pack_q8_0_to_q8_0x16   the layout tcrv_rvv.repack_gemv_q8_0_q8_0 reads
+//   tcrv_hip_repack_gemv_q4_0_q8_0  tcrv_rvv.repack_gemv_q4_0_q8_0
+//   tcrv_hip_repack_gemv_q8_0_q8_0  tcrv_rvv.repack_gemv_q8_0_q8_0
+//
+// Layouts (include/TianChenRV/Dialect/RVV/IR/RVVOps.td:4551-4577, :4846-4857):
+//   block_q4_0x16  288 B: fp16 d[16] @0, qs[256] @32, qs[i*16 + r] = byte i of
+//                  source block r, XOR 0x88 (both nibbles offset-binary biased)
+//   block_q8_0x16  544 B: fp16 d[16] @0, qs[512] @32, qs[i*16 + r] = quant i of
+//                  source block r
+// Repacked GEMV over nc/16 groups of 16 weight rows (group x at vx + x*nb*stride),
+// one plain block_q8_0 activation stream, output s[x*16 + r]; the fold of both
+// emitters (RVVToEmitCBlockQuantLinear.cpp:3245-3290, :4258-4330) is
+//   acc_r = fma((float)sumi_r, d_w[r]*d_a, acc_r)   (vfwmul exact, vfmacc fused)
+// in ascending block order.
+#include "tcrv_hip_internal.h"
+
+namespace tcrv {
+
+constexpr int kQ4x16Bytes = 288;
+constexpr int kQ8x16Bytes = 544;
+
+// ---------------------------------------------------------------------------
+// Packs: one thread per output dword (8 scale dwords + 64 or 128 quant dwords).
+// ---------------------------------------------------------------------------
+template <bool kQ4>
+__global__ __launch_bounds__(256) void pack_x16(size_t nblocks, const uint8_t *src,
+                                                uint8_t *dst) {
+  constexpr int kSrc = kQ4 ? kQ4Bytes : kQ8Bytes;
+  constexpr int kDst = kQ4 ? kQ4x16Bytes : kQ8x16Bytes;
+  constexpr int kDwords = kDst / 4;
+  const size_t t = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= nblocks * kDwords)
+    return;
+  const size_t o = t / kDwords;
+  const int k = static_cast<int>(t - o * kDwords);
+  const uint8_t *in = src + o * 16 * kSrc;
+  uint32_t v;
+  if (k < 8) {  // scales d[2k], d[2k+1]
+    const uint32_t d0 = *reinterpret_cast<const uint16_t *>(in + (2 * k) * kSrc);
+    const uint32_t d1 = *reinterpret_cast<const uint16_t *>(in + (2 * k + 1) * kSrc);
+    v = d0 | (d1 << 16);
+  } else {  // qs bytes 4q .. 4q+3: byte i -> source block i % 16, offset i / 16
+    const int q = k - 8;
+    const int off = 2 + q / 4;
+    const int r0 = 4 * (q % 4);
+    v = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      v |= static_cast<uint32_t>(in[(r0 + j) * kSrc + off]) << (8 * j);
+    if constexpr (kQ4)
+      v ^= 0x88888888u;
+  }
+  reinterpret_cast<uint32_t *>(dst + o * kDst)[k] = v;
+}
+
+// ---------------------------------------------------------------------------
+// Repacked GEMV.  Work-group = 4 waves for one group of 16 weight rows; each
+// wave step covers 4 blocks with 16 lanes per block: lane (rq = l & 3,
+// pq = (l >> 2) & 3) owns rows 4rq..4rq+3 and positions 4pq..4pq+3 (Q4_0; the
+// high nibbles are positions 16+4pq..) or 8pq..8pq+7 (Q8_0).  It loads one dword
+// per position (4 rows of it), turns the 4x4 bytes row-major with v_perm, and
+// takes v_dot4_i32_i8 against the activation; the four position lanes of a row
+// are summed with two shuffles.  Exact (float)sumi and d_w*d_a per (block, row)
+// go to LDS; 16 lanes then fold each row serially over the chunk.
+// ---------------------------------------------------------------------------
+constexpr int kRgChunk = 128;   // blocks per LDS chunk
+
+// 4x4 byte transpose: in[i] holds rows 0..3 of position i; out[r] holds
+// positions 0..3 of row r.
+__device__ __forceinline__ void transpose4x4(const uint32_t in[4], uint32_t out[4]) {
+  const uint32_t t0 = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);  // i0r0 i1r0 i0r1 i1r1
+  const uint32_t t1 = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);  // i2r0 i3r0 i2r1 i3r1
+  const uint32_t t2 = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);  // i0r2 i1r2 i0r3 i1r3
+  const uint32_t t3 = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);  // i2r2 i3r2 i2r3 i3r3
+  out[0] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(t3, t2, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
+}
+
+// Quant bytes 4k..4k+3 of activation block b staged raw (34-byte blocks) in
+// LDS: an even block starts on a dword (its quants sit 2 bytes in), an odd
+// block 2 bytes into one (its quants are dword aligned).
+__device__ __forceinline__ uint32_t act_dword(const uint8_t *act, int b, int k) {
+  if ((b & 1) == 0) {
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(act + b * kQ8Bytes);
+    return funnel16(w[k], w[k + 1]);
+  }
+  const uint32_t *w = reinterpret_cast<const uint32_t *>(act + b * kQ8Bytes - 2);
+  return w[k + 1];
+}
+
+template <bool kQ4>
+__global__ __launch_bounds__(256) void repack_gemv(size_t nb, float *s, const uint8_t *vx,
+                                                   const uint8_t *vy) {
+  constexpr int kW = kQ4 ? kQ4x16Bytes : kQ8x16Bytes;
+  __shared__ __align__(16) uint8_t act[kRgChunk * kQ8Bytes + 16];
+  __shared__ __align__(16) float2 terms[kRgChunk][16];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63;
+  const int jb = l >> 4, pq = (l >> 2) & 3, rq = l & 3;
+  const uint8_t *group = vx + static_cast<size_t>(blockIdx.x) * nb * kW;
+  float acc = 0.0f;  // lanes 0..15 of wave 0: row tid
+
+  for (size_t c0 = 0; c0 < nb; c0 += kRgChunk) {
+    const int nbc = static_cast<int>(min(static_cast<size_t>(kRgChunk), nb - c0));
+    copy_span_to_lds(act, vy + c0 * kQ8Bytes, nbc * kQ8Bytes, tid, 256);
+    __syncthreads();
+    for (int b = 4 * w + jb; b < nbc; b += 16) {
+      const uint8_t *blk = group + (c0 + b) * kW;
+      const uint32_t *qd = reinterpret_cast<const uint32_t *>(blk + 32);
+      int part[4];
+      if constexpr (kQ4) {
+        uint32_t raw[4], rows[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          raw[i] = qd[4 * (4 * pq + i) + rq];  // position 4pq+i, rows 4rq..4rq+3
+        transpose4x4(raw, rows);
+        // activation positions 4pq..4pq+3 (low nibbles) and 16+4pq.. (high)
+        const uint32_t alo = act_dword(act, b, pq);
+        const uint32_t ahi = act_dword(act, b, pq + 4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          // byte = (n_lo ^ 8) | (n_hi ^ 8) << 4; as a signed byte, the nibble
+          // moved to the high half is 16 * sext4(n ^ 8) = 16 * (n - 8)
+          const uint32_t lo16 = (rows[r] << 4) & 0xF0F0F0F0u;
+          const uint32_t hi16 = rows[r] & 0xF0F0F0F0u;
+          part[r] = sdot4(hi16, ahi, sdot4(lo16, alo, 0));
+        }
+      } else {
+        uint32_t raw[8], rows[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          raw[i] = qd[4 * (8 * pq + i) + rq];
+        transpose4x4(raw, rows);
+        transpose4x4(raw + 4, rows + 4);
+        const uint32_t a0 = act_dword(act, b, 2 * pq);
+        const uint32_t a1 = act_dword(act, b, 2 * pq + 1);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          part[r] = sdot4(rows[4 + r], a1, sdot4(rows[r], a0, 0));
+      }
+      // sum over the four position lanes (lane bits 2..3)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        part[r] += __shfl_xor(part[r], 4);
+        part[r] += __shfl_xor(part[r], 8);
+      }
+      if (pq == 0) {
+        const float da =
+            fp16_bits_to_f32(*reinterpret_cast<const uint16_t *>(act + b * kQ8Bytes));
+        const uint32_t *dq = reinterpret_cast<const uint32_t *>(blk + 8 * rq);  // d[4rq..4rq+3]
+        const uint32_t d01 = dq[0], d23 = dq[1];
+        const uint32_t dw[4] = {d01 & 0xffffu, d01 >> 16, d23 & 0xffffu, d23 >> 16};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int sumi = kQ4 ? (part[r] >> 4) : part[r];  // Q4_0: exact division by 16
+          terms[b][4 * rq + r] = make_float2(static_cast<float>(sumi), fp16_bits_to_f32(dw[r]) * da);
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < 16) {
+#pragma unroll 8
+      for (int b = 0; b < nbc; ++b) {
+        const float2 t = terms[b][tid];
+        acc = fmaf(t.x, t.y, acc);
+      }
+    }
+    __syncthreads();
+  }
+  if (tid < 16)
+    s[static_cast<size_t>(blockIdx.x) * 16 + tid] = acc;
+}
+
+}  // namespace tcrv
+
+namespace {
+
+template <bool kQ4>
+int launch_pack(size_t nblocks, const uint8_t *src, uint8_t *dst, void *stream) {
+  using namespace tcrv_host;
+  if (nblocks == 0)
+    return TCRV_HIP_OK;
+  if (!src || !dst)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned2(src) || !aligned4(dst))
+    return TCRV_HIP_ERR_MISALIGNED;
+  const size_t dwords = nblocks * ((kQ4 ? tcrv::kQ4x16Bytes : tcrv::kQ8x16Bytes) / 4);
+  const size_t grid = (dwords + 255) / 256;
+  if (grid > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  tcrv::pack_x16<kQ4><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, as_stream(stream)>>>(
+      nblocks, src, dst);
+  return launch_status();
+}
+
+template <bool kQ4>
+int launch_repack_gemv(size_t n, float *s, const uint8_t *vx, const uint8_t *vy, size_t nc,
+                       void *stream) {
+  using namespace tcrv_host;
+  const size_t groups = nc / 16;  // like the reference, a partial group is not written
+  const size_t nb = n / tcrv::kQK;
+  if (groups == 0)
+    return TCRV_HIP_OK;
+  if (!s)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (nb == 0)
+    return zero_outputs(s, groups * 16, 0, 0, stream);
+  if (!vx || !vy)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned4(vx) || !aligned2(vy))
+    return TCRV_HIP_ERR_MISALIGNED;
+  if (groups > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  tcrv::repack_gemv<kQ4><<<dim3(static_cast<unsigned>(groups)), dim3(256), 0,
+                           as_stream(stream)>>>(nb, s, vx, vy);
+  return launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+int tcrv_hip_pack_q4_0_to_q4_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst,
+                                  void *stream) {
+  return launch_pack<true>(nblocks, src, dst, stream);
+}
+
+int tcrv_hip_pack_q8_0_to_q8_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst,
+                                  void *stream) {
+  return launch_pack<false>(nblocks, src, dst, stream);
+}
+
+int tcrv_hip_repack_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
+                                   size_t nc, void *stream) {
+  return launch_repack_gemv<true>(n, s, vx, vy, nc, stream);
+}
+
+int tcrv_hip_repack_gemv_q8_0_q8_0(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
+                                   size_t nc, void *stream) {
+  return launch_repack_gemv<false>(n, s, vx, vy, nc, stream);
+}
+
+}  // extern "C"

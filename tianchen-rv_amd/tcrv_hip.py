@@ -60,6 +60,10 @@ SIGNATURES = {
     "tcrv_hip_q4_0_q8_0_gemm": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p],
     "tcrv_hip_gemv_q4_0_q8_0": [_sz, _p, _p, _sz, _p, _sz, _p],
     "tcrv_hip_q8_0_q8_0_gemm": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p],
+    "tcrv_hip_pack_q4_0_to_q4_0x16": [_sz, _p, _p, _p],
+    "tcrv_hip_pack_q8_0_to_q8_0x16": [_sz, _p, _p, _p],
+    "tcrv_hip_repack_gemv_q4_0_q8_0": [_sz, _p, _p, _p, _sz, _p],
+    "tcrv_hip_repack_gemv_q8_0_q8_0": [_sz, _p, _p, _p, _sz, _p],
 }
 STRING_FUNCS = {"tcrv_hip_status_string": [_int], "tcrv_hip_version": []}
 
@@ -191,6 +195,22 @@ def gemv_q4_0_q8_0(n: int, s, vx, bx: int, vy, nr: int, stream=None):
 def q8_0_q8_0_gemm(n: int, s, vx, vy, by: int, nr: int, nc: int, bx: int, bs: int,
                    stream=None):
     return call("tcrv_hip_q8_0_q8_0_gemm", n, s, vx, vy, by, nr, nc, bx, bs, _stream(stream))
+
+
+def pack_q4_0_to_q4_0x16(nblocks: int, src, dst, stream=None):
+    return call("tcrv_hip_pack_q4_0_to_q4_0x16", nblocks, src, dst, _stream(stream))
+
+
+def pack_q8_0_to_q8_0x16(nblocks: int, src, dst, stream=None):
+    return call("tcrv_hip_pack_q8_0_to_q8_0x16", nblocks, src, dst, _stream(stream))
+
+
+def repack_gemv_q4_0_q8_0(n: int, s, vx, vy, nc: int, stream=None):
+    return call("tcrv_hip_repack_gemv_q4_0_q8_0", n, s, vx, vy, nc, _stream(stream))
+
+
+def repack_gemv_q8_0_q8_0(n: int, s, vx, vy, nc: int, stream=None):
+    return call("tcrv_hip_repack_gemv_q8_0_q8_0", n, s, vx, vy, nc, _stream(stream))
 
 
 def synchronize(stream=None):
