@@ -190,7 +190,8 @@ def bench_gemm(torch, lib, stream, args):
 
 def bench_configs(torch, lib, stream, args):
     """configs[0..2]: add f32 2^24, Q8_0 dequant 4096x4096, Q8_0.Q8_0 block dot
-    16384 x 4096 -- each over rotating input sets larger than the MALL."""
+    16384 x 4096 -- each over rotating input sets larger than the MALL -- plus
+    the x16-repacked Q4_0 GEMV and the Q4_0 x Q8_0 prefill GEMM."""
     import synth
     dev = torch.device("cuda:0")
     sp = stream.cuda_stream
@@ -253,9 +254,51 @@ def bench_configs(torch, lib, stream, args):
     out["vec_dot_q8_0_q8_0"] = {"workload": "configs[2] Q8_0.Q8_0 block dot 16384 x 4096",
                                 "us": round(us, 3), "GB/s": round(DOT_BYTES / us / 1e3, 1),
                                 "sets": sets}
+    del X, Yd, S, reg
+
+    # x16 repacked decode GEMV (the reference's selected decode path at VLEN128)
+    w = synth.q4_0_matrix(N, N, synth.SEEDS["gemv_w"], 0.02)
+    x = synth.q8_0_matrix(1, N, synth.SEEDS["gemv_x"], 1.0).reshape(-1)
+    nb = N // 32
+    src = torch.from_numpy(w.reshape(N // 16, 16, nb, 18).transpose(0, 2, 1, 3).copy()).to(dev)
+    packed = torch.empty(N // 16 * nb * 288, dtype=torch.uint8, device=dev)
+    checked(lib.tcrv_hip_pack_q4_0_to_q4_0x16, "pack")(N // 16 * nb, src.data_ptr(),
+                                                        packed.data_ptr(), sp)
+    sets = copies_for(packed.numel(), 2)
+    P = torch.empty((sets, packed.numel()), dtype=torch.uint8, device=dev)
+    P[:] = packed
+    xd = torch.from_numpy(x).to(dev)
+    Yv = torch.empty((sets, N), device=dev)
+    fn = checked(lib.tcrv_hip_repack_gemv_q4_0_q8_0, "repack_gemv")
+    ptrs = [(Yv[i].data_ptr(), P[i].data_ptr()) for i in range(sets)]
+    reg = Region(torch, stream, lambda i: fn(N, ptrs[i % sets][0], ptrs[i % sets][1],
+                                             xd.data_ptr(), N, sp), 500)
+    reg.run()
+    us = reg.run() * 1e3 / 500
+    out["repack_gemv_q4_0_q8_0"] = {"workload": "a8 x16-repacked Q4_0 GEMV 4096x4096",
+                                    "us": round(us, 3), "GB/s": round(GEMV_BYTES / us / 1e3, 1),
+                                    "sets": sets}
+    del P, Yv, reg, src, packed
+
+    # Q4_0 x Q8_0 prefill GEMM 4096^3 (MFMA)
+    a = synth.q8_0_matrix(N, N, synth.SEEDS["gemm_a"], 1.0)
+    ad = torch.from_numpy(a).to(dev)
+    wd = torch.from_numpy(w).to(dev)
+    cd = torch.empty(N * N, device=dev)
+    fn = checked(lib.tcrv_hip_q4_0_q8_0_gemm, "q4_gemm")
+    reg = Region(torch, stream, lambda i: fn(N, cd.data_ptr(), wd.data_ptr(), ad.data_ptr(),
+                                             a.shape[1], N, N, w.shape[1], N, sp), 10)
+    reg.run()
+    us = reg.run() * 1e3 / 10
+    out["q4_0_q8_0_gemm"] = {"workload": "a7 Q4_0 x Q8_0 GEMM 4096 rows x 4096 tokens x 4096",
+                             "us": round(us, 1), "TOPS": round(GEMM_OPS / us / 1e6, 1)}
     for k, v in out.items():
-        log(f"{k}: {v['us']:.1f} us, {v['GB/s']:.0f} GB/s "
-            f"({100 * v['GB/s'] / HBM_PEAK_GBS:.1f}% of HBM peak)")
+        if "GB/s" in v:
+            log(f"{k}: {v['us']:.1f} us, {v['GB/s']:.0f} GB/s "
+                f"({100 * v['GB/s'] / HBM_PEAK_GBS:.1f}% of HBM peak)")
+        else:
+            log(f"{k}: {v['us']:.1f} us, {v['TOPS']:.0f} TOPS "
+                f"({100 * v['TOPS'] / INT8_PEAK_TOPS:.1f}% of dense int8 peak)")
     return out
 
 

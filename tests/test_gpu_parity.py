@@ -366,3 +366,37 @@ def test_repack_gemv_q8_0_equals_plain_gemv(hip, oracle, dev, nc, nb):
     assert_f32_parity(got, oracle.repack_gemv_q8_0(n, host_packed, x, nc), what="repack q8")
     assert_f32_parity(got, oracle.gemm_q8_0(n, w, x, 0, nc, 1, w.shape[1], 1, 8)[:nc],
                       what="repack q8 vs plain")
+
+
+# ------------------------------------------------ a7 Q4_0 GEMM on MFMA (nc > 1) ---
+
+@pytest.mark.parametrize("nr,nc,nb,pad", [(512, 512, 128, 0), (130, 70, 9, 16), (64, 2, 3, 0)])
+def test_q4_0_gemm_mfma_shapes(hip, oracle, dev, nr, nc, nb, pad):
+    n = nb * 32
+    w = np.pad(synth.q4_0_matrix(nr, n, 71, 0.02), ((0, 0), (0, pad)))
+    a = np.pad(synth.q8_0_matrix(nc, n, 72, 1.0), ((0, 0), (0, pad)))
+    bs = nc + 1
+    s = to_dev(np.zeros(nr * bs, np.float32), dev)
+    hip.q4_0_q8_0_gemm(n, s, to_dev(w, dev), to_dev(a, dev), a.shape[1], nr, nc, w.shape[1], bs)
+    want = oracle.gemm_q4_0(n, w, a, a.shape[1], nr, nc, w.shape[1], bs, 8)
+    got = from_dev(s).reshape(nr, bs)
+    assert_f32_parity(got[:, :nc], want.reshape(nr, bs)[:, :nc], what=f"q4 gemm {nr}x{nc}x{n}")
+
+
+def test_q4_0_gemm_full_size_sampled(hip, oracle, dev):
+    """4096 weight rows x 4096 tokens x K 4096 on the GPU; 64 rows and 64
+    columns checked against the oracle."""
+    n = nr = nc = 4096
+    w = synth.q4_0_matrix(nr, n, 1006, 0.02)
+    a = synth.q8_0_matrix(nc, n, 1008, 1.0)
+    s = empty_dev(nr * nc, torch.float32, dev)
+    hip.q4_0_q8_0_gemm(n, s, to_dev(w, dev), to_dev(a, dev), a.shape[1], nr, nc, w.shape[1], nc)
+    got = from_dev(s).reshape(nr, nc)
+    rng = np.random.default_rng(7)
+    for r in np.sort(rng.choice(nr, 64, replace=False)):
+        want = oracle.gemm_q4_0(n, w[r].copy(), a, a.shape[1], 1, nc, w.shape[1], nc, 8)
+        assert_f32_parity(got[r], want, what=f"row {r}")
+    cols = np.sort(rng.choice(nc, 64, replace=False))
+    sub = np.ascontiguousarray(a[cols])
+    want = oracle.gemm_q4_0(n, w, sub, sub.shape[1], nr, len(cols), w.shape[1], len(cols), 8)
+    assert_f32_parity(got[:, cols], want.reshape(nr, len(cols)), what="sampled cols")

@@ -12,7 +12,7 @@
 // order, so every output element sees the reference's sequence of roundings.
 //
 // Two kernels:
-//   gemm_q8_0_q8_0_occ     rows 4-byte aligned (the fast path, below);
+//   gemm_occ<false>        rows 4-byte aligned (the fast path, below);
 //   gemm_q8_0_q8_0_kernel  any 2-byte aligned rows: 4 waves, 2x2 tiles each,
 //                          raw block bytes through LDS, scalar scale epilogue.
 #include "tcrv_hip_internal.h"
@@ -270,7 +270,68 @@ __device__ __forceinline__ void store_pair(const PairRegs &p, bool two, int8_t *
   }
 }
 
-__global__ __launch_bounds__(kOcThreads, 1) void gemm_q8_0_q8_0_occ(
+// A Q4_0 weight block pair task (36 bytes, or 18 when only block 2m exists),
+// decoded into the same staged layout as a Q8_0 pair: 32 int8 quants per
+// block (element j < 16 = low nibble of byte j minus 8, element 16+j = its high
+// nibble minus 8) and the fp16 scale.
+__device__ __forceinline__ void load_pair_q4(PairRegs &p, const uint8_t *q, bool two) {
+  const uint32_t *g = reinterpret_cast<const uint32_t *>(q);
+  const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(g);
+  p.r[0] = v.x; p.r[1] = v.y; p.r[2] = v.z; p.r[3] = v.w;
+  if (two) {
+    const u32x4a4 u = *reinterpret_cast<const u32x4a4 *>(g + 4);
+    p.r[4] = u.x; p.r[5] = u.y; p.r[6] = u.z; p.r[7] = u.w;
+    p.r[8] = g[8];
+  } else {
+    p.r[4] = *reinterpret_cast<const uint16_t *>(q + 16);  // bytes 16-17: last two quant bytes
+  }
+}
+
+__device__ __forceinline__ void store_q4_block(const uint32_t q[4], int8_t *dst) {
+  uint4 *d = reinterpret_cast<uint4 *>(dst);
+  d[0] = make_uint4(nibbles_to_i8x4(q[0]), nibbles_to_i8x4(q[1]), nibbles_to_i8x4(q[2]),
+                    nibbles_to_i8x4(q[3]));
+  d[1] = make_uint4(nibbles_to_i8x4(q[0] >> 4), nibbles_to_i8x4(q[1] >> 4),
+                    nibbles_to_i8x4(q[2] >> 4), nibbles_to_i8x4(q[3] >> 4));
+}
+
+__device__ __forceinline__ void store_pair_q4(const PairRegs &p, bool two, int8_t *qrow,
+                                              uint16_t *d0, uint16_t *d1) {
+  const uint32_t *r = p.r;
+  const uint32_t qa[4] = {funnel16(r[0], r[1]), funnel16(r[1], r[2]), funnel16(r[2], r[3]),
+                          funnel16(r[3], r[4])};
+  store_q4_block(qa, qrow);
+  *d0 = static_cast<uint16_t>(r[0] & 0xffffu);
+  if (two) {
+    const uint32_t qb[4] = {r[5], r[6], r[7], r[8]};
+    store_q4_block(qb, qrow + kQK);
+    *d1 = static_cast<uint16_t>(r[4] >> 16);
+  }
+}
+
+// kQ4: the weight rows (vx) are Q4_0 and every output element is the a6 block
+// dot -- fold fma(fl((float)sumi * d_x), d_y, acc) (RVVToEmitCBlockQuantLinear.cpp:
+// 322-356).  The f16 MFMA then carries d_x against a constant 1.0 (k-slot 0),
+// which broadcasts d_x(row) into the accumulator layout exactly; d_y(col) is
+// one value per lane.  Otherwise both sides are Q8_0 and the f16 MFMA is the
+// outer product d_x*d_y of the a5 fold fma((float)sumi, d_x*d_y, acc).
+__device__ __forceinline__ void load_task(PairRegs &p, const uint8_t *q, bool two, bool q4) {
+  if (q4)
+    load_pair_q4(p, q, two);
+  else
+    load_pair(p, q, two);
+}
+
+__device__ __forceinline__ void store_task(const PairRegs &p, bool two, bool q4, int8_t *qrow,
+                                           uint16_t *d0, uint16_t *d1) {
+  if (q4)
+    store_pair_q4(p, two, qrow, d0, d1);
+  else
+    store_pair(p, two, qrow, d0, d1);
+}
+
+template <bool kQ4>
+__global__ __launch_bounds__(kOcThreads, 1) void gemm_occ(
     size_t nb, float *s, const uint8_t *vx, const uint8_t *vy, size_t by, size_t nr,
     size_t nc, size_t bx, size_t bs) {
   __shared__ __align__(16) int8_t q[2][kOcStage];
@@ -291,6 +352,8 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_q8_0_q8_0_occ(
   const int sp = tid >> 9;
   const int sr = (tid & 511) >> 2, sm = tid & 3;
   const uint8_t *sbase = sp == 0 ? vx + min(m0 + sr, nr - 1) * bx : vy + min(n0 + sr, nc - 1) * by;
+  const bool q4_task = kQ4 && sp == 0;  // wave-uniform: waves 0-7 stage weights
+  const int sblk = q4_task ? kQ4Bytes : kQ8Bytes;
 
   float acc[16];
 #pragma unroll
@@ -307,10 +370,10 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_q8_0_q8_0_occ(
   bool act, two;
   chunk_task(0, act, two);
   if (act)
-    load_pair(pr, sbase + 2 * sm * kQ8Bytes, two);
+    load_task(pr, sbase + 2 * sm * sblk, two, q4_task);
   if (act)
-    store_pair(pr, two, q[0] + (sp * kFbBM + sr) * kFbQRow + 64 * sm, &dsc[0][sp][2 * sm][sr],
-               &dsc[0][sp][2 * sm + 1][sr]);
+    store_task(pr, two, q4_task, q[0] + (sp * kFbBM + sr) * kFbQRow + 64 * sm,
+               &dsc[0][sp][2 * sm][sr], &dsc[0][sp][2 * sm + 1][sr]);
   __syncthreads();
 
   const int ra = wm * 32 + li, rb = kFbBM + wn * 32 + li;
@@ -321,7 +384,7 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_q8_0_q8_0_occ(
     if (c + 1 < nchunks) {
       chunk_task(c + 1, act1, two1);
       if (act1)
-        load_pair(pr, sbase + ((c + 1) * kFbKB + 2 * sm) * kQ8Bytes, two1);
+        load_task(pr, sbase + ((c + 1) * kFbKB + 2 * sm) * sblk, two1, q4_task);
     }
     const int8_t *qs = q[st];
     for (int b = 0; b < nbc; ++b) {
@@ -330,16 +393,24 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_q8_0_q8_0_occ(
       const uint32_t dxb = dsc[st][0][b][wm * 32 + li];
       const uint32_t dyb = dsc[st][1][b][wn * 32 + li];
       const v2i ax = v2i{h == 0 ? static_cast<int>(dxb) : 0, 0};
-      const v2i ay = v2i{h == 0 ? static_cast<int>(dyb) : 0, 0};
+      // Q4_0: 0x3C00 = 1.0 in f16, so the MFMA below yields d_x(row) itself
+      const v2i ay = v2i{h == 0 ? static_cast<int>(kQ4 ? 0x3C00u : dyb) : 0, 0};
       const v16i sumi = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, v16i{}, 0, 0, 0);
       const v16f dxy = __builtin_amdgcn_mfma_f32_32x32x8f16(
           __builtin_bit_cast(v4h, ax), __builtin_bit_cast(v4h, ay), v16f{}, 0, 0, 0);
+      if constexpr (kQ4) {
+        const float dy = fp16_bits_to_f32(dyb);
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        acc[e] = fmaf(static_cast<float>(sumi[e]), dxy[e], acc[e]);
+        for (int e = 0; e < 16; ++e)
+          acc[e] = fmaf(static_cast<float>(sumi[e]) * dxy[e], dy, acc[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          acc[e] = fmaf(static_cast<float>(sumi[e]), dxy[e], acc[e]);
+      }
     }
     if (c + 1 < nchunks && act1)
-      store_pair(pr, two1, q[st ^ 1] + (sp * kFbBM + sr) * kFbQRow + 64 * sm,
+      store_task(pr, two1, q4_task, q[st ^ 1] + (sp * kFbBM + sr) * kFbQRow + 64 * sm,
                  &dsc[st ^ 1][sp][2 * sm][sr], &dsc[st ^ 1][sp][2 * sm + 1][sr]);
     __syncthreads();
   }
@@ -353,6 +424,25 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_q8_0_q8_0_occ(
   }
 }
 }  // namespace tcrv
+
+namespace tcrv_host {
+
+// Q4_0 x Q8_0 GEMM (nc > 1) on the MFMA kernel; returns TCRV_HIP_ERR_UNSUPPORTED
+// when the rows are not 4-byte aligned (the caller then uses the block-dot grid).
+int q4_0_gemm_mfma(size_t nb, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy,
+                   size_t by, size_t nr, size_t nc, size_t bs, void *stream) {
+  if (!(aligned4(vx) && aligned4(vy) && (nr == 1 || bx % 4 == 0) && (nc == 1 || by % 4 == 0)))
+    return TCRV_HIP_ERR_UNSUPPORTED;
+  const size_t tiles =
+      ((nr + tcrv::kFbBM - 1) / tcrv::kFbBM) * ((nc + tcrv::kFbBN - 1) / tcrv::kFbBN);
+  if (tiles > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  tcrv::gemm_occ<true><<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kOcThreads), 0,
+                         as_stream(stream)>>>(nb, s, vx, vy, by, nr, nc, bx, bs);
+  return launch_status();
+}
+
+}  // namespace tcrv_host
 
 extern "C" int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx,
                                        const uint8_t *vy, size_t by, size_t nr, size_t nc,
@@ -377,8 +467,8 @@ extern "C" int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx,
         ((nr + tcrv::kFbBM - 1) / tcrv::kFbBM) * ((nc + tcrv::kFbBN - 1) / tcrv::kFbBN);
     if (tiles > 0x7fffffffu)
       return TCRV_HIP_ERR_TOO_LARGE;
-    tcrv::gemm_q8_0_q8_0_occ<<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kOcThreads), 0,
-                               as_stream(stream)>>>(nb, s, vx, vy, by, nr, nc, bx, bs);
+    tcrv::gemm_occ<false><<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kOcThreads), 0,
+                            as_stream(stream)>>>(nb, s, vx, vy, by, nr, nc, bx, bs);
     return launch_status();
   }
   const int rows16 = aligned16(vx) && aligned16(vy) && (nr == 1 || bx % 16 == 0) &&

@@ -387,6 +387,16 @@ int tcrv_hip_q4_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t
     return tcrv_host::zero_outputs(s, nr * nc, bs, nc, stream);
   if (nc == 1)
     return tcrv_host::gemv_q4_0_q8_0(n, s, bs, vx, bx, vy, nr, stream);
+  if (!s || !vx || !vy)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!tcrv_host::aligned2(vx) || !tcrv_host::aligned2(vy) || (nr > 1 && (bx & 1u)) || (by & 1u))
+    return TCRV_HIP_ERR_MISALIGNED;
+  const size_t nb = n / tcrv::kQK;
+  if ((nr > 1 && bx < nb * tcrv::kQ4Bytes) || by < nb * tcrv::kQ8Bytes)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  const int st = tcrv_host::q4_0_gemm_mfma(nb, s, vx, bx, vy, by, nr, nc, bs, stream);
+  if (st != TCRV_HIP_ERR_UNSUPPORTED)
+    return st;
   return tcrv_host::q4_0_grid(n, s, vx, bx, vy, by, nr, nc, bs, stream);
 }
 

@@ -120,6 +120,11 @@ inline hipStream_t as_stream(void *stream) { return reinterpret_cast<hipStream_t
 // s[(i / ncols) * stride + i % ncols] (what the reference writes when nb == 0).
 int zero_outputs(float *s, size_t count, size_t stride, size_t ncols, void *stream);
 
+// Q4_0 x Q8_0 GEMM for nc > 1 on MFMA (gemm.hip); TCRV_HIP_ERR_UNSUPPORTED when
+// rows are not 4-byte aligned.
+int q4_0_gemm_mfma(size_t nb, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy,
+                   size_t by, size_t nr, size_t nc, size_t bs, void *stream);
+
 // Q4_0 x Q8_0 GEMM for nc > 1 as one wave per output element (block_dot.hip).
 int q4_0_grid(size_t n, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by,
               size_t nr, size_t nc, size_t bs, void *stream);
