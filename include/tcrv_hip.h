@@ -72,6 +72,42 @@ TCRV_HIP_API int tcrv_hip_stream_synchronize(void *stream);
  * pointers take the 128-bit path.  out may alias lhs or rhs exactly. */
 TCRV_HIP_API int tcrv_hip_add_f32(const float *lhs, const float *rhs, float *out, size_t n, void *stream);
 
+/* Typed binary arithmetic: tcrv_rvv.binary {kind = "add" | "sub" | "mul"}
+ * (RVVOps.td:3217-3243; verifier RVVDialectArithmeticOps.cpp:38-82; emitBinary
+ * RVVToEmitC.cpp:1873-1911 selecting vadd/vsub/vmul or vfadd/vfsub/vfmul by
+ * binaryMnemonic :4976-4993) over the element types of the reference's vector
+ * type grid (RVVToEmitC.cpp:5040-5075).  out[i] = lhs[i] <kind> rhs[i], i < n.
+ * Integer kinds wrap modulo 2^width (RVV vadd/vsub/vmul keep the low bits, so
+ * signed and unsigned share one result); float kinds are single IEEE-754
+ * round-to-nearest-even operations (never contracted).  A NaN result may carry
+ * an input's payload where RISC-V returns its canonical NaN.  Pointers need the
+ * element's alignment; 16-byte aligned ones take the 128-bit path.  out may
+ * alias lhs or rhs exactly. */
+enum {
+  TCRV_HIP_BINARY_ADD = 0,
+  TCRV_HIP_BINARY_SUB = 1,
+  TCRV_HIP_BINARY_MUL = 2
+};
+enum {
+  TCRV_HIP_ELEM_I8 = 0,
+  TCRV_HIP_ELEM_U8 = 1,
+  TCRV_HIP_ELEM_I16 = 2,
+  TCRV_HIP_ELEM_U16 = 3,
+  TCRV_HIP_ELEM_I32 = 4,
+  TCRV_HIP_ELEM_U32 = 5,
+  TCRV_HIP_ELEM_I64 = 6,
+  TCRV_HIP_ELEM_F32 = 7,
+  TCRV_HIP_ELEM_F64 = 8
+};
+TCRV_HIP_API int tcrv_hip_binary(int kind, int elem, const void *lhs, const void *rhs, void *out,
+                    size_t n, void *stream);
+
+/* The reference's own add slice and golden are i32
+ * (test/Conversion/RVV/rvv-to-emitc-add-cpp-golden.mlir:15-18,33;
+ * examples/qemu/harness_add.cpp:11-12): (lhs, rhs, out, n). */
+TCRV_HIP_API int tcrv_hip_add_i32(const int32_t *lhs, const int32_t *rhs, int32_t *out, size_t n,
+                     void *stream);
+
 /* ---- a3: Q8_0 dequantize --------------------------------------------------
  * ggml dequantize_row_q8_0(const block_q8_0 *x, float *y, int64_t k) (no
  * reference op; block layout RVVDialectWideningOps.cpp:3358-3372).

@@ -102,6 +102,45 @@ void tcrv_oracle_add_i32(const int32_t *lhs, const int32_t *rhs, int32_t *out, s
     out[i] = (int32_t)((uint32_t)lhs[i] + (uint32_t)rhs[i]); /* vadd wraps */
 }
 
+#define TCRV_ORACLE_BINARY_LOOP(T)                                         \
+  do {                                                                     \
+    const T *a = (const T *)lhs, *b = (const T *)rhs;                      \
+    T *o = (T *)out;                                                       \
+    for (size_t i = 0; i < n; ++i)                                         \
+      o[i] = kind == 0 ? (T)(a[i] + b[i]) : kind == 1 ? (T)(a[i] - b[i])   \
+                                                      : (T)(a[i] * b[i]);  \
+  } while (0)
+
+int tcrv_oracle_binary(int kind, int elem, const void *lhs, const void *rhs, void *out,
+                       size_t n) {
+  if (kind < 0 || kind > 2)
+    return -1;
+  /* integer elements on unsigned types: the low bits of the result are the
+   * RVV vadd/vsub/vmul result for signed and unsigned elements alike
+   * (unsigned short promotes to int, so the product is taken in uint32_t) */
+  switch (elem) {
+  case 0:
+  case 1: TCRV_ORACLE_BINARY_LOOP(uint8_t); break;
+  case 2:
+  case 3: {
+    const uint16_t *a = (const uint16_t *)lhs, *b = (const uint16_t *)rhs;
+    uint16_t *o = (uint16_t *)out;
+    for (size_t i = 0; i < n; ++i) {
+      uint32_t x = a[i], y = b[i];
+      o[i] = (uint16_t)(kind == 0 ? x + y : kind == 1 ? x - y : x * y);
+    }
+    break;
+  }
+  case 4:
+  case 5: TCRV_ORACLE_BINARY_LOOP(uint32_t); break;
+  case 6: TCRV_ORACLE_BINARY_LOOP(uint64_t); break;
+  case 7: TCRV_ORACLE_BINARY_LOOP(float); break;
+  case 8: TCRV_ORACLE_BINARY_LOOP(double); break;
+  default: return -1;
+  }
+  return 0;
+}
+
 /* ------------------------------------------------------------------------ */
 /* a3: Q8_0 dequantize (ggml dequantize_row_q8_0; block layout pinned by     */
 /* RVVDialectWideningOps.cpp:3358-3372, fp16 read RVVToEmitCBlockQuantLinear */

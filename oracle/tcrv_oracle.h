@@ -43,6 +43,15 @@ uint16_t tcrv_oracle_f32_to_fp16(float f);
 void tcrv_oracle_add_f32(const float *lhs, const float *rhs, float *out, size_t n);
 void tcrv_oracle_add_i32(const int32_t *lhs, const int32_t *rhs, int32_t *out, size_t n);
 
+/* a1 over the reference's element grid: tcrv_rvv.binary {kind = add|sub|mul}
+ * (emitBinary RVVToEmitC.cpp:1873-1911, vadd/vsub/vmul or vfadd/vfsub/vfmul by
+ * binaryMnemonic :4976-4993).  kind 0 add, 1 sub, 2 mul; elem 0 i8, 1 u8,
+ * 2 i16, 3 u16, 4 i32, 5 u32, 6 i64, 7 f32, 8 f64.  Integers wrap modulo
+ * 2^width; floats are single IEEE operations.  Returns 0, or -1 for an unknown
+ * kind/elem. */
+int tcrv_oracle_binary(int kind, int elem, const void *lhs, const void *rhs, void *out,
+                       size_t n);
+
 /* a3: y[32b+j] = qs_b[j] * fp16->f32(d_b) (ggml dequantize_row_q8_0). */
 void tcrv_oracle_dequantize_row_q8_0(size_t n, float *y, const uint8_t *vx);
 

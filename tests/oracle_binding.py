@@ -25,6 +25,7 @@ _SIGS = {
     "tcrv_oracle_f32_to_fp16": ([ctypes.c_float], ctypes.c_uint16),
     "tcrv_oracle_add_f32": ([_p, _p, _p, _sz], None),
     "tcrv_oracle_add_i32": ([_p, _p, _p, _sz], None),
+    "tcrv_oracle_binary": ([_int, _int, _p, _p, _p, _sz], _int),
     "tcrv_oracle_dequantize_row_q8_0": ([_sz, _p, _p], None),
     "tcrv_oracle_q4_0_q8_0_block_sumi": ([_p, _p], _i32),
     "tcrv_oracle_q8_0_q8_0_block_sumi": ([_p, _p], _i32),
@@ -76,6 +77,11 @@ class Oracle:
     def add_i32(self, a: np.ndarray, b: np.ndarray) -> np.ndarray:
         out = np.empty_like(a)
         self.lib.tcrv_oracle_add_i32(_a(a), _a(b), _a(out), a.size)
+        return out
+
+    def binary(self, kind: int, elem: int, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+        out = np.empty_like(a)
+        assert self.lib.tcrv_oracle_binary(kind, elem, _a(a), _a(b), _a(out), a.size) == 0
         return out
 
     # -- a3 ----------------------------------------------------------------

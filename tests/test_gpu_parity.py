@@ -400,3 +400,51 @@ def test_q4_0_gemm_full_size_sampled(hip, oracle, dev):
     sub = np.ascontiguousarray(a[cols])
     want = oracle.gemm_q4_0(n, w, sub, sub.shape[1], nr, len(cols), w.shape[1], len(cols), 8)
     assert_f32_parity(got[:, cols], want.reshape(nr, len(cols)), what="sampled cols")
+
+
+# ---------------------------------------------------- typed tcrv_rvv.binary ---
+
+BINARY_ELEMS = [("i8", np.int8), ("u8", np.uint8), ("i16", np.int16), ("u16", np.uint16),
+                ("i32", np.int32), ("u32", np.uint32), ("i64", np.int64), ("f32", np.float32),
+                ("f64", np.float64)]
+
+
+def _binary_inputs(dtype, n, seed):
+    rng = np.random.default_rng(seed)
+    if np.issubdtype(dtype, np.integer):
+        info = np.iinfo(dtype)
+        a = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+        b = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+        a[:3] = [info.min, info.max, info.max]
+        b[:3] = [info.min, 1, info.max]
+    else:
+        a = (rng.standard_normal(n) * 1e3).astype(dtype)
+        b = rng.standard_normal(n).astype(dtype)
+        tiny = np.finfo(dtype).smallest_subnormal
+        a[:3] = [tiny, np.finfo(dtype).max, -0.0]
+        b[:3] = [tiny, np.finfo(dtype).max, 0.0]
+    return a, b
+
+
+@pytest.mark.parametrize("elem,dtype", BINARY_ELEMS)
+@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_binary_all_types(hip, oracle, dev, kind, elem, dtype):
+    for n, off in ((1031, 0), ((1 << 20) + 5, 0), (777, 1)):  # off 1: unaligned -> scalar path
+        a, b = _binary_inputs(dtype, n + off, 100 * kind + n % 97)
+        da, db = to_dev(a.view(np.uint8), dev), to_dev(b.view(np.uint8), dev)
+        out = empty_dev((n + off) * a.itemsize, torch.uint8, dev)
+        k = a.itemsize * off
+        hip.binary(kind, elem, da[k:], db[k:], out[k:], n)
+        want = oracle.binary(kind, hip.ELEM[elem], a[off:].copy(), b[off:].copy())
+        got = from_dev(out)[k:].view(dtype)
+        assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), (elem, kind, n)
+
+
+def test_add_i32_harness_vector(hip, dev):
+    n = 1031
+    i = np.arange(n, dtype=np.int64)
+    a = (3 * i - 17).astype(np.int32)
+    b = (41 - 2 * i).astype(np.int32)
+    out = empty_dev(n, torch.int32, dev)
+    hip.add_i32(to_dev(a, dev), to_dev(b, dev), out, n)
+    assert np.array_equal(from_dev(out), (i + 24).astype(np.int32))

@@ -485,3 +485,44 @@ def test_repack_gemv_q8_exact_fold_and_trailing_columns(oracle):
             acc = exact.fma32(np.float32(s), exact.mul32(dx[b], dy[b]), acc)
         assert got[row] == acc
     assert np.all(got[32:] == 0)
+
+
+BINARY_ELEMS = [(0, np.int8), (1, np.uint8), (2, np.int16), (3, np.uint16), (4, np.int32),
+                (5, np.uint32), (6, np.int64), (7, np.float32), (8, np.float64)]
+
+
+def binary_inputs(dtype, n, seed):
+    rng = np.random.default_rng(seed)
+    if np.issubdtype(dtype, np.integer):
+        info = np.iinfo(dtype)
+        a = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+        b = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
+        a[:4] = [info.min, info.max, info.max, 0]  # overflow / wrap cases
+        b[:4] = [info.min, 1, info.max, info.min]
+    else:
+        a = rng.standard_normal(n).astype(dtype) * dtype(1e3)
+        b = rng.standard_normal(n).astype(dtype)
+        tiny = np.finfo(dtype).smallest_subnormal
+        a[:4] = [tiny, np.finfo(dtype).max, -0.0, np.inf]
+        b[:4] = [tiny, np.finfo(dtype).max, 0.0, 1.0]
+    return a, b
+
+
+@pytest.mark.parametrize("elem,dtype", BINARY_ELEMS)
+@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_binary_matches_numpy(oracle, kind, elem, dtype):
+    """numpy's fixed-width integer ops wrap and its float ops are single IEEE
+    operations -- the semantics of RVV vadd/vsub/vmul and vfadd/vfsub/vfmul."""
+    a, b = binary_inputs(dtype, 1031, 10 * kind + elem)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = (a + b) if kind == 0 else (a - b) if kind == 1 else (a * b)
+    got = oracle.binary(kind, elem, a, b)
+    assert np.array_equal(got.view(np.uint8), want.astype(dtype).view(np.uint8))
+
+
+def test_binary_i32_add_is_the_harness(oracle):
+    n = 1031
+    i = np.arange(n, dtype=np.int64)
+    a = (3 * i - 17).astype(np.int32)
+    b = (41 - 2 * i).astype(np.int32)
+    assert np.array_equal(oracle.binary(0, 4, a, b), (i + 24).astype(np.int32))

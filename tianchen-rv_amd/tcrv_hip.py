@@ -31,6 +31,9 @@ ERR_MISALIGNED = -3
 ERR_TOO_LARGE = -4
 ERR_UNSUPPORTED = -5
 
+BINARY_ADD, BINARY_SUB, BINARY_MUL = 0, 1, 2
+ELEM = {"i8": 0, "u8": 1, "i16": 2, "u16": 3, "i32": 4, "u32": 5, "i64": 6, "f32": 7, "f64": 8}
+
 
 class TcrvHipError(RuntimeError):
     """A libtcrv_hip call returned a non-zero status, or the library is absent."""
@@ -49,6 +52,8 @@ _int = ctypes.c_int
 SIGNATURES = {
     "tcrv_hip_stream_synchronize": [_p],
     "tcrv_hip_add_f32": [_p, _p, _p, _sz, _p],
+    "tcrv_hip_add_i32": [_p, _p, _p, _sz, _p],
+    "tcrv_hip_binary": [_int, _int, _p, _p, _p, _sz, _p],
     "tcrv_hip_dequantize_row_q8_0": [_p, _p, _sz, _p],
     "tcrv_hip_quantize_row_q8_0": [_sz, _p, _p, _p],
     "tcrv_hip_q8_0_q8_0_block_dot": [_sz, _p, _p, _p, _p],
@@ -144,6 +149,17 @@ def call(name: str, *args, check: bool = True) -> int:
 def add_f32(lhs, rhs, out, n: Optional[int] = None, stream=None):
     n = lhs.numel() if n is None else n
     return call("tcrv_hip_add_f32", lhs, rhs, out, n, _stream(stream))
+
+
+def add_i32(lhs, rhs, out, n: Optional[int] = None, stream=None):
+    n = lhs.numel() if n is None else n
+    return call("tcrv_hip_add_i32", lhs, rhs, out, n, _stream(stream))
+
+
+def binary(kind: int, elem: str, lhs, rhs, out, n: Optional[int] = None, stream=None):
+    """tcrv_rvv.binary: kind BINARY_ADD/SUB/MUL, elem a key of ELEM."""
+    n = lhs.numel() if n is None else n
+    return call("tcrv_hip_binary", kind, ELEM[elem], lhs, rhs, out, n, _stream(stream))
 
 
 def dequantize_row_q8_0(vx, y, n: int, stream=None):
