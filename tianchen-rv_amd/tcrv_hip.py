@@ -85,6 +85,15 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
             ERR_UNSUPPORTED,
             f"libtcrv_hip.so not found at {path}: run __graft_entry__.build() "
             "(make -C tianchen-rv_amd); there is no CPU fallback")
+    # PyTorch-ROCm ships its own libamdhip64.  Importing torch first makes the
+    # library bind to that same HIP runtime (one runtime per process, so torch's
+    # streams and device pointers are valid here); loading the library first
+    # maps the system runtime beside torch's, and the second runtime to
+    # initialise finds no device.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(path)
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
