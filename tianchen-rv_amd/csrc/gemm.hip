@@ -181,14 +181,17 @@ __global__ __launch_bounds__(kGmThreads) void gemm_q8_0_q8_0_kernel(
 
 
 // ---------------------------------------------------------------------------
-// Fast path.  Per 32x32 output tile and Q8_0 block b:
-//   v_mfma_i32_32x32x32_i8  -> sumi(row, col, b) for the tile
-//   v_mfma_f32_32x32x8f16   -> dx(row, b) * dy(col, b) for the tile: the A
-//                              operand carries dx in k-slot 0 only, the B
-//                              operand dy in k-slot 0 only, so the product is a
-//                              rank-1 outer product, exact in fp32 (two 11-bit
-//                              significands) -- no per-element VALU multiply
+// Fast path.  Per 32x32 output tile and Q8_0 blocks b, b+1:
+//   v_mfma_i32_32x32x32_i8 (x2)  -> sumi(row, col, b) and sumi(row, col, b+1)
+//   v_mfma_f32_32x32x1_2b_f32    -> dx(row, b) * dy(col, b) and the same for
+//                                   b+1: two rank-1 outer products (K = 1), each
+//                                   product of two fp16 values, exact in fp32
+//                                   -- no per-element VALU multiply
 //   VALU: acc = fma((float)sumi, dxy, acc)   -- the reference fold, in order.
+// On this part the matrix core and the VALU do not overlap (a microbenchmark
+// of this loop runs in the sum of the two alone), so the loop is built to
+// issue the fewest VALU instructions: 32 per tile and block, no selects or
+// address arithmetic.
 // ---------------------------------------------------------------------------
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
@@ -222,11 +225,12 @@ __device__ __forceinline__ void tile_of(unsigned id, unsigned tiles_m, unsigned 
 }
 
 // Work-group: 16 waves, each owning one 32x32 tile of a 128x128 output tile
-// (four waves per SIMD hide LDS and MFMA latency; 90 VGPRs).  K chunks of 8
-// blocks are staged split -- each 34-byte block into its 32 quants (row-major,
-// 16-byte aligned) and its fp16 scale -- and double-buffered: each thread loads
-// its one 68-byte block pair of chunk c+1 into registers before computing chunk
-// c and writes it to the other LDS buffer afterwards.
+// (four waves per SIMD hide LDS and MFMA latency; at most 128 VGPRs).  K chunks
+// of 8 blocks are staged split -- each 34-byte block into its 32 quants
+// (row-major, 16-byte aligned) and its scale widened to f32 -- and
+// double-buffered: each thread loads its one 68-byte block pair of chunk c+1
+// into registers before computing chunk c and writes it to the other LDS buffer
+// afterwards.
 constexpr int kOcThreads = 1024;
 constexpr int kOcStage = (kFbBM + kFbBN) * kFbQRow;  // split quants of both panels
 
@@ -255,18 +259,18 @@ __device__ __forceinline__ void load_pair(PairRegs &p, const uint8_t *q, bool tw
 }
 
 __device__ __forceinline__ void store_pair(const PairRegs &p, bool two, int8_t *qrow,
-                                           uint16_t *d0, uint16_t *d1) {
+                                           float *d0, float *d1) {
   const uint32_t *r = p.r;
   uint4 *dst = reinterpret_cast<uint4 *>(qrow);
   dst[0] = make_uint4(funnel16(r[0], r[1]), funnel16(r[1], r[2]), funnel16(r[2], r[3]),
                       funnel16(r[3], r[4]));
   dst[1] = make_uint4(funnel16(r[4], r[5]), funnel16(r[5], r[6]), funnel16(r[6], r[7]),
                       funnel16(r[7], r[8]));
-  *d0 = static_cast<uint16_t>(r[0] & 0xffffu);
+  *d0 = fp16_bits_to_f32(r[0] & 0xffffu);
   if (two) {
     dst[2] = make_uint4(r[9], r[10], r[11], r[12]);
     dst[3] = make_uint4(r[13], r[14], r[15], r[16]);
-    *d1 = static_cast<uint16_t>(r[8] >> 16);
+    *d1 = fp16_bits_to_f32(r[8] >> 16);
   }
 }
 
@@ -296,16 +300,16 @@ __device__ __forceinline__ void store_q4_block(const uint32_t q[4], int8_t *dst)
 }
 
 __device__ __forceinline__ void store_pair_q4(const PairRegs &p, bool two, int8_t *qrow,
-                                              uint16_t *d0, uint16_t *d1) {
+                                              float *d0, float *d1) {
   const uint32_t *r = p.r;
   const uint32_t qa[4] = {funnel16(r[0], r[1]), funnel16(r[1], r[2]), funnel16(r[2], r[3]),
                           funnel16(r[3], r[4])};
   store_q4_block(qa, qrow);
-  *d0 = static_cast<uint16_t>(r[0] & 0xffffu);
+  *d0 = fp16_bits_to_f32(r[0] & 0xffffu);
   if (two) {
     const uint32_t qb[4] = {r[5], r[6], r[7], r[8]};
     store_q4_block(qb, qrow + kQK);
-    *d1 = static_cast<uint16_t>(r[4] >> 16);
+    *d1 = fp16_bits_to_f32(r[4] >> 16);
   }
 }
 
@@ -323,11 +327,47 @@ __device__ __forceinline__ void load_task(PairRegs &p, const uint8_t *q, bool tw
 }
 
 __device__ __forceinline__ void store_task(const PairRegs &p, bool two, bool q4, int8_t *qrow,
-                                           uint16_t *d0, uint16_t *d1) {
+                                           float *d0, float *d1) {
   if (q4)
     store_pair_q4(p, two, qrow, d0, d1);
   else
     store_pair(p, two, qrow, d0, d1);
+}
+
+typedef float v32f __attribute__((ext_vector_type(32)));
+
+// Blocks b and b+1 of the chunk for this wave's 32x32 tile (kTwo = false: block
+// b alone).  The scales are staged as f32, [block][row] per panel:
+//   sxh = this lane's weight-row scale of block h (h = lane / 32), so one
+//         v_mfma_f32_32x32x1_2b_f32 -- lanes 0-31 are its block 0, lanes 32-63
+//         its block 1 -- returns d_x*d_y of block b in dxy[0..15] and of block
+//         b+1 in dxy[16..31] (each product of two fp16 values, exact in f32);
+//   syh = the same for the token scale (Q8_0), or 1.0 (Q4_0: dxy = d_x);
+//   syc = this lane's token-column scale of block 0 (Q4_0 fold only).
+// qa/qb: this lane's 16 quant bytes of block 0 of the chunk.
+template <bool kQ4, bool kTwo>
+__device__ __forceinline__ void fold_pair(float (&acc)[16], const int8_t *qa, const int8_t *qb,
+                                          const float *sxh, const float *syh, const float *syc,
+                                          int b) {
+  const float dx = sxh[b * kFbBM];
+  const float dy_op = kQ4 ? 1.0f : syh[b * kFbBM];
+  const v32f dxy = __builtin_amdgcn_mfma_f32_32x32x1f32(dx, dy_op, v32f{}, 0, 0, 0);
+#pragma unroll
+  for (int j = 0; j < (kTwo ? 2 : 1); ++j) {
+    const v4i a = *reinterpret_cast<const v4i *>(qa + (b + j) * kQK);
+    const v4i bq = *reinterpret_cast<const v4i *>(qb + (b + j) * kQK);
+    const v16i sumi = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, v16i{}, 0, 0, 0);
+    if constexpr (kQ4) {
+      const float dy = syc[(b + j) * kFbBM];
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc[e] = fmaf(static_cast<float>(sumi[e]) * dxy[16 * j + e], dy, acc[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc[e] = fmaf(static_cast<float>(sumi[e]), dxy[16 * j + e], acc[e]);
+    }
+  }
 }
 
 template <bool kQ4>
@@ -335,7 +375,7 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_occ(
     size_t nb, float *s, const uint8_t *vx, const uint8_t *vy, size_t by, size_t nr,
     size_t nc, size_t bx, size_t bs) {
   __shared__ __align__(16) int8_t q[2][kOcStage];
-  __shared__ __align__(16) uint16_t dsc[2][2][kFbKB][kFbBM];  // [stage][panel][block][row]
+  __shared__ __align__(16) float dsc[2][2][kFbKB][kFbBM];  // [stage][panel][block][row]
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -376,43 +416,62 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_occ(
                &dsc[0][sp][2 * sm][sr], &dsc[0][sp][2 * sm + 1][sr]);
   __syncthreads();
 
-  const int ra = wm * 32 + li, rb = kFbBM + wn * 32 + li;
-  for (size_t c = 0; c < nchunks; ++c) {
+  // this lane's operand addresses in stage 0 (stage 1 is a fixed offset away)
+  const int8_t *qa0 = q[0] + (wm * 32 + li) * kFbQRow + 16 * h;
+  const int8_t *qb0 = q[0] + (kFbBM + wn * 32 + li) * kFbQRow + 16 * h;
+  const float *sxh0 = &dsc[0][0][h][wm * 32 + li];
+  const float *syh0 = &dsc[0][1][h][wn * 32 + li];
+  const float *syc0 = &dsc[0][1][0][wn * 32 + li];
+  constexpr int kDscStage = 2 * kFbKB * kFbBM;
+
+  // Full chunks: the next chunk's loads are in flight while this one is
+  // folded; a trailing partial chunk (nb % kFbKB blocks) is folded after the
+  // loop, so the loop body has a single path.
+  const size_t nfull = nb / kFbKB;
+  for (size_t c = 0; c < nfull; ++c) {
     const int st = static_cast<int>(c & 1);
-    const int nbc = static_cast<int>(min(static_cast<size_t>(kFbKB), nb - c * kFbKB));
     bool act1 = false, two1 = false;
     if (c + 1 < nchunks) {
       chunk_task(c + 1, act1, two1);
       if (act1)
         load_task(pr, sbase + ((c + 1) * kFbKB + 2 * sm) * sblk, two1, q4_task);
     }
-    const int8_t *qs = q[st];
-    for (int b = 0; b < nbc; ++b) {
-      const v4i a = *reinterpret_cast<const v4i *>(qs + ra * kFbQRow + b * kQK + 16 * h);
-      const v4i bq = *reinterpret_cast<const v4i *>(qs + rb * kFbQRow + b * kQK + 16 * h);
-      const uint32_t dxb = dsc[st][0][b][wm * 32 + li];
-      const uint32_t dyb = dsc[st][1][b][wn * 32 + li];
-      const v2i ax = v2i{h == 0 ? static_cast<int>(dxb) : 0, 0};
-      // Q4_0: 0x3C00 = 1.0 in f16, so the MFMA below yields d_x(row) itself
-      const v2i ay = v2i{h == 0 ? static_cast<int>(kQ4 ? 0x3C00u : dyb) : 0, 0};
-      const v16i sumi = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, v16i{}, 0, 0, 0);
-      const v16f dxy = __builtin_amdgcn_mfma_f32_32x32x8f16(
-          __builtin_bit_cast(v4h, ax), __builtin_bit_cast(v4h, ay), v16f{}, 0, 0, 0);
-      if constexpr (kQ4) {
-        const float dy = fp16_bits_to_f32(dyb);
+    const int8_t *qa = qa0 + st * kOcStage;
+    const int8_t *qb = qb0 + st * kOcStage;
+    const float *sxh = sxh0 + st * kDscStage;
+    const float *syh = syh0 + st * kDscStage;
+    const float *syc = syc0 + st * kDscStage;
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          acc[e] = fmaf(static_cast<float>(sumi[e]) * dxy[e], dy, acc[e]);
-      } else {
+    for (int b = 0; b < kFbKB; b += 2) {
+      fold_pair<kQ4, true>(acc, qa, qb, sxh, syh, syc, b);
+      // one block pair at a time (the folded accumulators are pinned here and
+      // nothing is scheduled across): keeps the live registers within the 128
+      // that four waves per SIMD allow
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          acc[e] = fmaf(static_cast<float>(sumi[e]), dxy[e], acc[e]);
-      }
+      for (int e = 0; e < 16; ++e)
+        asm volatile("" : "+v"(acc[e]));
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (c + 1 < nchunks && act1)
+    if (act1)
       store_task(pr, two1, q4_task, q[st ^ 1] + (sp * kFbBM + sr) * kFbQRow + 64 * sm,
                  &dsc[st ^ 1][sp][2 * sm][sr], &dsc[st ^ 1][sp][2 * sm + 1][sr]);
     __syncthreads();
+  }
+  const int nbc = static_cast<int>(nb - nfull * kFbKB);
+  if (nbc > 0) {
+    const int st = static_cast<int>(nfull & 1);
+    const int8_t *qa = qa0 + st * kOcStage;
+    const int8_t *qb = qb0 + st * kOcStage;
+    const float *sxh = sxh0 + st * kDscStage;
+    const float *syh = syh0 + st * kDscStage;
+    const float *syc = syc0 + st * kDscStage;
+    // nbc < kFbKB, so the 2-block scale read of a last odd block stays inside
+    // the stage (its second block is not used)
+    int b = 0;
+    for (; b + 1 < nbc; b += 2)
+      fold_pair<kQ4, true>(acc, qa, qb, sxh, syh, syc, b);
+    if (b < nbc)
+      fold_pair<kQ4, false>(acc, qa, qb, sxh, syh, syc, b);
   }
 
   const size_t col = n0 + wn * 32 + li;
