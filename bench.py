@@ -55,7 +55,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000, help="timed GEMV launches")
     ap.add_argument("--warmup", type=int, default=200, help="untimed GEMV launches")
-    ap.add_argument("--gemm-steps", type=int, default=20)
+    ap.add_argument("--gemm-steps", type=int, default=20, help="GEMM launches per timed region")
+    ap.add_argument("--gemm-regions", type=int, default=5,
+                    help="timed GEMM regions; the median region is reported")
     ap.add_argument("--config-steps", type=int, default=50,
                     help="timed launches for each of add / dequant / block dot")
     ap.add_argument("--copies", type=int, default=40,
@@ -175,17 +177,20 @@ def bench_gemm(torch, lib, stream, args):
         # s[ir*bs + col]: ir = weight row (B), col = token (A)
         fn(N, cd.data_ptr(), bd.data_ptr(), ad.data_ptr(), rb, N, N, rb, N, sp)
 
-    Region(torch, stream, launch, 2).run()
+    # ~50 launches (~10 ms of dense MFMA work) bring the clocks to their
+    # loaded state before anything is timed
+    Region(torch, stream, launch, 50).run()
     cd.zero_()
     timed = Region(torch, stream, launch, args.gemm_steps)
-    ms = timed.run()
+    per = sorted(timed.run() * 1e3 / args.gemm_steps for _ in range(args.gemm_regions))
     same_as_eager(torch, stream, cd,
                   lambda out: fn(N, out, bd.data_ptr(), ad.data_ptr(), rb, N, N, rb, N, sp), "GEMM")
-    us = ms * 1e3 / args.gemm_steps
+    us = per[len(per) // 2]
     tops = GEMM_OPS / (us * 1e-6) / 1e12
-    log(f"GEMM {us:.1f} us/launch: {tops:.0f} TOPS ({100 * tops / INT8_PEAK_TOPS:.1f}% of "
-        f"dense int8 peak)")
-    return {"us": us, "tops": tops}
+    log(f"GEMM {us:.1f} us/launch (median of {len(per)} regions of {args.gemm_steps}; "
+        f"min {per[0]:.1f}, max {per[-1]:.1f}): {tops:.0f} TOPS "
+        f"({100 * tops / INT8_PEAK_TOPS:.1f}% of dense int8 peak)")
+    return {"us": us, "tops": tops, "us_min": per[0], "us_max": per[-1], "regions": len(per)}
 
 
 def bench_configs(torch, lib, stream, args):
@@ -427,7 +432,8 @@ def main():
         line["gemm"] = {
             "workload": "q8_0_q8_0_gemm 4096 weight rows x 4096 tokens x 4096 (configs[4])",
             "value": round(m["tops"], 2), "unit": "TOPS", "ms_per_step": m["us"] / 1e3,
-            "steps": args.gemm_steps,
+            "steps": args.gemm_steps, "regions": m["regions"],
+            "us_min": round(m["us_min"], 2), "us_max": round(m["us_max"], 2),
             "roofline": {"bound": "mfma", "achieved": round(m["tops"], 2), "peak": INT8_PEAK_TOPS,
                          "unit": "TOPS", "frac": round(m["tops"] / INT8_PEAK_TOPS, 4),
                          "traffic": traffic.get("q8_0_q8_0_gemm", {}).get("bytes"),

@@ -5,6 +5,12 @@
 //     matrix core and the fp32 VALU overlap on one SIMD.
 //       0: MFMA only   1: VALU only   2: both in every wave
 //       3: waves 0-3 of a 512-thread work-group MFMA only, waves 4-7 VALU only
+//   fold<kMode>: the GEMM's per-tile inner loop with its operands resident in
+//     LDS (16 waves per CU, 4 per SIMD, no global memory), parts switched on
+//     one at a time, to price each against the full loop:
+//       0: i8 MFMA + 2-block f32 MFMA (d_x*d_y) + cvt/fma fold (the GEMM loop)
+//       1: MFMAs only   2: i8 MFMA only
+//       3: VALU only, 48 instructions per tile and block (xor, cvt, fma)
 //   empty: the cost of one launch with no work (launch floor in a HIP graph)
 //   read_only: streams `n16` 16-byte chunks, one 128-bit load per chunk (the
 //     floor for a kernel that reads the GEMV's 9.4 MB once)
@@ -48,6 +54,63 @@ __global__ __launch_bounds__(512) void mix(const int *in, float *out, int iters)
   out[blockIdx.x * 512 + threadIdx.x] = r;
 }
 
+typedef float v32f __attribute__((ext_vector_type(32)));
+
+template <int kMode>
+__global__ __launch_bounds__(1024, 1) void fold(const int *in, float *out, int iters) {
+  __shared__ __align__(16) int8_t q[256 * 272];
+  __shared__ __align__(16) float dsc[8][256];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < 256 * 272 / 4; i += 1024)
+    reinterpret_cast<int *>(q)[i] = in[i & 1023];
+  for (int i = tid; i < 8 * 256; i += 1024)
+    (&dsc[0][0])[i] = 1.0f / static_cast<float>(1 + (in[i & 1023] & 7));
+  __syncthreads();
+  const int wave = tid >> 6, lane = tid & 63, wm = wave >> 2, wn = wave & 3;
+  const int li = lane & 31, h = lane >> 5;
+  const int8_t *qa = q + (wm * 32 + li) * 272 + 16 * h;
+  const int8_t *qb = q + (128 + wn * 32 + li) * 272 + 16 * h;
+  const float *sx = &dsc[h][wm * 32 + li];
+  const float *sy = &dsc[h][128 + wn * 32 + li];
+  float acc[16];
+  for (int e = 0; e < 16; ++e)
+    acc[e] = 0.0f;
+  v16i iacc = {};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int b = 0; b < 8; b += 2) {
+      v32f dxy = {};
+      if constexpr (kMode == 0 || kMode == 1)
+        dxy = __builtin_amdgcn_mfma_f32_32x32x1f32(sx[b * 256], sy[b * 256], v32f{}, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const v4i a = *reinterpret_cast<const v4i *>(qa + (b + j) * 32);
+        const v4i bq = *reinterpret_cast<const v4i *>(qb + (b + j) * 32);
+        if constexpr (kMode == 0) {
+          const v16i sumi = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, v16i{}, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            acc[e] = fmaf(static_cast<float>(sumi[e]), dxy[16 * j + e], acc[e]);
+        } else if constexpr (kMode == 1 || kMode == 2) {
+          iacc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, iacc, 0, 0, 0);
+        } else {
+          const float d = sx[(b + j) * 256];
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            acc[e] = fmaf(static_cast<float>(a[e & 3] ^ bq[e >> 2]), d, acc[e]);
+        }
+      }
+      if constexpr (kMode == 1)
+        acc[b] += dxy[b] + dxy[31 - b];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  float r = 0.0f;
+  for (int e = 0; e < 16; ++e)
+    r += acc[e] + static_cast<float>(iacc[e]);
+  out[blockIdx.x * 1024 + tid] = r;
+}
+
 __global__ void empty_kernel() {}
 
 __global__ __launch_bounds__(256) void read_only(const uint4 *p, size_t n16, uint32_t *out) {
@@ -68,6 +131,18 @@ extern "C" __attribute__((visibility("default"))) int probe_mix(int mode, const 
   case 1: mix<1><<<grid, 512, 0, s>>>(in, out, iters); break;
   case 2: mix<2><<<grid, 512, 0, s>>>(in, out, iters); break;
   case 3: mix<3><<<grid, 512, 0, s>>>(in, out, iters); break;
+  default: return -1;
+  }
+  return hipGetLastError();
+}
+
+extern "C" __attribute__((visibility("default"))) int probe_fold(int mode, const int *in, float *out, int iters, int grid, void *st) {
+  hipStream_t s = static_cast<hipStream_t>(st);
+  switch (mode) {
+  case 0: fold<0><<<grid, 1024, 0, s>>>(in, out, iters); break;
+  case 1: fold<1><<<grid, 1024, 0, s>>>(in, out, iters); break;
+  case 2: fold<2><<<grid, 1024, 0, s>>>(in, out, iters); break;
+  case 3: fold<3><<<grid, 1024, 0, s>>>(in, out, iters); break;
   default: return -1;
   }
   return hipGetLastError();

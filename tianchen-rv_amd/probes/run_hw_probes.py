@@ -60,6 +60,27 @@ def main():
         torch.cuda.synchronize()
         print(f"mix mode {mode} ({name}): {e0.elapsed_time(e1):.3f} ms "
               f"[{grid} x 512 threads, {iters} iterations]", flush=True)
+    lib.probe_fold.argtypes = lib.probe_mix.argtypes
+    fold_out = torch.empty(256 * 1024, device=dev)
+    fold_iters = 2000
+    fold_names = ["full GEMM inner loop", "MFMAs only (i8 + 2-block f32)", "i8 MFMA only",
+                  "VALU only: xor + cvt + fma per element, 48 per tile-block"]
+    for mode, name in enumerate(fold_names):
+        assert lib.probe_fold(mode, inp.data_ptr(), fold_out.data_ptr(), 10, 256, sp) == 0
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            assert lib.probe_fold(mode, inp.data_ptr(), fold_out.data_ptr(), fold_iters, 256,
+                                  sp) == 0
+            e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        tile_blocks = 4 * fold_iters * 8  # per SIMD: 4 waves x iterations x 8 blocks
+        print(f"fold mode {mode} ({name}): {ms:.3f} ms = {ms * 1e6 / tile_blocks:.2f} ns per "
+              f"32x32 tile and block per SIMD [256 x 1024 threads, {fold_iters} x 8 blocks]",
+              flush=True)
     print(f"empty kernel, graph of 1000: {graph_us(stream, lambda: lib.probe_empty(sp)):.2f} "
           f"us per launch", flush=True)
     nbytes = 9437184
