@@ -140,7 +140,11 @@ def test_q4_0_block_dot_single_ggml_abi(hip, oracle, dev):
         assert_f32_parity(from_dev(s), [oracle.vec_dot_q4_0(n, vx, vy)], what=f"nb={nb}")
 
 
-@pytest.mark.parametrize("rows,nb,pad", [(16384, 128, 0), (33, 131, 16), (5, 1, 0), (9, 256, 32)])
+# even nb with 4-byte aligned rows take the register-direct kernel (partial
+# chunks, two chunks with a carried sum, pair counts that are not a multiple of
+# the 16 pairs per work-group); odd nb or 2-byte aligned rows the LDS one
+@pytest.mark.parametrize("rows,nb,pad", [(16384, 128, 0), (33, 131, 16), (5, 1, 0), (9, 256, 32),
+                                         (21, 6, 0), (7, 130, 4), (3, 4, 2)])
 def test_q8_0_block_dot_rows(hip, oracle, dev, rows, nb, pad):
     n = nb * 32
     vx = synth.q8_0_matrix(rows, n, 1004, 1.0)
@@ -155,7 +159,8 @@ def test_q8_0_block_dot_rows(hip, oracle, dev, rows, nb, pad):
     assert_f32_parity(from_dev(s), want, what=f"q8 rows={rows} nb={nb}")
 
 
-@pytest.mark.parametrize("rows,nb,pad", [(16384, 128, 0), (33, 131, 16), (5, 1, 0)])
+@pytest.mark.parametrize("rows,nb,pad", [(16384, 128, 0), (33, 131, 16), (5, 1, 0), (9, 256, 32),
+                                         (21, 6, 0), (7, 130, 4), (7, 130, 2)])
 def test_q4_0_block_dot_rows(hip, oracle, dev, rows, nb, pad):
     n = nb * 32
     vx = synth.q4_0_matrix(rows, n, 1006, 0.02)

@@ -182,6 +182,128 @@ __global__ __launch_bounds__(64) void block_dot_pairs(size_t nb, float *s, int32
   }
 }
 
+// ---------------------------------------------------------------------------
+// Register-direct row pairs (rows 4-byte aligned, even block count): a wave
+// owns kDdPairs row pairs, one per 16-lane DPP row.  For each pair, lane l
+// loads its block pair 2l, 2l+1 of both rows straight into registers (68 or
+// 36 bytes, dword aligned -- across the wave the loads cover the row chunk
+// contiguously), computes the two blocks' fold operands and writes them to
+// LDS; then DPP row r folds pair r with fold_chain, 8 consecutive blocks per
+// lane, so the four pairs' serial folds run side by side in the same
+// instructions and no LDS access sits on the dependency chain.
+// ---------------------------------------------------------------------------
+constexpr int kDdWaves = 4;
+constexpr int kDdPairs = 4;                           // one per DPP row
+constexpr int kDdLanes = 16;                          // fold lanes per pair
+constexpr int kDdTerms = kChunkBlocks / kDdLanes;     // 8 blocks per fold lane
+constexpr int kDdStride = kChunkBlocks + 8;           // float2 per pair row (padded)
+
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// Blocks 2l, 2l+1 of a Q8_0 row at p (68 bytes, dword aligned): quants as 8
+// aligned dwords each, fp16 scale bits.
+__device__ __forceinline__ void load_q8_pair(const uint8_t *p, uint32_t q0[8], uint32_t q1[8],
+                                             uint32_t &d0, uint32_t &d1) {
+  const uint32_t *g = reinterpret_cast<const uint32_t *>(p);
+  uint32_t r[17];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(g + 4 * k);
+    r[4 * k + 0] = v.x; r[4 * k + 1] = v.y; r[4 * k + 2] = v.z; r[4 * k + 3] = v.w;
+  }
+  r[16] = g[16];
+  d0 = r[0] & 0xffffu;  // block 2l: d at bytes 0-1, quants at 2..33
+  d1 = r[8] >> 16;      // block 2l+1: d at 34-35, quants at 36..67
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    q0[k] = funnel16(r[k], r[k + 1]);
+    q1[k] = r[k + 9];
+  }
+}
+
+// Blocks 2l, 2l+1 of a Q4_0 row at p (36 bytes, dword aligned).
+__device__ __forceinline__ void load_q4_pair(const uint8_t *p, uint32_t q0[4], uint32_t q1[4],
+                                             uint32_t &d0, uint32_t &d1) {
+  const uint32_t *g = reinterpret_cast<const uint32_t *>(p);
+  const u32x4a4 a = *reinterpret_cast<const u32x4a4 *>(g);
+  const u32x4a4 b = *reinterpret_cast<const u32x4a4 *>(g + 4);
+  const uint32_t r[9] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, g[8]};
+  d0 = r[0] & 0xffffu;  // block 2l: d at bytes 0-1, quants at 2..17
+  d1 = r[4] >> 16;      // block 2l+1: d at 18-19, quants at 20..35
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    q0[k] = funnel16(r[k], r[k + 1]);
+    q1[k] = r[k + 5];
+  }
+}
+
+// Fold operands of one block: fmaf(t.x, t.y, sumf) is the reference step.
+template <DotFmt F>
+__device__ __forceinline__ float2 fold_terms(int sumi, uint32_t dx_bits, uint32_t dy_bits) {
+  const float dx = fp16_bits_to_f32(dx_bits), dy = fp16_bits_to_f32(dy_bits);
+  if constexpr (F == DotFmt::kQ8Q8)
+    return make_float2(static_cast<float>(sumi), dx * dy);  // d_x*d_y exact
+  else
+    return make_float2(static_cast<float>(sumi) * dx, dy);
+}
+
+template <DotFmt F>
+__global__ __launch_bounds__(kDdWaves * 64) void block_dot_direct(size_t nb, float *s,
+                                                                   const uint8_t *vx, size_t bx,
+                                                                   const uint8_t *vy, size_t by,
+                                                                   size_t npairs) {
+  constexpr int kXBytes = F == DotFmt::kQ8Q8 ? kQ8Bytes : kQ4Bytes;
+  __shared__ __align__(16) float2 tl[kDdWaves][kDdPairs][kDdStride];
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const size_t p0 = (static_cast<size_t>(blockIdx.x) * kDdWaves + w) * kDdPairs;
+  const int fr = l >> 4, fp = l & (kDdLanes - 1);  // fold row (= pair) and lane in it
+  float sumf = 0.0f;
+
+  for (size_t c0 = 0; c0 < nb; c0 += kChunkBlocks) {
+    const int nbc = static_cast<int>(min(static_cast<size_t>(kChunkBlocks), nb - c0));
+    const int b0 = 2 * l;
+#pragma unroll
+    for (int r = 0; r < kDdPairs; ++r) {
+      const size_t p = min(p0 + r, npairs - 1);  // pairs past npairs: computed, never stored
+      float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);  // absent blocks: fma(0, 0, sumf) == sumf
+      if (b0 < nbc) {  // nbc is even: the pair is whole or absent
+        uint32_t y0[8], y1[8], dy0, dy1;
+        load_q8_pair(vy + p * by + (c0 + b0) * kQ8Bytes, y0, y1, dy0, dy1);
+        int s0, s1;
+        uint32_t dx0, dx1;
+        if constexpr (F == DotFmt::kQ8Q8) {
+          uint32_t x0[8], x1[8];
+          load_q8_pair(vx + p * bx + (c0 + b0) * kXBytes, x0, x1, dx0, dx1);
+          s0 = q8_q8_sumi(x0, y0);
+          s1 = q8_q8_sumi(x1, y1);
+        } else {
+          uint32_t x0[4], x1[4];
+          load_q4_pair(vx + p * bx + (c0 + b0) * kXBytes, x0, x1, dx0, dx1);
+          s0 = q4_q8_sumi(x0, y0);
+          s1 = q4_q8_sumi(x1, y1);
+        }
+        const float2 t0 = fold_terms<F>(s0, dx0, dy0);
+        const float2 t1 = fold_terms<F>(s1, dx1, dy1);
+        t = make_float4(t0.x, t0.y, t1.x, t1.y);
+      }
+      *reinterpret_cast<float4 *>(&tl[w][r][b0]) = t;
+    }
+    __syncthreads();
+    float ta[kDdTerms], tb[kDdTerms];
+#pragma unroll
+    for (int k = 0; k < kDdTerms; k += 2) {
+      const float4 v = *reinterpret_cast<const float4 *>(&tl[w][fr][fp * kDdTerms + k]);
+      ta[k] = v.x; tb[k] = v.y; ta[k + 1] = v.z; tb[k + 1] = v.w;
+    }
+    // the previous chunk's sum sits in the last lane of the fold row: seed lane 0
+    const float carry = __shfl(sumf, (l & ~(kDdLanes - 1)) + kDdLanes - 1);
+    sumf = fold_chain<kDdLanes, kDdTerms>(ta, tb, fp == 0 ? carry : 0.0f);
+    __syncthreads();
+  }
+  if (fp == kDdLanes - 1 && p0 + fr < npairs)
+    s[p0 + fr] = sumf;
+}
+
 }  // namespace tcrv
 
 namespace tcrv_host {
@@ -207,6 +329,15 @@ int launch_pairs(size_t n, float *s, int32_t *sums, const uint8_t *vx, size_t bx
   if (npairs > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
   hipStream_t st = as_stream(stream);
+  const bool direct = !sums && ncols == 0 && nb % 2 == 0 && aligned4(vx) && aligned4(vy) &&
+                      (xrows == 1 || bx % 4 == 0) && (yrows == 1 || by % 4 == 0);
+  if (direct) {
+    constexpr size_t per_group = tcrv::kDdWaves * tcrv::kDdPairs;
+    const size_t groups = (npairs + per_group - 1) / per_group;
+    tcrv::block_dot_direct<F><<<dim3(static_cast<unsigned>(groups)), dim3(tcrv::kDdWaves * 64),
+                                0, st>>>(nb, s, vx, bx, vy, by, npairs);
+    return launch_status();
+  }
   if (sums)
     tcrv::block_dot_pairs<F, true><<<dim3(static_cast<unsigned>(npairs)), dim3(64), 0, st>>>(
         nb, s, sums, vx, bx, vy, by, ncols, bs);

@@ -199,34 +199,6 @@ __device__ __forceinline__ int nibble_dot(const uint32_t q[4], const uint32_t y[
   return acc;
 }
 
-// Serial fold of one row spread over the kLanes lanes of a lane group (a
-// 16-lane DPP row, or half of one): lane p of the group holds the terms t[k]
-// and activation scales dy[k] of kTerms consecutive blocks, p*kTerms + k.
-// Phase ph runs the kTerms fmas of lane ph from the running sum it received,
-// then hands the sum to lane ph+1 with one DPP row shift (v_mov_b32 row_shr:1)
-// and a select; every lane executes every phase, and what the other lanes
-// compute is discarded.  The sum therefore sees the terms in ascending block
-// order, one fmaf each, exactly as a single scalar loop would.  The group's
-// result ends in lane kLanes-1; `sumf` seeds lane 0.
-template <int kLanes, int kTerms>
-__device__ __forceinline__ float fold_chain(const float t[kTerms], const float dy[kTerms],
-                                           float sumf) {
-  const int p = threadIdx.x & (kLanes - 1);
-#pragma unroll
-  for (int ph = 0; ph < kLanes; ++ph) {
-#pragma unroll
-    for (int k = 0; k < kTerms; ++k)
-      sumf = fmaf(t[k], dy[k], sumf);
-    if (ph + 1 < kLanes) {
-      const float moved = __builtin_bit_cast(
-          float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sumf), 0x111 /* row_shr:1 */,
-                                             0xf, 0xf, false));
-      sumf = (p == ph + 1) ? moved : sumf;
-    }
-  }
-  return sumf;
-}
-
 // kOneChunk: nb == kGvChunk exactly (n = 4096), so every lane owns a whole
 // block pair, there is one chunk and no carry between chunks.
 template <int kWaves, int kR, bool kOneChunk>
