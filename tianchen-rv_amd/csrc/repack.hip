@@ -62,8 +62,10 @@ __global__ __launch_bounds__(256) void pack_x16(size_t nblocks, const uint8_t *s
 // high nibbles are positions 16+4pq..) or 8pq..8pq+7 (Q8_0).  It loads one dword
 // per position (4 rows of it), turns the 4x4 bytes row-major with v_perm, and
 // takes v_dot4_i32_i8 against the activation; the four position lanes of a row
-// are summed with two shuffles.  Exact (float)sumi and d_w*d_a per (block, row)
-// go to LDS; 16 lanes then fold each row serially over the chunk.
+// are summed with two shuffles.  All weight loads of a chunk are issued before
+// the first use.  Exact (float)sumi and d_w*d_a per (row, block) go to LDS;
+// then DPP row fr of wave w folds weight row 4w+fr with fold_chain (8
+// consecutive blocks per lane), so no LDS access sits on the serial chain.
 // ---------------------------------------------------------------------------
 constexpr int kRgChunk = 128;   // blocks per LDS chunk
 
@@ -96,84 +98,106 @@ template <bool kQ4>
 __global__ __launch_bounds__(256) void repack_gemv(size_t nb, float *s, const uint8_t *vx,
                                                    const uint8_t *vy) {
   constexpr int kW = kQ4 ? kQ4x16Bytes : kQ8x16Bytes;
+  constexpr int kDw = kQ4 ? 4 : 8;          // quant dwords per lane and block
+  constexpr int kSteps = kRgChunk / 16;     // blocks per lane and chunk
+  constexpr int kFoldLanes = 16, kFoldTerms = kRgChunk / kFoldLanes;
   __shared__ __align__(16) uint8_t act[kRgChunk * kQ8Bytes + 16];
-  __shared__ __align__(16) float2 terms[kRgChunk][16];
+  __shared__ __align__(16) float2 terms[16][kRgChunk + 8];  // [row][block]
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63;
   const int jb = l >> 4, pq = (l >> 2) & 3, rq = l & 3;
+  const int fr = l >> 4, fp = l & (kFoldLanes - 1);  // fold: DPP row fr folds row 4w+fr
   const uint8_t *group = vx + static_cast<size_t>(blockIdx.x) * nb * kW;
-  float acc = 0.0f;  // lanes 0..15 of wave 0: row tid
+  float acc = 0.0f;
 
   for (size_t c0 = 0; c0 < nb; c0 += kRgChunk) {
     const int nbc = static_cast<int>(min(static_cast<size_t>(kRgChunk), nb - c0));
+    uint32_t raw[kSteps][kDw], dsc[kSteps][2];
+#pragma unroll
+    for (int k = 0; k < kSteps; ++k) {
+      const int b = 16 * k + 4 * w + jb;
+      if (b < nbc) {
+        const uint8_t *blk = group + (c0 + b) * kW;
+        const uint32_t *qd = reinterpret_cast<const uint32_t *>(blk + 32);
+#pragma unroll
+        for (int i = 0; i < kDw; ++i)
+          raw[k][i] = qd[4 * (kDw * pq + i) + rq];  // position kDw*pq+i, rows 4rq..4rq+3
+        const uint32_t *dq = reinterpret_cast<const uint32_t *>(blk + 8 * rq);  // d[4rq..4rq+3]
+        dsc[k][0] = dq[0];
+        dsc[k][1] = dq[1];
+      }
+    }
     copy_span_to_lds(act, vy + c0 * kQ8Bytes, nbc * kQ8Bytes, tid, 256);
     __syncthreads();
-    for (int b = 4 * w + jb; b < nbc; b += 16) {
-      const uint8_t *blk = group + (c0 + b) * kW;
-      const uint32_t *qd = reinterpret_cast<const uint32_t *>(blk + 32);
-      int part[4];
-      if constexpr (kQ4) {
-        uint32_t raw[4], rows[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          raw[i] = qd[4 * (4 * pq + i) + rq];  // position 4pq+i, rows 4rq..4rq+3
-        transpose4x4(raw, rows);
-        // activation positions 4pq..4pq+3 (low nibbles) and 16+4pq.. (high)
-        const uint32_t alo = act_dword(act, b, pq);
-        const uint32_t ahi = act_dword(act, b, pq + 4);
+    for (int k = 0; k < kSteps; ++k) {
+      const int b = 16 * k + 4 * w + jb;
+      if (b < nbc) {
+        int part[4];
+        if constexpr (kQ4) {
+          uint32_t rows[4];
+          transpose4x4(raw[k], rows);
+          // activation positions 4pq..4pq+3 (low nibbles) and 16+4pq.. (high)
+          const uint32_t alo = act_dword(act, b, pq);
+          const uint32_t ahi = act_dword(act, b, pq + 4);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            // byte = (n_lo ^ 8) | (n_hi ^ 8) << 4; as a signed byte, the nibble
+            // moved to the high half is 16 * sext4(n ^ 8) = 16 * (n - 8)
+            const uint32_t lo16 = (rows[r] << 4) & 0xF0F0F0F0u;
+            const uint32_t hi16 = rows[r] & 0xF0F0F0F0u;
+            part[r] = sdot4(hi16, ahi, sdot4(lo16, alo, 0));
+          }
+        } else {
+          uint32_t rows[8];
+          transpose4x4(raw[k], rows);
+          transpose4x4(raw[k] + 4, rows + 4);
+          const uint32_t a0 = act_dword(act, b, 2 * pq);
+          const uint32_t a1 = act_dword(act, b, 2 * pq + 1);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            part[r] = sdot4(rows[4 + r], a1, sdot4(rows[r], a0, 0));
+        }
+        // sum over the four position lanes (lane bits 2..3)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          // byte = (n_lo ^ 8) | (n_hi ^ 8) << 4; as a signed byte, the nibble
-          // moved to the high half is 16 * sext4(n ^ 8) = 16 * (n - 8)
-          const uint32_t lo16 = (rows[r] << 4) & 0xF0F0F0F0u;
-          const uint32_t hi16 = rows[r] & 0xF0F0F0F0u;
-          part[r] = sdot4(hi16, ahi, sdot4(lo16, alo, 0));
+          part[r] += __shfl_xor(part[r], 4);
+          part[r] += __shfl_xor(part[r], 8);
         }
-      } else {
-        uint32_t raw[8], rows[8];
+        if (pq == 0) {
+          const float da =
+              fp16_bits_to_f32(*reinterpret_cast<const uint16_t *>(act + b * kQ8Bytes));
+          const uint32_t dw[4] = {dsc[k][0] & 0xffffu, dsc[k][0] >> 16, dsc[k][1] & 0xffffu,
+                                  dsc[k][1] >> 16};
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          raw[i] = qd[4 * (8 * pq + i) + rq];
-        transpose4x4(raw, rows);
-        transpose4x4(raw + 4, rows + 4);
-        const uint32_t a0 = act_dword(act, b, 2 * pq);
-        const uint32_t a1 = act_dword(act, b, 2 * pq + 1);
+          for (int r = 0; r < 4; ++r) {
+            const int sumi = kQ4 ? (part[r] >> 4) : part[r];  // Q4_0: exact division by 16
+            terms[4 * rq + r][b] =
+                make_float2(static_cast<float>(sumi), fp16_bits_to_f32(dw[r]) * da);
+          }
+        }
+      } else if (pq == 0 && b < kRgChunk) {
+        // blocks past the chunk: fma(0, 0, acc) == acc (acc is never -0)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          part[r] = sdot4(rows[4 + r], a1, sdot4(rows[r], a0, 0));
-      }
-      // sum over the four position lanes (lane bits 2..3)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        part[r] += __shfl_xor(part[r], 4);
-        part[r] += __shfl_xor(part[r], 8);
-      }
-      if (pq == 0) {
-        const float da =
-            fp16_bits_to_f32(*reinterpret_cast<const uint16_t *>(act + b * kQ8Bytes));
-        const uint32_t *dq = reinterpret_cast<const uint32_t *>(blk + 8 * rq);  // d[4rq..4rq+3]
-        const uint32_t d01 = dq[0], d23 = dq[1];
-        const uint32_t dw[4] = {d01 & 0xffffu, d01 >> 16, d23 & 0xffffu, d23 >> 16};
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int sumi = kQ4 ? (part[r] >> 4) : part[r];  // Q4_0: exact division by 16
-          terms[b][4 * rq + r] = make_float2(static_cast<float>(sumi), fp16_bits_to_f32(dw[r]) * da);
-        }
+          terms[4 * rq + r][b] = make_float2(0.0f, 0.0f);
       }
     }
     __syncthreads();
-    if (tid < 16) {
-#pragma unroll 8
-      for (int b = 0; b < nbc; ++b) {
-        const float2 t = terms[b][tid];
-        acc = fmaf(t.x, t.y, acc);
-      }
+    float ta[kFoldTerms], tb[kFoldTerms];
+#pragma unroll
+    for (int k = 0; k < kFoldTerms; k += 2) {
+      const float4 v = *reinterpret_cast<const float4 *>(&terms[4 * w + fr][fp * kFoldTerms + k]);
+      ta[k] = v.x; tb[k] = v.y; ta[k + 1] = v.z; tb[k + 1] = v.w;
     }
+    // the previous chunk's sum sits in the last lane of the fold row: seed lane 0
+    const float carry = __shfl(acc, (l & ~(kFoldLanes - 1)) + kFoldLanes - 1);
+    acc = fold_chain<kFoldLanes, kFoldTerms>(ta, tb, fp == 0 ? carry : 0.0f);
     __syncthreads();
   }
-  if (tid < 16)
-    s[static_cast<size_t>(blockIdx.x) * 16 + tid] = acc;
+  if (fp == kFoldLanes - 1)
+    s[static_cast<size_t>(blockIdx.x) * 16 + 4 * w + fr] = acc;
 }
 
 }  // namespace tcrv
