@@ -175,7 +175,8 @@ TCRV_HIP_API int tcrv_hip_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx, 
  * Same ABI as the q4_0 GEMM above; elements are the a5 block dot:
  * s[ir*bs + col] = q8_0 block_dot(vx + ir*bx, vy + col*by).
  * Runs on v_mfma_i32_32x32x32_i8 with one MFMA per 32-element block and the
- * per-block fp32 fold in ascending block order.
+ * per-block fp32 fold in ascending block order; nc = 1 (decode) runs as a
+ * bandwidth-bound GEMV instead (same results).
  * bx, by >= the row bytes when nr, nc > 1; bs >= nc when nr > 1. */
 TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
                             size_t by, size_t nr, size_t nc, size_t bx, size_t bs,

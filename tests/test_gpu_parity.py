@@ -219,7 +219,10 @@ def test_q4_0_gemm_multi_column(hip, oracle, dev, nr, nc, nb):
     (128, 128, 8, 0, 0),      # one tile, one K chunk
     (256, 128, 128, 0, 0),    # full K, two tiles
     (100, 70, 9, 16, 32),     # partial tiles, partial K chunk, padded strides
-    (33, 1, 3, 0, 0),         # single column (decode-shaped)
+    (33, 1, 3, 0, 0),         # single column (decode-shaped), odd nb: the MFMA path
+    (4096, 1, 128, 0, 0),     # decode: the register-direct GEMV
+    (77, 1, 6, 4, 0),         # decode, padded rows, output stride bs = 6
+    (1, 1, 2, 0, 0),          # one output
     (1, 45, 1, 0, 0),         # single weight row, one block
     (512, 512, 128, 0, 0),
 ])

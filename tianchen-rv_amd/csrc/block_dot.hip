@@ -247,8 +247,10 @@ __device__ __forceinline__ float2 fold_terms(int sumi, uint32_t dx_bits, uint32_
     return make_float2(static_cast<float>(sumi) * dx, dy);
 }
 
+// Output of pair p: s[p * os].  by = 0 pairs every x row with one y row (the
+// GEMM's nc = 1 decode shape).
 template <DotFmt F>
-__global__ __launch_bounds__(kDdWaves * 64) void block_dot_direct(size_t nb, float *s,
+__global__ __launch_bounds__(kDdWaves * 64) void block_dot_direct(size_t nb, float *s, size_t os,
                                                                    const uint8_t *vx, size_t bx,
                                                                    const uint8_t *vy, size_t by,
                                                                    size_t npairs) {
@@ -301,7 +303,7 @@ __global__ __launch_bounds__(kDdWaves * 64) void block_dot_direct(size_t nb, flo
     __syncthreads();
   }
   if (fp == kDdLanes - 1 && p0 + fr < npairs)
-    s[p0 + fr] = sumf;
+    s[(p0 + fr) * os] = sumf;
 }
 
 }  // namespace tcrv
@@ -335,7 +337,7 @@ int launch_pairs(size_t n, float *s, int32_t *sums, const uint8_t *vx, size_t bx
     constexpr size_t per_group = tcrv::kDdWaves * tcrv::kDdPairs;
     const size_t groups = (npairs + per_group - 1) / per_group;
     tcrv::block_dot_direct<F><<<dim3(static_cast<unsigned>(groups)), dim3(tcrv::kDdWaves * 64),
-                                0, st>>>(nb, s, vx, bx, vy, by, npairs);
+                                0, st>>>(nb, s, 1, vx, bx, vy, by, npairs);
     return launch_status();
   }
   if (sums)
@@ -375,6 +377,20 @@ int zero_outputs(float *s, size_t count, size_t stride, size_t ncols, void *stre
     return TCRV_HIP_ERR_TOO_LARGE;
   store_zeros<<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, as_stream(stream)>>>(
       s, count, stride, ncols);
+  return launch_status();
+}
+
+int q8_0_gemv_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
+                     const uint8_t *vy, size_t nr, void *stream) {
+  if (nb % 2 != 0 || !aligned4(vx) || !aligned4(vy) || (nr > 1 && bx % 4 != 0))
+    return TCRV_HIP_ERR_UNSUPPORTED;
+  constexpr size_t per_group = tcrv::kDdWaves * tcrv::kDdPairs;
+  const size_t groups = (nr + per_group - 1) / per_group;
+  if (groups > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  tcrv::block_dot_direct<DotFmt::kQ8Q8><<<dim3(static_cast<unsigned>(groups)),
+                                          dim3(tcrv::kDdWaves * 64), 0, as_stream(stream)>>>(
+      nb, s, os, vx, bx, vy, 0, nr);
   return launch_status();
 }
 

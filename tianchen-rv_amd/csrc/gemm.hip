@@ -521,6 +521,11 @@ extern "C" int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx,
   const size_t rowbytes = nb * tcrv::kQ8Bytes;
   if ((nr > 1 && bx < rowbytes) || (nc > 1 && by < rowbytes))
     return TCRV_HIP_ERR_BAD_SIZE;
+  if (nc == 1) {  // decode: a bandwidth-bound GEMV, not an MFMA tile
+    const int st = q8_0_gemv_direct(nb, s, nr > 1 ? bs : 0, vx, bx, vy, nr, stream);
+    if (st != TCRV_HIP_ERR_UNSUPPORTED)
+      return st;
+  }
   if (aligned4(vx) && aligned4(vy) && (nr == 1 || bx % 4 == 0) && (nc == 1 || by % 4 == 0)) {
     const size_t tiles =
         ((nr + tcrv::kFbBM - 1) / tcrv::kFbBM) * ((nc + tcrv::kFbBN - 1) / tcrv::kFbBN);

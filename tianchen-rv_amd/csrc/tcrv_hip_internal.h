@@ -154,6 +154,12 @@ int zero_outputs(float *s, size_t count, size_t stride, size_t ncols, void *stre
 int q4_0_gemm_mfma(size_t nb, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy,
                    size_t by, size_t nr, size_t nc, size_t bs, void *stream);
 
+// Q8_0 x Q8_0 GEMM with nc = 1 (decode): one weight row per pair against the
+// single activation row, s[ir * os] (block_dot.hip); TCRV_HIP_ERR_UNSUPPORTED
+// for an odd block count or rows that are not 4-byte aligned.
+int q8_0_gemv_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
+                     const uint8_t *vy, size_t nr, void *stream);
+
 // Q4_0 x Q8_0 GEMM for nc > 1 as one wave per output element (block_dot.hip).
 int q4_0_grid(size_t n, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by,
               size_t nr, size_t nc, size_t bs, void *stream);
