@@ -1,0 +1,256 @@
+// tcrv_hip_route.cpp -- the host-side HIP provider of TianChen-RV's
+// contraction path: typed facts -> gfx950 algorithm, and op identity -> the
+// libtcrv_hip entry point with its runtime-ABI parameters.  Host C++ only;
+// every launch goes through the C-ABI of libtcrv_hip.
+#include "tcrv_hip_route.h"
+
+#include <cstring>
+#include <iterator>
+
+namespace tianchenrv::plugin::hip {
+namespace {
+
+// Fact 1: libtcrv_hip has a gfx950 kernel for this weight block format.  The
+// K-quants have none (out of this path's scope), so the request is declined
+// and stays on the caller's existing route.
+bool hipKernelExists(QuantType weight) {
+  switch (weight) {
+  case QuantType::Q4_0:
+  case QuantType::Q8_0:
+    return true;
+  case QuantType::Q4_K:
+    return false;
+  }
+  return false;
+}
+
+// Fact 2: the weights already sit in the x16 interleave.  On gfx950 the
+// interleave only has a decode consumer (the repacked GEMV); a prefill over
+// x16 weights has no kernel here (the reference's repack GEMM is not built),
+// so it is declined rather than silently unpacked.
+bool weightsAreX16(WeightLayout layout) { return layout == WeightLayout::BlockX16; }
+
+// Fact 3: decode is one activation row: the weight stream is read once and
+// the work is HBM-bound, so it runs as a GEMV; prefill is a dense contraction
+// and runs on the int8 matrix cores.
+bool isDecode(MRegime m) { return m == MRegime::Decode; }
+
+const char *gemmEntry(QuantType weight) {
+  return weight == QuantType::Q4_0 ? "tcrv_hip_q4_0_q8_0_gemm" : "tcrv_hip_q8_0_q8_0_gemm";
+}
+
+const char *repackEntry(QuantType weight) {
+  return weight == QuantType::Q4_0 ? "tcrv_hip_repack_gemv_q4_0_q8_0"
+                                   : "tcrv_hip_repack_gemv_q8_0_q8_0";
+}
+
+}  // namespace
+
+HipContractionSelection selectHipContractionAlgorithm(QuantType weight, MRegime mRegime,
+                                                      WeightLayout layout) {
+  if (!hipKernelExists(weight))
+    return {HipContractionAlgorithm::Decline, "hip-decline-no-gfx950-kernel-for-quant", nullptr};
+  if (weightsAreX16(layout)) {
+    if (isDecode(mRegime))
+      return {HipContractionAlgorithm::RepackGemv, weight == QuantType::Q4_0
+                                                       ? "hip-repack-gemv-q4_0x16-decode"
+                                                       : "hip-repack-gemv-q8_0x16-decode",
+              repackEntry(weight)};
+    return {HipContractionAlgorithm::Decline,
+            weight == QuantType::Q4_0 ? "hip-decline-q4_0x16-prefill-no-repack-gemm"
+                                      : "hip-decline-q8_0x16-prefill-no-repack-gemm",
+            nullptr};
+  }
+  if (isDecode(mRegime))
+    return {HipContractionAlgorithm::DecodeGemv,
+            weight == QuantType::Q4_0 ? "hip-decode-gemv-q4_0-hbm-bound"
+                                      : "hip-decode-gemv-q8_0-hbm-bound",
+            gemmEntry(weight)};
+  return {HipContractionAlgorithm::MfmaGemm,
+          weight == QuantType::Q4_0 ? "hip-prefill-mfma-i8-gemm-q4_0-decoded-at-staging"
+                                    : "hip-prefill-mfma-i8-gemm-q8_0",
+          gemmEntry(weight)};
+}
+
+MRegime deriveMRegime(size_t nc) { return nc <= 1 ? MRegime::Decode : MRegime::Prefill; }
+
+namespace {
+
+struct AbiParam {
+  const char *cName;
+  const char *cType;
+  const char *role;
+};
+
+struct HipKernelRoute {
+  const char *op;
+  const char *entry;
+  AbiParam params[9];
+  size_t nparams;
+};
+
+// Parameter names, C types and roles as the reference's fixtures declare them
+// (test/Conversion/RVV/...):
+//   add:            rvv-to-emitc-add-cpp-golden.mlir (i32 there; f32 entry here)
+//   q8_0 block dot: rvv-to-emitc-q8-0-q8-0-block-dot.mlir:16-19
+//   q4_0 block dot: rvv-to-emitc-q4-0-q8-0-block-dot.mlir:24-31
+//   q4_0 gemm:      rvv-to-emitc-q4-0-q8-0-gemm.mlir:23-31
+//   repack gemvs:   rvv-to-emitc-repack-gemv-q4-0-q8-0.mlir:26-30,
+//                   rvv-to-emitc-repack-gemv-q8-0-q8-0-vlen256.mlir
+//   pack:           rvv-to-emitc-pack-q4-0-to-q4-0x16.mlir:19-21
+//   quantize:       rvv-to-emitc-ggml-quantize-row-q8-0.mlir
+// The Q8_0 GEMM has no reference op; it takes the q4_0 GEMM's ABI with Q8_0
+// weights.  A row is found by its exact op identity: the op name, and for
+// tcrv_rvv.binary also its kind and element type (".add.f32").
+constexpr const char *kN = "runtime-element-count";
+constexpr const char *kOut = "output-buffer";
+constexpr const char *kLhs = "lhs-input-buffer";
+constexpr const char *kRhs = "rhs-input-buffer";
+
+const HipKernelRoute kHipKernelRoutes[] = {
+    {"tcrv_rvv.binary.add.f32", "tcrv_hip_add_f32",
+     {{"lhs", "const float *", kLhs}, {"rhs", "const float *", kRhs}, {"out", "float *", kOut},
+      {"n", "size_t", kN}},
+     4},
+    {"tcrv_rvv.binary.add.i32", "tcrv_hip_add_i32",
+     {{"lhs", "const int32_t *", kLhs}, {"rhs", "const int32_t *", kRhs},
+      {"out", "int32_t *", kOut}, {"n", "size_t", kN}},
+     4},
+    {"tcrv_rvv.q4_0_q8_0_block_dot", "tcrv_hip_q4_0_q8_0_block_dot",
+     {{"n", "size_t", kN}, {"s", "float *", kOut}, {"bs", "size_t", "output-stride"},
+      {"vx", "const uint8_t *", kLhs}, {"bx", "size_t", "lhs-input-stride"},
+      {"vy", "const uint8_t *", kRhs}, {"by", "size_t", "rhs-input-stride"},
+      {"nrc", "int32_t", "rhs-scalar-value"}},
+     8},
+    {"tcrv_rvv.q4_0_q8_0_gemm", "tcrv_hip_q4_0_q8_0_gemm",
+     {{"n", "size_t", kN}, {"s", "float *", kOut}, {"vx", "const uint8_t *", kLhs},
+      {"vy", "const uint8_t *", kRhs}, {"by", "size_t", "rhs-input-stride"},
+      {"nr", "size_t", "source-byte-stride"}, {"nc", "size_t", "destination-byte-stride"},
+      {"bx", "size_t", "lhs-input-stride"}, {"bs", "size_t", "output-stride"}},
+     9},
+    {"tcrv_rvv.repack_gemv_q4_0_q8_0", "tcrv_hip_repack_gemv_q4_0_q8_0",
+     {{"n", "size_t", kN}, {"s", "float *", kOut}, {"vx", "const uint8_t *", kLhs},
+      {"vy", "const uint8_t *", kRhs}, {"nc", "size_t", "destination-byte-stride"}},
+     5},
+    {"tcrv_rvv.pack_q4_0_to_q4_0x16", "tcrv_hip_pack_q4_0_to_q4_0x16",
+     {{"nblocks", "size_t", kN}, {"src", "const uint8_t *", kLhs}, {"dst", "uint8_t *", kOut}},
+     3},
+    {"tcrv_rvv.repack_gemv_q8_0_q8_0", "tcrv_hip_repack_gemv_q8_0_q8_0",
+     {{"n", "size_t", kN}, {"s", "float *", kOut}, {"vx", "const uint8_t *", kLhs},
+      {"vy", "const uint8_t *", kRhs}, {"nc", "size_t", "destination-byte-stride"}},
+     5},
+    {"tcrv_rvv.q8_0_q8_0_block_dot", "tcrv_hip_q8_0_q8_0_block_dot",
+     {{"n", "size_t", kN}, {"s", "float *", kOut}, {"vx", "const uint8_t *", kLhs},
+      {"vy", "const uint8_t *", kRhs}},
+     4},
+    {"tcrv_rvv.q8_0_q8_0_gemm", "tcrv_hip_q8_0_q8_0_gemm",
+     {{"n", "size_t", kN}, {"s", "float *", kOut}, {"vx", "const uint8_t *", kLhs},
+      {"vy", "const uint8_t *", kRhs}, {"by", "size_t", "rhs-input-stride"},
+      {"nr", "size_t", "source-byte-stride"}, {"nc", "size_t", "destination-byte-stride"},
+      {"bx", "size_t", "lhs-input-stride"}, {"bs", "size_t", "output-stride"}},
+     9},
+    {"tcrv_rvv.quantize_row_q8_0", "tcrv_hip_quantize_row_q8_0",
+     {{"n", "size_t", kN}, {"x", "const float *", kLhs}, {"vy", "uint8_t *", kOut}},
+     3},
+};
+constexpr size_t kNumRoutes = std::size(kHipKernelRoutes);
+
+bool validFacts(int quant, int regime, int layout) {
+  return quant >= TCRV_HIP_QUANT_Q4_0 && quant <= TCRV_HIP_QUANT_Q4_K &&
+         (regime == TCRV_HIP_M_DECODE || regime == TCRV_HIP_M_PREFILL) &&
+         (layout == TCRV_HIP_LAYOUT_PLAIN || layout == TCRV_HIP_LAYOUT_X16);
+}
+
+}  // namespace
+}  // namespace tianchenrv::plugin::hip
+
+using namespace tianchenrv::plugin::hip;
+
+extern "C" {
+
+int tcrv_hip_route_select(int weight_quant, int m_regime, int weight_layout, int *algorithm,
+                          const char **reason, const char **entry) {
+  if (!validFacts(weight_quant, m_regime, weight_layout))
+    return TCRV_HIP_ERR_BAD_SIZE;
+  const HipContractionSelection sel = selectHipContractionAlgorithm(
+      static_cast<QuantType>(weight_quant), static_cast<MRegime>(m_regime),
+      static_cast<WeightLayout>(weight_layout));
+  if (algorithm)
+    *algorithm = static_cast<int>(sel.algorithm);
+  if (reason)
+    *reason = sel.reason;
+  if (entry)
+    *entry = sel.entry;
+  return TCRV_HIP_OK;
+}
+
+int tcrv_hip_route_m_regime(size_t nc) { return static_cast<int>(deriveMRegime(nc)); }
+
+int tcrv_hip_route_contraction(int weight_quant, int weight_layout, size_t n, float *s,
+                               const uint8_t *vx, const uint8_t *vy, size_t by, size_t nr,
+                               size_t nc, size_t bx, size_t bs, void *stream, int *algorithm) {
+  const int regime = static_cast<int>(deriveMRegime(nc));
+  if (!validFacts(weight_quant, regime, weight_layout))
+    return TCRV_HIP_ERR_BAD_SIZE;
+  const HipContractionSelection sel = selectHipContractionAlgorithm(
+      static_cast<QuantType>(weight_quant), static_cast<MRegime>(regime),
+      static_cast<WeightLayout>(weight_layout));
+  if (algorithm)
+    *algorithm = static_cast<int>(sel.algorithm);
+  const bool q4 = weight_quant == TCRV_HIP_QUANT_Q4_0;
+  switch (sel.algorithm) {
+  case HipContractionAlgorithm::Decline:
+    return TCRV_HIP_ERR_UNSUPPORTED;
+  case HipContractionAlgorithm::RepackGemv:
+    if (nr == 0 || nc == 0)
+      return TCRV_HIP_OK;
+    if (nr % 16 != 0 || (nr > 1 && bs != 1))
+      return TCRV_HIP_ERR_UNSUPPORTED;
+    return q4 ? tcrv_hip_repack_gemv_q4_0_q8_0(n, s, vx, vy, nr, stream)
+              : tcrv_hip_repack_gemv_q8_0_q8_0(n, s, vx, vy, nr, stream);
+  case HipContractionAlgorithm::DecodeGemv:
+  case HipContractionAlgorithm::MfmaGemm:
+    return q4 ? tcrv_hip_q4_0_q8_0_gemm(n, s, vx, vy, by, nr, nc, bx, bs, stream)
+              : tcrv_hip_q8_0_q8_0_gemm(n, s, vx, vy, by, nr, nc, bx, bs, stream);
+  }
+  return TCRV_HIP_ERR_UNSUPPORTED;
+}
+
+size_t tcrv_hip_route_count(void) { return kNumRoutes; }
+
+const char *tcrv_hip_route_op(size_t row) {
+  return row < kNumRoutes ? kHipKernelRoutes[row].op : nullptr;
+}
+
+const char *tcrv_hip_route_entry(size_t row) {
+  return row < kNumRoutes ? kHipKernelRoutes[row].entry : nullptr;
+}
+
+size_t tcrv_hip_route_param_count(size_t row) {
+  return row < kNumRoutes ? kHipKernelRoutes[row].nparams : 0;
+}
+
+int tcrv_hip_route_param(size_t row, size_t param, const char **c_name, const char **c_type,
+                         const char **role) {
+  if (row >= kNumRoutes || param >= kHipKernelRoutes[row].nparams)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  const AbiParam &p = kHipKernelRoutes[row].params[param];
+  if (c_name)
+    *c_name = p.cName;
+  if (c_type)
+    *c_type = p.cType;
+  if (role)
+    *role = p.role;
+  return TCRV_HIP_OK;
+}
+
+long tcrv_hip_route_find(const char *op) {
+  if (!op)
+    return -1;
+  for (size_t i = 0; i < kNumRoutes; ++i)
+    if (std::strcmp(kHipKernelRoutes[i].op, op) == 0)
+      return static_cast<long>(i);
+  return -1;
+}
+
+}  // extern "C"

@@ -240,3 +240,92 @@ def repack_gemv_q8_0_q8_0(n: int, s, vx, vy, nc: int, stream=None):
 
 def synchronize(stream=None):
     return call("tcrv_hip_stream_synchronize", _stream(stream))
+
+
+# ---------------------------------------------------------------------------
+# libtcrv_hip_route.so: the host-side provider (include/tcrv_hip_route.h).
+# ---------------------------------------------------------------------------
+ROUTE_LIB_PATH = os.path.join(HERE, "libtcrv_hip_route.so")
+
+QUANT = {"q4_0": 0, "q8_0": 1, "q4_K": 2}
+M_DECODE, M_PREFILL = 0, 1
+LAYOUT = {"plain": 0, "x16": 1}
+ALGO = {0: "decline", 1: "decode_gemv", 2: "repack_gemv", 3: "mfma_gemm"}
+
+_cs = ctypes.c_char_p
+ROUTE_SIGNATURES = {
+    "tcrv_hip_route_select": ([_int, _int, _int, ctypes.POINTER(_int), ctypes.POINTER(_cs),
+                               ctypes.POINTER(_cs)], _int),
+    "tcrv_hip_route_m_regime": ([_sz], _int),
+    "tcrv_hip_route_contraction": ([_int, _int, _sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p,
+                                    ctypes.POINTER(_int)], _int),
+    "tcrv_hip_route_count": ([], _sz),
+    "tcrv_hip_route_op": ([_sz], _cs),
+    "tcrv_hip_route_entry": ([_sz], _cs),
+    "tcrv_hip_route_param_count": ([_sz], _sz),
+    "tcrv_hip_route_param": ([_sz, _sz, ctypes.POINTER(_cs), ctypes.POINTER(_cs),
+                              ctypes.POINTER(_cs)], _int),
+    "tcrv_hip_route_find": ([_cs], ctypes.c_long),
+}
+
+_route: Optional[ctypes.CDLL] = None
+
+
+def load_route(path: str = ROUTE_LIB_PATH) -> ctypes.CDLL:
+    """Loads the route provider (after libtcrv_hip itself, so both share one
+    HIP runtime); raises TcrvHipError if it is not built."""
+    global _route
+    if _route is not None:
+        return _route
+    load()
+    if not os.path.exists(path):
+        raise TcrvHipError(ERR_UNSUPPORTED, f"libtcrv_hip_route.so not found at {path}: run "
+                           "__graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    for name, (argtypes, restype) in ROUTE_SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
+    _route = lib
+    return lib
+
+
+def route_select(quant: str, m_regime: int, layout: str):
+    """(algorithm name, audit token, entry symbol or None) for typed facts."""
+    lib = load_route()
+    algo, reason, entry = _int(), _cs(), _cs()
+    st = lib.tcrv_hip_route_select(QUANT[quant], m_regime, LAYOUT[layout], ctypes.byref(algo),
+                                   ctypes.byref(reason), ctypes.byref(entry))
+    _check("tcrv_hip_route_select", st)
+    return ALGO[algo.value], reason.value.decode(), entry.value.decode() if entry.value else None
+
+
+def route_table():
+    """The op-identity route table: [{op, entry, params: [(c_name, c_type, role)]}]."""
+    lib = load_route()
+    rows = []
+    for i in range(lib.tcrv_hip_route_count()):
+        params = []
+        for j in range(lib.tcrv_hip_route_param_count(i)):
+            c_name, c_type, role = _cs(), _cs(), _cs()
+            _check("tcrv_hip_route_param", lib.tcrv_hip_route_param(
+                i, j, ctypes.byref(c_name), ctypes.byref(c_type), ctypes.byref(role)))
+            params.append((c_name.value.decode(), c_type.value.decode(), role.value.decode()))
+        rows.append({"op": lib.tcrv_hip_route_op(i).decode(),
+                     "entry": lib.tcrv_hip_route_entry(i).decode(), "params": params})
+    return rows
+
+
+def route_contraction(quant: str, layout: str, n: int, s, vx, vy, by: int, nr: int, nc: int,
+                      bx: int, bs: int, stream=None, check: bool = True):
+    """Runs a contraction (reference GEMM ABI) on the routed kernel; returns
+    (status, algorithm name)."""
+    lib = load_route()
+    algo = _int(-1)
+    st = lib.tcrv_hip_route_contraction(QUANT[quant], LAYOUT[layout], n, _ptr(s), _ptr(vx),
+                                        _ptr(vy), by, nr, nc, bx, bs,
+                                        _stream(stream) if stream != 0 else 0,
+                                        ctypes.byref(algo))
+    if check:
+        _check("tcrv_hip_route_contraction", st)
+    return st, ALGO.get(algo.value)
