@@ -206,7 +206,10 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
     size_t nb_arg, float *s, size_t os, const uint8_t *vx, size_t bx, const uint8_t *vy,
     size_t nr) {
   const size_t nb = kOneChunk ? static_cast<size_t>(kGvChunk) : nb_arg;
-  constexpr int kLanes = 64 / kR;              // fold lanes per row
+  // fold lanes per row: a whole DPP row (16 lanes) for up to 4 rows per wave,
+  // half of one for 8; with fewer than 4 rows the spare DPP rows fold copies
+  // of the last row, which are never stored
+  constexpr int kLanes = kR >= 4 ? 64 / kR : 16;
   constexpr int kTerms = kGvChunk / kLanes;    // blocks per fold lane
   static_assert(kLanes == 8 || kLanes == 16, "fold groups live inside one DPP row");
   __shared__ __align__(16) float tl[kWaves][kR][kGvChunk + 4];
@@ -216,7 +219,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
   const int w = tid >> 6;
   const int l = tid & 63;
   const size_t row0 = (static_cast<size_t>(blockIdx.x) * kWaves + w) * kR;
-  const int fr = l / kLanes;          // row of this lane in the fold
+  const int fr = min(l / kLanes, kR - 1);  // row of this lane in the fold
   const int fp = l & (kLanes - 1);    // position of this lane in its row's chain
   float sumf = 0.0f;
 
@@ -277,7 +280,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
       __syncthreads();
     }
   }
-  if (fp == kLanes - 1 && row0 + fr < nr)
+  if (fp == kLanes - 1 && l / kLanes < kR && row0 + fr < nr)
     s[(row0 + fr) * os] = sumf;
 }
 
