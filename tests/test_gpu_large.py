@@ -1,0 +1,104 @@
+"""GPU parity at the sizes where 32-bit indexing would break: more than 2^32
+elements (add, dequant), more than 2^31 bytes in one operand (block dot rows,
+GEMV).  Outputs are checked on sampled indices -- every sample against numpy or
+the CPU oracle on the same bytes -- including the last elements, where an
+index that wrapped would land."""
+import numpy as np
+import pytest
+import torch
+
+import synth
+from gpu_util import assert_f32_parity
+
+pytestmark = pytest.mark.gpu
+
+BIG = (1 << 32) + 1031  # elements: past 2^32, and ragged for the 16-element vector path
+
+
+def free():
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def sample_indices(n, k=4096, seed=0):
+    rng = np.random.default_rng(seed)
+    edges = np.concatenate([np.arange(64), np.arange(n - 2048, n),
+                            (1 << 31) + np.arange(-8, 8), (1 << 32) + np.arange(-8, 8)])
+    edges = edges[(edges >= 0) & (edges < n)]
+    return np.unique(np.concatenate([edges, rng.integers(0, n, k)]))
+
+
+def test_add_f32_beyond_2_pow_32(hip, dev):
+    a = torch.rand(BIG, dtype=torch.float32, device=dev) * 2 - 1
+    b = torch.rand(BIG, dtype=torch.float32, device=dev) * 2 - 1
+    out = torch.empty(BIG, dtype=torch.float32, device=dev)
+    hip.add_f32(a, b, out, BIG)
+    idx = torch.from_numpy(sample_indices(BIG)).to(dev)
+    av, bv, ov = (t[idx].cpu().numpy() for t in (a, b, out))
+    del a, b, out
+    free()
+    assert np.array_equal(ov.view(np.uint32), (av + bv).view(np.uint32))
+
+
+def test_dequantize_beyond_2_pow_32(hip, dev):
+    nb = BIG // 32 + 1  # 134217761 blocks: 4.56 GB in, 17.2 GB out
+    n = nb * 32
+    vx = torch.randint(0, 256, (nb, 34), dtype=torch.uint8, device=dev)
+    # finite, varied fp16 scales: exponent field 1..30, any mantissa and sign
+    sc = torch.randint(0, 1 << 16, (nb,), dtype=torch.int32, device=dev)
+    exp = (torch.remainder(sc >> 10, 30) + 1) << 10
+    half = ((sc & 0x83FF) | exp).to(torch.int32)
+    vx[:, 0] = (half & 0xFF).to(torch.uint8)
+    vx[:, 1] = ((half >> 8) & 0xFF).to(torch.uint8)
+    y = torch.empty(n, dtype=torch.float32, device=dev)
+    hip.dequantize_row_q8_0(vx, y, n)
+    blocks = np.unique(np.concatenate([sample_indices(nb, 2048, 1), [nb - 1]]))
+    bi = torch.from_numpy(blocks).to(dev)
+    raw = vx[bi].cpu().numpy()
+    got = y.view(nb, 32)[bi].cpu().numpy()
+    del vx, y, sc, exp, half
+    free()
+    d = raw[:, :2].copy().view(np.float16).astype(np.float32)
+    want = raw[:, 2:].view(np.int8).astype(np.float32) * d
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_q8_0_block_dot_rows_operands_over_2_gib(hip, oracle, dev):
+    rows, nb = 520000, 128  # 2.26 GB per operand
+    n = nb * 32
+    rb = nb * 34
+    base_x = synth.q8_0_matrix(64, n, 1004, 1.0)
+    base_y = synth.q8_0_matrix(64, n, 1005, 1.0)
+    # rows repeat a 64-row pattern shifted by the row index, so each sampled
+    # row's bytes are known on the host
+    dx = torch.from_numpy(base_x).to(dev)
+    dy = torch.from_numpy(base_y).to(dev)
+    vx = dx.repeat(rows // 64 + 1, 1)[:rows].contiguous()
+    vy = dy.roll(7, 0).repeat(rows // 64 + 1, 1)[:rows].contiguous()
+    s = torch.empty(rows, dtype=torch.float32, device=dev)
+    hip.q8_0_q8_0_block_dot_rows(n, s, vx, rb, vy, rb, rows)
+    got = s.cpu().numpy()
+    del vx, vy, s
+    free()
+    pick = np.unique(np.concatenate([sample_indices(rows, 256, 2), [rows - 1]]))
+    bx = base_x[pick % 64]
+    by = np.roll(base_y, 7, 0)[pick % 64]
+    want = oracle.vec_dot_q8_0_rows(n, bx, rb, by, rb, len(pick), 8)
+    assert_f32_parity(got[pick], want, what="q8 rows over 2 GiB")
+
+
+def test_gemv_weights_over_2_gib(hip, oracle, dev):
+    nr, nb = 1000000, 128  # Q4_0 weights: 2.3 GB
+    n = nb * 32
+    rb = nb * 18
+    base = synth.q4_0_matrix(96, n, 1006, 0.02)
+    x = synth.q8_0_matrix(1, n, 1007, 1.0).reshape(-1)
+    w = torch.from_numpy(base).to(dev).repeat(nr // 96 + 1, 1)[:nr].contiguous()
+    s = torch.empty(nr, dtype=torch.float32, device=dev)
+    hip.gemv_q4_0_q8_0(n, s, w, rb, torch.from_numpy(x).to(dev), nr)
+    got = s.cpu().numpy()
+    del w, s
+    free()
+    pick = np.unique(np.concatenate([sample_indices(nr, 256, 3), [nr - 1]]))
+    want = oracle.gemm_q4_0(n, base[pick % 96], x, 0, len(pick), 1, rb, 1, 8)
+    assert_f32_parity(got[pick], want, what="gemv over 2 GiB")
