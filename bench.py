@@ -291,12 +291,16 @@ def bench_configs(torch, lib, stream, args):
     wd = torch.from_numpy(w).to(dev)
     cd = torch.empty(N * N, device=dev)
     fn = checked(lib.tcrv_hip_q4_0_q8_0_gemm, "q4_gemm")
-    reg = Region(torch, stream, lambda i: fn(N, cd.data_ptr(), wd.data_ptr(), ad.data_ptr(),
-                                             a.shape[1], N, N, w.shape[1], N, sp), 10)
-    reg.run()
-    us = reg.run() * 1e3 / 10
+    def q4_gemm(i):
+        fn(N, cd.data_ptr(), wd.data_ptr(), ad.data_ptr(), a.shape[1], N, N, w.shape[1], N, sp)
+
+    Region(torch, stream, q4_gemm, 50).run()  # loaded clocks, as for the Q8_0 GEMM
+    reg = Region(torch, stream, q4_gemm, 10)
+    per = sorted(reg.run() * 1e3 / 10 for _ in range(3))
+    us = per[1]
     out["q4_0_q8_0_gemm"] = {"workload": "a7 Q4_0 x Q8_0 GEMM 4096 rows x 4096 tokens x 4096",
-                             "us": round(us, 1), "TOPS": round(GEMM_OPS / us / 1e6, 1)}
+                             "us": round(us, 1), "TOPS": round(GEMM_OPS / us / 1e6, 1),
+                             "regions": 3}
     for k, v in out.items():
         if "GB/s" in v:
             log(f"{k}: {v['us']:.1f} us, {v['GB/s']:.0f} GB/s "
