@@ -167,6 +167,17 @@ TCRV_HIP_API int tcrv_hip_q4_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, 
                             size_t by, size_t nr, size_t nc, size_t bx, size_t bs,
                             void *stream);
 
+/* Replaces tcrv_emitc_..._q4_0_q8_0_gemm_tile(size_t n, float *s,
+ * const uint8_t *vx, const uint8_t *vy, size_t by)
+ * (test/Conversion/RVV/rvv-to-emitc-q4-0-q8-0-gemm-tile.mlir; op RVVOps.td:
+ * 4048-4133, emitter RVVToEmitCBlockQuantLinear.cpp:1392-1690): ONE weight row
+ * vx times m activation columns vy + j*by, s[j] = q4_0 block_dot(vx, vy + j*by)
+ * for j < m.  The reference fixes m as the op's `activation_cols` attribute;
+ * here it is an argument.  Same results as the G2 GEMM with nr = 1. */
+TCRV_HIP_API int tcrv_hip_q4_0_q8_0_gemm_tile(size_t n, float *s, const uint8_t *vx,
+                                              const uint8_t *vy, size_t by, size_t m,
+                                              void *stream);
+
 /* The decode GEMV (the q4_0 GEMM with nc = 1): s[ir] for ir < nr. */
 TCRV_HIP_API int tcrv_hip_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx, size_t bx,
                             const uint8_t *vy, size_t nr, void *stream);

@@ -200,7 +200,19 @@ def test_q4_0_gemm_entry_nc1_strided_output(hip, oracle, dev):
     assert np.all(got.reshape(nr, bs)[:, 1:] == -1.0)  # untouched between rows
 
 
-@pytest.mark.parametrize("nr,nc,nb", [(37, 5, 8), (16, 64, 128), (3, 2, 1)])
+@pytest.mark.parametrize("m,nb,pad", [(4, 128, 0), (6, 5, 0), (1, 2, 0), (33, 64, 8), (4, 130, 2)])
+def test_q4_0_gemm_tile(hip, oracle, dev, m, nb, pad):
+    """tcrv_rvv.q4_0_q8_0_gemm_tile: one weight row x m activation columns."""
+    n = nb * 32
+    w = synth.q4_0_matrix(1, n, 1006, 0.02)
+    a = np.pad(synth.q8_0_matrix(m, n, 1007, 1.0), ((0, 0), (0, pad)))
+    s = empty_dev(m, torch.float32, dev)
+    hip.q4_0_q8_0_gemm_tile(n, s, to_dev(w, dev), to_dev(a, dev), a.shape[1], m)
+    want = oracle.gemm_q4_0(n, w, a, a.shape[1], 1, m, w.shape[1], m, 8)
+    assert_f32_parity(from_dev(s), want, what=f"gemm tile m={m} nb={nb}")
+
+
+@pytest.mark.parametrize("nr,nc,nb", [(37, 5, 8), (16, 64, 128), (3, 2, 1), (1, 70, 128)])
 def test_q4_0_gemm_multi_column(hip, oracle, dev, nr, nc, nb):
     n = nb * 32
     w = synth.q4_0_matrix(nr, n, 7, 0.02)
@@ -224,6 +236,7 @@ def test_q4_0_gemm_multi_column(hip, oracle, dev, nr, nc, nb):
     (77, 1, 6, 4, 0),         # decode, padded rows, output stride bs = 6
     (1, 1, 2, 0, 0),          # one output
     (1, 45, 1, 0, 0),         # single weight row, one block
+    (1, 300, 64, 0, 8),       # single weight row: register-direct block dots
     (512, 512, 128, 0, 0),
 ])
 def test_q8_0_gemm(hip, oracle, dev, nr, nc, nb, xpad, ypad):

@@ -380,18 +380,28 @@ int zero_outputs(float *s, size_t count, size_t stride, size_t ncols, void *stre
   return launch_status();
 }
 
-int q8_0_gemv_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
-                     const uint8_t *vy, size_t nr, void *stream) {
-  if (nb % 2 != 0 || !aligned4(vx) || !aligned4(vy) || (nr > 1 && bx % 4 != 0))
+template <DotFmt F>
+int rows_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx, const uint8_t *vy,
+                size_t by, size_t npairs, void *stream) {
+  if (nb % 2 != 0 || !aligned4(vx) || !aligned4(vy) || bx % 4 != 0 || by % 4 != 0)
     return TCRV_HIP_ERR_UNSUPPORTED;
   constexpr size_t per_group = tcrv::kDdWaves * tcrv::kDdPairs;
-  const size_t groups = (nr + per_group - 1) / per_group;
+  const size_t groups = (npairs + per_group - 1) / per_group;
   if (groups > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
-  tcrv::block_dot_direct<DotFmt::kQ8Q8><<<dim3(static_cast<unsigned>(groups)),
-                                          dim3(tcrv::kDdWaves * 64), 0, as_stream(stream)>>>(
-      nb, s, os, vx, bx, vy, 0, nr);
+  tcrv::block_dot_direct<F><<<dim3(static_cast<unsigned>(groups)), dim3(tcrv::kDdWaves * 64), 0,
+                              as_stream(stream)>>>(nb, s, os, vx, bx, vy, by, npairs);
   return launch_status();
+}
+
+int q8_0_rows_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
+                     const uint8_t *vy, size_t by, size_t npairs, void *stream) {
+  return rows_direct<DotFmt::kQ8Q8>(nb, s, os, vx, bx, vy, by, npairs, stream);
+}
+
+int q4_0_rows_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
+                     const uint8_t *vy, size_t by, size_t npairs, void *stream) {
+  return rows_direct<DotFmt::kQ4Q8>(nb, s, os, vx, bx, vy, by, npairs, stream);
 }
 
 int q4_0_grid(size_t n, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by,

@@ -521,8 +521,10 @@ extern "C" int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx,
   const size_t rowbytes = nb * tcrv::kQ8Bytes;
   if ((nr > 1 && bx < rowbytes) || (nc > 1 && by < rowbytes))
     return TCRV_HIP_ERR_BAD_SIZE;
-  if (nc == 1) {  // decode: a bandwidth-bound GEMV, not an MFMA tile
-    const int st = q8_0_gemv_direct(nb, s, nr > 1 ? bs : 0, vx, bx, vy, nr, stream);
+  if (nc == 1 || nr == 1) {  // one operand is a single row: bandwidth-bound block dots
+    const int st = nc == 1 ? q8_0_rows_direct(nb, s, nr > 1 ? bs : 0, vx, nr > 1 ? bx : 0, vy,
+                                              0, nr, stream)
+                           : q8_0_rows_direct(nb, s, 1, vx, 0, vy, by, nc, stream);
     if (st != TCRV_HIP_ERR_UNSUPPORTED)
       return st;
   }

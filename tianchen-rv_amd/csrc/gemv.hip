@@ -369,10 +369,22 @@ int tcrv_hip_q4_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t
   const size_t nb = n / tcrv::kQK;
   if ((nr > 1 && bx < nb * tcrv::kQ4Bytes) || by < nb * tcrv::kQ8Bytes)
     return TCRV_HIP_ERR_BAD_SIZE;
+  if (nr == 1) {  // one weight row against nc columns: bandwidth-bound block dots
+    const int st = tcrv_host::q4_0_rows_direct(nb, s, 1, vx, 0, vy, by, nc, stream);
+    if (st != TCRV_HIP_ERR_UNSUPPORTED)
+      return st;
+  }
   const int st = tcrv_host::q4_0_gemm_mfma(nb, s, vx, bx, vy, by, nr, nc, bs, stream);
   if (st != TCRV_HIP_ERR_UNSUPPORTED)
     return st;
   return tcrv_host::q4_0_grid(n, s, vx, bx, vy, by, nr, nc, bs, stream);
+}
+
+int tcrv_hip_q4_0_q8_0_gemm_tile(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
+                                 size_t by, size_t m, void *stream) {
+  // one weight row times m activation columns, outputs s[0..m-1] contiguous:
+  // the G2 GEMM with nr = 1 (its bx and bs are then unused)
+  return tcrv_hip_q4_0_q8_0_gemm(n, s, vx, vy, by, 1, m, 0, m, stream);
 }
 
 }  // extern "C"

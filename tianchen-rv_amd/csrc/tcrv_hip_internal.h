@@ -154,11 +154,14 @@ int zero_outputs(float *s, size_t count, size_t stride, size_t ncols, void *stre
 int q4_0_gemm_mfma(size_t nb, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy,
                    size_t by, size_t nr, size_t nc, size_t bs, void *stream);
 
-// Q8_0 x Q8_0 GEMM with nc = 1 (decode): one weight row per pair against the
-// single activation row, s[ir * os] (block_dot.hip); TCRV_HIP_ERR_UNSUPPORTED
-// for an odd block count or rows that are not 4-byte aligned.
-int q8_0_gemv_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
-                     const uint8_t *vy, size_t nr, void *stream);
+// npairs register-direct block dots (block_dot.hip): s[p * os] = dot(vx + p*bx,
+// vy + p*by); a stride of 0 pairs every row of the other operand with one row
+// (the GEMM's nc = 1 and nr = 1 shapes).  TCRV_HIP_ERR_UNSUPPORTED for an odd
+// block count or operands/strides that are not 4-byte aligned.
+int q8_0_rows_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
+                     const uint8_t *vy, size_t by, size_t npairs, void *stream);
+int q4_0_rows_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
+                     const uint8_t *vy, size_t by, size_t npairs, void *stream);
 
 // Q4_0 x Q8_0 GEMM for nc > 1 as one wave per output element (block_dot.hip).
 int q4_0_grid(size_t n, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by,

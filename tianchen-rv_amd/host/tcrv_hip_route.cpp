@@ -95,6 +95,7 @@ struct HipKernelRoute {
 //   q8_0 block dot: rvv-to-emitc-q8-0-q8-0-block-dot.mlir:16-19
 //   q4_0 block dot: rvv-to-emitc-q4-0-q8-0-block-dot.mlir:24-31
 //   q4_0 gemm:      rvv-to-emitc-q4-0-q8-0-gemm.mlir:23-31
+//   q4_0 gemm tile: rvv-to-emitc-q4-0-q8-0-gemm-tile.mlir (+ its activation_cols)
 //   repack gemvs:   rvv-to-emitc-repack-gemv-q4-0-q8-0.mlir:26-30,
 //                   rvv-to-emitc-repack-gemv-q8-0-q8-0-vlen256.mlir
 //   pack:           rvv-to-emitc-pack-q4-0-to-q4-0x16.mlir:19-21
@@ -106,6 +107,9 @@ constexpr const char *kN = "runtime-element-count";
 constexpr const char *kOut = "output-buffer";
 constexpr const char *kLhs = "lhs-input-buffer";
 constexpr const char *kRhs = "rhs-input-buffer";
+// Not a runtime-ABI value in the reference: an op attribute the emitted C bakes
+// in (q4_0_q8_0_gemm_tile's activation_cols), passed at run time here.
+constexpr const char *kOpAttr = "op-attribute";
 
 const HipKernelRoute kHipKernelRoutes[] = {
     {"tcrv_rvv.binary.add.f32", "tcrv_hip_add_f32",
@@ -128,6 +132,11 @@ const HipKernelRoute kHipKernelRoutes[] = {
       {"nr", "size_t", "source-byte-stride"}, {"nc", "size_t", "destination-byte-stride"},
       {"bx", "size_t", "lhs-input-stride"}, {"bs", "size_t", "output-stride"}},
      9},
+    {"tcrv_rvv.q4_0_q8_0_gemm_tile", "tcrv_hip_q4_0_q8_0_gemm_tile",
+     {{"n", "size_t", kN}, {"s", "float *", kOut}, {"vx", "const uint8_t *", kLhs},
+      {"vy", "const uint8_t *", kRhs}, {"by", "size_t", "rhs-input-stride"},
+      {"m", "size_t", kOpAttr}},
+     6},
     {"tcrv_rvv.repack_gemv_q4_0_q8_0", "tcrv_hip_repack_gemv_q4_0_q8_0",
      {{"n", "size_t", kN}, {"s", "float *", kOut}, {"vx", "const uint8_t *", kLhs},
       {"vy", "const uint8_t *", kRhs}, {"nc", "size_t", "destination-byte-stride"}},

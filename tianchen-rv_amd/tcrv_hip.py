@@ -63,6 +63,7 @@ SIGNATURES = {
     "tcrv_hip_q8_0_q8_0_block_sums": [_sz, _p, _p, _sz, _p, _sz, _sz, _p],
     "tcrv_hip_q4_0_q8_0_block_sums": [_sz, _p, _p, _sz, _p, _sz, _sz, _p],
     "tcrv_hip_q4_0_q8_0_gemm": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p],
+    "tcrv_hip_q4_0_q8_0_gemm_tile": [_sz, _p, _p, _p, _sz, _sz, _p],
     "tcrv_hip_gemv_q4_0_q8_0": [_sz, _p, _p, _sz, _p, _sz, _p],
     "tcrv_hip_q8_0_q8_0_gemm": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p],
     "tcrv_hip_pack_q4_0_to_q4_0x16": [_sz, _p, _p, _p],
@@ -211,6 +212,10 @@ def q4_0_q8_0_block_sums(n: int, sumi, vx, bx: int, vy, by: int, nrows: int, str
 def q4_0_q8_0_gemm(n: int, s, vx, vy, by: int, nr: int, nc: int, bx: int, bs: int,
                    stream=None):
     return call("tcrv_hip_q4_0_q8_0_gemm", n, s, vx, vy, by, nr, nc, bx, bs, _stream(stream))
+
+
+def q4_0_q8_0_gemm_tile(n: int, s, vx, vy, by: int, m: int, stream=None):
+    return call("tcrv_hip_q4_0_q8_0_gemm_tile", n, s, vx, vy, by, m, _stream(stream))
 
 
 def gemv_q4_0_q8_0(n: int, s, vx, bx: int, vy, nr: int, stream=None):
