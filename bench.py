@@ -363,6 +363,33 @@ def cpu_baseline(seconds: float):
     }
 
 
+def cpu_baseline_gemm(seconds: float):
+    """The oracle's Q8_0 x Q8_0 GEMM on the host, for the GEMM object: slices
+    of 16 weight rows x all 4096 tokens x K 4096 (1/256 of the GEMM each),
+    repeated for `seconds` on all threads (OpenMP over rows, serial fold)."""
+    import synth
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_binding
+
+    ora = oracle_binding.load()
+    threads = cpu_threads()
+    rows = 16
+    a = synth.q8_0_matrix(N, N, synth.SEEDS["gemm_a"], 1.0)
+    b = synth.q8_0_matrix(rows, N, synth.SEEDS["gemm_b"], 0.02)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        ora.gemm_q8_0(N, b, a, a.shape[1], rows, N, b.shape[1], N, threads)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds:
+            break
+    tops = 2.0 * rows * N * N * reps / dt / 1e12
+    log(f"CPU oracle GEMM: {tops * 1e3:.1f} GOPS on {threads} threads")
+    return {"value": round(tops, 5), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": (f"oracle/ scalar C, OpenMP over rows: {reps} slices of {rows} weight rows "
+                       f"x 4096 tokens x 4096 (1/256 of the GEMM each) in {dt:.1f} s")}
+
+
 def load_traffic():
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(path):
@@ -404,6 +431,8 @@ def main():
     if args.only in ("all", "configs"):
         res["configs"] = bench_configs(torch, lib, stream, args)
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+    cpu_gemm = (cpu_baseline_gemm(args.cpu_seconds / 2)
+                if args.cpu_seconds > 0 and "gemm" in res else None)
     traffic = load_traffic()
 
     line = {
@@ -414,7 +443,9 @@ def main():
         "warmup": args.warmup,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 (q4_0/q8_0 block quants) -> int32 block sums, fp32 fold",
+        "dtype": "int8",
+        "arith": "int8 block quants (q4_0 / q8_0) -> exact int32 block sums -> fp32 fold in the "
+                 "reference order",
         "data": "synthetic: splitmix64 Box-Muller, seeds 1001-1009 (tianchen-rv_amd/synth.py)",
         "config": {"workload": "gemv_q4_0_q8_0 W 4096x4096 Q4_0 x Q8_0 vector (configs[3])",
                    "rows": N, "cols": N, "launch": "HIP graph of `steps` launches",
@@ -436,7 +467,7 @@ def main():
         line["gemm"] = {
             "workload": "q8_0_q8_0_gemm 4096 weight rows x 4096 tokens x 4096 (configs[4])",
             "value": round(m["tops"], 2), "unit": "TOPS", "ms_per_step": m["us"] / 1e3,
-            "steps": args.gemm_steps, "regions": m["regions"],
+            "steps": args.gemm_steps, "regions": m["regions"], "cpu_baseline": cpu_gemm,
             "us_min": round(m["us_min"], 2), "us_max": round(m["us_max"], 2),
             "roofline": {"bound": "mfma", "achieved": round(m["tops"], 2), "peak": INT8_PEAK_TOPS,
                          "unit": "TOPS", "frac": round(m["tops"] / INT8_PEAK_TOPS, 4),
