@@ -290,7 +290,7 @@ __global__ __launch_bounds__(kDdWaves * 64) void block_dot_direct(size_t nb, flo
       }
       *reinterpret_cast<float4 *>(&tl[w][r][b0]) = t;
     }
-    __syncthreads();
+    wave_lds_sync();  // the LDS rows are this wave's own
     float ta[kDdTerms], tb[kDdTerms];
 #pragma unroll
     for (int k = 0; k < kDdTerms; k += 2) {
@@ -300,7 +300,7 @@ __global__ __launch_bounds__(kDdWaves * 64) void block_dot_direct(size_t nb, flo
     // the previous chunk's sum sits in the last lane of the fold row: seed lane 0
     const float carry = __shfl(sumf, (l & ~(kDdLanes - 1)) + kDdLanes - 1);
     sumf = fold_chain<kDdLanes, kDdTerms>(ta, tb, fp == 0 ? carry : 0.0f);
-    __syncthreads();
+    wave_lds_sync();  // the LDS rows are this wave's own
   }
   if (fp == kDdLanes - 1 && p0 + fr < npairs)
     s[(p0 + fr) * os] = sumf;

@@ -262,7 +262,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
       for (int r = 0; r < kR; ++r)
         *reinterpret_cast<float2 *>(&tl[w][r][b0]) = make_float2(0.0f, 0.0f);
     }
-    __syncthreads();
+    wave_lds_sync();  // the LDS rows are this wave's own
     float t[kTerms], dy[kTerms];
 #pragma unroll
     for (int k = 0; k < kTerms; k += 4) {
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
       // the previous chunk's sum sits in the last lane of the group: seed lane 0
       const float carry = __shfl(sumf, (l & ~(kLanes - 1)) + kLanes - 1);
       sumf = fold_chain<kLanes, kTerms>(t, dy, fp == 0 ? carry : 0.0f);
-      __syncthreads();
+      wave_lds_sync();  // the LDS rows are this wave's own
     }
   }
   if (fp == kLanes - 1 && l / kLanes < kR && row0 + fr < nr)

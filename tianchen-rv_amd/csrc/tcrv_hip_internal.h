@@ -100,6 +100,16 @@ __device__ __forceinline__ void copy_lds_to_span(uint8_t *dst, const uint8_t *sr
   }
 }
 
+// Orders this wave's LDS writes before its later LDS reads by other lanes of
+// the same wave (for data no other wave touches): the LDS executes one wave's
+// accesses in order, so a wave-scope fence plus a scheduling barrier suffice
+// where a work-group barrier would also wait for the other waves.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Serial fold of one row spread over the kLanes lanes of a lane group (a
 // 16-lane DPP row, or half of one): lane p of the group holds the two fold
 // operands t[k], dy[k] of kTerms consecutive blocks, p*kTerms + k, and each
