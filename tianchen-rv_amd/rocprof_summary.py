@@ -3,6 +3,9 @@
 
   rocprof_summary.py stats <run_kernel_stats.csv> [name-substring ...]
       per-kernel call count and average / min / max duration (us)
+  rocprof_summary.py counters <pmc-root> <COUNTER> [name-substring ...]
+      median KiB per dispatch of each matching kernel in
+      <pmc-root>/pmc_<COUNTER>_configs/run_counter_collection.csv
   rocprof_summary.py traffic <pmc-root>
       HBM bytes per dispatch of the GEMV and GEMM kernels from the two
       counter passes (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled by
@@ -28,6 +31,18 @@ KERNELS = {
 CALIB_BYTES = {"FETCH_SIZE": 8 << 24, "WRITE_SIZE": 4 << 24}  # per add_f32 launch, n = 2^24
 
 
+def short_name(name):
+    """Kernel name without its parameter list (the last balanced "(...)")."""
+    name = name.replace("(anonymous namespace)::", "")
+    if name.endswith(")"):
+        depth = 0
+        for i in range(len(name) - 1, -1, -1):
+            depth += {")": 1, "(": -1}.get(name[i], 0)
+            if depth == 0:
+                return name[:i].strip()
+    return name
+
+
 def stats(path, needles):
     rows = []
     with open(path) as f:
@@ -38,8 +53,24 @@ def stats(path, needles):
             rows.append((name, int(r["Calls"]), float(r["AverageNs"]) / 1e3,
                          float(r["MinNs"]) / 1e3, float(r["MaxNs"]) / 1e3))
     for name, calls, avg, mn, mx in rows:
-        short = name.split("(")[0]
-        print(f"| {short} | {calls} | {avg:.3f} | {mn:.3f} | {mx:.3f} |")
+        print(f"| {short_name(name)} | {calls} | {avg:.3f} | {mn:.3f} | {mx:.3f} |")
+
+
+def counters(root, ctr, needles):
+    """Median counter value (KiB) per dispatch of every kernel matching a needle."""
+    per = {}
+    with open(os.path.join(root, f"pmc_{ctr}_configs", "run_counter_collection.csv")) as f:
+        for r in csv.DictReader(f):
+            name = short_name(r["Kernel_Name"])
+            if needles and not any(n in name for n in needles):
+                continue
+            key = (name, r["Dispatch_Id"])
+            per[key] = per.get(key, 0.0) + float(r["Counter_Value"])
+    by = {}
+    for (name, _), v in per.items():
+        by.setdefault(name, []).append(v)
+    for name, vals in sorted(by.items()):
+        print(f"| {name} | {ctr} | {len(vals)} | {statistics.median(vals):.1f} |")
 
 
 def counter_per_dispatch(path, kernel):
@@ -83,6 +114,8 @@ def main():
         stats(sys.argv[2], sys.argv[3:])
     elif len(sys.argv) == 3 and sys.argv[1] == "traffic":
         traffic(sys.argv[2])
+    elif len(sys.argv) >= 4 and sys.argv[1] == "counters":
+        counters(sys.argv[2], sys.argv[3], sys.argv[4:])
     else:
         print(__doc__)
         sys.exit(2)
