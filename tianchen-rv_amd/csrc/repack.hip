@@ -200,6 +200,119 @@ __global__ __launch_bounds__(256) void repack_gemv(size_t nb, float *s, const ui
     s[static_cast<size_t>(blockIdx.x) * 16 + 4 * w + fr] = acc;
 }
 
+
+// ---------------------------------------------------------------------------
+// Wave-per-row-quad form (activation 4-byte aligned; the LDS-staged form above
+// serves 2-byte aligned activations).  Wave w of the group's work-group owns
+// rows 4w..4w+3 and folds them itself, so no work-group barrier is needed:
+// lane l takes blocks 2l, 2l+1 of the chunk; per block it loads the dword at
+// position i of its row quad for every position i (the x16 interleave puts
+// rows 4w..4w+3 of position i in dword 4i + w), turns each 4x4 group
+// row-major with v_perm and dots it with the activation, which the lane loads
+// straight from global memory (68 bytes, like the plain GEMV).  Exact
+// (float)sumi and d_w*d_a go to the wave's own LDS rows; DPP row r then folds
+// weight row 4w + r with fold_chain.
+// ---------------------------------------------------------------------------
+template <bool kQ4>
+__global__ __launch_bounds__(256) void repack_gemv_rows(size_t nb, float *s, const uint8_t *vx,
+                                                        const uint8_t *vy) {
+  constexpr int kW = kQ4 ? kQ4x16Bytes : kQ8x16Bytes;
+  constexpr int kPos = kQ4 ? 16 : 32;  // quant-byte positions per block
+  constexpr int kFoldLanes = 16, kFoldTerms = kRgChunk / kFoldLanes;
+  __shared__ __align__(16) float2 terms[4][4][kRgChunk + 8];  // [wave][row][block]
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63;
+  const int fr = l >> 4, fp = l & (kFoldLanes - 1);
+  const uint8_t *group = vx + static_cast<size_t>(blockIdx.x) * nb * kW;
+  float acc = 0.0f;
+
+  for (size_t c0 = 0; c0 < nb; c0 += kRgChunk) {
+    const int nbc = static_cast<int>(min(static_cast<size_t>(kRgChunk), nb - c0));
+    const int b0 = 2 * l;
+    uint32_t raw[2][kPos], dq[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (b0 + j < nbc) {
+        const uint8_t *blk = group + (c0 + b0 + j) * kW;
+        const uint32_t *qd = reinterpret_cast<const uint32_t *>(blk + 32);
+#pragma unroll
+        for (int i = 0; i < kPos; ++i)
+          raw[j][i] = qd[4 * i + w];
+        const uint32_t *d = reinterpret_cast<const uint32_t *>(blk + 8 * w);  // d[4w..4w+3]
+        dq[j][0] = d[0];
+        dq[j][1] = d[1];
+      }
+    }
+    // activation blocks 2l, 2l+1: 68 bytes from a dword-aligned start (34 when
+    // only block 2l exists)
+    uint32_t ar[17];
+    const uint32_t *ag = reinterpret_cast<const uint32_t *>(vy + (c0 + b0) * kQ8Bytes);
+    if (b0 + 1 < nbc) {
+#pragma unroll
+      for (int k = 0; k < 17; ++k)
+        ar[k] = ag[k];
+    } else if (b0 < nbc) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        ar[k] = ag[k];
+      ar[8] = *reinterpret_cast<const uint16_t *>(ag + 8);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float2 t[4] = {make_float2(0.0f, 0.0f), make_float2(0.0f, 0.0f), make_float2(0.0f, 0.0f),
+                     make_float2(0.0f, 0.0f)};  // absent blocks: fma(0, 0, acc) == acc
+      if (b0 + j < nbc) {
+        uint32_t a[8];  // the block's 32 activation quants, dword aligned
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          a[k] = j == 0 ? funnel16(ar[k], ar[k + 1]) : ar[k + 9];
+        const float da = fp16_bits_to_f32(j == 0 ? (ar[0] & 0xffffu) : (ar[8] >> 16));
+        int part[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int g = 0; g < kPos / 4; ++g) {
+          uint32_t rows[4];
+          transpose4x4(&raw[j][4 * g], rows);  // positions 4g..4g+3 of rows 4w..4w+3
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if constexpr (kQ4) {
+              // byte = (n_lo ^ 8) | (n_hi ^ 8) << 4: as signed bytes the masked
+              // nibbles are 16 * (n - 8); low nibbles pair with quants 4g..,
+              // high nibbles with 16+4g..
+              part[r] = sdot4((rows[r] << 4) & 0xF0F0F0F0u, a[g], part[r]);
+              part[r] = sdot4(rows[r] & 0xF0F0F0F0u, a[g + 4], part[r]);
+            } else {
+              part[r] = sdot4(rows[r], a[g], part[r]);
+            }
+          }
+        }
+        const uint32_t dw[4] = {dq[j][0] & 0xffffu, dq[j][0] >> 16, dq[j][1] & 0xffffu,
+                                dq[j][1] >> 16};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int sumi = kQ4 ? (part[r] >> 4) : part[r];  // Q4_0: exact division by 16
+          t[r] = make_float2(static_cast<float>(sumi), fp16_bits_to_f32(dw[r]) * da);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        terms[w][r][b0 + j] = t[r];
+    }
+    wave_lds_sync();  // the LDS rows are this wave's own
+    float ta[kFoldTerms], tb[kFoldTerms];
+#pragma unroll
+    for (int k = 0; k < kFoldTerms; k += 2) {
+      const float4 v = *reinterpret_cast<const float4 *>(&terms[w][fr][fp * kFoldTerms + k]);
+      ta[k] = v.x; tb[k] = v.y; ta[k + 1] = v.z; tb[k + 1] = v.w;
+    }
+    // the previous chunk's sum sits in the last lane of the fold row: seed lane 0
+    const float carry = __shfl(acc, (l & ~(kFoldLanes - 1)) + kFoldLanes - 1);
+    acc = fold_chain<kFoldLanes, kFoldTerms>(ta, tb, fp == 0 ? carry : 0.0f);
+    wave_lds_sync();
+  }
+  if (fp == kFoldLanes - 1)
+    s[static_cast<size_t>(blockIdx.x) * 16 + 4 * w + fr] = acc;
+}
 }  // namespace tcrv
 
 namespace {
@@ -240,8 +353,12 @@ int launch_repack_gemv(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
     return TCRV_HIP_ERR_MISALIGNED;
   if (groups > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
-  tcrv::repack_gemv<kQ4><<<dim3(static_cast<unsigned>(groups)), dim3(256), 0,
-                           as_stream(stream)>>>(nb, s, vx, vy);
+  if (aligned4(vy))
+    tcrv::repack_gemv_rows<kQ4><<<dim3(static_cast<unsigned>(groups)), dim3(256), 0,
+                                  as_stream(stream)>>>(nb, s, vx, vy);
+  else
+    tcrv::repack_gemv<kQ4><<<dim3(static_cast<unsigned>(groups)), dim3(256), 0,
+                             as_stream(stream)>>>(nb, s, vx, vy);
   return launch_status();
 }
 
