@@ -398,6 +398,36 @@ def load_traffic():
     return {}
 
 
+def device_peaks(torch):
+    """The GPU's CU count and top shader clock (rocminfo, run as a child
+    process) and the int8 MFMA peak they imply at 8192 int8 ops per clock and
+    CU, next to the published figure used for `frac`."""
+    props = torch.cuda.get_device_properties(0)
+    out = {"name": props.name, "arch": props.gcnArchName, "cus": props.multi_processor_count,
+           "max_sclk_mhz": None, "int8_tops_derived": None, "int8_tops_published": INT8_PEAK_TOPS,
+           "hbm_gbs_published": HBM_PEAK_GBS}
+    try:
+        import subprocess
+        text = subprocess.run(["rocminfo"], capture_output=True, text=True, timeout=60).stdout
+    except (OSError, subprocess.SubprocessError):
+        return out
+    for agent in text.split("Agent ")[1:]:
+        fields = {}
+        for ln in agent.splitlines():
+            if ":" in ln:
+                k, v = ln.split(":", 1)
+                fields.setdefault(k.strip(), v.strip())
+        if fields.get("Device Type") == "GPU":
+            try:
+                mhz, cus = int(fields["Max Clock Freq. (MHz)"]), int(fields["Compute Unit"])
+            except (KeyError, ValueError):
+                break
+            out.update({"max_sclk_mhz": mhz, "cus_rocminfo": cus,
+                        "int8_tops_derived": round(cus * mhz * 1e6 * 8192 / 1e12, 1)})
+            break
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -483,6 +513,8 @@ def main():
             first = next(iter(res["configs"].values()))
             line.update({"value": first["GB/s"], "unit": "GB/s", "ms_per_step": first["us"] / 1e3})
     line["cpu_baseline"] = cpu
+    if args.only == "all":
+        line["device"] = device_peaks(torch)
     print(json.dumps(line), flush=True)
 
 
