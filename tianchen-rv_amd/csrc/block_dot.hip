@@ -184,16 +184,21 @@ __global__ __launch_bounds__(64) void block_dot_pairs(size_t nb, float *s, int32
 
 // ---------------------------------------------------------------------------
 // Register-direct row pairs (rows 4-byte aligned, even block count): a wave
-// owns kDdPairs row pairs, one per 16-lane DPP row.  For each pair, lane l
-// loads its block pair 2l, 2l+1 of both rows straight into registers (68 or
-// 36 bytes, dword aligned -- across the wave the loads cover the row chunk
-// contiguously), computes the two blocks' fold operands and writes them to
-// LDS; then DPP row r folds pair r with fold_chain, 8 consecutive blocks per
-// lane, so the four pairs' serial folds run side by side in the same
-// instructions and no LDS access sits on the dependency chain.
+// owns kDdPairs row pairs.  For each pair, lane l loads its block pair 2l,
+// 2l+1 of both rows straight into registers (68 or 36 bytes, dword aligned --
+// across the wave the loads cover the row chunk contiguously), computes the
+// two blocks' fold operands and writes them to LDS; then DPP row r folds pair
+// r % kDdPairs with fold_chain, 8 consecutive blocks per lane, so the pairs'
+// serial folds run side by side in the same instructions and no LDS access
+// sits on the dependency chain (with two pairs per wave, DPP rows 2 and 3
+// fold copies of pairs 0 and 1, which are not stored).  Two pairs per wave
+// measured faster than four (25.6 vs 26.8 us for 16384 Q8_0 pairs of 4096):
+// a wave walks its pairs one after another, so fewer pairs per wave means
+// more, shorter waves.
 // ---------------------------------------------------------------------------
 constexpr int kDdWaves = 4;
-constexpr int kDdPairs = 4;                           // one per DPP row
+constexpr int kDdPairs = 2;                           // pairs per wave
+static_assert(4 % kDdPairs == 0, "each DPP row folds one pair");
 constexpr int kDdLanes = 16;                          // fold lanes per pair
 constexpr int kDdTerms = kChunkBlocks / kDdLanes;     // 8 blocks per fold lane
 constexpr int kDdStride = kChunkBlocks + 8;           // float2 per pair row (padded)
@@ -258,7 +263,7 @@ __global__ __launch_bounds__(kDdWaves * 64) void block_dot_direct(size_t nb, flo
   __shared__ __align__(16) float2 tl[kDdWaves][kDdPairs][kDdStride];
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
   const size_t p0 = (static_cast<size_t>(blockIdx.x) * kDdWaves + w) * kDdPairs;
-  const int fr = l >> 4, fp = l & (kDdLanes - 1);  // fold row (= pair) and lane in it
+  const int fr = (l >> 4) % kDdPairs, fp = l & (kDdLanes - 1);  // pair folded, lane in chain
   float sumf = 0.0f;
 
   for (size_t c0 = 0; c0 < nb; c0 += kChunkBlocks) {
@@ -302,7 +307,7 @@ __global__ __launch_bounds__(kDdWaves * 64) void block_dot_direct(size_t nb, flo
     sumf = fold_chain<kDdLanes, kDdTerms>(ta, tb, fp == 0 ? carry : 0.0f);
     wave_lds_sync();  // the LDS rows are this wave's own
   }
-  if (fp == kDdLanes - 1 && p0 + fr < npairs)
+  if (fp == kDdLanes - 1 && (l >> 4) < kDdPairs && p0 + fr < npairs)
     s[(p0 + fr) * os] = sumf;
 }
 

@@ -21,11 +21,12 @@ __device__ __forceinline__ void store_stream(float4 v, float4 *p) {
 // a1: out[i] = lhs[i] + rhs[i].  The reference emits a VL strip loop of
 // vle32/vfadd/vse32 (lib/Conversion/RVV/RVVToEmitC.cpp:605, :1873-1911); here
 // each thread moves kAddUnroll 128-bit vectors per operand, all loads issued
-// before the adds.  IEEE binary32 addition is correctly rounded, so the result
-// is bit-identical to the scalar loop.
+// before the adds (2 measured fastest for n = 2^24: 28.1 us against 28.4, 28.8
+// and 29.3 us for 1, 4 and 8).  IEEE binary32 addition is correctly rounded,
+// so the result is bit-identical to the scalar loop.
 // ---------------------------------------------------------------------------
 constexpr int kAddThreads = 256;
-constexpr int kAddUnroll = 4;
+constexpr int kAddUnroll = 2;
 
 __global__ __launch_bounds__(kAddThreads) void add_f32_vec4(const float4 *lhs,
                                                             const float4 *rhs, float4 *out,
@@ -65,12 +66,15 @@ __global__ __launch_bounds__(kAddThreads) void add_f32_scalar(const float *lhs, 
 
 // ---------------------------------------------------------------------------
 // a3: y[32b+j] = qs_b[j] * d_b.  A work-group stages kDqBlocks contiguous
-// 34-byte blocks (a 16-byte multiple: 128*34 = 4352) through LDS with 128-bit
-// loads, then writes 128-bit float4 rows of the output.  int8 * fp16-valued
-// float is exact in binary32, so the result is bit-exact.
+// 34-byte blocks (a 16-byte multiple: 64*34 = 2176) through LDS with 128-bit
+// loads, then writes 128-bit float4 rows of the output, one per thread.
+// int8 * fp16-valued float is exact in binary32, so the result is bit-exact.
+// One float4 per thread measured fastest: 64 blocks per 512 threads 12.8 us
+// for 4096^2, 32 per 256 13.0 us, 16 per 128 13.4 us; 128 blocks per 256
+// threads 13.9 us and 256-1024 blocks per 256 threads 14.0-15.5 us.
 // ---------------------------------------------------------------------------
-constexpr int kDqThreads = 256;
-constexpr int kDqBlocks = 128;
+constexpr int kDqThreads = 512;
+constexpr int kDqBlocks = 64;
 
 template <bool kVecOut>
 __global__ __launch_bounds__(kDqThreads) void dequantize_q8_0(const uint8_t *vx, float *y,
