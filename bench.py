@@ -64,7 +64,8 @@ def parse():
                     help="distinct GEMV weight copies rotated over (> 256 MB in total)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall time of the CPU-baseline sample (0 disables it)")
-    ap.add_argument("--only", choices=["all", "gemv", "gemm", "configs", "calib"], default="all",
+    ap.add_argument("--only", choices=["all", "gemv", "gemv_rows", "gemm", "configs", "calib"],
+                    default="all",
                     help="calib: 10 launches of add_f32 over n = 2^24 (reads 128 MiB, writes "
                          "64 MiB each), the known-size kernel the HBM byte counters are "
                          "scaled against")
@@ -158,6 +159,49 @@ def bench_gemv(torch, lib, stream, args):
     log(f"GEMV {us:.2f} us/launch over {args.steps} launches, {copies} weight copies: "
         f"{gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
     return {"us": us, "gbs": gbs, "copies": copies, "ms_region": ms}
+
+
+def bench_gemv_rows(torch, lib, stream, args):
+    """The same GEMV kernel at more weight rows (K = 4096): the weight matrix
+    is the 4096-row configs[3] matrix repeated, one launch per rotating copy.
+    Past a few tens of MB the fixed cost of a launch (the launch itself and one
+    short read) is amortised and the kernel's own streaming rate shows."""
+    import synth
+    w = synth.q4_0_matrix(N, N, synth.SEEDS["gemv_w"], 0.02)
+    x = synth.q8_0_matrix(1, N, synth.SEEDS["gemv_x"], 1.0).reshape(-1)
+    dev = torch.device("cuda:0")
+    wt = torch.from_numpy(w).to(dev)
+    xd = torch.from_numpy(x).to(dev)
+    fn = checked(lib.tcrv_hip_gemv_q4_0_q8_0, "gemv")
+    sp, bx = stream.cuda_stream, w.shape[1]
+    out = {}
+    for nr, steps in ((16384, 200), (65536, 100), (262144, 40)):
+        rows_bytes = nr * bx
+        copies = copies_for(rows_bytes, 2)
+        wd = wt.repeat(copies * (nr // N), 1).view(copies, rows_bytes)
+        yd = torch.empty((copies, nr), dtype=torch.float32, device=dev)
+        wp = [wd[i].data_ptr() for i in range(copies)]
+        yp = [yd[i].data_ptr() for i in range(copies)]
+
+        def launch(i, nr=nr, wp=wp, yp=yp, copies=copies):
+            k = i % copies
+            fn(N, yp[k], wp[k], bx, xd.data_ptr(), nr, sp)
+
+        Region(torch, stream, launch, max(steps // 4, 4)).run()
+        ms = Region(torch, stream, launch, steps).run()
+        same_as_eager(torch, stream, yd[(steps - 1) % copies],
+                      lambda o, nr=nr, k=(steps - 1) % copies, wp=wp:
+                      fn(N, o, wp[k], bx, xd.data_ptr(), nr, sp), f"GEMV {nr} rows")
+        us = ms * 1e3 / steps
+        nbytes = rows_bytes + (N // 32) * 34 + nr * 4
+        gbs = nbytes / (us * 1e-6) / 1e9
+        log(f"GEMV {nr}x{N}: {us:.2f} us/launch, {gbs:.0f} GB/s "
+            f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak), {copies} copies")
+        out[str(nr)] = {"us": round(us, 3), "GB/s": round(gbs, 1),
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes, "copies": copies}
+        del wd, yd
+        torch.cuda.empty_cache()
+    return out
 
 
 def bench_gemm(torch, lib, stream, args):
@@ -456,6 +500,8 @@ def main():
     res = {}
     if args.only in ("all", "gemv"):
         res["gemv"] = bench_gemv(torch, lib, stream, args)
+    if args.only in ("all", "gemv_rows"):
+        res["gemv_rows"] = bench_gemv_rows(torch, lib, stream, args)
     if args.only in ("all", "gemm"):
         res["gemm"] = bench_gemm(torch, lib, stream, args)
     if args.only in ("all", "configs"):
@@ -507,6 +553,10 @@ def main():
         if "gemv" not in res:
             line.update({"value": line["gemm"]["value"], "unit": "TOPS",
                          "ms_per_step": line["gemm"]["ms_per_step"]})
+    if "gemv_rows" in res:
+        line["gemv_rows"] = {
+            "workload": "gemv_q4_0_q8_0 at more weight rows, K 4096 (the configs[3] matrix "
+                        "repeated); same kernel as `value`", "by_rows": res["gemv_rows"]}
     if "configs" in res:
         line["configs"] = res["configs"]
         if "value" not in line:
