@@ -492,3 +492,51 @@ def test_add_i32_harness_vector(hip, dev):
     out = empty_dev(n, torch.int32, dev)
     hip.add_i32(to_dev(a, dev), to_dev(b, dev), out, n)
     assert np.array_equal(from_dev(out), (i + 24).astype(np.int32))
+
+
+# ------------------------------------------- several host threads, own streams ---
+
+def test_concurrent_host_threads_on_own_streams(hip, oracle, dev):
+    """The library keeps no global state: four host threads, each launching on
+    its own stream, interleave decode GEMVs and Q8_0 GEMMs on their own inputs;
+    every output must still be the oracle's, bit for bit."""
+    import threading
+
+    n, nr, nc, nw = 1024, 256, 64, 96
+    jobs = []
+    for t in range(4):
+        w4 = synth.q4_0_matrix(nr, n, 2000 + t, 0.02)
+        x = synth.q8_0_matrix(1, n, 2100 + t, 1.0).reshape(-1)
+        a8 = synth.q8_0_matrix(nc, n, 2200 + t, 1.0)
+        b8 = synth.q8_0_matrix(nw, n, 2300 + t, 0.02)
+        jobs.append({
+            "w4": to_dev(w4, dev), "x": to_dev(x, dev), "a8": to_dev(a8, dev),
+            "b8": to_dev(b8, dev), "y": empty_dev(nr, torch.float32, dev),
+            "c": empty_dev(nw * nc, torch.float32, dev),
+            "want_y": oracle.gemm_q4_0(n, w4, x, 0, nr, 1, w4.shape[1], 1, 8)[:nr],
+            "want_c": oracle.gemm_q8_0(n, b8, a8, a8.shape[1], nw, nc, b8.shape[1], nc, 8),
+            "bx4": w4.shape[1], "rb8": a8.shape[1]})
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(j):
+        try:
+            st = torch.cuda.Stream(device=dev)
+            for _ in range(25):
+                hip.gemv_q4_0_q8_0(n, j["y"], j["w4"], j["bx4"], j["x"], nr, stream=st)
+                hip.q8_0_q8_0_gemm(n, j["c"], j["b8"], j["a8"], j["rb8"], nw, nc, j["rb8"], nc,
+                                   stream=st)
+            st.synchronize()
+        except Exception as e:  # reported below, on the test's thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(j,)) for j in jobs]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    assert not any(th.is_alive() for th in threads), "a launching thread did not finish"
+    assert not errors, errors
+    for t, j in enumerate(jobs):
+        assert_f32_parity(from_dev(j["y"]), j["want_y"], what=f"thread {t} gemv")
+        assert_f32_parity(from_dev(j["c"]), j["want_c"], what=f"thread {t} gemm")
