@@ -113,6 +113,26 @@ __global__ __launch_bounds__(1024, 1) void fold(const int *in, float *out, int i
 
 __global__ void empty_kernel() {}
 
+// read_wide<kU>: every thread loads kU 16-byte chunks, each wave instruction a
+// contiguous 1 KB, one pass over the buffer (grid = n16 / (256 * kU)): the
+// streaming-read rate of a large buffer, the roofline of a read-only kernel.
+template <int kU>
+__global__ __launch_bounds__(256) void read_wide(const uint4 *p, size_t n16, uint32_t *out) {
+  const size_t base = static_cast<size_t>(blockIdx.x) * (256 * kU) + threadIdx.x;
+  uint4 v[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const size_t i = base + static_cast<size_t>(u) * 256;
+    v[u] = i < n16 ? p[i] : make_uint4(0, 0, 0, 0);
+  }
+  uint32_t acc = 0;
+#pragma unroll
+  for (int u = 0; u < kU; ++u)
+    acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  if (acc == 0x9e3779b9u)  // data-dependent store keeps the loads alive
+    out[threadIdx.x] = acc;
+}
+
 __global__ __launch_bounds__(256) void read_only(const uint4 *p, size_t n16, uint32_t *out) {
   uint32_t acc = 0;
   for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n16;
@@ -156,5 +176,17 @@ extern "C" __attribute__((visibility("default"))) int probe_empty(void *st) {
 extern "C" __attribute__((visibility("default"))) int probe_read(const void *p, size_t nbytes, uint32_t *out, int grid, void *st) {
   read_only<<<grid, 256, 0, static_cast<hipStream_t>(st)>>>(static_cast<const uint4 *>(p),
                                                             nbytes / 16, out);
+  return hipGetLastError();
+}
+
+extern "C" __attribute__((visibility("default"))) int probe_read_wide(const void *p, size_t nbytes, uint32_t *out, int unroll, void *st) {
+  const size_t n16 = nbytes / 16;
+  hipStream_t s = static_cast<hipStream_t>(st);
+  switch (unroll) {
+  case 1: read_wide<1><<<(n16 + 255) / 256, 256, 0, s>>>(static_cast<const uint4 *>(p), n16, out); break;
+  case 2: read_wide<2><<<(n16 + 511) / 512, 256, 0, s>>>(static_cast<const uint4 *>(p), n16, out); break;
+  case 4: read_wide<4><<<(n16 + 1023) / 1024, 256, 0, s>>>(static_cast<const uint4 *>(p), n16, out); break;
+  default: return -1;
+  }
   return hipGetLastError();
 }

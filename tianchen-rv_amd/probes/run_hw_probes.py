@@ -96,6 +96,24 @@ def main():
         us = graph_us(stream, launch)
         print(f"read-only {nbytes} B over {copies} rotating buffers, grid {grid} x 256: "
               f"{us:.2f} us per launch ({nbytes / us / 1e3:.0f} GB/s)", flush=True)
+    del bufs
+    torch.cuda.empty_cache()
+    # the streaming-read roofline at the block dot's size (configs[2] reads
+    # 142 606 336 B per launch), over 3 rotating buffers (> 256 MB MALL)
+    lib.probe_read_wide.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                    ctypes.c_int, ctypes.c_void_p]
+    nbytes, copies = 142606336, 3
+    bufs = torch.empty((copies, nbytes), dtype=torch.uint8, device=dev)
+    for unroll in (1, 2, 4):
+        k = [0]
+
+        def launch():
+            assert lib.probe_read_wide(bufs[k[0] % copies].data_ptr(), nbytes, sink.data_ptr(),
+                                       unroll, sp) == 0
+            k[0] += 1
+        us = graph_us(stream, launch, n=60)
+        print(f"read-wide {nbytes} B over {copies} rotating buffers, {unroll} x 16 B per thread: "
+              f"{us:.2f} us per launch ({nbytes / us / 1e3:.0f} GB/s)", flush=True)
 
 
 if __name__ == "__main__":
