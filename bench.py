@@ -34,6 +34,7 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published
 N = 4096
 MALL_BYTES = 256 << 20       # Infinity Cache
+HOST_COPIES = 48             # CPU-baseline GEMV weight copies (453 MB > host last-level cache)
 
 METRIC = "Q4_0 GEMV GB/s (% HBM peak); Q8_0 GEMM int8 TOPS (% MFMA peak)"
 
@@ -44,6 +45,31 @@ DEQ_BYTES = (N * N // 32) * (34 + 128)                          # 84 934 656
 DOT_ROWS = 16384
 DOT_BYTES = DOT_ROWS * (2 * (N // 32) * 34 + 4)                 # 142 671 872
 GEMM_OPS = 2.0 * N * N * N                                      # 137 438 953 472
+
+
+_INPUTS = {}
+
+
+def inputs(name: str):
+    """The synthetic host arrays, built once per process: the same bytes feed
+    the GPU runs and the CPU baselines."""
+    if name not in _INPUTS:
+        import synth
+        seeds = synth.SEEDS
+        make = {
+            "gemv_w": lambda: synth.q4_0_matrix(N, N, seeds["gemv_w"], 0.02),
+            "gemv_x": lambda: synth.q8_0_matrix(1, N, seeds["gemv_x"], 1.0).reshape(-1),
+            "gemm_a": lambda: synth.q8_0_matrix(N, N, seeds["gemm_a"], 1.0),
+            "gemm_b": lambda: synth.q8_0_matrix(N, N, seeds["gemm_b"], 0.02),
+            "add_a": lambda: synth.uniform_f32(seeds["add_a"], 1 << 24),
+            "add_b": lambda: synth.uniform_f32(seeds["add_b"], 1 << 24),
+            "dequant_q": lambda: synth.quantize_q8_0(
+                synth.normal_f32(seeds["dequant_w"], N * N, 0.0, 0.02)),
+            "dot_x": lambda: synth.q8_0_matrix(DOT_ROWS, N, seeds["dot_x"], 1.0),
+            "dot_y": lambda: synth.q8_0_matrix(DOT_ROWS, N, seeds["dot_y"], 1.0),
+        }[name]
+        _INPUTS[name] = make()
+    return _INPUTS[name]
 
 
 def log(msg: str) -> None:
@@ -126,10 +152,9 @@ def copies_for(nbytes: int, minimum: int = 2) -> int:
 
 
 def bench_gemv(torch, lib, stream, args):
-    import synth
     log("GEMV inputs: W 4096x4096 Q4_0 (seed 1006, N(0,0.02)), x Q8_0 (seed 1007, N(0,1))")
-    w = synth.q4_0_matrix(N, N, synth.SEEDS["gemv_w"], 0.02)
-    x = synth.q8_0_matrix(1, N, synth.SEEDS["gemv_x"], 1.0).reshape(-1)
+    w = inputs("gemv_w")
+    x = inputs("gemv_x")
     dev = torch.device("cuda:0")
     copies = max(args.copies, copies_for(w.size, 2))
     wd = torch.empty((copies, w.size), dtype=torch.uint8, device=dev)
@@ -166,9 +191,8 @@ def bench_gemv_rows(torch, lib, stream, args):
     is the 4096-row configs[3] matrix repeated, one launch per rotating copy.
     Past a few tens of MB the fixed cost of a launch (the launch itself and one
     short read) is amortised and the kernel's own streaming rate shows."""
-    import synth
-    w = synth.q4_0_matrix(N, N, synth.SEEDS["gemv_w"], 0.02)
-    x = synth.q8_0_matrix(1, N, synth.SEEDS["gemv_x"], 1.0).reshape(-1)
+    w = inputs("gemv_w")
+    x = inputs("gemv_x")
     dev = torch.device("cuda:0")
     wt = torch.from_numpy(w).to(dev)
     xd = torch.from_numpy(x).to(dev)
@@ -205,11 +229,10 @@ def bench_gemv_rows(torch, lib, stream, args):
 
 
 def bench_gemm(torch, lib, stream, args):
-    import synth
     log("GEMM inputs: A 4096 tokens x 4096 Q8_0 (seed 1008, N(0,1)), "
         "B 4096x4096 Q8_0 (seed 1009, N(0,0.02))")
-    a = synth.q8_0_matrix(N, N, synth.SEEDS["gemm_a"], 1.0)
-    b = synth.q8_0_matrix(N, N, synth.SEEDS["gemm_b"], 0.02)
+    a = inputs("gemm_a")
+    b = inputs("gemm_b")
     dev = torch.device("cuda:0")
     ad = torch.from_numpy(a).to(dev)
     bd = torch.from_numpy(b).to(dev)
@@ -241,7 +264,6 @@ def bench_configs(torch, lib, stream, args):
     """configs[0..2]: add f32 2^24, Q8_0 dequant 4096x4096, Q8_0.Q8_0 block dot
     16384 x 4096 -- each over rotating input sets larger than the MALL -- plus
     the x16-repacked Q4_0 GEMV and the Q4_0 x Q8_0 prefill GEMM."""
-    import synth
     dev = torch.device("cuda:0")
     sp = stream.cuda_stream
     out = {}
@@ -250,8 +272,8 @@ def bench_configs(torch, lib, stream, args):
     # add
     n = 1 << 24
     sets = copies_for(12 * n, 2)
-    a = torch.from_numpy(synth.uniform_f32(synth.SEEDS["add_a"], n)).to(dev)
-    b = torch.from_numpy(synth.uniform_f32(synth.SEEDS["add_b"], n)).to(dev)
+    a = torch.from_numpy(inputs("add_a")).to(dev)
+    b = torch.from_numpy(inputs("add_b")).to(dev)
     A = torch.empty((sets, n), device=dev); A[:] = a
     B = torch.empty((sets, n), device=dev); B[:] = b
     C = torch.empty((sets, n), device=dev)
@@ -266,7 +288,7 @@ def bench_configs(torch, lib, stream, args):
 
     # dequant
     nb = N * N // 32
-    q = synth.quantize_q8_0(synth.normal_f32(synth.SEEDS["dequant_w"], N * N, 0.0, 0.02))
+    q = inputs("dequant_q")
     sets = copies_for(DEQ_BYTES, 2)
     Q = torch.empty((sets, q.size), dtype=torch.uint8, device=dev)
     Q[:] = torch.from_numpy(q).to(dev)
@@ -281,8 +303,8 @@ def bench_configs(torch, lib, stream, args):
     del Q, Y, reg
 
     # block dot
-    xq = synth.q8_0_matrix(DOT_ROWS, N, synth.SEEDS["dot_x"], 1.0)
-    yq = synth.q8_0_matrix(DOT_ROWS, N, synth.SEEDS["dot_y"], 1.0)
+    xq = inputs("dot_x")
+    yq = inputs("dot_y")
     sets = copies_for(DOT_BYTES, 2)
     X = torch.empty((sets, xq.size), dtype=torch.uint8, device=dev)
     X[:] = torch.from_numpy(xq.reshape(-1)).to(dev)
@@ -306,8 +328,8 @@ def bench_configs(torch, lib, stream, args):
     del X, Yd, S, reg
 
     # x16 repacked decode GEMV (the reference's selected decode path at VLEN128)
-    w = synth.q4_0_matrix(N, N, synth.SEEDS["gemv_w"], 0.02)
-    x = synth.q8_0_matrix(1, N, synth.SEEDS["gemv_x"], 1.0).reshape(-1)
+    w = inputs("gemv_w")
+    x = inputs("gemv_x")
     nb = N // 32
     src = torch.from_numpy(w.reshape(N // 16, 16, nb, 18).transpose(0, 2, 1, 3).copy()).to(dev)
     packed = torch.empty(N // 16 * nb * 288, dtype=torch.uint8, device=dev)
@@ -330,7 +352,7 @@ def bench_configs(torch, lib, stream, args):
     del P, Yv, reg, src, packed
 
     # Q4_0 x Q8_0 prefill GEMM 4096^3 (MFMA)
-    a = synth.q8_0_matrix(N, N, synth.SEEDS["gemm_a"], 1.0)
+    a = inputs("gemm_a")
     ad = torch.from_numpy(a).to(dev)
     wd = torch.from_numpy(w).to(dev)
     cd = torch.empty(N * N, device=dev)
@@ -367,19 +389,23 @@ def cpu_baseline(seconds: float):
     the host: whole 4096x4096 Q4_0 x Q8_0 GEMVs repeated for `seconds`, OpenMP
     over rows (each row's fold stays serial, so results equal the 1-thread
     run), plus a 1-thread figure over a quarter of the time."""
-    import synth
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_binding
 
+    import numpy as np
+
     ora = oracle_binding.load()
     threads = cpu_threads()
-    w = synth.q4_0_matrix(N, N, synth.SEEDS["gemv_w"], 0.02)
-    x = synth.q8_0_matrix(1, N, synth.SEEDS["gemv_x"], 1.0).reshape(-1)
+    w = inputs("gemv_w")
+    x = inputs("gemv_x")
+    # rotating weight copies, 453 MB in all: more than the host's last-level
+    # cache, as the GPU's copies exceed its Infinity Cache
+    ws = np.ascontiguousarray(np.broadcast_to(w, (HOST_COPIES,) + w.shape))
 
     def rate(nt, budget):
         reps, t0 = 0, time.perf_counter()
         while True:
-            ora.gemm_q4_0(N, w, x, 0, N, 1, w.shape[1], 1, nt)
+            ora.gemm_q4_0(N, ws[reps % HOST_COPIES], x, 0, N, 1, w.shape[1], 1, nt)
             reps += 1
             dt = time.perf_counter() - t0
             if dt >= budget:
@@ -400,9 +426,9 @@ def cpu_baseline(seconds: float):
     return {
         "value": round(many, 3), "unit": "GB/s", "cores": threads, "kind": "port",
         "sample": (f"oracle/ scalar C (gcc -O3 -march=x86-64-v3, OpenMP over rows, serial "
-                   f"fmaf fold per row): {reps} whole 4096x4096 Q4_0xQ8_0 GEMVs in "
-                   f"{seconds:.0f} s on {threads} threads of {cpu}; 1 thread: "
-                   f"{one:.3f} GB/s ({reps1} GEMVs)"),
+                   f"fmaf fold per row): {reps} whole 4096x4096 Q4_0xQ8_0 GEMVs over "
+                   f"{HOST_COPIES} rotating weight copies in {seconds:.0f} s on {threads} "
+                   f"threads of {cpu}; 1 thread: {one:.3f} GB/s ({reps1} GEMVs)"),
         "value_1thread": round(one, 4),
     }
 
@@ -418,7 +444,7 @@ def cpu_baseline_gemm(seconds: float):
     ora = oracle_binding.load()
     threads = cpu_threads()
     rows = 16
-    a = synth.q8_0_matrix(N, N, synth.SEEDS["gemm_a"], 1.0)
+    a = inputs("gemm_a")
     b = synth.q8_0_matrix(rows, N, synth.SEEDS["gemm_b"], 0.02)
     reps, t0 = 0, time.perf_counter()
     while True:
@@ -432,6 +458,76 @@ def cpu_baseline_gemm(seconds: float):
     return {"value": round(tops, 5), "unit": "TOPS", "cores": threads, "kind": "port",
             "sample": (f"oracle/ scalar C, OpenMP over rows: {reps} slices of {rows} weight rows "
                        f"x 4096 tokens x 4096 (1/256 of the GEMM each) in {dt:.1f} s")}
+
+
+def cpu_baseline_configs(seconds: float):
+    """The oracle on the host beside each of configs[0..2], the x16 GEMV and
+    the Q4_0 GEMM, each timed for `seconds` on a bounded sample of its workload
+    (the element-wise oracles are single-threaded C loops; the row-parallel
+    ones use OpenMP over rows with every row's fold serial)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_binding
+
+    ora = oracle_binding.load()
+    threads = cpu_threads()
+
+    def timed(call):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            call()
+            reps += 1
+            dt = time.perf_counter() - t0
+            if dt >= seconds:
+                return reps, dt
+
+    def entry(value, unit, cores, sample):
+        return {"value": round(value, 4), "unit": unit, "cores": cores, "kind": "port",
+                "sample": sample}
+
+    out = {}
+    n = 1 << 24  # the whole config: 201 MB per call
+    a = inputs("add_a")
+    b = inputs("add_b")
+    reps, dt = timed(lambda: ora.add_f32(a, b))
+    out["add_f32"] = entry(ADD_BYTES * reps / dt / 1e9, "GB/s", 1,
+                           f"{reps} whole adds of n = 2^24 in {dt:.1f} s")
+    q = inputs("dequant_q")
+    reps, dt = timed(lambda: ora.dequantize_row_q8_0(q, N * N))
+    out["dequant_q8_0"] = entry(DEQ_BYTES * reps / dt / 1e9, "GB/s", 1,
+                                f"{reps} whole 4096x4096 dequants in {dt:.1f} s")
+    xq = inputs("dot_x")
+    yq = inputs("dot_y")
+    rb = xq.shape[1]
+    reps, dt = timed(lambda: ora.vec_dot_q8_0_rows(N, xq, rb, yq, rb, DOT_ROWS, threads))
+    out["vec_dot_q8_0_q8_0"] = entry(DOT_BYTES * reps / dt / 1e9, "GB/s", threads,
+                                     f"{reps} whole 16384 x 4096 block dots (143 MB each) in "
+                                     f"{dt:.1f} s, OpenMP over rows")
+    w = inputs("gemv_w")
+    x = inputs("gemv_x")
+    nb = N // 32
+    packed = ora.pack_q4_0x16(
+        w.reshape(N // 16, 16, nb, 18).transpose(0, 2, 1, 3).copy().reshape(-1), N // 16 * nb)
+    import numpy as np
+    ps = np.ascontiguousarray(np.broadcast_to(packed, (HOST_COPIES,) + packed.shape))
+    k = [0]
+
+    def repack():
+        ora.repack_gemv_q4_0(N, ps[k[0] % HOST_COPIES], x, N)
+        k[0] += 1
+    reps, dt = timed(repack)
+    out["repack_gemv_q4_0_q8_0"] = entry(GEMV_BYTES * reps / dt / 1e9, "GB/s", 1,
+                                         f"{reps} whole 4096x4096 x16 GEMVs over {HOST_COPIES} "
+                                         f"rotating weight copies in {dt:.1f} s")
+    a8 = inputs("gemm_a")
+    w16 = w[:16].copy()
+    reps, dt = timed(lambda: ora.gemm_q4_0(N, w16, a8, a8.shape[1], 16, N, w16.shape[1], N,
+                                           threads))
+    out["q4_0_q8_0_gemm"] = entry(2.0 * 16 * N * N * reps / dt / 1e12, "TOPS", threads,
+                                  f"{reps} slices of 16 weight rows x 4096 tokens x 4096 "
+                                  f"(1/256 of the GEMM each) in {dt:.1f} s, OpenMP over rows")
+    log("CPU oracle configs: " + ", ".join(f"{k} {v['value']} {v['unit']}"
+                                           for k, v in out.items()))
+    return out
 
 
 def load_traffic():
@@ -558,6 +654,9 @@ def main():
             "workload": "gemv_q4_0_q8_0 at more weight rows, K 4096 (the configs[3] matrix "
                         "repeated); same kernel as `value`", "by_rows": res["gemv_rows"]}
     if "configs" in res:
+        if args.cpu_seconds > 0:
+            for k, v in cpu_baseline_configs(max(0.5, args.cpu_seconds / 10)).items():
+                res["configs"][k]["cpu_baseline"] = v
         line["configs"] = res["configs"]
         if "value" not in line:
             first = next(iter(res["configs"].values()))
