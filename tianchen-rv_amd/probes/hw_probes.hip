@@ -56,8 +56,9 @@ __global__ __launch_bounds__(512) void mix(const int *in, float *out, int iters)
 
 typedef float v32f __attribute__((ext_vector_type(32)));
 
-template <int kMode>
-__global__ __launch_bounds__(1024, 1) void fold(const int *in, float *out, int iters) {
+template <int kMode, bool kClock = false>
+__global__ __launch_bounds__(1024, 1) void fold(const int *in, float *out, int iters,
+                                                long long *clk = nullptr) {
   __shared__ __align__(16) int8_t q[256 * 272];
   __shared__ __align__(16) float dsc[8][256];
   const int tid = threadIdx.x;
@@ -76,6 +77,11 @@ __global__ __launch_bounds__(1024, 1) void fold(const int *in, float *out, int i
   for (int e = 0; e < 16; ++e)
     acc[e] = 0.0f;
   v16i iacc = {};
+  long long c0 = 0, w0 = 0;
+  if (kClock && blockIdx.x == 0 && tid == 0) {
+    c0 = clock64();
+    w0 = wall_clock64();
+  }
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
     for (int b = 0; b < 8; b += 2) {
@@ -104,6 +110,10 @@ __global__ __launch_bounds__(1024, 1) void fold(const int *in, float *out, int i
         acc[b] += dxy[b] + dxy[31 - b];
       __builtin_amdgcn_sched_barrier(0);
     }
+  }
+  if (kClock && blockIdx.x == 0 && tid == 0) {
+    clk[0] = clock64() - c0;       // shader-clock cycles of this wave's loop
+    clk[1] = wall_clock64() - w0;  // constant-rate ticks over the same span
   }
   float r = 0.0f;
   for (int e = 0; e < 16; ++e)
@@ -188,5 +198,12 @@ extern "C" __attribute__((visibility("default"))) int probe_read_wide(const void
   case 4: read_wide<4><<<(n16 + 1023) / 1024, 256, 0, s>>>(static_cast<const uint4 *>(p), n16, out); break;
   default: return -1;
   }
+  return hipGetLastError();
+}
+
+// The shader clock during the GEMM inner loop (fold mode 0): wave 0 of
+// work-group 0 records its loop's clock64 and wall_clock64 deltas in clk[0..1].
+extern "C" __attribute__((visibility("default"))) int probe_fold_clock(const int *in, float *out, long long *clk, int iters, int grid, void *st) {
+  fold<0, true><<<grid, 1024, 0, static_cast<hipStream_t>(st)>>>(in, out, iters, clk);
   return hipGetLastError();
 }

@@ -81,6 +81,17 @@ def main():
         print(f"fold mode {mode} ({name}): {ms:.3f} ms = {ms * 1e6 / tile_blocks:.2f} ns per "
               f"32x32 tile and block per SIMD [256 x 1024 threads, {fold_iters} x 8 blocks]",
               flush=True)
+    # the shader clock while the GEMM inner loop runs: one wave's clock64 cycles
+    # over its wall_clock64 ticks (a constant 100 MHz counter on this part)
+    lib.probe_fold_clock.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    clk = torch.zeros(2, dtype=torch.int64, device=dev)
+    assert lib.probe_fold_clock(inp.data_ptr(), fold_out.data_ptr(), clk.data_ptr(),
+                                fold_iters, 256, sp) == 0
+    torch.cuda.synchronize()
+    cycles, ticks = (int(v) for v in clk.cpu())
+    print(f"shader clock in the GEMM inner loop: {cycles / ticks * 0.1:.2f} GHz ({cycles} cycles "
+          f"over {ticks} ticks of the 100 MHz wall clock, wave 0 of work-group 0)", flush=True)
     print(f"empty kernel, graph of 1000: {graph_us(stream, lambda: lib.probe_empty(sp)):.2f} "
           f"us per launch", flush=True)
     nbytes = 9437184
