@@ -644,7 +644,7 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(m["tops"], 2), "peak": INT8_PEAK_TOPS,
                          "unit": "TOPS", "frac": round(m["tops"] / INT8_PEAK_TOPS, 4),
                          "traffic": traffic.get("q8_0_q8_0_gemm", {}).get("bytes"),
-                         "kernel": "tcrv::gemm_occ<false>", "ops_per_launch": GEMM_OPS},
+                         "kernel": "tcrv::gemm_wide<false>", "ops_per_launch": GEMM_OPS},
         }
         if "gemv" not in res:
             line.update({"value": line["gemm"]["value"], "unit": "TOPS",

@@ -238,6 +238,10 @@ def test_q4_0_gemm_multi_column(hip, oracle, dev, nr, nc, nb):
     (1, 45, 1, 0, 0),         # single weight row, one block
     (1, 300, 64, 0, 8),       # single weight row: register-direct block dots
     (512, 512, 128, 0, 0),
+    # 256+ weight rows take the wide 256x128 tile with 4-block K chunks
+    (300, 130, 7, 16, 32),    # partial wide tiles both ways, 4 + 3 blocks, padded strides
+    (256, 2, 1, 0, 0),        # one block: only the partial chunk
+    (520, 257, 13, 0, 4),     # three tile rows, 3 full chunks + 1 block
 ])
 def test_q8_0_gemm(hip, oracle, dev, nr, nc, nb, xpad, ypad):
     n = nb * 32
@@ -414,7 +418,8 @@ def test_repack_gemv_two_byte_aligned_activation(hip, oracle, dev, quant, nc, nb
 
 # ------------------------------------------------ a7 Q4_0 GEMM on MFMA (nc > 1) ---
 
-@pytest.mark.parametrize("nr,nc,nb,pad", [(512, 512, 128, 0), (130, 70, 9, 16), (64, 2, 3, 0)])
+@pytest.mark.parametrize("nr,nc,nb,pad", [(512, 512, 128, 0), (130, 70, 9, 16), (64, 2, 3, 0),
+                                          (300, 130, 7, 16), (256, 3, 1, 0)])
 def test_q4_0_gemm_mfma_shapes(hip, oracle, dev, nr, nc, nb, pad):
     n = nb * 32
     w = np.pad(synth.q4_0_matrix(nr, n, 71, 0.02), ((0, 0), (0, pad)))

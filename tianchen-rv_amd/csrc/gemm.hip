@@ -11,8 +11,10 @@
 // fold of that block is applied to the tile right away, in ascending block
 // order, so every output element sees the reference's sequence of roundings.
 //
-// Two kernels:
-//   gemm_occ<false>        rows 4-byte aligned (the fast path, below);
+// Three kernels:
+//   gemm_wide<false>       rows 4-byte aligned, at least 256 weight rows: 256 x 128
+//                          output tile per work-group (the fast path, below);
+//   gemm_occ<false>        rows 4-byte aligned, fewer weight rows: 128 x 128;
 //   gemm_q8_0_q8_0_kernel  any 2-byte aligned rows: 4 waves, 2x2 tiles each,
 //                          raw block bytes through LDS, scalar scale epilogue.
 #include "tcrv_hip_internal.h"
@@ -345,12 +347,12 @@ typedef float v32f __attribute__((ext_vector_type(32)));
 //   syh = the same for the token scale (Q8_0), or 1.0 (Q4_0: dxy = d_x);
 //   syc = this lane's token-column scale of block 0 (Q4_0 fold only).
 // qa/qb: this lane's 16 quant bytes of block 0 of the chunk.
-template <bool kQ4, bool kTwo>
+template <bool kQ4, bool kTwo, int kSStride = kFbBM>
 __device__ __forceinline__ void fold_pair(float (&acc)[16], const int8_t *qa, const int8_t *qb,
                                           const float *sxh, const float *syh, const float *syc,
                                           int b) {
-  const float dx = sxh[b * kFbBM];
-  const float dy_op = kQ4 ? 1.0f : syh[b * kFbBM];
+  const float dx = sxh[b * kSStride];
+  const float dy_op = kQ4 ? 1.0f : syh[b * kSStride];
   const v32f dxy = __builtin_amdgcn_mfma_f32_32x32x1f32(dx, dy_op, v32f{}, 0, 0, 0);
 #pragma unroll
   for (int j = 0; j < (kTwo ? 2 : 1); ++j) {
@@ -358,7 +360,7 @@ __device__ __forceinline__ void fold_pair(float (&acc)[16], const int8_t *qa, co
     const v4i bq = *reinterpret_cast<const v4i *>(qb + (b + j) * kQK);
     const v16i sumi = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, v16i{}, 0, 0, 0);
     if constexpr (kQ4) {
-      const float dy = syc[(b + j) * kFbBM];
+      const float dy = syc[(b + j) * kSStride];
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         acc[e] = fmaf(static_cast<float>(sumi[e]) * dxy[16 * j + e], dy, acc[e]);
@@ -482,6 +484,132 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_occ(
       s[row * bs + col] = acc[e];
   }
 }
+
+// Wide tile: 256 weight rows x 128 tokens per work-group, 16 waves, each wave
+// two 32x32 tiles stacked in M (64 weight rows x 32 tokens), so every staged
+// token row serves twice as many tiles as in gemm_occ; K chunks of 4 blocks,
+// double-buffered (384 staged rows of 8 blocks would not fit twice).
+constexpr int kWBM = 256, kWBN = 128, kWKB = 4;
+constexpr int kWQRow = kWKB * kQK + 16;           // 144: quant bytes per staged row (+16 pad)
+constexpr int kWRows = kWBM + kWBN;               // 384 staged rows per chunk
+constexpr int kWStage = kWRows * kWQRow;
+constexpr int kWTasks = kWRows * (kWKB / 2);      // 768 block-pair tasks per chunk
+
+template <bool kQ4>
+__global__ __launch_bounds__(kOcThreads, 1) void gemm_wide(
+    size_t nb, float *s, const uint8_t *vx, const uint8_t *vy, size_t by, size_t nr,
+    size_t nc, size_t bx, size_t bs) {
+  __shared__ __align__(16) int8_t q[2][kWStage];
+  __shared__ __align__(16) float dsc[2][kWKB][kWRows];  // [stage][block][row]
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int wm = wave >> 2, wn = wave & 3;  // 64 weight rows x 32 tokens per wave
+  const int li = lane & 31, h = lane >> 5;
+  const unsigned tiles_m = static_cast<unsigned>((nr + kWBM - 1) / kWBM);
+  const unsigned tiles_n = static_cast<unsigned>((nc + kWBN - 1) / kWBN);
+  unsigned tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const size_t m0 = static_cast<size_t>(tm) * kWBM;
+  const size_t n0 = static_cast<size_t>(tn) * kWBN;
+
+  // staging task: thread t < 768 stages row t/2 (weights 0..255, tokens
+  // 256..383), block pair t%2 of the chunk; waves 12-15 stage nothing
+  const bool stager = tid < kWTasks;
+  const int sr = min(tid >> 1, kWRows - 1), sm = tid & 1;
+  const bool wrow = sr < kWBM;
+  const uint8_t *sbase = wrow ? vx + min(m0 + sr, nr - 1) * bx
+                              : vy + min(n0 + (sr - kWBM), nc - 1) * by;
+  const bool q4_task = kQ4 && wrow;  // wave-uniform: waves 0-7 stage weights
+  const int sblk = q4_task ? kQ4Bytes : kQ8Bytes;
+
+  float acc[2][16];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      acc[i][e] = 0.0f;
+
+  const size_t nchunks = (nb + kWKB - 1) / kWKB;
+  PairRegs pr;
+  auto chunk_task = [&](size_t c, bool &active, bool &two) {
+    const int nbc = static_cast<int>(min(static_cast<size_t>(kWKB), nb - c * kWKB));
+    active = stager && 2 * sm < nbc;
+    two = 2 * sm + 1 < nbc;
+  };
+  bool act, two;
+  chunk_task(0, act, two);
+  if (act)
+    load_task(pr, sbase + 2 * sm * sblk, two, q4_task);
+  if (act)
+    store_task(pr, two, q4_task, q[0] + sr * kWQRow + 64 * sm, &dsc[0][2 * sm][sr],
+               &dsc[0][2 * sm + 1][sr]);
+  __syncthreads();
+
+  // this lane's operand addresses in stage 0 for the wave's first tile (the
+  // second tile and stage 1 are fixed offsets away)
+  const int8_t *qa0 = q[0] + (wm * 64 + li) * kWQRow + 16 * h;
+  const int8_t *qb0 = q[0] + (kWBM + wn * 32 + li) * kWQRow + 16 * h;
+  const float *sxh0 = &dsc[0][h][wm * 64 + li];
+  const float *syh0 = &dsc[0][h][kWBM + wn * 32 + li];
+  const float *syc0 = &dsc[0][0][kWBM + wn * 32 + li];
+  constexpr int kDscStage = kWKB * kWRows;
+
+  const size_t nfull = nb / kWKB;
+  for (size_t c = 0; c < nfull; ++c) {
+    const int st = static_cast<int>(c & 1);
+    bool act1 = false, two1 = false;
+    if (c + 1 < nchunks) {
+      chunk_task(c + 1, act1, two1);
+      if (act1)
+        load_task(pr, sbase + ((c + 1) * kWKB + 2 * sm) * sblk, two1, q4_task);
+    }
+#pragma unroll
+    for (int b = 0; b < kWKB; b += 2) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        fold_pair<kQ4, true, kWRows>(acc[i], qa0 + i * 32 * kWQRow + st * kWStage,
+                                     qb0 + st * kWStage, sxh0 + i * 32 + st * kDscStage,
+                                     syh0 + st * kDscStage, syc0 + st * kDscStage, b);
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          asm volatile("" : "+v"(acc[i][e]));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (act1)
+      store_task(pr, two1, q4_task, q[st ^ 1] + sr * kWQRow + 64 * sm,
+                 &dsc[st ^ 1][2 * sm][sr], &dsc[st ^ 1][2 * sm + 1][sr]);
+    __syncthreads();
+  }
+  const int nbc = static_cast<int>(nb - nfull * kWKB);
+  if (nbc > 0) {
+    const int st = static_cast<int>(nfull & 1);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int8_t *qa = qa0 + i * 32 * kWQRow + st * kWStage;
+      const int8_t *qb = qb0 + st * kWStage;
+      const float *sxh = sxh0 + i * 32 + st * kDscStage;
+      const float *syh = syh0 + st * kDscStage;
+      const float *syc = syc0 + st * kDscStage;
+      int b = 0;
+      for (; b + 1 < nbc; b += 2)
+        fold_pair<kQ4, true, kWRows>(acc[i], qa, qb, sxh, syh, syc, b);
+      if (b < nbc)
+        fold_pair<kQ4, false, kWRows>(acc[i], qa, qb, sxh, syh, syc, b);
+    }
+  }
+
+  const size_t col = n0 + wn * 32 + li;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const size_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (row < nr && col < nc)
+        s[row * bs + col] = acc[i][e];
+    }
+}
 }  // namespace tcrv
 
 namespace tcrv_host {
@@ -496,6 +624,13 @@ int q4_0_gemm_mfma(size_t nb, float *s, const uint8_t *vx, size_t bx, const uint
       ((nr + tcrv::kFbBM - 1) / tcrv::kFbBM) * ((nc + tcrv::kFbBN - 1) / tcrv::kFbBN);
   if (tiles > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
+  if (nr >= static_cast<size_t>(tcrv::kWBM)) {  // at least one full wide tile of weight rows
+    const size_t wtiles =
+        ((nr + tcrv::kWBM - 1) / tcrv::kWBM) * ((nc + tcrv::kWBN - 1) / tcrv::kWBN);
+    tcrv::gemm_wide<true><<<dim3(static_cast<unsigned>(wtiles)), dim3(tcrv::kOcThreads), 0,
+                            as_stream(stream)>>>(nb, s, vx, vy, by, nr, nc, bx, bs);
+    return launch_status();
+  }
   tcrv::gemm_occ<true><<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kOcThreads), 0,
                          as_stream(stream)>>>(nb, s, vx, vy, by, nr, nc, bx, bs);
   return launch_status();
@@ -533,6 +668,13 @@ extern "C" int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx,
         ((nr + tcrv::kFbBM - 1) / tcrv::kFbBM) * ((nc + tcrv::kFbBN - 1) / tcrv::kFbBN);
     if (tiles > 0x7fffffffu)
       return TCRV_HIP_ERR_TOO_LARGE;
+    if (nr >= static_cast<size_t>(tcrv::kWBM)) {  // at least one full wide tile of weight rows
+      const size_t wtiles =
+          ((nr + tcrv::kWBM - 1) / tcrv::kWBM) * ((nc + tcrv::kWBN - 1) / tcrv::kWBN);
+      tcrv::gemm_wide<false><<<dim3(static_cast<unsigned>(wtiles)), dim3(tcrv::kOcThreads), 0,
+                               as_stream(stream)>>>(nb, s, vx, vy, by, nr, nc, bx, bs);
+      return launch_status();
+    }
     tcrv::gemm_occ<false><<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kOcThreads), 0,
                             as_stream(stream)>>>(nb, s, vx, vy, by, nr, nc, bx, bs);
     return launch_status();

@@ -25,7 +25,7 @@ import sys
 
 KERNELS = {
     "gemv_q4_0_q8_0": "gemv_q4_0_q8_0_direct",
-    "q8_0_q8_0_gemm": "gemm_occ<false>",
+    "q8_0_q8_0_gemm": "gemm_wide<false>",
     "calib": "add_f32_vec4",
 }
 CALIB_BYTES = {"FETCH_SIZE": 8 << 24, "WRITE_SIZE": 4 << 24}  # per add_f32 launch, n = 2^24
