@@ -45,6 +45,8 @@ DEQ_BYTES = (N * N // 32) * (34 + 128)                          # 84 934 656
 DOT_ROWS = 16384
 DOT_BYTES = DOT_ROWS * (2 * (N // 32) * 34 + 4)                 # 142 671 872
 GEMM_OPS = 2.0 * N * N * N                                      # 137 438 953 472
+PACK_BYTES = 2 * N * (N // 32) * 18                             # 18 874 368
+QUANT_BYTES = N * N * 4 + (N * N // 32) * 34                    # 84 934 656
 
 
 _INPUTS = {}
@@ -60,6 +62,7 @@ def inputs(name: str):
             "gemv_w": lambda: synth.q4_0_matrix(N, N, seeds["gemv_w"], 0.02),
             "gemv_x": lambda: synth.q8_0_matrix(1, N, seeds["gemv_x"], 1.0).reshape(-1),
             "gemm_a": lambda: synth.q8_0_matrix(N, N, seeds["gemm_a"], 1.0),
+            "gemm_a_f32": lambda: synth.normal_f32(seeds["gemm_a"], N * N, 0.0, 1.0),
             "gemm_b": lambda: synth.q8_0_matrix(N, N, seeds["gemm_b"], 0.02),
             "add_a": lambda: synth.uniform_f32(seeds["add_a"], 1 << 24),
             "add_b": lambda: synth.uniform_f32(seeds["add_b"], 1 << 24),
@@ -349,7 +352,39 @@ def bench_configs(torch, lib, stream, args):
     out["repack_gemv_q4_0_q8_0"] = {"workload": "a8 x16-repacked Q4_0 GEMV 4096x4096",
                                     "us": round(us, 3), "GB/s": round(GEMV_BYTES / us / 1e3, 1),
                                     "sets": sets}
-    del P, Yv, reg, src, packed
+    # the x16 pack of the same weights (read 9.4 MB, write 9.4 MB)
+    src_all = torch.empty((sets, packed.numel()), dtype=torch.uint8, device=dev)
+    src_all[:] = src.view(-1)
+    fn = checked(lib.tcrv_hip_pack_q4_0_to_q4_0x16, "pack")
+    ptrs = [(src_all[i].data_ptr(), P[i].data_ptr()) for i in range(sets)]
+    reg = Region(torch, stream, lambda i: fn(N // 16 * nb, ptrs[i % sets][0], ptrs[i % sets][1],
+                                             sp), 200)
+    reg.run()
+    us = reg.run() * 1e3 / 200
+    same_as_eager(torch, stream, P[199 % sets],
+                  lambda o: fn(N // 16 * nb, src_all[199 % sets].data_ptr(), o, sp), "pack")
+    out["pack_q4_0_to_q4_0x16"] = {"workload": "a8 pack_q4_0_to_q4_0x16, 4096x4096 Q4_0 weights",
+                                   "us": round(us, 3), "GB/s": round(PACK_BYTES / us / 1e3, 1),
+                                   "sets": sets}
+    del P, Yv, reg, src, packed, src_all
+
+    # a10 quantize_row_q8_0: 4096 activation rows x 4096 f32 -> Q8_0 (the prefill
+    # GEMM's activation operand; read 64 MiB, write 17.8 MB)
+    xf = torch.from_numpy(inputs("gemm_a_f32")).to(dev)
+    sets = copies_for(QUANT_BYTES, 2)
+    XF = torch.empty((sets, N * N), device=dev)
+    XF[:] = xf
+    QO = torch.empty((sets, N * N // 32 * 34), dtype=torch.uint8, device=dev)
+    fn = checked(lib.tcrv_hip_quantize_row_q8_0, "quantize")
+    ptrs = [(XF[i].data_ptr(), QO[i].data_ptr()) for i in range(sets)]
+    reg = Region(torch, stream, lambda i: fn(N * N, ptrs[i % sets][0], ptrs[i % sets][1], sp),
+                 steps)
+    reg.run()
+    us = reg.run() * 1e3 / steps
+    out["quantize_row_q8_0"] = {"workload": "a10 quantize_row_q8_0, 4096 x 4096 f32 -> Q8_0",
+                                "us": round(us, 3), "GB/s": round(QUANT_BYTES / us / 1e3, 1),
+                                "sets": sets}
+    del XF, QO, xf, reg
 
     # Q4_0 x Q8_0 prefill GEMM 4096^3 (MFMA)
     a = inputs("gemm_a")
@@ -518,6 +553,14 @@ def cpu_baseline_configs(seconds: float):
     out["repack_gemv_q4_0_q8_0"] = entry(GEMV_BYTES * reps / dt / 1e9, "GB/s", 1,
                                          f"{reps} whole 4096x4096 x16 GEMVs over {HOST_COPIES} "
                                          f"rotating weight copies in {dt:.1f} s")
+    src = w.reshape(N // 16, 16, nb, 18).transpose(0, 2, 1, 3).copy().reshape(-1)
+    reps, dt = timed(lambda: ora.pack_q4_0x16(src, N // 16 * nb))
+    out["pack_q4_0_to_q4_0x16"] = entry(PACK_BYTES * reps / dt / 1e9, "GB/s", 1,
+                                        f"{reps} packs of the 4096x4096 Q4_0 weights in {dt:.1f} s")
+    xf = inputs("gemm_a_f32")
+    reps, dt = timed(lambda: ora.quantize_q8_0(xf))
+    out["quantize_row_q8_0"] = entry(QUANT_BYTES * reps / dt / 1e9, "GB/s", 1,
+                                     f"{reps} quantizations of 4096 x 4096 f32 in {dt:.1f} s")
     a8 = inputs("gemm_a")
     w16 = w[:16].copy()
     reps, dt = timed(lambda: ora.gemm_q4_0(N, w16, a8, a8.shape[1], 16, N, w16.shape[1], N,
