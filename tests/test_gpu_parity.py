@@ -359,6 +359,24 @@ def test_pack_q8_0x16(hip, oracle, dev, nblocks):
     assert np.array_equal(from_dev(dst), oracle.pack_q8_0x16(src, nblocks))
 
 
+@pytest.mark.parametrize("quant,nblocks", [("q4_0", 33), ("q8_0", 17)])
+def test_pack_x16_two_byte_aligned_source(hip, oracle, dev, quant, nblocks):
+    """16-byte aligned spans take the LDS-staged pack; a source only 2-byte
+    aligned takes the per-dword gather: both give the oracle's bytes."""
+    q4 = quant == "q4_0"
+    mat = synth.q4_0_matrix if q4 else synth.q8_0_matrix
+    src = mat(1, 16 * nblocks * 32, 63, 0.02).reshape(-1)
+    xb = 288 if q4 else 544
+    pack = hip.pack_q4_0_to_q4_0x16 if q4 else hip.pack_q8_0_to_q8_0x16
+    want = (oracle.pack_q4_0x16 if q4 else oracle.pack_q8_0x16)(src, nblocks)
+    buf = empty_dev(src.size + 16, torch.uint8, dev)
+    buf[2:2 + src.size] = to_dev(src, dev)
+    for what, s_dev in (("aligned", to_dev(src, dev)), ("2-byte", buf[2:2 + src.size])):
+        dst = empty_dev(nblocks * xb, torch.uint8, dev)
+        pack(nblocks, s_dev, dst)
+        assert np.array_equal(from_dev(dst), want), f"{quant} {what} source"
+
+
 @pytest.mark.parametrize("nc,nb", [(4096, 128), (48, 131), (40, 3), (16, 1), (32, 256)])
 def test_repack_gemv_q4_0(hip, oracle, dev, nc, nb):
     n = nb * 32

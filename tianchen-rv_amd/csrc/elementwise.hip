@@ -139,6 +139,21 @@ __device__ __forceinline__ uint32_t quant_byte(float x, float id) {
   return static_cast<uint32_t>(w) & 0xffu;  // narrowing keeps the low byte
 }
 
+// max of v over the 8 lanes of its group: quad_perm [1,0,3,2] and [2,3,0,1]
+// give each quad's max, row_half_mirror pairs lane i with lane 7-i of the
+// other quad (fmaxf is exact and order-free)
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v),
+                                                                  0xB1, 0xf, 0xf, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v),
+                                                                  0x4E, 0xf, 0xf, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v),
+                                                                  0x141, 0xf, 0xf, false)));
+  return v;
+}
+
+// kVec: x is 16-byte aligned (one 128-bit load per lane); otherwise 4-byte loads
+template <bool kVec>
 __global__ __launch_bounds__(kQzThreads) void quantize_q8_0(const float *x, uint8_t *vy,
                                                             size_t nb) {
   __shared__ __align__(16) uint8_t lds[kQzBlocks * kQ8Bytes];
@@ -150,16 +165,13 @@ __global__ __launch_bounds__(kQzThreads) void quantize_q8_0(const float *x, uint
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
   if (active) {
     const float *xp = x + (blk0 + lb) * kQK + 4 * part;
-    if ((reinterpret_cast<uintptr_t>(x) & 15u) == 0)
+    if constexpr (kVec)
       v = *reinterpret_cast<const float4 *>(xp);
     else
       v = make_float4(xp[0], xp[1], xp[2], xp[3]);
   }
-  float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  // max over the 8 lanes of the block (exact, order-free)
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-  amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+  const float amax =
+      max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
   const float d = __fdiv_rn(amax, 127.0f);
   const float id = d != 0.0f ? __frcp_rn(d) : 0.0f;
   if (active) {
@@ -274,8 +286,12 @@ int tcrv_hip_quantize_row_q8_0(size_t n, const float *x, uint8_t *vy, void *stre
   const size_t grid = (nb + kQzBlocks - 1) / kQzBlocks;
   if (grid > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
-  quantize_q8_0<<<dim3(static_cast<unsigned>(grid)), dim3(kQzThreads), 0, as_stream(stream)>>>(
-      x, vy, nb);
+  if (aligned16(x))
+    quantize_q8_0<true><<<dim3(static_cast<unsigned>(grid)), dim3(kQzThreads), 0,
+                          as_stream(stream)>>>(x, vy, nb);
+  else
+    quantize_q8_0<false><<<dim3(static_cast<unsigned>(grid)), dim3(kQzThreads), 0,
+                           as_stream(stream)>>>(x, vy, nb);
   return launch_status();
 }
 
