@@ -368,6 +368,28 @@ def bench_configs(torch, lib, stream, args):
                                    "sets": sets}
     del P, Yv, reg, src, packed, src_all
 
+    # the decode GEMV over the split (SoA) layout of the same weights
+    wd = torch.from_numpy(inputs("gemv_w")).to(dev)
+    soa = torch.empty(N * nb * 18, dtype=torch.uint8, device=dev)
+    checked(lib.tcrv_hip_pack_q4_0_to_soa, "pack_soa")(N, nb, wd.data_ptr(), nb * 18,
+                                                      soa.data_ptr(), sp)
+    sets = max(args.copies, copies_for(soa.numel(), 2))
+    S = torch.empty((sets, soa.numel()), dtype=torch.uint8, device=dev)
+    S[:] = soa
+    Yv = torch.empty((sets, N), device=dev)
+    fn = checked(lib.tcrv_hip_gemv_q4_0_soa_q8_0, "gemv_soa")
+    ptrs = [(Yv[i].data_ptr(), S[i].data_ptr()) for i in range(sets)]
+    reg = Region(torch, stream, lambda i: fn(N, ptrs[i % sets][0], ptrs[i % sets][1],
+                                             xd.data_ptr(), N, sp), 2000)
+    reg.run()
+    us = reg.run() * 1e3 / 2000
+    same_as_eager(torch, stream, Yv[1999 % sets],
+                  lambda o: fn(N, o, S[1999 % sets].data_ptr(), xd.data_ptr(), N, sp), "gemv_soa")
+    out["gemv_q4_0_soa_q8_0"] = {"workload": "decode GEMV 4096x4096 over the split (SoA) Q4_0 layout",
+                                 "us": round(us, 3), "GB/s": round(GEMV_BYTES / us / 1e3, 1),
+                                 "sets": sets}
+    del S, Yv, soa, wd, reg
+
     # a10 quantize_row_q8_0: 4096 activation rows x 4096 f32 -> Q8_0 (the prefill
     # GEMM's activation operand; read 64 MiB, write 17.8 MB)
     xf = torch.from_numpy(inputs("gemm_a_f32")).to(dev)

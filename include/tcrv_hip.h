@@ -225,6 +225,22 @@ TCRV_HIP_API int tcrv_hip_repack_gemv_q4_0_q8_0(size_t n, float *s, const uint8_
 TCRV_HIP_API int tcrv_hip_repack_gemv_q8_0_q8_0(size_t n, float *s, const uint8_t *vx,
                                    const uint8_t *vy, size_t nc, void *stream);
 
+/* ---- the split (SoA) Q4_0 weight layout: no reference counterpart --------
+ * A GPU layout of the same bytes: for nrows rows of nb blocks, the 16 quant
+ * bytes of row r block b at dst + (r*nb + b)*16 and its fp16 scale at
+ * dst + nrows*nb*16 + (r*nb + b)*2 (nrows*nb*18 bytes in all), so a block
+ * pair is two aligned 128-bit loads and one dword.  The pack reads rows at
+ * stride bx (2-byte aligned source, dst 16-byte aligned). */
+TCRV_HIP_API int tcrv_hip_pack_q4_0_to_soa(size_t nrows, size_t nb, const uint8_t *src, size_t bx,
+                              uint8_t *dst, void *stream);
+
+/* The decode GEMV over split-layout weights: s[r] for r < nr is the a6 block
+ * dot of weight row r with the plain Q8_0 activation row vy, bit-identical to
+ * tcrv_hip_gemv_q4_0_q8_0 over the same rows (same fold, same order).
+ * n/32 even; vx 16-byte aligned (as the pack writes it), vy 4-byte aligned. */
+TCRV_HIP_API int tcrv_hip_gemv_q4_0_soa_q8_0(size_t n, float *s, const uint8_t *vx,
+                                const uint8_t *vy, size_t nr, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

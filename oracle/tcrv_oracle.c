@@ -499,6 +499,26 @@ void tcrv_oracle_pack_q8_0_to_q8_0x16(size_t nblocks, const uint8_t *src, uint8_
   }
 }
 
+/* The split (SoA) layout: a byte permutation of the plain rows, no arithmetic. */
+void tcrv_oracle_pack_q4_0_to_soa(size_t nrows, size_t nb, const uint8_t *src, size_t bx,
+                                  uint8_t *dst) {
+  uint8_t *scales = dst + nrows * nb * 16;
+  for (size_t r = 0; r < nrows; ++r)
+    for (size_t b = 0; b < nb; ++b) {
+      const uint8_t *blk = src + r * bx + b * TCRV_Q4_0_BLOCK_BYTES;
+      memcpy(dst + (r * nb + b) * 16, blk + 2, 16);
+      memcpy(scales + (r * nb + b) * 2, blk, 2);
+    }
+}
+
+void tcrv_oracle_unpack_q4_0_soa(size_t nrows, size_t nb, const uint8_t *src, uint8_t *dst) {
+  const uint8_t *scales = src + nrows * nb * 16;
+  for (size_t t = 0; t < nrows * nb; ++t) {
+    memcpy(dst + t * TCRV_Q4_0_BLOCK_BYTES, scales + t * 2, 2);
+    memcpy(dst + t * TCRV_Q4_0_BLOCK_BYTES + 2, src + t * 16, 16);
+  }
+}
+
 void tcrv_oracle_unpack_q4_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst) {
   for (size_t o = 0; o < nblocks; ++o) {
     const uint8_t *in = src + o * TCRV_Q4_0X16_BLOCK_BYTES;

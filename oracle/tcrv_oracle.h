@@ -116,6 +116,13 @@ void tcrv_oracle_repack_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx,
  * consumer's addressing. */
 #define TCRV_Q8_0X16_BLOCK_BYTES 544
 void tcrv_oracle_pack_q8_0_to_q8_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst);
+/* The split (SoA) Q4_0 layout (a GPU layout; no reference counterpart): for
+ * nrows rows of nb blocks read at stride bx, quants of row r block b at
+ * dst + (r*nb + b)*16, its fp16 scale at dst + nrows*nb*16 + (r*nb + b)*2. */
+void tcrv_oracle_pack_q4_0_to_soa(size_t nrows, size_t nb, const uint8_t *src, size_t bx,
+                                  uint8_t *dst);
+/* Its inverse (test helper): back to nrows contiguous plain rows. */
+void tcrv_oracle_unpack_q4_0_soa(size_t nrows, size_t nb, const uint8_t *src, uint8_t *dst);
 /* Inverse of both packs (test helper): x16 blocks back to 16 plain blocks each. */
 void tcrv_oracle_unpack_q4_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst);
 void tcrv_oracle_unpack_q8_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst);

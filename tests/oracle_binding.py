@@ -43,6 +43,8 @@ _SIGS = {
     "tcrv_oracle_repack_gemv_q4_0_q8_0": ([_sz, _p, _p, _p, _sz], None),
     "tcrv_oracle_pack_q8_0_to_q8_0x16": ([_sz, _p, _p], None),
     "tcrv_oracle_unpack_q4_0x16": ([_sz, _p, _p], None),
+    "tcrv_oracle_pack_q4_0_to_soa": ([_sz, _sz, _p, _sz, _p], None),
+    "tcrv_oracle_unpack_q4_0_soa": ([_sz, _sz, _p, _p], None),
     "tcrv_oracle_unpack_q8_0x16": ([_sz, _p, _p], None),
     "tcrv_oracle_repack_gemv_q8_0_q8_0": ([_sz, _p, _p, _p, _sz], None),
 }
@@ -167,6 +169,16 @@ class Oracle:
     def pack_q8_0x16(self, src: np.ndarray, nblocks: int) -> np.ndarray:
         dst = np.zeros(nblocks * 544, dtype=np.uint8)
         self.lib.tcrv_oracle_pack_q8_0_to_q8_0x16(nblocks, _a(src), _a(dst))
+        return dst
+
+    def pack_q4_0_soa(self, src: np.ndarray, nrows: int, nb: int, bx: int) -> np.ndarray:
+        dst = np.zeros(nrows * nb * 18, dtype=np.uint8)
+        self.lib.tcrv_oracle_pack_q4_0_to_soa(nrows, nb, _a(src), bx, _a(dst))
+        return dst
+
+    def unpack_q4_0_soa(self, src: np.ndarray, nrows: int, nb: int) -> np.ndarray:
+        dst = np.zeros(nrows * nb * 18, dtype=np.uint8)
+        self.lib.tcrv_oracle_unpack_q4_0_soa(nrows, nb, _a(src), _a(dst))
         return dst
 
     def unpack_q4_0x16(self, src: np.ndarray, nblocks: int) -> np.ndarray:

@@ -563,3 +563,36 @@ def test_concurrent_host_threads_on_own_streams(hip, oracle, dev):
     for t, j in enumerate(jobs):
         assert_f32_parity(from_dev(j["y"]), j["want_y"], what=f"thread {t} gemv")
         assert_f32_parity(from_dev(j["c"]), j["want_c"], what=f"thread {t} gemm")
+
+
+# ------------------------------------------------ split (SoA) Q4_0 layout ---
+
+@pytest.mark.parametrize("nr,nb,pad", [(4096, 128, 0), (33, 6, 14), (1, 2, 0), (1000, 256, 0)])
+def test_soa_pack_and_gemv(hip, oracle, dev, nr, nb, pad):
+    """The GPU pack writes the oracle's split layout byte for byte, and the
+    GEMV over it gives the same bits as the plain-row GEMV and the oracle."""
+    n = nb * 32
+    w = np.pad(synth.q4_0_matrix(nr, n, 1012, 0.02), ((0, 0), (0, pad)))
+    x = synth.q8_0_matrix(1, n, 1013, 1.0).reshape(-1)
+    bx = w.shape[1]
+    soa = empty_dev(nr * nb * 18, torch.uint8, dev)
+    hip.pack_q4_0_to_soa(nr, nb, to_dev(w, dev), bx, soa)
+    want_soa = oracle.pack_q4_0_soa(np.ascontiguousarray(w).reshape(-1), nr, nb, bx)
+    assert np.array_equal(from_dev(soa), want_soa)
+    s = empty_dev(nr, torch.float32, dev)
+    hip.gemv_q4_0_soa_q8_0(n, s, soa, to_dev(x, dev), nr)
+    plain = empty_dev(nr, torch.float32, dev)
+    hip.gemv_q4_0_q8_0(n, plain, to_dev(w, dev), bx, to_dev(x, dev), nr)
+    want = oracle.gemm_q4_0(n, w, x, 0, nr, 1, bx, 1, 8)[:nr]
+    assert_f32_parity(from_dev(s), want, what=f"soa gemv {nr}x{n}")
+    assert np.array_equal(from_dev(s).view(np.uint32), from_dev(plain).view(np.uint32))
+
+
+def test_soa_gemv_rejects_what_it_does_not_cover(hip, dev):
+    soa = empty_dev(4 * 3 * 18 + 16, torch.uint8, dev)
+    x = empty_dev(3 * 34, torch.uint8, dev)
+    s = empty_dev(4, torch.float32, dev)
+    st = hip.call("tcrv_hip_gemv_q4_0_soa_q8_0", 96, s, soa, x, 4, 0, check=False)
+    assert st == hip.ERR_UNSUPPORTED  # odd block count
+    st = hip.call("tcrv_hip_gemv_q4_0_soa_q8_0", 64, s, soa[2:], x, 4, 0, check=False)
+    assert st == hip.ERR_MISALIGNED   # not 16-byte aligned

@@ -526,3 +526,20 @@ def test_binary_i32_add_is_the_harness(oracle):
     a = (3 * i - 17).astype(np.int32)
     b = (41 - 2 * i).astype(np.int32)
     assert np.array_equal(oracle.binary(0, 4, a, b), (i + 24).astype(np.int32))
+
+
+# ------------------------------------------------ split (SoA) Q4_0 layout ---
+
+def test_pack_q4_0_soa_matches_an_independent_gather_and_round_trips(oracle):
+    """The split layout is a byte permutation: quants of (row r, block b) at
+    (r*nb + b)*16, scales after all quants at (r*nb + b)*2 -- checked with a
+    numpy gather written here, on padded rows (bx > the row bytes)."""
+    nrows, nb, pad = 5, 7, 6
+    plain = synth.q4_0_matrix(nrows, nb * 32, 71, 0.02)
+    rows = np.pad(plain, ((0, 0), (0, pad)))
+    bx = rows.shape[1]
+    soa = oracle.pack_q4_0_soa(np.ascontiguousarray(rows).reshape(-1), nrows, nb, bx)
+    blocks = plain.reshape(nrows * nb, 18)
+    assert np.array_equal(soa[:nrows * nb * 16].reshape(-1, 16), blocks[:, 2:])
+    assert np.array_equal(soa[nrows * nb * 16:].reshape(-1, 2), blocks[:, :2])
+    assert np.array_equal(oracle.unpack_q4_0_soa(soa, nrows, nb), plain.reshape(-1))

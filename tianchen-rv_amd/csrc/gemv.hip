@@ -201,7 +201,11 @@ __device__ __forceinline__ int nibble_dot(const uint32_t q[4], const uint32_t y[
 
 // kOneChunk: nb == kGvChunk exactly (n = 4096), so every lane owns a whole
 // block pair, there is one chunk and no carry between chunks.
-template <int kWaves, int kR, bool kOneChunk>
+// kSoA: the weights are in the split layout (tcrv_hip_pack_q4_0_to_soa): for
+// nr rows of nb blocks, the 16 quant bytes of row r block b at (r*nb + b)*16
+// and its fp16 scale at nr*nb*16 + (r*nb + b)*2, so a lane's block pair is two
+// aligned 128-bit loads and one dword (bx is unused).
+template <int kWaves, int kR, bool kOneChunk, bool kSoA = false>
 __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
     size_t nb_arg, float *s, size_t os, const uint8_t *vx, size_t bx, const uint8_t *vy,
     size_t nr) {
@@ -231,7 +235,16 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
 #pragma unroll
       for (int r = 0; r < kR; ++r) {
         const size_t row = min(row0 + r, nr - 1);  // rows past nr: computed, never stored
-        load36(vx + row * bx + (c0 + b0) * kQ4Bytes, wr[r]);
+        if constexpr (kSoA) {
+          const size_t blk = row * nb + c0 + b0;
+          const uint4 *q = reinterpret_cast<const uint4 *>(vx + blk * 16);
+          const uint4 qa4 = q[0], qb4 = q[1];
+          wr[r][0] = qa4.x; wr[r][1] = qa4.y; wr[r][2] = qa4.z; wr[r][3] = qa4.w;
+          wr[r][4] = qb4.x; wr[r][5] = qb4.y; wr[r][6] = qb4.z; wr[r][7] = qb4.w;
+          wr[r][8] = *reinterpret_cast<const uint32_t *>(vx + nr * nb * 16 + blk * 2);
+        } else {
+          load36(vx + row * bx + (c0 + b0) * kQ4Bytes, wr[r]);
+        }
       }
       ActPair ap;
       load_act_pair(vy + (c0 + b0) * kQ8Bytes, ap);
@@ -242,13 +255,24 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
         // block 2l: d = bytes 0-1, quants bytes 2..17 (shift by 2 bytes);
         // block 2l+1: d = bytes 18-19, quants bytes 20..35 (dwords 5..8)
         uint32_t qa[4], qb[4];
+        float dx0, dx1;
+        if constexpr (kSoA) {  // quants dwords 0-3 and 4-7, the two scales in dword 8
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          qa[k] = funnel16(wr[r][k], wr[r][k + 1]);
-          qb[k] = wr[r][k + 5];
+          for (int k = 0; k < 4; ++k) {
+            qa[k] = wr[r][k];
+            qb[k] = wr[r][k + 4];
+          }
+          dx0 = fp16_bits_to_f32(wr[r][8] & 0xffffu);
+          dx1 = fp16_bits_to_f32(wr[r][8] >> 16);
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            qa[k] = funnel16(wr[r][k], wr[r][k + 1]);
+            qb[k] = wr[r][k + 5];
+          }
+          dx0 = fp16_bits_to_f32(wr[r][0] & 0xffffu);
+          dx1 = fp16_bits_to_f32(wr[r][4] >> 16);
         }
-        const float dx0 = fp16_bits_to_f32(wr[r][0] & 0xffffu);
-        const float dx1 = fp16_bits_to_f32(wr[r][4] >> 16);
         float2 t;
         t.x = static_cast<float>(nibble_dot(qa, ap.q0, ap.c0)) * dx0;
         t.y = static_cast<float>(nibble_dot(qb, ap.q1, ap.c1)) * dx1;
@@ -338,9 +362,81 @@ int gemv_q4_0_q8_0(size_t n, float *s, size_t os, const uint8_t *vx, size_t bx,
   return launch_status();
 }
 
+int gemv_q4_0_soa_q8_0(size_t nb, float *s, const uint8_t *vx, const uint8_t *vy, size_t nr,
+                       void *stream) {
+  if (!s || !vx || !vy)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (nb % 2 != 0)
+    return TCRV_HIP_ERR_UNSUPPORTED;  // a lane owns whole block pairs
+  if (!aligned16(vx) || !aligned4(vy))
+    return TCRV_HIP_ERR_MISALIGNED;
+  constexpr int kW = kDirectWaves, kR = kDirectRows;
+  const size_t rows_per_wg = static_cast<size_t>(kW) * kR;
+  const size_t grid = (nr + rows_per_wg - 1) / rows_per_wg;
+  if (grid > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  hipStream_t st = as_stream(stream);
+  if (nb == static_cast<size_t>(tcrv::kGvChunk))
+    tcrv::gemv_q4_0_q8_0_direct<kW, kR, true, true>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(nb, s, 1, vx, 0, vy, nr);
+  else
+    tcrv::gemv_q4_0_q8_0_direct<kW, kR, false, true>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(nb, s, 1, vx, 0, vy, nr);
+  return launch_status();
+}
+
 }  // namespace tcrv_host
 
+namespace tcrv {
+
+// Q4_0 rows -> the split layout: thread t moves block t (row t / nb, block
+// t % nb): its 16 quant bytes to (t*16) and its fp16 scale to nr*nb*16 + t*2.
+__global__ __launch_bounds__(256) void pack_q4_0_soa(size_t nrows, size_t nb, const uint8_t *src,
+                                                     size_t bx, uint8_t *dst) {
+  const size_t t = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= nrows * nb)
+    return;
+  const size_t r = t / nb, b = t - r * nb;
+  const uint16_t *blk = reinterpret_cast<const uint16_t *>(src + r * bx + b * kQ4Bytes);
+  uint32_t q[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    q[k] = static_cast<uint32_t>(blk[1 + 2 * k]) | (static_cast<uint32_t>(blk[2 + 2 * k]) << 16);
+  reinterpret_cast<uint4 *>(dst)[t] = make_uint4(q[0], q[1], q[2], q[3]);
+  reinterpret_cast<uint16_t *>(dst + nrows * nb * 16)[t] = blk[0];
+}
+
+}  // namespace tcrv
+
 extern "C" {
+
+int tcrv_hip_pack_q4_0_to_soa(size_t nrows, size_t nb, const uint8_t *src, size_t bx,
+                              uint8_t *dst, void *stream) {
+  using namespace tcrv_host;
+  if (nrows == 0 || nb == 0)
+    return TCRV_HIP_OK;
+  if (!src || !dst)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned2(src) || (nrows > 1 && (bx & 1u)) || !aligned16(dst))
+    return TCRV_HIP_ERR_MISALIGNED;
+  if (nrows > 1 && bx < nb * tcrv::kQ4Bytes)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  const size_t grid = (nrows * nb + 255) / 256;
+  if (grid > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  tcrv::pack_q4_0_soa<<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, as_stream(stream)>>>(
+      nrows, nb, src, bx, dst);
+  return launch_status();
+}
+
+int tcrv_hip_gemv_q4_0_soa_q8_0(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
+                                size_t nr, void *stream) {
+  if (nr == 0)
+    return TCRV_HIP_OK;
+  if (n / tcrv::kQK == 0)
+    return tcrv_host::zero_outputs(s, nr, 1, 1, stream);
+  return tcrv_host::gemv_q4_0_soa_q8_0(n / tcrv::kQK, s, vx, vy, nr, stream);
+}
 
 int tcrv_hip_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx, size_t bx,
                             const uint8_t *vy, size_t nr, void *stream) {

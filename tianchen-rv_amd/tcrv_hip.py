@@ -70,6 +70,8 @@ SIGNATURES = {
     "tcrv_hip_pack_q8_0_to_q8_0x16": [_sz, _p, _p, _p],
     "tcrv_hip_repack_gemv_q4_0_q8_0": [_sz, _p, _p, _p, _sz, _p],
     "tcrv_hip_repack_gemv_q8_0_q8_0": [_sz, _p, _p, _p, _sz, _p],
+    "tcrv_hip_pack_q4_0_to_soa": [_sz, _sz, _p, _sz, _p, _p],
+    "tcrv_hip_gemv_q4_0_soa_q8_0": [_sz, _p, _p, _p, _sz, _p],
 }
 STRING_FUNCS = {"tcrv_hip_status_string": [_int], "tcrv_hip_version": []}
 
@@ -241,6 +243,14 @@ def repack_gemv_q4_0_q8_0(n: int, s, vx, vy, nc: int, stream=None):
 
 def repack_gemv_q8_0_q8_0(n: int, s, vx, vy, nc: int, stream=None):
     return call("tcrv_hip_repack_gemv_q8_0_q8_0", n, s, vx, vy, nc, _stream(stream))
+
+
+def pack_q4_0_to_soa(nrows: int, nb: int, src, bx: int, dst, stream=None):
+    return call("tcrv_hip_pack_q4_0_to_soa", nrows, nb, src, bx, dst, _stream(stream))
+
+
+def gemv_q4_0_soa_q8_0(n: int, s, vx, vy, nr: int, stream=None):
+    return call("tcrv_hip_gemv_q4_0_soa_q8_0", n, s, vx, vy, nr, _stream(stream))
 
 
 def synchronize(stream=None):
