@@ -412,11 +412,13 @@ def test_repack_gemv_q8_0_equals_plain_gemv(hip, oracle, dev, nc, nb):
 
 
 
-@pytest.mark.parametrize("quant,nc,nb", [("q4_0", 48, 131), ("q8_0", 32, 37), ("q4_0", 16, 1)])
-def test_repack_gemv_two_byte_aligned_activation(hip, oracle, dev, quant, nc, nb):
-    """A 4-byte aligned activation takes the per-wave kernel, a 2-byte aligned
-    one (an activation row that follows an odd number of 34-byte blocks) the
-    LDS-staged kernel: both must give the same bits as the oracle."""
+@pytest.mark.parametrize("quant,nc,nb", [("q4_0", 48, 131), ("q8_0", 32, 37), ("q4_0", 16, 1),
+                                         ("q8_0", 16, 256)])
+def test_repack_gemv_unaligned_operands(hip, oracle, dev, quant, nc, nb):
+    """The kernel stages a wave's share with 128-bit loads only when weights
+    and activation are 16-byte aligned; a 2-byte aligned activation (one that
+    follows an odd number of 34-byte blocks) and 4-byte aligned weights take
+    the narrower copies: every combination gives the oracle's bits."""
     n = nb * 32
     q4 = quant == "q4_0"
     w = (synth.q4_0_matrix if q4 else synth.q8_0_matrix)(nc, n, 1010, 0.02)
@@ -426,13 +428,16 @@ def test_repack_gemv_two_byte_aligned_activation(hip, oracle, dev, quant, nc, nb
     packed = pack(x16_source(w, nb, w.shape[1] // nb), groups * nb)
     ref = (oracle.repack_gemv_q4_0 if q4 else oracle.repack_gemv_q8_0)(n, packed, x, nc)
     run = hip.repack_gemv_q4_0_q8_0 if q4 else hip.repack_gemv_q8_0_q8_0
-    dpacked = to_dev(packed, dev)
+    wbuf = empty_dev(packed.size + 16, torch.uint8, dev)
+    wbuf[4:4 + packed.size] = to_dev(packed, dev)
     buf = empty_dev(x.size + 16, torch.uint8, dev)
     buf[2:2 + x.size] = to_dev(x, dev)
-    for what, act in (("4-byte", to_dev(x, dev)), ("2-byte", buf[2:2 + x.size])):
-        s = empty_dev(nc, torch.float32, dev)
-        run(n, s, dpacked, act, nc)
-        assert_f32_parity(from_dev(s), ref, what=f"repack {quant} {what} aligned activation")
+    for wwhat, wdev in (("16-byte", to_dev(packed, dev)), ("4-byte", wbuf[4:4 + packed.size])):
+        for what, act in (("16-byte", to_dev(x, dev)), ("2-byte", buf[2:2 + x.size])):
+            s = empty_dev(nc, torch.float32, dev)
+            run(n, s, wdev, act, nc)
+            assert_f32_parity(from_dev(s), ref,
+                              what=f"repack {quant} {wwhat} weights, {what} activation")
 
 # ------------------------------------------------ a7 Q4_0 GEMM on MFMA (nc > 1) ---
 

@@ -102,20 +102,6 @@ __global__ __launch_bounds__(256) void pack_x16(size_t nblocks, const uint8_t *s
   reinterpret_cast<uint32_t *>(dst + o * kDst)[k] = v;
 }
 
-// ---------------------------------------------------------------------------
-// Repacked GEMV.  Work-group = 4 waves for one group of 16 weight rows; each
-// wave step covers 4 blocks with 16 lanes per block: lane (rq = l & 3,
-// pq = (l >> 2) & 3) owns rows 4rq..4rq+3 and positions 4pq..4pq+3 (Q4_0; the
-// high nibbles are positions 16+4pq..) or 8pq..8pq+7 (Q8_0).  It loads one dword
-// per position (4 rows of it), turns the 4x4 bytes row-major with v_perm, and
-// takes v_dot4_i32_i8 against the activation; the four position lanes of a row
-// are summed with two shuffles.  All weight loads of a chunk are issued before
-// the first use.  Exact (float)sumi and d_w*d_a per (row, block) go to LDS;
-// then DPP row fr of wave w folds weight row 4w+fr with fold_chain (8
-// consecutive blocks per lane), so no LDS access sits on the serial chain.
-// ---------------------------------------------------------------------------
-constexpr int kRgChunk = 128;   // blocks per LDS chunk
-
 // 4x4 byte transpose: in[i] holds rows 0..3 of position i; out[r] holds
 // positions 0..3 of row r.
 __device__ __forceinline__ void transpose4x4(const uint32_t in[4], uint32_t out[4]) {
@@ -141,223 +127,163 @@ __device__ __forceinline__ uint32_t act_dword(const uint8_t *act, int b, int k) 
   return w[k + 1];
 }
 
-template <bool kQ4>
-__global__ __launch_bounds__(256) void repack_gemv(size_t nb, float *s, const uint8_t *vx,
-                                                   const uint8_t *vy) {
-  constexpr int kW = kQ4 ? kQ4x16Bytes : kQ8x16Bytes;
-  constexpr int kDw = kQ4 ? 4 : 8;          // quant dwords per lane and block
-  constexpr int kSteps = kRgChunk / 16;     // blocks per lane and chunk
-  constexpr int kFoldLanes = 16, kFoldTerms = kRgChunk / kFoldLanes;
-  __shared__ __align__(16) uint8_t act[kRgChunk * kQ8Bytes + 16];
-  __shared__ __align__(16) float2 terms[16][kRgChunk + 8];  // [row][block]
+// ---------------------------------------------------------------------------
+// Repacked GEMV, wave-staged.  Work-group = 8 waves for one group of 16
+// weight rows, each wave a share of kRwBlocks blocks per chunk.  A group's x16
+// blocks are contiguous, so each wave's share of a chunk -- kRwBlocks blocks,
+// 4608 or 8704 bytes -- is one span: the wave copies it into its own LDS
+// region with consecutive 128-bit loads (dword loads for a group that is only
+// 4-byte aligned), each block at a 16-byte padded stride (kW + 16: 76 or 140
+// dwords, 12 banks apart, so the wave's 16 blocks x 4 row quads read 64
+// different banks), with its share of the activation beside it.  Lane (block
+// b, row quad g) then reads position dword 4i + g of block b for every
+// position i, turns each 4x4 group row-major with v_perm and dots it with the
+// activation; exact (float)sumi and d_w*d_a go to LDS.  Only the fold needs
+// every wave's terms: after one work-group barrier DPP row fr of wave w
+// (w < 4) folds weight row 4w + fr with fold_chain.
+// ---------------------------------------------------------------------------
+constexpr int kRwWaves = 8, kRwBlocks = 16;
+constexpr int kRwChunk = kRwWaves * kRwBlocks;  // x16 blocks per chunk
 
-  const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63;
-  const int jb = l >> 4, pq = (l >> 2) & 3, rq = l & 3;
-  const int fr = l >> 4, fp = l & (kFoldLanes - 1);  // fold: DPP row fr folds row 4w+fr
-  const uint8_t *group = vx + static_cast<size_t>(blockIdx.x) * nb * kW;
-  float acc = 0.0f;
-
-  for (size_t c0 = 0; c0 < nb; c0 += kRgChunk) {
-    const int nbc = static_cast<int>(min(static_cast<size_t>(kRgChunk), nb - c0));
-    uint32_t raw[kSteps][kDw], dsc[kSteps][2];
+// Piece u = tid + k*kThreads (k < kPer) of a span of np 16-byte pieces, loaded
+// into v[k].  Lanes past the span re-read its last piece (and store_pieces
+// re-stores it: the same bytes to the same place), so no lane branches and
+// every load is issued before the first store waits.
+template <int kPer, int kThreads>
+__device__ __forceinline__ void load_pieces(uint4 v[kPer], const uint8_t *src, int np, int tid) {
+  const uint4 *s4 = reinterpret_cast<const uint4 *>(src);
 #pragma unroll
-    for (int k = 0; k < kSteps; ++k) {
-      const int b = 16 * k + 4 * w + jb;
-      if (b < nbc) {
-        const uint8_t *blk = group + (c0 + b) * kW;
-        const uint32_t *qd = reinterpret_cast<const uint32_t *>(blk + 32);
-#pragma unroll
-        for (int i = 0; i < kDw; ++i)
-          raw[k][i] = qd[4 * (kDw * pq + i) + rq];  // position kDw*pq+i, rows 4rq..4rq+3
-        const uint32_t *dq = reinterpret_cast<const uint32_t *>(blk + 8 * rq);  // d[4rq..4rq+3]
-        dsc[k][0] = dq[0];
-        dsc[k][1] = dq[1];
-      }
-    }
-    copy_span_to_lds(act, vy + c0 * kQ8Bytes, nbc * kQ8Bytes, tid, 256);
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < kSteps; ++k) {
-      const int b = 16 * k + 4 * w + jb;
-      if (b < nbc) {
-        int part[4];
-        if constexpr (kQ4) {
-          uint32_t rows[4];
-          transpose4x4(raw[k], rows);
-          // activation positions 4pq..4pq+3 (low nibbles) and 16+4pq.. (high)
-          const uint32_t alo = act_dword(act, b, pq);
-          const uint32_t ahi = act_dword(act, b, pq + 4);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            // byte = (n_lo ^ 8) | (n_hi ^ 8) << 4; as a signed byte, the nibble
-            // moved to the high half is 16 * sext4(n ^ 8) = 16 * (n - 8)
-            const uint32_t lo16 = (rows[r] << 4) & 0xF0F0F0F0u;
-            const uint32_t hi16 = rows[r] & 0xF0F0F0F0u;
-            part[r] = sdot4(hi16, ahi, sdot4(lo16, alo, 0));
-          }
-        } else {
-          uint32_t rows[8];
-          transpose4x4(raw[k], rows);
-          transpose4x4(raw[k] + 4, rows + 4);
-          const uint32_t a0 = act_dword(act, b, 2 * pq);
-          const uint32_t a1 = act_dword(act, b, 2 * pq + 1);
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            part[r] = sdot4(rows[4 + r], a1, sdot4(rows[r], a0, 0));
-        }
-        // sum over the four position lanes (lane bits 2..3)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          part[r] += __shfl_xor(part[r], 4);
-          part[r] += __shfl_xor(part[r], 8);
-        }
-        if (pq == 0) {
-          const float da =
-              fp16_bits_to_f32(*reinterpret_cast<const uint16_t *>(act + b * kQ8Bytes));
-          const uint32_t dw[4] = {dsc[k][0] & 0xffffu, dsc[k][0] >> 16, dsc[k][1] & 0xffffu,
-                                  dsc[k][1] >> 16};
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int sumi = kQ4 ? (part[r] >> 4) : part[r];  // Q4_0: exact division by 16
-            terms[4 * rq + r][b] =
-                make_float2(static_cast<float>(sumi), fp16_bits_to_f32(dw[r]) * da);
-          }
-        }
-      } else if (pq == 0 && b < kRgChunk) {
-        // blocks past the chunk: fma(0, 0, acc) == acc (acc is never -0)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          terms[4 * rq + r][b] = make_float2(0.0f, 0.0f);
-      }
-    }
-    __syncthreads();
-    float ta[kFoldTerms], tb[kFoldTerms];
-#pragma unroll
-    for (int k = 0; k < kFoldTerms; k += 2) {
-      const float4 v = *reinterpret_cast<const float4 *>(&terms[4 * w + fr][fp * kFoldTerms + k]);
-      ta[k] = v.x; tb[k] = v.y; ta[k + 1] = v.z; tb[k + 1] = v.w;
-    }
-    // the previous chunk's sum sits in the last lane of the fold row: seed lane 0
-    const float carry = __shfl(acc, (l & ~(kFoldLanes - 1)) + kFoldLanes - 1);
-    acc = fold_chain<kFoldLanes, kFoldTerms>(ta, tb, fp == 0 ? carry : 0.0f);
-    __syncthreads();
-  }
-  if (fp == kFoldLanes - 1)
-    s[static_cast<size_t>(blockIdx.x) * 16 + 4 * w + fr] = acc;
+  for (int k = 0; k < kPer; ++k)
+    v[k] = s4[min(tid + k * kThreads, np - 1)];
 }
 
+// Stores the pieces to LDS, piece u of a run of kRun at (u / kRun) * kStride +
+// 16 * (u % kRun): a padded stride per block of kRun pieces.
+template <int kPer, int kThreads, int kRun, int kStride>
+__device__ __forceinline__ void store_pieces(const uint4 v[kPer], uint8_t *dst, int np, int tid) {
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int u = min(tid + k * kThreads, np - 1);
+    const int b = u / kRun;
+    *reinterpret_cast<uint4 *>(dst + b * kStride + 16 * (u - b * kRun)) = v[k];
+  }
+}
 
-// ---------------------------------------------------------------------------
-// Wave-per-row-quad form (activation 4-byte aligned; the LDS-staged form above
-// serves 2-byte aligned activations).  Wave w of the group's work-group owns
-// rows 4w..4w+3 and folds them itself, so no work-group barrier is needed:
-// lane l takes blocks 2l, 2l+1 of the chunk; per block it loads the dword at
-// position i of its row quad for every position i (the x16 interleave puts
-// rows 4w..4w+3 of position i in dword 4i + w), turns each 4x4 group
-// row-major with v_perm and dots it with the activation, which the lane loads
-// straight from global memory (68 bytes, like the plain GEMV).  Exact
-// (float)sumi and d_w*d_a go to the wave's own LDS rows; DPP row r then folds
-// weight row 4w + r with fold_chain.
-// ---------------------------------------------------------------------------
 template <bool kQ4>
-__global__ __launch_bounds__(256) void repack_gemv_rows(size_t nb, float *s, const uint8_t *vx,
-                                                        const uint8_t *vy) {
+__global__ __launch_bounds__(64 * kRwWaves) void repack_gemv_waves(size_t nb, float *s,
+                                                                   const uint8_t *vx,
+                                                                   const uint8_t *vy) {
   constexpr int kW = kQ4 ? kQ4x16Bytes : kQ8x16Bytes;
-  constexpr int kPos = kQ4 ? 16 : 32;  // quant-byte positions per block
-  constexpr int kFoldLanes = 16, kFoldTerms = kRgChunk / kFoldLanes;
-  __shared__ __align__(16) float2 terms[4][4][kRgChunk + 8];  // [wave][row][block]
+  constexpr int kLw = kW + 16;          // LDS bytes per staged block
+  constexpr int kPieces = kW / 16;      // 128-bit pieces per block
+  constexpr int kWords = kW / 4;
+  constexpr int kPos = kQ4 ? 16 : 32;   // quant-byte positions per block
+  constexpr int kPer = (kRwBlocks * kPieces + 63) / 64;
+  constexpr int kFoldLanes = 16, kFoldTerms = kRwChunk / kFoldLanes;
+  constexpr int kTermRow = kRwChunk + 4;  // float2 per terms row (264 dwords)
+  constexpr int kActPieces = kRwBlocks * kQ8Bytes / 16;  // a wave's activation share
+  static_assert(kRwBlocks * 4 == 64, "one (block, row quad) item per lane");
+  static_assert((kRwBlocks * kQ8Bytes) % 16 == 0 && kActPieces <= 64, "one piece per lane");
+  __shared__ __align__(16) uint8_t wq[kRwChunk * kLw];
+  __shared__ __align__(16) uint8_t act[kRwChunk * kQ8Bytes + 16];
+  __shared__ __align__(16) float2 terms[16][kTermRow];  // [row][block]
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63;
   const int fr = l >> 4, fp = l & (kFoldLanes - 1);
   const uint8_t *group = vx + static_cast<size_t>(blockIdx.x) * nb * kW;
+  const bool wide = (reinterpret_cast<uintptr_t>(vx) & 15u) == 0;  // every group then is
+  const bool act16 = (reinterpret_cast<uintptr_t>(vy) & 15u) == 0;  // every wave's share then is
+  const int wb0 = w * kRwBlocks;  // this wave's first block of a chunk
   float acc = 0.0f;
 
-  for (size_t c0 = 0; c0 < nb; c0 += kRgChunk) {
-    const int nbc = static_cast<int>(min(static_cast<size_t>(kRgChunk), nb - c0));
-    const int b0 = 2 * l;
-    uint32_t raw[2][kPos], dq[2][2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      if (b0 + j < nbc) {
-        const uint8_t *blk = group + (c0 + b0 + j) * kW;
-        const uint32_t *qd = reinterpret_cast<const uint32_t *>(blk + 32);
-#pragma unroll
-        for (int i = 0; i < kPos; ++i)
-          raw[j][i] = qd[4 * i + w];
-        const uint32_t *d = reinterpret_cast<const uint32_t *>(blk + 8 * w);  // d[4w..4w+3]
-        dq[j][0] = d[0];
-        dq[j][1] = d[1];
+  for (size_t c0 = 0; c0 < nb; c0 += kRwChunk) {
+    const int nbc = static_cast<int>(min(static_cast<size_t>(kRwChunk), nb - c0));
+    const int wnb = max(0, min(kRwBlocks, nbc - wb0));  // this wave's blocks
+    if (wnb > 0) {
+      const uint8_t *src = group + (c0 + wb0) * kW;
+      const uint8_t *asrc = vy + (c0 + wb0) * kQ8Bytes;
+      if (wide && act16 && wnb == kRwBlocks) {
+        // weights and activation in flight together (no lane branches)
+        uint4 av[1], v[kPer];
+        load_pieces<1, 64>(av, asrc, kActPieces, l);
+        load_pieces<kPer, 64>(v, src, kRwBlocks * kPieces, l);
+        store_pieces<kPer, 64, kPieces, kLw>(v, wq + wb0 * kLw, kRwBlocks * kPieces, l);
+        store_pieces<1, 64, kActPieces, 16 * kActPieces>(av, act + wb0 * kQ8Bytes, kActPieces, l);
+      } else if (wide) {
+        copy_span_to_lds(act + wb0 * kQ8Bytes, asrc, wnb * kQ8Bytes, l, 64);
+        uint4 v[kPer];
+        load_pieces<kPer, 64>(v, src, wnb * kPieces, l);
+        store_pieces<kPer, 64, kPieces, kLw>(v, wq + wb0 * kLw, wnb * kPieces, l);
+      } else {
+        copy_span_to_lds(act + wb0 * kQ8Bytes, asrc, wnb * kQ8Bytes, l, 64);
+        const uint32_t *s1 = reinterpret_cast<const uint32_t *>(src);
+        for (int u = l; u < wnb * kWords; u += 64) {
+          const int b = u / kWords;
+          *reinterpret_cast<uint32_t *>(wq + (wb0 + b) * kLw + 4 * (u - b * kWords)) = s1[u];
+        }
       }
+      wave_lds_sync();  // the wave reads only its own region
     }
-    // activation blocks 2l, 2l+1: 68 bytes from a dword-aligned start (34 when
-    // only block 2l exists)
-    uint32_t ar[17];
-    const uint32_t *ag = reinterpret_cast<const uint32_t *>(vy + (c0 + b0) * kQ8Bytes);
-    if (b0 + 1 < nbc) {
+    const int b = wb0 + (l >> 2), g = l & 3;
+    float2 t[4] = {make_float2(0.0f, 0.0f), make_float2(0.0f, 0.0f), make_float2(0.0f, 0.0f),
+                   make_float2(0.0f, 0.0f)};  // absent blocks: fma(0, 0, acc) == acc
+    if (b < nbc) {
+      const uint8_t *blk = wq + b * kLw;
+      uint32_t raw[kPos];
 #pragma unroll
-      for (int k = 0; k < 17; ++k)
-        ar[k] = ag[k];
-    } else if (b0 < nbc) {
+      for (int i = 0; i < kPos; ++i)
+        raw[i] = *reinterpret_cast<const uint32_t *>(blk + 32 + 16 * i + 4 * g);
+      const uint2 dq = *reinterpret_cast<const uint2 *>(blk + 8 * g);  // d[4g..4g+3]
+      uint32_t a[8];  // the block's 32 activation quants
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        ar[k] = ag[k];
-      ar[8] = *reinterpret_cast<const uint16_t *>(ag + 8);
-    }
+        a[k] = act_dword(act, b, k);
+      const float da = fp16_bits_to_f32(*reinterpret_cast<const uint16_t *>(act + b * kQ8Bytes));
+      int part[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      float2 t[4] = {make_float2(0.0f, 0.0f), make_float2(0.0f, 0.0f), make_float2(0.0f, 0.0f),
-                     make_float2(0.0f, 0.0f)};  // absent blocks: fma(0, 0, acc) == acc
-      if (b0 + j < nbc) {
-        uint32_t a[8];  // the block's 32 activation quants, dword aligned
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-          a[k] = j == 0 ? funnel16(ar[k], ar[k + 1]) : ar[k + 9];
-        const float da = fp16_bits_to_f32(j == 0 ? (ar[0] & 0xffffu) : (ar[8] >> 16));
-        int part[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int g = 0; g < kPos / 4; ++g) {
-          uint32_t rows[4];
-          transpose4x4(&raw[j][4 * g], rows);  // positions 4g..4g+3 of rows 4w..4w+3
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            if constexpr (kQ4) {
-              // byte = (n_lo ^ 8) | (n_hi ^ 8) << 4: as signed bytes the masked
-              // nibbles are 16 * (n - 8); low nibbles pair with quants 4g..,
-              // high nibbles with 16+4g..
-              part[r] = sdot4((rows[r] << 4) & 0xF0F0F0F0u, a[g], part[r]);
-              part[r] = sdot4(rows[r] & 0xF0F0F0F0u, a[g + 4], part[r]);
-            } else {
-              part[r] = sdot4(rows[r], a[g], part[r]);
-            }
-          }
-        }
-        const uint32_t dw[4] = {dq[j][0] & 0xffffu, dq[j][0] >> 16, dq[j][1] & 0xffffu,
-                                dq[j][1] >> 16};
+      for (int q = 0; q < kPos / 4; ++q) {
+        uint32_t rows[4];
+        transpose4x4(&raw[4 * q], rows);  // positions 4q..4q+3 of rows 4g..4g+3
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int sumi = kQ4 ? (part[r] >> 4) : part[r];  // Q4_0: exact division by 16
-          t[r] = make_float2(static_cast<float>(sumi), fp16_bits_to_f32(dw[r]) * da);
+          if constexpr (kQ4) {
+            // byte = (n_lo ^ 8) | (n_hi ^ 8) << 4: as signed bytes the masked
+            // nibbles are 16 * (n - 8); low nibbles pair with quants 4q..,
+            // high nibbles with 16+4q..
+            part[r] = sdot4((rows[r] << 4) & 0xF0F0F0F0u, a[q], part[r]);
+            part[r] = sdot4(rows[r] & 0xF0F0F0F0u, a[q + 4], part[r]);
+          } else {
+            part[r] = sdot4(rows[r], a[q], part[r]);
+          }
         }
       }
+      const uint32_t dw[4] = {dq.x & 0xffffu, dq.x >> 16, dq.y & 0xffffu, dq.y >> 16};
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        terms[w][r][b0 + j] = t[r];
+      for (int r = 0; r < 4; ++r) {
+        const int sumi = kQ4 ? (part[r] >> 4) : part[r];  // Q4_0: exact division by 16
+        t[r] = make_float2(static_cast<float>(sumi), fp16_bits_to_f32(dw[r]) * da);
+      }
     }
-    wave_lds_sync();  // the LDS rows are this wave's own
-    float ta[kFoldTerms], tb[kFoldTerms];
 #pragma unroll
-    for (int k = 0; k < kFoldTerms; k += 2) {
-      const float4 v = *reinterpret_cast<const float4 *>(&terms[w][fr][fp * kFoldTerms + k]);
-      ta[k] = v.x; tb[k] = v.y; ta[k + 1] = v.z; tb[k + 1] = v.w;
+    for (int r = 0; r < 4; ++r)
+      terms[4 * g + r][b] = t[r];
+    __syncthreads();
+    if (w < 4) {
+      float ta[kFoldTerms], tb[kFoldTerms];
+#pragma unroll
+      for (int k = 0; k < kFoldTerms; k += 2) {
+        const float4 v =
+            *reinterpret_cast<const float4 *>(&terms[4 * w + fr][fp * kFoldTerms + k]);
+        ta[k] = v.x; tb[k] = v.y; ta[k + 1] = v.z; tb[k + 1] = v.w;
+      }
+      // the previous chunk's sum sits in the last lane of the fold row: seed lane 0
+      const float carry = __shfl(acc, (l & ~(kFoldLanes - 1)) + kFoldLanes - 1);
+      acc = fold_chain<kFoldLanes, kFoldTerms>(ta, tb, fp == 0 ? carry : 0.0f);
     }
-    // the previous chunk's sum sits in the last lane of the fold row: seed lane 0
-    const float carry = __shfl(acc, (l & ~(kFoldLanes - 1)) + kFoldLanes - 1);
-    acc = fold_chain<kFoldLanes, kFoldTerms>(ta, tb, fp == 0 ? carry : 0.0f);
-    wave_lds_sync();
+    __syncthreads();  // the next chunk rewrites terms
   }
-  if (fp == kFoldLanes - 1)
+  if (w < 4 && fp == kFoldLanes - 1)
     s[static_cast<size_t>(blockIdx.x) * 16 + 4 * w + fr] = acc;
 }
 }  // namespace tcrv
@@ -408,12 +334,8 @@ int launch_repack_gemv(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
     return TCRV_HIP_ERR_MISALIGNED;
   if (groups > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
-  if (aligned4(vy))
-    tcrv::repack_gemv_rows<kQ4><<<dim3(static_cast<unsigned>(groups)), dim3(256), 0,
-                                  as_stream(stream)>>>(nb, s, vx, vy);
-  else
-    tcrv::repack_gemv<kQ4><<<dim3(static_cast<unsigned>(groups)), dim3(256), 0,
-                             as_stream(stream)>>>(nb, s, vx, vy);
+  tcrv::repack_gemv_waves<kQ4><<<dim3(static_cast<unsigned>(groups)), dim3(64 * tcrv::kRwWaves),
+                                 0, as_stream(stream)>>>(nb, s, vx, vy);
   return launch_status();
 }
 
