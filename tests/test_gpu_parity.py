@@ -67,7 +67,7 @@ def test_dequant_q8_0(hip, oracle, dev, nb):
 
 # -------------------------------------------------------------- a10 quantize ---
 
-@pytest.mark.parametrize("nb", [1, 31, 32, 33, 4096 * 4096 // 32])
+@pytest.mark.parametrize("nb", [1, 31, 32, 33, 63, 64, 65, 100, 4096 * 4096 // 32])
 def test_quantize_q8_0(hip, oracle, dev, nb):
     n = nb * 32
     x = synth.normal_f32(1007, n, 0.0, 1.0)

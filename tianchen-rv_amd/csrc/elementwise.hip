@@ -118,11 +118,12 @@ __global__ __launch_bounds__(kDqThreads) void dequantize_q8_0(const uint8_t *vx,
 //   q = (int8)(int16)sat_rne(x*id)   (vfncvt_x_f_w_i16 then vncvt_x_x_w_i8).
 // Division and reciprocal are the correctly rounded IEEE operations, as the
 // reference's scalar `amax / 127.0f` and `1.0f/d` are.  A work-group stages
-// its kQzBlocks output blocks (32*34 = 1088 bytes, a 16-byte multiple) in LDS
+// its kQzBlocks output blocks (64*34 = 2176 bytes, a 16-byte multiple) in LDS
 // and writes them with 128-bit stores.
 // ---------------------------------------------------------------------------
 constexpr int kQzThreads = 256;
-constexpr int kQzBlocks = kQzThreads / 8;
+constexpr int kQzPer = 2;  // blocks per 8-lane group (1/2/4: 18.3/16.5/17.3 us at 4096^2)
+constexpr int kQzBlocks = kQzPer * kQzThreads / 8;
 
 __device__ __forceinline__ uint32_t quant_byte(float x, float id) {
   const float v = x * id;
@@ -152,36 +153,42 @@ __device__ __forceinline__ float max8(float v) {
   return v;
 }
 
-// kVec: x is 16-byte aligned (one 128-bit load per lane); otherwise 4-byte loads
+// kVec: x is 16-byte aligned (128-bit loads); otherwise 4-byte loads.  Each
+// thread quantizes kQzPer blocks' parts; all its loads are issued first
+// (lanes of absent blocks re-read the last block and store nothing).
 template <bool kVec>
 __global__ __launch_bounds__(kQzThreads) void quantize_q8_0(const float *x, uint8_t *vy,
                                                             size_t nb) {
   __shared__ __align__(16) uint8_t lds[kQzBlocks * kQ8Bytes];
   const size_t blk0 = static_cast<size_t>(blockIdx.x) * kQzBlocks;
   const int nblk = static_cast<int>(min(static_cast<size_t>(kQzBlocks), nb - blk0));
-  const int lb = threadIdx.x >> 3;  // block within the work-group
-  const int part = threadIdx.x & 7; // float4 within the block
-  const bool active = lb < nblk;
-  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (active) {
-    const float *xp = x + (blk0 + lb) * kQK + 4 * part;
+  const int part = threadIdx.x & 7;  // float4 within the block
+  float4 v[kQzPer];
+#pragma unroll
+  for (int k = 0; k < kQzPer; ++k) {
+    const int lb = (threadIdx.x >> 3) + k * (kQzThreads / 8);  // block within the work-group
+    const float *xp = x + (blk0 + min(lb, nblk - 1)) * kQK + 4 * part;
     if constexpr (kVec)
-      v = *reinterpret_cast<const float4 *>(xp);
+      v[k] = *reinterpret_cast<const float4 *>(xp);
     else
-      v = make_float4(xp[0], xp[1], xp[2], xp[3]);
+      v[k] = make_float4(xp[0], xp[1], xp[2], xp[3]);
   }
-  const float amax =
-      max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-  const float d = __fdiv_rn(amax, 127.0f);
-  const float id = d != 0.0f ? __frcp_rn(d) : 0.0f;
-  if (active) {
-    uint16_t *l16 = reinterpret_cast<uint16_t *>(lds + lb * kQ8Bytes);
-    const uint32_t b0 = quant_byte(v.x, id), b1 = quant_byte(v.y, id);
-    const uint32_t b2 = quant_byte(v.z, id), b3 = quant_byte(v.w, id);
-    l16[1 + part * 2] = static_cast<uint16_t>(b0 | (b1 << 8));
-    l16[2 + part * 2] = static_cast<uint16_t>(b2 | (b3 << 8));
-    if (part == 0)
-      l16[0] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(d));
+#pragma unroll
+  for (int k = 0; k < kQzPer; ++k) {
+    const int lb = (threadIdx.x >> 3) + k * (kQzThreads / 8);
+    const float amax = max8(fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)),
+                                  fmaxf(fabsf(v[k].z), fabsf(v[k].w))));
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float id = d != 0.0f ? __frcp_rn(d) : 0.0f;
+    if (lb < nblk) {
+      uint16_t *l16 = reinterpret_cast<uint16_t *>(lds + lb * kQ8Bytes);
+      const uint32_t b0 = quant_byte(v[k].x, id), b1 = quant_byte(v[k].y, id);
+      const uint32_t b2 = quant_byte(v[k].z, id), b3 = quant_byte(v[k].w, id);
+      l16[1 + part * 2] = static_cast<uint16_t>(b0 | (b1 << 8));
+      l16[2 + part * 2] = static_cast<uint16_t>(b2 | (b3 << 8));
+      if (part == 0)
+        l16[0] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(d));
+    }
   }
   __syncthreads();
   copy_lds_to_span(vy + blk0 * kQ8Bytes, lds, nblk * kQ8Bytes, threadIdx.x, kQzThreads);
