@@ -343,7 +343,7 @@ def x16_source(w, nb, k):
     ).reshape(-1))
 
 
-@pytest.mark.parametrize("nblocks", [1, 7, 4096 * 128 // 16])
+@pytest.mark.parametrize("nblocks", [1, 7, 64, 65, 100, 4096 * 128 // 16])
 def test_pack_q4_0x16(hip, oracle, dev, nblocks):
     src = synth.q4_0_matrix(1, 16 * nblocks * 32, 61, 0.02).reshape(-1)
     dst = empty_dev(nblocks * 288, torch.uint8, dev)
@@ -351,7 +351,7 @@ def test_pack_q4_0x16(hip, oracle, dev, nblocks):
     assert np.array_equal(from_dev(dst), oracle.pack_q4_0x16(src, nblocks))
 
 
-@pytest.mark.parametrize("nblocks", [1, 9, 4096 * 128 // 16])
+@pytest.mark.parametrize("nblocks", [1, 9, 32, 33, 70, 4096 * 128 // 16])
 def test_pack_q8_0x16(hip, oracle, dev, nblocks):
     src = synth.q8_0_matrix(1, 16 * nblocks * 32, 62, 1.0).reshape(-1)
     dst = empty_dev(nblocks * 544, torch.uint8, dev)
@@ -361,8 +361,9 @@ def test_pack_q8_0x16(hip, oracle, dev, nblocks):
 
 @pytest.mark.parametrize("quant,nblocks", [("q4_0", 33), ("q8_0", 17)])
 def test_pack_x16_two_byte_aligned_source(hip, oracle, dev, quant, nblocks):
-    """16-byte aligned spans take the LDS-staged pack; a source only 2-byte
-    aligned takes the per-dword gather: both give the oracle's bytes."""
+    """16-byte aligned spans take the LDS-staged quad-transpose pack; a source
+    only 2-byte aligned takes the per-dword gather: both give the oracle's
+    bytes."""
     q4 = quant == "q4_0"
     mat = synth.q4_0_matrix if q4 else synth.q8_0_matrix
     src = mat(1, 16 * nblocks * 32, 63, 0.02).reshape(-1)

@@ -22,54 +22,8 @@ constexpr int kQ4x16Bytes = 288;
 constexpr int kQ8x16Bytes = 544;
 
 // ---------------------------------------------------------------------------
-// Packs, 16-byte aligned spans: the 16 source blocks of an x16 block are
-// contiguous and as long as it (16 x 18 = 288, 16 x 34 = 544 bytes), so a
-// work-group copies kPkBlocks of them into LDS with coalesced 128-bit loads,
-// gathers each output dword from LDS and writes the output span with
-// consecutive dword stores.
-// ---------------------------------------------------------------------------
-constexpr int kPkBlocks = 16;  // x16 blocks per work-group
-
-template <bool kQ4>
-__global__ __launch_bounds__(256) void pack_x16_lds(size_t nblocks, const uint8_t *src,
-                                                    uint8_t *dst) {
-  constexpr int kSrc = kQ4 ? kQ4Bytes : kQ8Bytes;
-  constexpr int kDst = kQ4 ? kQ4x16Bytes : kQ8x16Bytes;  // 16 * kSrc, a multiple of 16
-  constexpr int kDwords = kDst / 4;
-  __shared__ __align__(16) uint8_t in[kPkBlocks * kDst];
-  const size_t o0 = static_cast<size_t>(blockIdx.x) * kPkBlocks;
-  const int nblk = static_cast<int>(min(static_cast<size_t>(kPkBlocks), nblocks - o0));
-  const uint4 *s4 = reinterpret_cast<const uint4 *>(src + o0 * kDst);
-  uint4 *l4 = reinterpret_cast<uint4 *>(in);
-  for (int c = threadIdx.x; c < nblk * (kDst / 16); c += 256)
-    l4[c] = s4[c];
-  __syncthreads();
-  uint32_t *d = reinterpret_cast<uint32_t *>(dst + o0 * kDst);
-  for (int t = threadIdx.x; t < nblk * kDwords; t += 256) {
-    const int o = t / kDwords, k = t - o * kDwords;
-    const uint8_t *b = in + o * kDst;  // the output block's 16 source blocks
-    uint32_t v;
-    if (k < 8) {  // scales d[2k], d[2k+1]
-      const uint32_t d0 = *reinterpret_cast<const uint16_t *>(b + (2 * k) * kSrc);
-      const uint32_t d1 = *reinterpret_cast<const uint16_t *>(b + (2 * k + 1) * kSrc);
-      v = d0 | (d1 << 16);
-    } else {  // qs bytes 4q .. 4q+3: byte i -> source block i % 16, offset i / 16
-      const int q = k - 8;
-      const int off = 2 + q / 4;
-      const int r0 = 4 * (q % 4);
-      v = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        v |= static_cast<uint32_t>(b[(r0 + j) * kSrc + off]) << (8 * j);
-      if constexpr (kQ4)
-        v ^= 0x88888888u;
-    }
-    d[t] = v;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Packs: one thread per output dword (8 scale dwords + 64 or 128 quant dwords).
+// Packs, spans that are only 2-byte aligned: one thread per output dword (8
+// scale dwords + 64 or 128 quant dwords).
 // ---------------------------------------------------------------------------
 template <bool kQ4>
 __global__ __launch_bounds__(256) void pack_x16(size_t nblocks, const uint8_t *src,
@@ -286,6 +240,56 @@ __global__ __launch_bounds__(64 * kRwWaves) void repack_gemv_waves(size_t nb, fl
   if (w < 4 && fp == kFoldLanes - 1)
     s[static_cast<size_t>(blockIdx.x) * 16 + 4 * w + fr] = acc;
 }
+
+// ---------------------------------------------------------------------------
+// Packs, 16-byte aligned spans.  The 16 source blocks of an x16 block are
+// contiguous and as long as it (16 x 18 = 288, 16 x 34 = 544 bytes), so a
+// work-group copies kPkBlocks of them into LDS with consecutive 128-bit loads
+// (all issued before the first store), gathers each output dword from LDS and
+// writes the output span with consecutive dword stores.
+// ---------------------------------------------------------------------------
+constexpr int kPkBlocks = 16;  // x16 blocks per work-group (4/8/16/32: 8.4/6.5/6.0/6.6 us)
+
+template <bool kQ4>
+__global__ __launch_bounds__(256) void pack_x16_lds(size_t nblocks, const uint8_t *src,
+                                                    uint8_t *dst) {
+  constexpr int kSrc = kQ4 ? kQ4Bytes : kQ8Bytes;
+  constexpr int kDst = kQ4 ? kQ4x16Bytes : kQ8x16Bytes;
+  constexpr int kDwords = kDst / 4;
+  constexpr int kPieces = kPkBlocks * kDst / 16;
+  constexpr int kPer = (kPieces + 255) / 256;
+  __shared__ __align__(16) uint8_t in[kPkBlocks * kDst];
+  const size_t o0 = static_cast<size_t>(blockIdx.x) * kPkBlocks;
+  const int nblk = static_cast<int>(min(static_cast<size_t>(kPkBlocks), nblocks - o0));
+  const int np = nblk * (kDst / 16);
+  uint4 v[kPer];
+  load_pieces<kPer, 256>(v, src + o0 * kDst, np, threadIdx.x);
+  store_pieces<kPer, 256, kPieces, 16 * kPieces>(v, in, np, threadIdx.x);
+  __syncthreads();
+  uint32_t *d = reinterpret_cast<uint32_t *>(dst + o0 * kDst);
+  for (int t = threadIdx.x; t < nblk * kDwords; t += 256) {
+    const int o = t / kDwords, k = t - o * kDwords;
+    const uint8_t *b = in + o * kDst;  // the output block's 16 source blocks
+    uint32_t w;
+    if (k < 8) {  // scales d[2k], d[2k+1]
+      const uint32_t d0 = *reinterpret_cast<const uint16_t *>(b + (2 * k) * kSrc);
+      const uint32_t d1 = *reinterpret_cast<const uint16_t *>(b + (2 * k + 1) * kSrc);
+      w = d0 | (d1 << 16);
+    } else {  // qs bytes 4q .. 4q+3: byte i -> source block i % 16, offset i / 16
+      const int q = k - 8;
+      const int off = 2 + q / 4;
+      const int r0 = 4 * (q % 4);
+      w = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        w |= static_cast<uint32_t>(b[(r0 + j) * kSrc + off]) << (8 * j);
+      if constexpr (kQ4)
+        w ^= 0x88888888u;
+    }
+    d[t] = w;
+  }
+}
+
 }  // namespace tcrv
 
 namespace {
