@@ -602,3 +602,64 @@ def test_soa_gemv_rejects_what_it_does_not_cover(hip, dev):
     assert st == hip.ERR_UNSUPPORTED  # odd block count
     st = hip.call("tcrv_hip_gemv_q4_0_soa_q8_0", 64, s, soa[2:], x, 4, 0, check=False)
     assert st == hip.ERR_MISALIGNED   # not 16-byte aligned
+
+
+# ------------------------------------------------------------ HIP graph replay ---
+
+def test_graph_replays_match_the_oracle(hip, oracle, dev):
+    """Launches captured into a HIP graph (as the bench times them) replay to
+    the oracle's bits every time: five replays with eager work, output
+    clearing and synchronizations between them.  The captured set includes a
+    zero-block call, whose outputs come from a small fill kernel (no
+    hipMemsetAsync is ever recorded)."""
+    n, nr = 1024, 512
+    w4 = synth.q4_0_matrix(nr, n, 3000, 0.02)
+    x = synth.q8_0_matrix(1, n, 3001, 1.0).reshape(-1)
+    b8 = synth.q8_0_matrix(160, 512, 3002, 0.02)
+    a8 = synth.q8_0_matrix(96, 512, 3003, 1.0)
+    xf = synth.normal_f32(3004, 4096 + 32, 0.0, 1.0)
+    nbr = 16
+    wr = synth.q4_0_matrix(32, nbr * 32, 3005, 0.02)
+    packed = oracle.pack_q4_0x16(x16_source(wr, nbr, 18), 2 * nbr)
+    xr = synth.q8_0_matrix(1, nbr * 32, 3006, 1.0).reshape(-1)
+    want = {
+        "gemv": oracle.gemm_q4_0(n, w4, x, 0, nr, 1, w4.shape[1], 1, 8)[:nr],
+        "gemm": oracle.gemm_q8_0(512, b8, a8, a8.shape[1], 160, 96, b8.shape[1], 96, 8),
+        "quant": oracle.quantize_q8_0(xf),
+        "repack": oracle.repack_gemv_q4_0(nbr * 32, packed, xr, 32),
+        "zero": np.zeros(7, np.float32),
+    }
+    d = {"w4": to_dev(w4, dev), "x": to_dev(x, dev), "b8": to_dev(b8, dev), "a8": to_dev(a8, dev),
+         "xf": to_dev(xf, dev), "packed": to_dev(packed, dev), "xr": to_dev(xr, dev)}
+    out = {"gemv": empty_dev(nr, torch.float32, dev), "gemm": empty_dev(160 * 96, torch.float32, dev),
+           "quant": empty_dev(want["quant"].size, torch.uint8, dev),
+           "repack": empty_dev(32, torch.float32, dev), "zero": empty_dev(7, torch.float32, dev)}
+    st = torch.cuda.Stream(device=dev)
+
+    def launch_all():
+        hip.gemv_q4_0_q8_0(n, out["gemv"], d["w4"], w4.shape[1], d["x"], nr, stream=st)
+        hip.q8_0_q8_0_gemm(512, out["gemm"], d["b8"], d["a8"], a8.shape[1], 160, 96,
+                           b8.shape[1], 96, stream=st)
+        hip.quantize_row_q8_0(xf.size, d["xf"], out["quant"], stream=st)
+        hip.repack_gemv_q4_0_q8_0(nbr * 32, out["repack"], d["packed"], d["xr"], 32, stream=st)
+        hip.gemv_q4_0_q8_0(16, out["zero"], d["w4"], w4.shape[1], d["x"], 7, stream=st)
+
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(graph, stream=st):
+            launch_all()
+    torch.cuda.synchronize()
+    side = empty_dev(nr, torch.float32, dev)
+    for rep in range(5):
+        for k, t in out.items():
+            t.fill_(0xAB if t.dtype == torch.uint8 else float("nan"))
+        hip.gemv_q4_0_q8_0(n, side, d["w4"], w4.shape[1], d["x"], nr)  # eager work between
+        torch.cuda.synchronize()
+        with torch.cuda.stream(st):
+            graph.replay()
+        torch.cuda.synchronize()
+        for k in ("gemv", "gemm", "repack", "zero"):
+            assert_f32_parity(from_dev(out[k]), want[k], what=f"graph replay {rep} {k}")
+        assert np.array_equal(from_dev(out["quant"]), want["quant"]), f"graph replay {rep} quant"
+    assert_f32_parity(from_dev(side), want["gemv"], what="eager GEMV between replays")
