@@ -315,7 +315,7 @@ namespace tcrv_host {
 // Rows per wave of the LDS-staged decode GEMV (odd nb or 2-byte aligned rows).
 constexpr int kGemvRows = 2;
 // Shape of the register-direct GEMV: waves per work-group, rows per wave
-// (4096^2, us: 1x4 4.16, 2x4 4.46, 4x4 4.00, 8x4 5.06, 2x8 4.80, 4x2 4.28).
+// (4096^2, us: 1x4 4.16, 2x4 4.46, 4x4 4.00, 8x2 4.13, 8x4 5.06, 2x8 4.80, 4x2 4.28).
 constexpr int kDirectWaves = 4;
 constexpr int kDirectRows = 4;
 
