@@ -46,6 +46,7 @@ DOT_ROWS = 16384
 DOT_BYTES = DOT_ROWS * (2 * (N // 32) * 34 + 4)                 # 142 671 872
 GEMM_OPS = 2.0 * N * N * N                                      # 137 438 953 472
 PACK_BYTES = 2 * N * (N // 32) * 18                             # 18 874 368
+REPACK8_BYTES = N * (N // 32) * 34 + (N // 32) * 34 + N * 4     # 17 846 528
 QUANT_BYTES = N * N * 4 + (N * N // 32) * 34                    # 84 934 656
 
 
@@ -352,6 +353,26 @@ def bench_configs(torch, lib, stream, args):
     out["repack_gemv_q4_0_q8_0"] = {"workload": "a8 x16-repacked Q4_0 GEMV 4096x4096",
                                     "us": round(us, 3), "GB/s": round(GEMV_BYTES / us / 1e3, 1),
                                     "sets": sets}
+    # the Q8_0 x16 GEMV (tcrv_rvv.repack_gemv_q8_0_q8_0) over the configs[4] weights
+    w8 = inputs("gemm_b")
+    src8 = torch.from_numpy(w8.reshape(N // 16, 16, nb, 34).transpose(0, 2, 1, 3).copy()).to(dev)
+    packed8 = torch.empty(N // 16 * nb * 544, dtype=torch.uint8, device=dev)
+    checked(lib.tcrv_hip_pack_q8_0_to_q8_0x16, "pack8")(N // 16 * nb, src8.data_ptr(),
+                                                         packed8.data_ptr(), sp)
+    sets8 = copies_for(packed8.numel(), 2)
+    P8 = torch.empty((sets8, packed8.numel()), dtype=torch.uint8, device=dev)
+    P8[:] = packed8
+    fn8 = checked(lib.tcrv_hip_repack_gemv_q8_0_q8_0, "repack_gemv_q8")
+    ptrs8 = [(Yv[i % sets].data_ptr(), P8[i].data_ptr()) for i in range(sets8)]
+    reg = Region(torch, stream, lambda i: fn8(N, ptrs8[i % sets8][0], ptrs8[i % sets8][1],
+                                              xd.data_ptr(), N, sp), 500)
+    reg.run()
+    us = reg.run() * 1e3 / 500
+    out["repack_gemv_q8_0_q8_0"] = {"workload": "a8 x16-repacked Q8_0 GEMV 4096x4096 "
+                                                "(configs[4] weights)",
+                                    "us": round(us, 3),
+                                    "GB/s": round(REPACK8_BYTES / us / 1e3, 1), "sets": sets8}
+    del P8, src8, packed8, reg
     # the x16 pack of the same weights (read 9.4 MB, write 9.4 MB)
     src_all = torch.empty((sets, packed.numel()), dtype=torch.uint8, device=dev)
     src_all[:] = src.view(-1)
@@ -575,6 +596,21 @@ def cpu_baseline_configs(seconds: float):
     out["repack_gemv_q4_0_q8_0"] = entry(GEMV_BYTES * reps / dt / 1e9, "GB/s", 1,
                                          f"{reps} whole 4096x4096 x16 GEMVs over {HOST_COPIES} "
                                          f"rotating weight copies in {dt:.1f} s")
+    w8 = inputs("gemm_b")
+    packed8 = ora.pack_q8_0x16(
+        w8.reshape(N // 16, 16, nb, 34).transpose(0, 2, 1, 3).copy().reshape(-1), N // 16 * nb)
+    copies8 = HOST_COPIES // 2
+    ps8 = np.ascontiguousarray(np.broadcast_to(packed8, (copies8,) + packed8.shape))
+    k8 = [0]
+
+    def repack8():
+        ora.repack_gemv_q8_0(N, ps8[k8[0] % copies8], x, N)
+        k8[0] += 1
+    reps, dt = timed(repack8)
+    out["repack_gemv_q8_0_q8_0"] = entry(REPACK8_BYTES * reps / dt / 1e9, "GB/s", 1,
+                                         f"{reps} whole 4096x4096 Q8_0 x16 GEMVs over {copies8} "
+                                         f"rotating weight copies in {dt:.1f} s")
+    del ps8
     src = w.reshape(N // 16, 16, nb, 18).transpose(0, 2, 1, 3).copy().reshape(-1)
     reps, dt = timed(lambda: ora.pack_q4_0x16(src, N // 16 * nb))
     out["pack_q4_0_to_q4_0x16"] = entry(PACK_BYTES * reps / dt / 1e9, "GB/s", 1,
