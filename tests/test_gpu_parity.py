@@ -242,6 +242,9 @@ def test_q4_0_gemm_multi_column(hip, oracle, dev, nr, nc, nb):
     (300, 130, 7, 16, 32),    # partial wide tiles both ways, 4 + 3 blocks, padded strides
     (256, 2, 1, 0, 0),        # one block: only the partial chunk
     (520, 257, 13, 0, 4),     # three tile rows, 3 full chunks + 1 block
+    (300, 130, 8, 0, 0),      # two full chunks, partial tiles both ways
+    (520, 257, 16, 16, 32),   # four full chunks, padded strides, three tile rows
+    (256, 64, 8, 4, 0),       # one full tile row, a stride of 276 bytes
 ])
 def test_q8_0_gemm(hip, oracle, dev, nr, nc, nb, xpad, ypad):
     n = nb * 32
