@@ -351,20 +351,38 @@ template <bool kQ4, bool kTwo, int kSStride = kFbBM>
 __device__ __forceinline__ void fold_pair(float (&acc)[16], const int8_t *qa, const int8_t *qb,
                                           const float *sxh, const float *syh, const float *syc,
                                           int b) {
-  const float dx = sxh[b * kSStride];
-  const float dy_op = kQ4 ? 1.0f : syh[b * kSStride];
-  const v32f dxy = __builtin_amdgcn_mfma_f32_32x32x1f32(dx, dy_op, v32f{}, 0, 0, 0);
+  if constexpr (kQ4) {
+    // d_x of this lane's 16 accumulator rows (rows 8g + 4h + 0..3 of the tile,
+    // h = lane / 32) read straight from the staged scales: four 128-bit reads
+    // per block instead of a broadcasting MFMA (the fold needs no product of
+    // scales)
+    const int lane = threadIdx.x & 63;
+    const float *sxt = sxh - (lane >> 5) * kSStride - (lane & 31) + 4 * (lane >> 5);
 #pragma unroll
-  for (int j = 0; j < (kTwo ? 2 : 1); ++j) {
-    const v4i a = *reinterpret_cast<const v4i *>(qa + (b + j) * kQK);
-    const v4i bq = *reinterpret_cast<const v4i *>(qb + (b + j) * kQK);
-    const v16i sumi = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, v16i{}, 0, 0, 0);
-    if constexpr (kQ4) {
+    for (int j = 0; j < (kTwo ? 2 : 1); ++j) {
+      const v4i a = *reinterpret_cast<const v4i *>(qa + (b + j) * kQK);
+      const v4i bq = *reinterpret_cast<const v4i *>(qb + (b + j) * kQK);
+      float dxe[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 d4 = *reinterpret_cast<const float4 *>(sxt + (b + j) * kSStride + 8 * g);
+        dxe[4 * g] = d4.x; dxe[4 * g + 1] = d4.y; dxe[4 * g + 2] = d4.z; dxe[4 * g + 3] = d4.w;
+      }
       const float dy = syc[(b + j) * kSStride];
+      const v16i sumi = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, v16i{}, 0, 0, 0);
 #pragma unroll
       for (int e = 0; e < 16; ++e)
-        acc[e] = fmaf(static_cast<float>(sumi[e]) * dxy[16 * j + e], dy, acc[e]);
-    } else {
+        acc[e] = fmaf(static_cast<float>(sumi[e]) * dxe[e], dy, acc[e]);
+    }
+  } else {
+    const float dx = sxh[b * kSStride];
+    const float dy_op = syh[b * kSStride];
+    const v32f dxy = __builtin_amdgcn_mfma_f32_32x32x1f32(dx, dy_op, v32f{}, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < (kTwo ? 2 : 1); ++j) {
+      const v4i a = *reinterpret_cast<const v4i *>(qa + (b + j) * kQK);
+      const v4i bq = *reinterpret_cast<const v4i *>(qb + (b + j) * kQK);
+      const v16i sumi = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, bq, v16i{}, 0, 0, 0);
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         acc[e] = fmaf(static_cast<float>(sumi[e]), dxy[16 * j + e], acc[e]);
