@@ -445,6 +445,29 @@ def bench_configs(torch, lib, stream, args):
     out["q4_0_q8_0_gemm"] = {"workload": "a7 Q4_0 x Q8_0 GEMM 4096 rows x 4096 tokens x 4096",
                              "us": round(us, 1), "TOPS": round(GEMM_OPS / us / 1e6, 1),
                              "regions": 3}
+    # the repack GEMM over the same weights (x16) and activations (x4), 4096^3
+    nb = N // 32
+    srcw = torch.from_numpy(w.reshape(N // 16, 16, nb, 18).transpose(0, 2, 1, 3).copy()).to(dev)
+    wx16 = torch.empty(N // 16 * nb * 288, dtype=torch.uint8, device=dev)
+    checked(lib.tcrv_hip_pack_q4_0_to_q4_0x16, "pack")(N // 16 * nb, srcw.data_ptr(),
+                                                        wx16.data_ptr(), sp)
+    ax4 = torch.empty(N // 4 * nb * 136, dtype=torch.uint8, device=dev)
+    checked(lib.tcrv_hip_pack_q8_0_to_q8_0x4, "pack_x4")(N, nb, ad.data_ptr(), a.shape[1],
+                                                          ax4.data_ptr(), sp)
+    del srcw
+    fn = checked(lib.tcrv_hip_repack_gemm_q4_0_q8_0, "repack_gemm")
+
+    def rp_gemm(i):
+        fn(N, cd.data_ptr(), wx16.data_ptr(), ax4.data_ptr(), N, N, N, sp)
+
+    Region(torch, stream, rp_gemm, 50).run()
+    reg = Region(torch, stream, rp_gemm, 10)
+    per = sorted(reg.run() * 1e3 / 10 for _ in range(3))
+    us = per[1]
+    out["repack_gemm_q4_0_q8_0"] = {"workload": "a8 repack GEMM: x16 Q4_0 weights 4096 x x4 "
+                                                "Q8_0 activations 4096 x K 4096",
+                                    "us": round(us, 1), "TOPS": round(GEMM_OPS / us / 1e6, 1),
+                                    "regions": 3}
     for k, v in out.items():
         if "GB/s" in v:
             log(f"{k}: {v['us']:.1f} us, {v['GB/s']:.0f} GB/s "
@@ -626,6 +649,14 @@ def cpu_baseline_configs(seconds: float):
     out["q4_0_q8_0_gemm"] = entry(2.0 * 16 * N * N * reps / dt / 1e12, "TOPS", threads,
                                   f"{reps} slices of 16 weight rows x 4096 tokens x 4096 "
                                   f"(1/256 of the GEMM each) in {dt:.1f} s, OpenMP over rows")
+    ax4 = ora.pack_q8_0x4(a8[:16].copy(), 16, N // 32, a8.shape[1])
+    wx16 = ora.pack_q4_0x16(w.reshape(N // 16, 16, N // 32, 18).transpose(0, 2, 1, 3).copy()
+                            .reshape(-1), N // 16 * (N // 32))
+    reps, dt = timed(lambda: ora.repack_gemm_q4_0(N, wx16, ax4, 16, N, N))
+    out["repack_gemm_q4_0_q8_0"] = entry(2.0 * 16 * N * N * reps / dt / 1e12, "TOPS", 1,
+                                         f"{reps} slices of 16 activation rows x 4096 weight rows "
+                                         f"x 4096 (1/256 of the GEMM each) in {dt:.1f} s, "
+                                         f"one thread")
     log("CPU oracle configs: " + ", ".join(f"{k} {v['value']} {v['unit']}"
                                            for k, v in out.items()))
     return out

@@ -225,6 +225,25 @@ TCRV_HIP_API int tcrv_hip_repack_gemv_q4_0_q8_0(size_t n, float *s, const uint8_
 TCRV_HIP_API int tcrv_hip_repack_gemv_q8_0_q8_0(size_t n, float *s, const uint8_t *vx,
                                    const uint8_t *vy, size_t nc, void *stream);
 
+/* tcrv_rvv.repack_gemm_q4_0_q8_0 (RVVOps.td:4228-4338, emitRepackGemmQ4_0Q8_0
+ * RVVToEmitCBlockQuantLinear.cpp:2122-2600; ABI (n, s, vx, vy, nr, nc, bs) as in
+ * rvv-to-emitc-repack-gemm-q4-0-q8-0.mlir:22-28): x16 Q4_0 weights (nc/16
+ * groups, group x at vx + x*(n/32)*288) times 4-row-interleaved Q8_0
+ * activations (block_q8_0x4, 136 B: fp16 d[4] @0, quant e of row c at
+ * 8 + 4e + c; nr/4 groups, group y at vy + y*(n/32)*136):
+ * s[(4y + c)*bs + 16x + r] = fold_b fma((float)sumi, d_w[r]*d_a[c], .) in
+ * ascending b.  Partial groups (nr % 4, nc % 16) are not written, as in the
+ * reference.  vx, vy and s 4-byte aligned; bs >= 16*(nc/16) when nr >= 8. */
+TCRV_HIP_API int tcrv_hip_repack_gemm_q4_0_q8_0(size_t n, float *s, const uint8_t *vx,
+                                   const uint8_t *vy, size_t nr, size_t nc, size_t bs,
+                                   void *stream);
+/* No reference counterpart (ggml repacks the activations itself): groups of 4
+ * plain Q8_0 rows of nb blocks (row stride by, 2-byte aligned) -> nrows/4
+ * groups of nb block_q8_0x4, the layout tcrv_hip_repack_gemm_q4_0_q8_0 reads.
+ * dst 4-byte aligned. */
+TCRV_HIP_API int tcrv_hip_pack_q8_0_to_q8_0x4(size_t nrows, size_t nb, const uint8_t *src,
+                                 size_t by, uint8_t *dst, void *stream);
+
 /* ---- the split (SoA) Q4_0 weight layout: no reference counterpart --------
  * A GPU layout of the same bytes: for nrows rows of nb blocks, the 16 quant
  * bytes of row r block b at dst + (r*nb + b)*16 and its fp16 scale at

@@ -41,7 +41,8 @@ enum {
   TCRV_HIP_ALGO_DECLINE = 0,     /* no gfx950 kernel: the caller keeps its own route */
   TCRV_HIP_ALGO_DECODE_GEMV = 1, /* bandwidth-bound GEMV over plain rows */
   TCRV_HIP_ALGO_REPACK_GEMV = 2, /* GEMV over block_q*_0x16 weights */
-  TCRV_HIP_ALGO_MFMA_GEMM = 3    /* int8 MFMA GEMM */
+  TCRV_HIP_ALGO_MFMA_GEMM = 3,   /* int8 MFMA GEMM */
+  TCRV_HIP_ALGO_REPACK_GEMM = 4  /* int8 MFMA GEMM over block_q4_0x16 x block_q8_0x4 */
 };
 
 /* Selection from typed facts.  Writes the algorithm, its audit token and the
@@ -59,12 +60,16 @@ TCRV_HIP_API int tcrv_hip_route_m_regime(size_t nc);
  * (n, s, vx, vy, by, nr, nc, bx, bs) -- q4_0_q8_0_gemm's parameter order,
  * test/Conversion/RVV/rvv-to-emitc-q4-0-q8-0-gemm.mlir:23-31 -- on the
  * algorithm tcrv_hip_route_select picks for (weight_quant, the regime of nc,
- * weight_layout); the activation is always plain Q8_0 rows.  For x16 weights vx
- * holds nr/16 groups of 16 rows in the x16 layout, bx is ignored, and the call
- * needs nc == 1, nr % 16 == 0 and bs == 1 (or nr == 1): the repacked GEMV
- * writes s[ir] and leaves a partial group unwritten.  A declined request
- * returns TCRV_HIP_ERR_UNSUPPORTED before touching anything.  *algorithm (may
- * be NULL) receives the algorithm used. */
+ * weight_layout).  Plain weights: the activation is plain Q8_0 rows.  x16
+ * weights: vx holds nr/16 groups of 16 rows in the x16 layout, bx and by are
+ * ignored, and nr % 16 == 0.  Decode (nc == 1) runs the repacked GEMV on one
+ * plain Q8_0 activation row and needs bs == 1 (or nr == 1): it writes s[ir].
+ * Prefill runs the repack GEMM in that op's contract
+ * (tcrv_hip_repack_gemm_q4_0_q8_0): vy holds nc/4 groups of block_q8_0x4,
+ * nc % 4 == 0, and the output is activation-row major, s[col*bs + ir].  A
+ * declined request, or an x16 shape outside these, returns
+ * TCRV_HIP_ERR_UNSUPPORTED before touching anything.  *algorithm (may be
+ * NULL) receives the algorithm used. */
 TCRV_HIP_API int tcrv_hip_route_contraction(int weight_quant, int weight_layout, size_t n,
                                             float *s, const uint8_t *vx, const uint8_t *vy,
                                             size_t by, size_t nr, size_t nc, size_t bx,
@@ -103,6 +108,7 @@ enum class HipContractionAlgorithm {
   DecodeGemv = TCRV_HIP_ALGO_DECODE_GEMV,
   RepackGemv = TCRV_HIP_ALGO_REPACK_GEMV,
   MfmaGemm = TCRV_HIP_ALGO_MFMA_GEMM,
+  RepackGemm = TCRV_HIP_ALGO_REPACK_GEMM,
 };
 
 struct HipContractionSelection {

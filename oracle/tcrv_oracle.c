@@ -570,3 +570,59 @@ void tcrv_oracle_repack_gemv_q8_0_q8_0(size_t n, float *s, const uint8_t *vx,
       s[x * 16 + r] = acc[r];
   }
 }
+
+/* Inverse of the repack GEMM's activation addressing (RVVToEmitCBlockQuantLinear.cpp:
+ * 2344-2600: al.d[c], al.qs[i*4 + c] low half, al.qs[64 + i*4 + c] high half). */
+void tcrv_oracle_pack_q8_0_to_q8_0x4(size_t nrows, size_t nb, const uint8_t *src, size_t by,
+                                     uint8_t *dst) {
+  for (size_t y = 0; y < nrows / 4; ++y)
+    for (size_t b = 0; b < nb; ++b) {
+      uint8_t *o = dst + (y * nb + b) * TCRV_Q8_0X4_BLOCK_BYTES;
+      for (int c = 0; c < 4; ++c) {
+        const uint8_t *blk = src + (y * 4 + c) * by + b * TCRV_Q8_0_BLOCK_BYTES;
+        o[2 * c] = blk[0];
+        o[2 * c + 1] = blk[1];
+        for (int e = 0; e < TCRV_QK; ++e)
+          o[8 + 4 * e + c] = blk[2 + e];
+      }
+    }
+}
+
+/* emitRepackGemmQ4_0Q8_0 (RVVToEmitCBlockQuantLinear.cpp:2122-2600), RVV 1.0 form:
+ * per (row group y, weight group x, block l) the lane-wise i16 lo/hi sums over
+ * the 16 nibble steps, widened and added, then the fp16 x fp16 scale product
+ * and one fused multiply-add per (activation row c, weight row r). */
+void tcrv_oracle_repack_gemm_q4_0_q8_0(size_t n, float *s, const uint8_t *vx,
+                                       const uint8_t *vy, size_t nr, size_t nc, size_t bs) {
+  size_t nb = n / TCRV_QK;
+  for (size_t y = 0; y < nr / 4; ++y)
+    for (size_t x = 0; x < nc / 16; ++x) {
+      float acc[4][16];
+      for (int c = 0; c < 4; ++c)
+        for (int r = 0; r < 16; ++r)
+          acc[c][r] = 0.0f;
+      for (size_t l = 0; l < nb; ++l) {
+        const uint8_t *bl = vx + (x * nb + l) * TCRV_Q4_0X16_BLOCK_BYTES;
+        const uint8_t *al = vy + (y * nb + l) * TCRV_Q8_0X4_BLOCK_BYTES;
+        for (int c = 0; c < 4; ++c) {
+          float da = load_d(al + 2 * c);
+          for (int r = 0; r < 16; ++r) {
+            int16_t sumi_lo = 0, sumi_hi = 0;
+            for (int i = 0; i < 16; ++i) {
+              int8_t v = (int8_t)bl[32 + i * 16 + r];
+              int8_t lo = (int8_t)((int8_t)(uint8_t)((uint8_t)v << 4) >> 4);
+              int8_t hi = (int8_t)(v >> 4);
+              sumi_lo = (int16_t)(sumi_lo + (int16_t)lo * (int16_t)(int8_t)al[8 + i * 4 + c]);
+              sumi_hi = (int16_t)(sumi_hi + (int16_t)hi * (int16_t)(int8_t)al[8 + 64 + i * 4 + c]);
+            }
+            int32_t sumi = (int32_t)sumi_lo + (int32_t)sumi_hi;
+            float d = load_d(bl + 2 * r) * da;
+            acc[c][r] = fmaf((float)sumi, d, acc[c][r]);
+          }
+        }
+      }
+      for (int c = 0; c < 4; ++c)
+        for (int r = 0; r < 16; ++r)
+          s[(y * 4 + c) * bs + x * 16 + r] = acc[c][r];
+    }
+}

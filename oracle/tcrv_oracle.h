@@ -133,6 +133,27 @@ void tcrv_oracle_unpack_q8_0x16(size_t nblocks, const uint8_t *src, uint8_t *dst
 void tcrv_oracle_repack_gemv_q8_0_q8_0(size_t n, float *s, const uint8_t *vx,
                                        const uint8_t *vy, size_t nc);
 
+/* block_q8_0x4 (136 B): fp16 d[4] @0 (row c at byte 2c), int8 qs[128] @8 with
+ * quant e of row c at qs[4e + c] -- the layout tcrv_rvv.repack_gemm_q4_0_q8_0
+ * reads (RVVOps.td:4228-4338: stride 136, quants at +8, 4-row interleave; the
+ * emitter reads al.qs[i*4 + c] and al.qs[64 + i*4 + c] for nibble step i and
+ * al.d[c], RVVToEmitCBlockQuantLinear.cpp:2344-2600).  The reference has no
+ * producer op for it (ggml repacks the activations); this pack is the inverse
+ * of the consumer's addressing: groups of 4 plain Q8_0 rows (stride by), nb
+ * blocks each, into nrows/4 groups of nb x4 blocks. */
+#define TCRV_Q8_0X4_BLOCK_BYTES 136
+void tcrv_oracle_pack_q8_0_to_q8_0x4(size_t nrows, size_t nb, const uint8_t *src, size_t by,
+                                     uint8_t *dst);
+/* The repack GEMM (emitRepackGemmQ4_0Q8_0, RVVToEmitCBlockQuantLinear.cpp:2122-2600):
+ * activation row group y < nr/4 (x4 blocks at vy + y*nb*136), weight group
+ * x < nc/16 (x16 blocks at vx + x*nb*288); for activation row c and weight row
+ * r, per block: sumi = i16 lo/hi sums of the nibble decode against
+ * qs[4i + c] and qs[64 + 4i + c] widened to i32, and the fold
+ * acc = fma((float)sumi, d_w[r]*d_a[c], acc) (vfwmul exact, vfmacc fused) in
+ * ascending block order; s[(y*4 + c)*bs + x*16 + r] = acc. */
+void tcrv_oracle_repack_gemm_q4_0_q8_0(size_t n, float *s, const uint8_t *vx,
+                                       const uint8_t *vy, size_t nr, size_t nc, size_t bs);
+
 #ifdef __cplusplus
 }
 #endif

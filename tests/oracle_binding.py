@@ -47,6 +47,8 @@ _SIGS = {
     "tcrv_oracle_unpack_q4_0_soa": ([_sz, _sz, _p, _p], None),
     "tcrv_oracle_unpack_q8_0x16": ([_sz, _p, _p], None),
     "tcrv_oracle_repack_gemv_q8_0_q8_0": ([_sz, _p, _p, _p, _sz], None),
+    "tcrv_oracle_pack_q8_0_to_q8_0x4": ([_sz, _sz, _p, _sz, _p], None),
+    "tcrv_oracle_repack_gemm_q4_0_q8_0": ([_sz, _p, _p, _p, _sz, _sz, _sz], None),
 }
 
 
@@ -194,6 +196,17 @@ class Oracle:
     def repack_gemv_q8_0(self, n: int, vx: np.ndarray, vy: np.ndarray, nc: int) -> np.ndarray:
         s = np.zeros(nc, dtype=np.float32)
         self.lib.tcrv_oracle_repack_gemv_q8_0_q8_0(n, _a(s), _a(vx), _a(vy), nc)
+        return s
+
+    def pack_q8_0x4(self, src: np.ndarray, nrows: int, nb: int, by: int) -> np.ndarray:
+        dst = np.zeros(nrows // 4 * nb * 136, dtype=np.uint8)
+        self.lib.tcrv_oracle_pack_q8_0_to_q8_0x4(nrows, nb, _a(src), by, _a(dst))
+        return dst
+
+    def repack_gemm_q4_0(self, n: int, vx: np.ndarray, vy: np.ndarray, nr: int, nc: int,
+                         bs: int) -> np.ndarray:
+        s = np.zeros(nr * bs, dtype=np.float32)
+        self.lib.tcrv_oracle_repack_gemm_q4_0_q8_0(n, _a(s), _a(vx), _a(vy), nr, nc, bs)
         return s
 
 

@@ -443,6 +443,60 @@ def test_repack_gemv_unaligned_operands(hip, oracle, dev, quant, nc, nb):
             assert_f32_parity(from_dev(s), ref,
                               what=f"repack {quant} {wwhat} weights, {what} activation")
 
+# ------------------------------------------------------ a8 repack GEMM (x16 x x4) ---
+
+@pytest.mark.parametrize("nr,nb,pad", [(4, 1, 0), (12, 5, 6), (130, 9, 0)])
+def test_pack_q8_0x4(hip, oracle, dev, nr, nb, pad):
+    a = np.pad(synth.q8_0_matrix(nr, nb * 32, 70, 1.0), ((0, 0), (0, pad)))
+    dst = to_dev(np.full(nr // 4 * nb * 136, 0xEE, np.uint8), dev)
+    hip.pack_q8_0_to_q8_0x4(nr, nb, to_dev(a, dev), a.shape[1], dst)
+    assert np.array_equal(from_dev(dst), oracle.pack_q8_0x4(a, nr, nb, a.shape[1]))
+
+
+@pytest.mark.parametrize("nr,nc,nb,bpad", [
+    (4, 16, 1, 0),        # one group each way, one block
+    (128, 256, 128, 0),   # one full 256 x 128 tile, full K
+    (38, 40, 7, 3),       # partial chunk (4 + 3 blocks); trailing rows and columns unwritten
+    (520, 300, 13, 5),    # five token tiles, two weight tiles (the second partial)
+])
+def test_repack_gemm_q4_0(hip, oracle, dev, nr, nc, nb, bpad):
+    n = nb * 32
+    w = synth.q4_0_matrix(nc, n, 71, 0.02)
+    a = synth.q8_0_matrix(nr, n, 72, 1.0)
+    a[0, 2:34] = 0x80  # -128 activations: the i16 lo/hi bound against -8 weights
+    groups = nc // 16
+    packed = oracle.pack_q4_0x16(x16_source(w[:16 * groups], nb, 18), groups * nb)
+    ax4 = to_dev(np.zeros(nr // 4 * nb * 136, np.uint8), dev)
+    hip.pack_q8_0_to_q8_0x4(nr, nb, to_dev(a, dev), a.shape[1], ax4)
+    bs = nc + bpad
+    s = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+    hip.repack_gemm_q4_0_q8_0(n, s, to_dev(packed, dev), ax4, nr, nc, bs)
+    got = from_dev(s).reshape(nr, bs)
+    want = oracle.repack_gemm_q4_0(n, packed, from_dev(ax4), nr, nc, bs).reshape(nr, bs)
+    rows, cols = nr // 4 * 4, 16 * groups
+    assert_f32_parity(got[:rows, :cols], want[:rows, :cols], what=f"repack gemm {nr}x{nc}x{n}")
+    assert np.all(got[rows:] == -7.0) and np.all(got[:, cols:] == -7.0)  # unwritten
+
+
+def test_repack_gemm_full_size_sampled_tokens(hip, oracle, dev):
+    """4096 weight rows x 4096 tokens x K 4096 on the GPU; the oracle checks three
+    4-token groups (first, middle, last) against all 4096 weight rows."""
+    n = 4096
+    nb = n // 32
+    w = synth.q4_0_matrix(4096, n, 1006, 0.02)
+    a = synth.q8_0_matrix(4096, n, 1008, 1.0)
+    packed = oracle.pack_q4_0x16(x16_source(w, nb, 18), 256 * nb)
+    ax4 = empty_dev(1024 * nb * 136, torch.uint8, dev)
+    hip.pack_q8_0_to_q8_0x4(4096, nb, to_dev(a, dev), a.shape[1], ax4)
+    s = empty_dev(4096 * 4096, torch.float32, dev)
+    hip.repack_gemm_q4_0_q8_0(n, s, to_dev(packed, dev), ax4, 4096, 4096, 4096)
+    got = from_dev(s).reshape(4096, 4096)
+    hx4 = from_dev(ax4).reshape(1024, nb * 136)
+    for y in (0, 517, 1023):
+        want = oracle.repack_gemm_q4_0(n, packed, np.ascontiguousarray(hx4[y]), 4, 4096, 4096)
+        assert_f32_parity(got[4 * y:4 * y + 4], want.reshape(4, 4096), what=f"group {y}")
+
+
 # ------------------------------------------------ a7 Q4_0 GEMM on MFMA (nc > 1) ---
 
 @pytest.mark.parametrize("nr,nc,nb,pad", [(512, 512, 128, 0), (130, 70, 9, 16), (64, 2, 3, 0),

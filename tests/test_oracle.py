@@ -488,6 +488,51 @@ def test_repack_gemv_q8_exact_fold_and_trailing_columns(oracle):
     assert np.all(got[32:] == 0)
 
 
+def unpack_q8_0x4_np(packed, ngroups, nb):
+    """Independent numpy inverse of block_q8_0x4 (scale of row c at bytes 2c,
+    quant e of row c at qs[4e + c]): back to 4 plain rows per group."""
+    p = packed.reshape(ngroups, nb, 136)
+    out = np.zeros((ngroups, 4, nb, 34), dtype=np.uint8)
+    out[:, :, :, 0:2] = p[:, :, 0:8].reshape(ngroups, nb, 4, 2).transpose(0, 2, 1, 3)
+    out[:, :, :, 2:] = p[:, :, 8:].reshape(ngroups, nb, 32, 4).transpose(0, 3, 1, 2)
+    return out.reshape(ngroups * 4, nb * 34)
+
+
+def test_pack_q8_0x4_round_trip(oracle):
+    nr, nb = 12, 5
+    a = synth.q8_0_matrix(nr, nb * 32, 55, 1.0)
+    packed = oracle.pack_q8_0x4(a, nr, nb, a.shape[1])
+    assert packed.size == nr // 4 * nb * 136
+    assert np.array_equal(unpack_q8_0x4_np(packed, nr // 4, nb), a)
+    # a padded source stride reads the same rows
+    ap = np.pad(a, ((0, 0), (0, 6)))
+    assert np.array_equal(oracle.pack_q8_0x4(ap, nr, nb, ap.shape[1]), packed)
+
+
+def test_repack_gemm_rows_equal_the_repack_gemv(oracle):
+    """Every activation row of the repack GEMM is the (separately pinned) x16
+    GEMV of that row: same nibble decode, same i16 lo/hi sums, same fold
+    fma((float)sumi, d_w*d_a, acc).  Trailing activation rows (nr % 4) and
+    weight rows (nc % 16) are not written."""
+    nb, nc, nr = 7, 40, 10
+    n = nb * 32
+    w = synth.q4_0_matrix(nc, n, 56, 0.02)
+    a = synth.q8_0_matrix(nr, n, 57, 1.0)
+    a[1, 2:34] = 0x80          # -128 activations ...
+    w[5, 2:18] = 0x00          # ... against -8 weights: the i16 lo/hi bound (16 * 1024)
+    groups = nc // 16
+    packed = oracle.pack_q4_0x16(x16_gather(w[:16 * groups], nb, 18), groups * nb)
+    ax4 = oracle.pack_q8_0x4(a, nr, nb, a.shape[1])
+    bs = nc + 3
+    got = oracle.repack_gemm_q4_0(n, packed, ax4, nr, nc, bs).reshape(nr, bs)
+    for c in range(nr // 4 * 4):
+        want = oracle.repack_gemv_q4_0(n, packed, a[c].copy(), nc)
+        assert np.array_equal(got[c, :16 * groups].view(np.uint32),
+                              want[:16 * groups].view(np.uint32)), c
+    assert np.all(got[:, 16 * groups:] == 0)
+    assert np.all(got[nr // 4 * 4:] == 0)
+
+
 BINARY_ELEMS = [(0, np.int8), (1, np.uint8), (2, np.int16), (3, np.uint16), (4, np.int32),
                 (5, np.uint32), (6, np.int64), (7, np.float32), (8, np.float64)]
 

@@ -55,7 +55,7 @@ def test_route_library_exports_its_header():
     ("q8_0", tcrv_hip.M_PREFILL, "plain", "mfma_gemm", "tcrv_hip_q8_0_q8_0_gemm"),
     ("q4_0", tcrv_hip.M_DECODE, "x16", "repack_gemv", "tcrv_hip_repack_gemv_q4_0_q8_0"),
     ("q8_0", tcrv_hip.M_DECODE, "x16", "repack_gemv", "tcrv_hip_repack_gemv_q8_0_q8_0"),
-    ("q4_0", tcrv_hip.M_PREFILL, "x16", "decline", None),
+    ("q4_0", tcrv_hip.M_PREFILL, "x16", "repack_gemm", "tcrv_hip_repack_gemm_q4_0_q8_0"),
     ("q8_0", tcrv_hip.M_PREFILL, "x16", "decline", None),
     ("q4_K", tcrv_hip.M_DECODE, "plain", "decline", None),
     ("q4_K", tcrv_hip.M_PREFILL, "plain", "decline", None),
@@ -129,6 +129,9 @@ def test_route_table_keeps_the_reference_gemm_abi():
     # rvv-to-emitc-q4-0-q8-0-gemm.mlir:23-31
     assert [p[0] for p in gemm] == ["n", "s", "vx", "vy", "by", "nr", "nc", "bx", "bs"]
     assert rows["tcrv_rvv.q8_0_q8_0_gemm"]["params"] == gemm
+    rgemm = rows["tcrv_rvv.repack_gemm_q4_0_q8_0"]["params"]
+    # rvv-to-emitc-repack-gemm-q4-0-q8-0.mlir:22-28
+    assert [p[0] for p in rgemm] == ["n", "s", "vx", "vy", "nr", "nc", "bs"]
     dot = rows["tcrv_rvv.q4_0_q8_0_block_dot"]["params"]
     # the ggml vec_dot ABI, rvv-to-emitc-q4-0-q8-0-block-dot.mlir:24-31
     assert [p[0] for p in dot] == ["n", "s", "bs", "vx", "bx", "vy", "by", "nrc"]
@@ -137,7 +140,9 @@ def test_route_table_keeps_the_reference_gemm_abi():
 
 @pytest.mark.parametrize("quant,layout,nr,nc,bs", [
     ("q4_K", "plain", 16, 1, 1),   # no kernel for the format
-    ("q4_0", "x16", 32, 8, 8),     # x16 prefill: declined
+    ("q8_0", "x16", 32, 8, 8),     # Q8_0 x16 prefill: no repack GEMM in the reference
+    ("q4_0", "x16", 32, 6, 8),     # Q4_0 x16 prefill with a partial 4-row activation group
+    ("q4_0", "x16", 24, 8, 8),     # Q4_0 x16 prefill with a partial 16-row weight group
     ("q4_0", "x16", 24, 1, 1),     # x16 decode with a partial 16-row group
     ("q8_0", "x16", 32, 1, 4),     # x16 decode into a strided output
 ])
@@ -195,3 +200,18 @@ def test_routed_contractions_match_the_oracle(oracle, dev):
         assert algo == "repack_gemv"
         assert packed.size == nr // 16 * nb * xbytes
         assert_f32_parity(from_dev(s), ref(n, packed, x, nr), what=f"routed {quant} x16")
+
+    # prefill over x16 Q4_0 weights -> the repack GEMM (x4 activations, output
+    # activation-row major)
+    nc = 8
+    plain = synth.q4_0_matrix(nr, n, 1006, 0.02)
+    src = plain.reshape(nr // 16, 16, nb, 18).transpose(0, 2, 1, 3).reshape(-1)
+    packed = oracle.pack_q4_0x16(np.ascontiguousarray(src), nr // 16 * nb)
+    a8 = synth.q8_0_matrix(nc, n, 1008, 1.0)
+    ax4 = oracle.pack_q8_0x4(a8, nc, nb, a8.shape[1])
+    s = empty_dev(nc * nr, torch.float32, dev)
+    _, algo = tcrv_hip.route_contraction("q4_0", "x16", n, s, to_dev(packed, dev),
+                                         to_dev(ax4, dev), 0, nr, nc, 0, nr)
+    assert algo == "repack_gemm"
+    assert_f32_parity(from_dev(s), oracle.repack_gemm_q4_0(n, packed, ax4, nc, nr, nr),
+                      what="routed q4_0 x16 prefill")

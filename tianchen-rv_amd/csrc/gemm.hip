@@ -628,6 +628,225 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_wide(
         s[row * bs + col] = acc[i][e];
     }
 }
+
+// ---------------------------------------------------------------------------
+// Repack GEMM (tcrv_rvv.repack_gemm_q4_0_q8_0, RVVOps.td:4228-4338; emitter
+// RVVToEmitCBlockQuantLinear.cpp:2122-2600): x16-interleaved Q4_0 weights
+// (block_q4_0x16, 288 B: 16 rows per group, nibble bytes biased ^0x88) times
+// 4-row-interleaved Q8_0 activations (block_q8_0x4, 136 B: fp16 d[4] @0, quant
+// e of row c at 8 + 4e + c), output s[token*bs + weight_row].  Per element and
+// block: exact int32 sum, then acc = fma((float)sumi, d_w*d_a, acc) -- the
+// x16 fold, the same as the Q8_0 fold -- in ascending block order.
+// The kernel is gemm_wide<false>'s pipeline with another staging: each chunk's
+// x16 and x4 blocks are turned into the row-major staged layout (int8 quants of
+// a row at kWQRow stride, f32 scales [block][row]) with 4x4 byte transposes, so
+// the MFMA tiles and the fold are unchanged.  Staging tasks per 4-block chunk:
+// 256 weight tasks (x16 group, block, position quad: four 128-bit loads, 16
+// rows x 4 positions) on waves 0-3 and 256 activation tasks (x4 group, block,
+// half: four 128-bit loads, 4 rows x 16 elements) on waves 4-7.
+// ---------------------------------------------------------------------------
+constexpr int kQ4x16 = 288, kQ8x4 = 136;
+
+struct RgRegs {
+  uint32_t r[18];
+};
+
+// A staging task's 64 quant bytes (four 128-bit loads, 4-byte aligned) and 8
+// scale bytes.  Weight task (x16 block, position quad q): positions 4q..4q+3,
+// 16 rows each, and the scales of rows 4q..4q+3.  Activation task (x4 block,
+// half hf): elements 16hf..16hf+15 (dword e: element e of rows 0..3) and the 4
+// scales.
+__device__ __forceinline__ void rg_load(RgRegs &p, const uint8_t *quant, const uint8_t *scale) {
+  const u32x4a4 *src = reinterpret_cast<const u32x4a4 *>(quant);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const u32x4a4 v = src[m];
+    p.r[4 * m] = v.x; p.r[4 * m + 1] = v.y; p.r[4 * m + 2] = v.z; p.r[4 * m + 3] = v.w;
+  }
+  const uint32_t *d = reinterpret_cast<const uint32_t *>(scale);
+  p.r[16] = d[0];
+  p.r[17] = d[1];
+}
+
+// -> rows 16g + 0..15, quants 32j + 4q.. (low nibbles) and 32j + 16 + 4q..
+// (high nibbles) as int8, scales dsc_j[16g + 4q .. +3]
+__device__ __forceinline__ void rg_store_w(const RgRegs &p, int8_t *stage, float *dsc_j, int g,
+                                           int j, int q) {
+#pragma unroll
+  for (int rq = 0; rq < 4; ++rq) {
+    const uint32_t in[4] = {p.r[rq], p.r[4 + rq], p.r[8 + rq], p.r[12 + rq]};
+    uint32_t rows[4];
+    transpose4x4(in, rows);  // rows[rr]: positions 4q..4q+3 of row 4rq + rr
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const uint32_t raw = rows[rr] ^ 0x88888888u;  // the plain Q4_0 quant bytes
+      int8_t *dst = stage + (16 * g + 4 * rq + rr) * kWQRow + kQK * j + 4 * q;
+      *reinterpret_cast<uint32_t *>(dst) = nibbles_to_i8x4(raw);
+      *reinterpret_cast<uint32_t *>(dst + 16) = nibbles_to_i8x4(raw >> 4);
+    }
+  }
+  *reinterpret_cast<float4 *>(dsc_j + 16 * g + 4 * q) =
+      make_float4(fp16_bits_to_f32(p.r[16] & 0xffffu), fp16_bits_to_f32(p.r[16] >> 16),
+                  fp16_bits_to_f32(p.r[17] & 0xffffu), fp16_bits_to_f32(p.r[17] >> 16));
+}
+
+// -> rows kWBM + 4t + 0..3, quants 32j + 16hf + 0..15, scales dsc_j[kWBM + 4t ..]
+__device__ __forceinline__ void rg_store_a(const RgRegs &p, int8_t *stage, float *dsc_j, int t,
+                                           int j, int hf) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    uint32_t rows[4];
+    transpose4x4(&p.r[4 * m], rows);  // rows[c]: elements 16hf + 4m .. +3 of row c
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      *reinterpret_cast<uint32_t *>(stage + (kWBM + 4 * t + c) * kWQRow + kQK * j + 16 * hf +
+                                    4 * m) = rows[c];
+  }
+  if (hf == 0)
+    *reinterpret_cast<float4 *>(dsc_j + kWBM + 4 * t) =
+        make_float4(fp16_bits_to_f32(p.r[16] & 0xffffu), fp16_bits_to_f32(p.r[16] >> 16),
+                    fp16_bits_to_f32(p.r[17] & 0xffffu), fp16_bits_to_f32(p.r[17] >> 16));
+}
+
+__global__ __launch_bounds__(kOcThreads, 1) void gemm_repack_q4_0(
+    size_t nb, float *s, const uint8_t *vx, const uint8_t *vy, size_t ngw, size_t nga,
+    size_t bs) {
+  __shared__ __align__(16) int8_t q[2][kWStage];
+  __shared__ __align__(16) float dsc[2][kWKB][kWRows];  // [stage][block][row]
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int wm = wave >> 2, wn = wave & 3;  // 64 weight rows x 32 tokens per wave
+  const int li = lane & 31, h = lane >> 5;
+  const size_t nrw = ngw * 16, ntok = nga * 4;  // rows and tokens written
+  const unsigned tiles_m = static_cast<unsigned>((nrw + kWBM - 1) / kWBM);
+  const unsigned tiles_n = static_cast<unsigned>((ntok + kWBN - 1) / kWBN);
+  unsigned tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const size_t m0 = static_cast<size_t>(tm) * kWBM;
+  const size_t n0 = static_cast<size_t>(tn) * kWBN;
+
+  // staging task of this thread: waves 0-3 weights, 4-7 activations, 8-15
+  // none (the kind is wave-uniform: taken from the first lane)
+  const int swave = __builtin_amdgcn_readfirstlane(wave);
+  const bool wtask = swave < 4, atask = swave >= 4 && swave < 8;
+  const int k = tid & 255;
+  const int sg = wtask ? k >> 4 : k >> 3;              // x16 group / x4 group in the tile
+  const int sj = wtask ? (k >> 2) & 3 : (k >> 1) & 3;  // block of the chunk
+  const int sq = wtask ? k & 3 : k & 1;                // position quad / half
+  const int sblk = wtask ? kQ4x16 : kQ8x4;
+  const uint8_t *sblk0 = (wtask ? vx + min(m0 / 16 + sg, ngw - 1) * nb * kQ4x16
+                                : vy + min(n0 / 4 + sg, nga - 1) * nb * kQ8x4) + sj * sblk;
+  // this task's quant bytes and scale dwords in block sj of chunk 0
+  const uint8_t *squant = sblk0 + (wtask ? 32 + 64 * sq : 8 + 64 * sq);
+  const uint8_t *sscale = sblk0 + (wtask ? 8 * sq : 0);
+  const size_t cstride = static_cast<size_t>(kWKB) * sblk;  // bytes per chunk
+
+  float acc[2][16];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      acc[i][e] = 0.0f;
+
+  const size_t nchunks = (nb + kWKB - 1) / kWKB;
+  RgRegs pr;
+  if ((wtask || atask) && sj < static_cast<int>(min(static_cast<size_t>(kWKB), nb))) {
+    rg_load(pr, squant, sscale);
+    if (wtask)
+      rg_store_w(pr, q[0], dsc[0][sj], sg, sj, sq);
+    else
+      rg_store_a(pr, q[0], dsc[0][sj], sg, sj, sq);
+  }
+  __syncthreads();
+
+  const int8_t *qa0 = q[0] + (wm * 64 + li) * kWQRow + 16 * h;
+  const int8_t *qb0 = q[0] + (kWBM + wn * 32 + li) * kWQRow + 16 * h;
+  const float *sxh0 = &dsc[0][h][wm * 64 + li];
+  const float *syh0 = &dsc[0][h][kWBM + wn * 32 + li];
+  constexpr int kDscStage = kWKB * kWRows;
+
+  const size_t nfull = nb / kWKB;
+  for (size_t c = 0; c < nfull; ++c) {
+    const int st = static_cast<int>(c & 1);
+    const bool act1 = (wtask || atask) && c + 1 < nchunks &&
+                      static_cast<size_t>(sj) < min(static_cast<size_t>(kWKB), nb - (c + 1) * kWKB);
+    if (act1)
+      rg_load(pr, squant + (c + 1) * cstride, sscale + (c + 1) * cstride);
+#pragma unroll
+    for (int b = 0; b < kWKB; b += 2) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        fold_pair<false, true, kWRows>(acc[i], qa0 + i * 32 * kWQRow + st * kWStage,
+                                       qb0 + st * kWStage, sxh0 + i * 32 + st * kDscStage,
+                                       syh0 + st * kDscStage, nullptr, b);
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          asm volatile("" : "+v"(acc[i][e]));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (act1) {
+      if (wtask)
+        rg_store_w(pr, q[st ^ 1], dsc[st ^ 1][sj], sg, sj, sq);
+      else
+        rg_store_a(pr, q[st ^ 1], dsc[st ^ 1][sj], sg, sj, sq);
+    }
+    __syncthreads();
+  }
+  const int nbc = static_cast<int>(nb - nfull * kWKB);
+  if (nbc > 0) {
+    const int st = static_cast<int>(nfull & 1);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int8_t *qa = qa0 + i * 32 * kWQRow + st * kWStage;
+      const int8_t *qb = qb0 + st * kWStage;
+      const float *sxh = sxh0 + i * 32 + st * kDscStage;
+      const float *syh = syh0 + st * kDscStage;
+      int b = 0;
+      for (; b + 1 < nbc; b += 2)
+        fold_pair<false, true, kWRows>(acc[i], qa, qb, sxh, syh, nullptr, b);
+      if (b < nbc)
+        fold_pair<false, false, kWRows>(acc[i], qa, qb, sxh, syh, nullptr, b);
+    }
+  }
+
+  const size_t tok = n0 + wn * 32 + li;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const size_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (row < nrw && tok < ntok)
+        s[tok * bs + row] = acc[i][e];
+    }
+}
+
+// Plain Q8_0 rows (stride by), groups of 4, -> block_q8_0x4: thread per output
+// dword (2 scale dwords + 32 quant dwords, dword 2 + e = element e of rows 0..3).
+__global__ __launch_bounds__(256) void pack_q8_0x4(size_t ngroups, size_t nb, const uint8_t *src,
+                                                   size_t by, uint8_t *dst) {
+  const size_t t = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= ngroups * nb * (kQ8x4 / 4))
+    return;
+  const size_t o = t / (kQ8x4 / 4);
+  const int k = static_cast<int>(t - o * (kQ8x4 / 4));
+  const size_t y = o / nb, b = o - y * nb;
+  const uint8_t *row0 = src + (y * 4) * by + b * kQ8Bytes;
+  uint32_t v;
+  if (k < 2) {  // scales of rows 2k, 2k+1
+    v = static_cast<uint32_t>(*reinterpret_cast<const uint16_t *>(row0 + (2 * k) * by)) |
+        (static_cast<uint32_t>(*reinterpret_cast<const uint16_t *>(row0 + (2 * k + 1) * by))
+         << 16);
+  } else {
+    const int e = k - 2;
+    v = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      v |= static_cast<uint32_t>(row0[c * by + 2 + e]) << (8 * c);
+  }
+  reinterpret_cast<uint32_t *>(dst + o * kQ8x4)[k] = v;
+}
 }  // namespace tcrv
 
 namespace tcrv_host {
@@ -706,5 +925,50 @@ extern "C" int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx,
   tcrv::gemm_q8_0_q8_0_kernel<<<dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)),
                                 dim3(tcrv::kGmThreads), 0, as_stream(stream)>>>(
       nb, s, vx, vy, by, nr, nc, bx, bs, rows16);
+  return launch_status();
+}
+
+extern "C" int tcrv_hip_repack_gemm_q4_0_q8_0(size_t n, float *s, const uint8_t *vx,
+                                              const uint8_t *vy, size_t nr, size_t nc,
+                                              size_t bs, void *stream) {
+  using namespace tcrv_host;
+  const size_t nb = n / tcrv::kQK;
+  const size_t nga = nr / 4, ngw = nc / 16;  // like the reference, partial groups are not written
+  if (nga == 0 || ngw == 0)
+    return TCRV_HIP_OK;
+  if (nga > 1 && bs < ngw * 16)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  if (nb == 0)
+    return zero_outputs(s, nga * 4 * ngw * 16, bs, ngw * 16, stream);
+  if (!s || !vx || !vy)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned4(vx) || !aligned4(vy) || !aligned4(s))
+    return TCRV_HIP_ERR_MISALIGNED;
+  const size_t tiles = ((ngw * 16 + tcrv::kWBM - 1) / tcrv::kWBM) *
+                       ((nga * 4 + tcrv::kWBN - 1) / tcrv::kWBN);
+  if (tiles > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  tcrv::gemm_repack_q4_0<<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kOcThreads), 0,
+                           as_stream(stream)>>>(nb, s, vx, vy, ngw, nga, bs);
+  return launch_status();
+}
+
+extern "C" int tcrv_hip_pack_q8_0_to_q8_0x4(size_t nrows, size_t nb, const uint8_t *src,
+                                            size_t by, uint8_t *dst, void *stream) {
+  using namespace tcrv_host;
+  const size_t ngroups = nrows / 4;
+  if (ngroups == 0 || nb == 0)
+    return TCRV_HIP_OK;
+  if (!src || !dst)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned2(src) || (by & 1u) || !aligned4(dst))
+    return TCRV_HIP_ERR_MISALIGNED;
+  if (by < nb * tcrv::kQ8Bytes)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  const size_t grid = (ngroups * nb * (tcrv::kQ8x4 / 4) + 255) / 256;
+  if (grid > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  tcrv::pack_q8_0x4<<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, as_stream(stream)>>>(
+      ngroups, nb, src, by, dst);
   return launch_status();
 }

@@ -56,19 +56,6 @@ __global__ __launch_bounds__(256) void pack_x16(size_t nblocks, const uint8_t *s
   reinterpret_cast<uint32_t *>(dst + o * kDst)[k] = v;
 }
 
-// 4x4 byte transpose: in[i] holds rows 0..3 of position i; out[r] holds
-// positions 0..3 of row r.
-__device__ __forceinline__ void transpose4x4(const uint32_t in[4], uint32_t out[4]) {
-  const uint32_t t0 = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);  // i0r0 i1r0 i0r1 i1r1
-  const uint32_t t1 = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);  // i2r0 i3r0 i2r1 i3r1
-  const uint32_t t2 = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);  // i0r2 i1r2 i0r3 i1r3
-  const uint32_t t3 = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);  // i2r2 i3r2 i2r3 i3r3
-  out[0] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
-  out[1] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
-  out[2] = __builtin_amdgcn_perm(t3, t2, 0x05040100u);
-  out[3] = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
-}
-
 // Quant bytes 4k..4k+3 of activation block b staged raw (34-byte blocks) in
 // LDS: an even block starts on a dword (its quants sit 2 bytes in), an odd
 // block 2 bytes into one (its quants are dword aligned).

@@ -36,6 +36,19 @@ __device__ __forceinline__ uint32_t nibbles_to_i8x4(uint32_t u) {
   return ((u & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
 }
 
+// 4x4 byte transpose: in[i] holds rows 0..3 of position i; out[r] holds
+// positions 0..3 of row r.
+__device__ __forceinline__ void transpose4x4(const uint32_t in[4], uint32_t out[4]) {
+  const uint32_t t0 = __builtin_amdgcn_perm(in[1], in[0], 0x05010400u);  // i0r0 i1r0 i0r1 i1r1
+  const uint32_t t1 = __builtin_amdgcn_perm(in[3], in[2], 0x05010400u);  // i2r0 i3r0 i2r1 i3r1
+  const uint32_t t2 = __builtin_amdgcn_perm(in[1], in[0], 0x07030602u);  // i0r2 i1r2 i0r3 i1r3
+  const uint32_t t3 = __builtin_amdgcn_perm(in[3], in[2], 0x07030602u);  // i2r2 i3r2 i2r3 i3r3
+  out[0] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(t3, t2, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
+}
+
 // Bytes 2..5 of the 8-byte little-endian value hi:lo (v_alignbyte_b32).
 __device__ __forceinline__ uint32_t funnel16(uint32_t lo, uint32_t hi) {
   return __builtin_amdgcn_alignbyte(hi, lo, 2);

@@ -24,10 +24,10 @@ bool hipKernelExists(QuantType weight) {
   return false;
 }
 
-// Fact 2: the weights already sit in the x16 interleave.  On gfx950 the
-// interleave only has a decode consumer (the repacked GEMV); a prefill over
-// x16 weights has no kernel here (the reference's repack GEMM is not built),
-// so it is declined rather than silently unpacked.
+// Fact 2: the weights already sit in the x16 interleave.  Decode runs the
+// repacked GEMV; prefill runs the repack GEMM, which the reference defines for
+// Q4_0 only (tcrv_rvv.repack_gemm_q4_0_q8_0, RVVOps.td:4228), so a Q8_0 x16
+// prefill is declined rather than silently unpacked.
 bool weightsAreX16(WeightLayout layout) { return layout == WeightLayout::BlockX16; }
 
 // Fact 3: decode is one activation row: the weight stream is read once and
@@ -56,9 +56,10 @@ HipContractionSelection selectHipContractionAlgorithm(QuantType weight, MRegime 
                                                        ? "hip-repack-gemv-q4_0x16-decode"
                                                        : "hip-repack-gemv-q8_0x16-decode",
               repackEntry(weight)};
-    return {HipContractionAlgorithm::Decline,
-            weight == QuantType::Q4_0 ? "hip-decline-q4_0x16-prefill-no-repack-gemm"
-                                      : "hip-decline-q8_0x16-prefill-no-repack-gemm",
+    if (weight == QuantType::Q4_0)
+      return {HipContractionAlgorithm::RepackGemm, "hip-repack-gemm-q4_0x16-prefill-mfma-i8",
+              "tcrv_hip_repack_gemm_q4_0_q8_0"};
+    return {HipContractionAlgorithm::Decline, "hip-decline-q8_0x16-prefill-no-repack-gemm",
             nullptr};
   }
   if (isDecode(mRegime))
@@ -98,6 +99,7 @@ struct HipKernelRoute {
 //   q4_0 gemm tile: rvv-to-emitc-q4-0-q8-0-gemm-tile.mlir (+ its activation_cols)
 //   repack gemvs:   rvv-to-emitc-repack-gemv-q4-0-q8-0.mlir:26-30,
 //                   rvv-to-emitc-repack-gemv-q8-0-q8-0-vlen256.mlir
+//   repack gemm:    rvv-to-emitc-repack-gemm-q4-0-q8-0.mlir:22-28
 //   pack:           rvv-to-emitc-pack-q4-0-to-q4-0x16.mlir:19-21
 //   quantize:       rvv-to-emitc-ggml-quantize-row-q8-0.mlir
 // The Q8_0 GEMM has no reference op; it takes the q4_0 GEMM's ABI with Q8_0
@@ -141,6 +143,11 @@ const HipKernelRoute kHipKernelRoutes[] = {
      {{"n", "size_t", kN}, {"s", "float *", kOut}, {"vx", "const uint8_t *", kLhs},
       {"vy", "const uint8_t *", kRhs}, {"nc", "size_t", "destination-byte-stride"}},
      5},
+    {"tcrv_rvv.repack_gemm_q4_0_q8_0", "tcrv_hip_repack_gemm_q4_0_q8_0",
+     {{"n", "size_t", kN}, {"s", "float *", kOut}, {"vx", "const uint8_t *", kLhs},
+      {"vy", "const uint8_t *", kRhs}, {"nr", "size_t", "source-byte-stride"},
+      {"nc", "size_t", "destination-byte-stride"}, {"bs", "size_t", "output-stride"}},
+     7},
     {"tcrv_rvv.pack_q4_0_to_q4_0x16", "tcrv_hip_pack_q4_0_to_q4_0x16",
      {{"nblocks", "size_t", kN}, {"src", "const uint8_t *", kLhs}, {"dst", "uint8_t *", kOut}},
      3},
@@ -217,6 +224,14 @@ int tcrv_hip_route_contraction(int weight_quant, int weight_layout, size_t n, fl
       return TCRV_HIP_ERR_UNSUPPORTED;
     return q4 ? tcrv_hip_repack_gemv_q4_0_q8_0(n, s, vx, vy, nr, stream)
               : tcrv_hip_repack_gemv_q8_0_q8_0(n, s, vx, vy, nr, stream);
+  case HipContractionAlgorithm::RepackGemm:
+    // the op's own contract: nc activation rows in nc/4 block_q8_0x4 groups,
+    // output s[col*bs + ir]; shapes that would leave groups unwritten are refused
+    if (nr == 0 || nc == 0)
+      return TCRV_HIP_OK;
+    if (nr % 16 != 0 || nc % 4 != 0)
+      return TCRV_HIP_ERR_UNSUPPORTED;
+    return tcrv_hip_repack_gemm_q4_0_q8_0(n, s, vx, vy, nc, nr, bs, stream);
   case HipContractionAlgorithm::DecodeGemv:
   case HipContractionAlgorithm::MfmaGemm:
     return q4 ? tcrv_hip_q4_0_q8_0_gemm(n, s, vx, vy, by, nr, nc, bx, bs, stream)

@@ -70,6 +70,8 @@ SIGNATURES = {
     "tcrv_hip_pack_q8_0_to_q8_0x16": [_sz, _p, _p, _p],
     "tcrv_hip_repack_gemv_q4_0_q8_0": [_sz, _p, _p, _p, _sz, _p],
     "tcrv_hip_repack_gemv_q8_0_q8_0": [_sz, _p, _p, _p, _sz, _p],
+    "tcrv_hip_repack_gemm_q4_0_q8_0": [_sz, _p, _p, _p, _sz, _sz, _sz, _p],
+    "tcrv_hip_pack_q8_0_to_q8_0x4": [_sz, _sz, _p, _sz, _p, _p],
     "tcrv_hip_pack_q4_0_to_soa": [_sz, _sz, _p, _sz, _p, _p],
     "tcrv_hip_gemv_q4_0_soa_q8_0": [_sz, _p, _p, _p, _sz, _p],
 }
@@ -245,6 +247,14 @@ def repack_gemv_q8_0_q8_0(n: int, s, vx, vy, nc: int, stream=None):
     return call("tcrv_hip_repack_gemv_q8_0_q8_0", n, s, vx, vy, nc, _stream(stream))
 
 
+def repack_gemm_q4_0_q8_0(n: int, s, vx, vy, nr: int, nc: int, bs: int, stream=None):
+    return call("tcrv_hip_repack_gemm_q4_0_q8_0", n, s, vx, vy, nr, nc, bs, _stream(stream))
+
+
+def pack_q8_0_to_q8_0x4(nrows: int, nb: int, src, by: int, dst, stream=None):
+    return call("tcrv_hip_pack_q8_0_to_q8_0x4", nrows, nb, src, by, dst, _stream(stream))
+
+
 def pack_q4_0_to_soa(nrows: int, nb: int, src, bx: int, dst, stream=None):
     return call("tcrv_hip_pack_q4_0_to_soa", nrows, nb, src, bx, dst, _stream(stream))
 
@@ -265,7 +275,7 @@ ROUTE_LIB_PATH = os.path.join(HERE, "libtcrv_hip_route.so")
 QUANT = {"q4_0": 0, "q8_0": 1, "q4_K": 2}
 M_DECODE, M_PREFILL = 0, 1
 LAYOUT = {"plain": 0, "x16": 1}
-ALGO = {0: "decline", 1: "decode_gemv", 2: "repack_gemv", 3: "mfma_gemm"}
+ALGO = {0: "decline", 1: "decode_gemv", 2: "repack_gemv", 3: "mfma_gemm", 4: "repack_gemm"}
 
 _cs = ctypes.c_char_p
 ROUTE_SIGNATURES = {
