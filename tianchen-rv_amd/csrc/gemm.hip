@@ -710,7 +710,7 @@ __device__ __forceinline__ void rg_store_a(const RgRegs &p, int8_t *stage, float
 
 __global__ __launch_bounds__(kOcThreads, 1) void gemm_repack_q4_0(
     size_t nb, float *s, const uint8_t *vx, const uint8_t *vy, size_t ngw, size_t nga,
-    size_t bs) {
+    size_t bs, bool vec_out) {
   __shared__ __align__(16) int8_t q[2][kWStage];
   __shared__ __align__(16) float dsc[2][kWKB][kWRows];  // [stage][block][row]
 
@@ -811,15 +811,29 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_repack_q4_0(
     }
   }
 
+  // a lane holds 4 consecutive weight rows per group of 4 elements: one
+  // 128-bit store each when the output allows (nrw is a multiple of 16, so a
+  // group is written whole or not at all)
   const size_t tok = n0 + wn * 32 + li;
+  if (tok < ntok) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const size_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-      if (row < nrw && tok < ntok)
-        s[tok * bs + row] = acc[i][e];
-    }
+      for (int g = 0; g < 4; ++g) {
+        const size_t row = m0 + wm * 64 + i * 32 + 8 * g + 4 * h;
+        if (row >= nrw)
+          continue;
+        float *d = s + tok * bs + row;
+        if (vec_out) {
+          *reinterpret_cast<float4 *>(d) =
+              make_float4(acc[i][4 * g], acc[i][4 * g + 1], acc[i][4 * g + 2], acc[i][4 * g + 3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            d[e] = acc[i][4 * g + e];
+        }
+      }
+  }
 }
 
 // Plain Q8_0 rows (stride by), groups of 4, -> block_q8_0x4: thread per output
@@ -949,7 +963,8 @@ extern "C" int tcrv_hip_repack_gemm_q4_0_q8_0(size_t n, float *s, const uint8_t 
   if (tiles > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
   tcrv::gemm_repack_q4_0<<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kOcThreads), 0,
-                           as_stream(stream)>>>(nb, s, vx, vy, ngw, nga, bs);
+                           as_stream(stream)>>>(nb, s, vx, vy, ngw, nga, bs,
+                                                aligned16(s) && bs % 4 == 0);
   return launch_status();
 }
 
