@@ -89,6 +89,13 @@ def main():
                          s4=ora.repack_gemv_q4_0(n, p4, act, 32),
                          s8=ora.repack_gemv_q8_0(n, p8, act, 32))
 
+    # a8: repack GEMM of those x16 Q4_0 weights against 8 activation rows in the
+    # 4-row interleave (block_q8_0x4)
+    a8r = synth.q8_0_matrix(8, n, 25, 1.0)
+    ax4 = ora.pack_q8_0x4(a8r, 8, nb, a8r.shape[1])
+    out["repack_gemm"] = dict(n=np.int64(n), p4=p4, act=a8r, ax4=ax4,
+                              s=ora.repack_gemm_q4_0(n, p4, ax4, 8, 32, 32))
+
     for name, arrays in out.items():
         path = os.path.join(HERE, f"{name}.npz")
         np.savez(path, **arrays)

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-NAMES = ["add", "quant", "dot_q8", "dot_q4", "gemm_q8", "gemm_q4", "repack"]
+NAMES = ["add", "quant", "dot_q8", "dot_q4", "gemm_q8", "gemm_q4", "repack", "repack_gemm"]
 
 
 def load(name):
@@ -52,6 +52,12 @@ def test_oracle_reproduces_fixtures(oracle):
     assert np.array_equal(oracle.pack_q8_0x16(g["src8"], nblk), g["p8"])
     assert np.array_equal(bits(oracle.repack_gemv_q4_0(n, g["p4"], g["act"], 32)), bits(g["s4"]))
     assert np.array_equal(bits(oracle.repack_gemv_q8_0(n, g["p8"], g["act"], 32)), bits(g["s8"]))
+    g = load("repack_gemm")
+    n = int(g["n"])
+    a = g["act"]
+    assert np.array_equal(oracle.pack_q8_0x4(a, 8, n // 32, a.shape[1]), g["ax4"])
+    assert np.array_equal(bits(oracle.repack_gemm_q4_0(n, g["p4"], g["ax4"], 8, 32, 32)),
+                          bits(g["s"]))
 
 
 def test_fixture_block_sums_brute_force():
@@ -127,3 +133,13 @@ def test_kernels_reproduce_fixtures(hip, dev):
     assert np.array_equal(bits(from_dev(s)), bits(g["s4"]))
     hip.repack_gemv_q8_0_q8_0(n, s, p8, to_dev(g["act"], dev), 32)
     assert np.array_equal(bits(from_dev(s)), bits(g["s8"]))
+
+    g = load("repack_gemm")
+    n = int(g["n"])
+    a = g["act"]
+    ax4 = empty_dev(g["ax4"].size, torch.uint8, dev)
+    hip.pack_q8_0_to_q8_0x4(8, n // 32, to_dev(a, dev), a.shape[1], ax4)
+    assert np.array_equal(from_dev(ax4), g["ax4"])
+    s = empty_dev(8 * 32, torch.float32, dev)
+    hip.repack_gemm_q4_0_q8_0(n, s, to_dev(g["p4"], dev), ax4, 8, 32, 32)
+    assert np.array_equal(bits(from_dev(s)), bits(g["s"]))
