@@ -233,7 +233,7 @@ TCRV_HIP_API int tcrv_hip_repack_gemv_q8_0_q8_0(size_t n, float *s, const uint8_
  * 8 + 4e + c; nr/4 groups, group y at vy + y*(n/32)*136):
  * s[(4y + c)*bs + 16x + r] = fold_b fma((float)sumi, d_w[r]*d_a[c], .) in
  * ascending b.  Partial groups (nr % 4, nc % 16) are not written, as in the
- * reference.  vx, vy and s 4-byte aligned; bs >= 16*(nc/16) when nr >= 8. */
+ * reference.  vx, vy and s 4-byte aligned; bs >= 16*(nc/16). */
 TCRV_HIP_API int tcrv_hip_repack_gemm_q4_0_q8_0(size_t n, float *s, const uint8_t *vx,
                                    const uint8_t *vy, size_t nr, size_t nc, size_t bs,
                                    void *stream);

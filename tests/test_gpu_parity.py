@@ -478,6 +478,15 @@ def test_repack_gemm_q4_0(hip, oracle, dev, nr, nc, nb, bpad):
     assert np.all(got[rows:] == -7.0) and np.all(got[:, cols:] == -7.0)  # unwritten
 
 
+def test_repack_gemm_rejects_overlapping_rows(hip, dev):
+    """Each group writes 4 activation rows at stride bs: a stride shorter than
+    the written row is refused before anything runs (fake addresses would fault
+    if a launch happened)."""
+    st = hip.call("tcrv_hip_repack_gemm_q4_0_q8_0", 64, 0x1000, 0x2000, 0x3000, 4, 32, 31,
+                  hip._stream(None), check=False)
+    assert st == hip.ERR_BAD_SIZE
+
+
 def test_repack_gemm_full_size_sampled_tokens(hip, oracle, dev):
     """4096 weight rows x 4096 tokens x K 4096 on the GPU; the oracle checks three
     4-token groups (first, middle, last) against all 4096 weight rows."""

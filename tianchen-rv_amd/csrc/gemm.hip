@@ -950,7 +950,7 @@ extern "C" int tcrv_hip_repack_gemm_q4_0_q8_0(size_t n, float *s, const uint8_t 
   const size_t nga = nr / 4, ngw = nc / 16;  // like the reference, partial groups are not written
   if (nga == 0 || ngw == 0)
     return TCRV_HIP_OK;
-  if (nga > 1 && bs < ngw * 16)
+  if (bs < ngw * 16)  // every group writes 4 activation rows at stride bs
     return TCRV_HIP_ERR_BAD_SIZE;
   if (nb == 0)
     return zero_outputs(s, nga * 4 * ngw * 16, bs, ngw * 16, stream);
