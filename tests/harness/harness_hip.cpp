@@ -7,7 +7,8 @@
 //   1. the reference's own add proof (i32, n = 1031, lhs = 3i - 17,
 //      rhs = 41 - 2i) through tcrv_hip_add_i32;
 //   2. the route provider's selection for every combination of typed facts;
-//   3. routed decode GEMVs and prefill GEMMs (Q4_0 and Q8_0 weights) on
+//   3. routed decode GEMVs and prefill GEMMs (Q4_0 and Q8_0 weights, and the
+//      repack GEMM over x16 Q4_0 weights) on
 //      quantized synthetic rows, each output compared bit for bit with the
 //      oracle.
 // Prints one line per step and "harness ok" last; exits non-zero on any
@@ -167,6 +168,52 @@ int routed_contraction(const char *name, int quant, size_t nr, size_t nc, size_t
   return 0;
 }
 
+// Prefill over x16 Q4_0 weights: the route runs the repack GEMM in its own
+// contract (activations in block_q8_0x4, output activation-row major); both
+// layouts are built here with the oracle's packs.
+int routed_repack_gemm(size_t nr, size_t nc, size_t n) {
+  const char *name = "routed q4_0 x16 prefill";
+  const size_t nb = n / 32;
+  const std::vector<uint8_t> w = quantized_rows(nr, n, 1006 + nr, 0.02f, false);
+  const std::vector<uint8_t> a = quantized_rows(nc, n, 1007 + nc, 1.0f, true);
+  // group x, block b of the x16 source: block b of rows 16x .. 16x+15
+  std::vector<uint8_t> src(w.size()), wx16(nr / 16 * nb * 288), ax4(nc / 4 * nb * 136);
+  for (size_t x = 0; x < nr / 16; ++x)
+    for (size_t b = 0; b < nb; ++b)
+      for (size_t r = 0; r < 16; ++r)
+        std::memcpy(&src[((x * nb + b) * 16 + r) * 18], &w[(16 * x + r) * nb * 18 + b * 18], 18);
+  tcrv_oracle_pack_q4_0_to_q4_0x16(nr / 16 * nb, src.data(), wx16.data());
+  tcrv_oracle_pack_q8_0_to_q8_0x4(nc, nb, a.data(), nb * 34, ax4.data());
+  std::vector<float> got(nc * nr), want(nc * nr);
+  tcrv_oracle_repack_gemm_q4_0_q8_0(n, want.data(), wx16.data(), ax4.data(), nc, nr, nr);
+  DeviceBuffer<uint8_t> dw(wx16.size()), da(ax4.size());
+  DeviceBuffer<float> ds(got.size());
+  if (!dw.p || !da.p || !ds.p) {
+    std::printf("FAIL hipMalloc (is a GPU visible?)\n");
+    return 1;
+  }
+  HIP_OK(hipMemcpy(dw.p, wx16.data(), wx16.size(), hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(da.p, ax4.data(), ax4.size(), hipMemcpyHostToDevice));
+  int algo = -1;
+  const int st = tcrv_hip_route_contraction(TCRV_HIP_QUANT_Q4_0, TCRV_HIP_LAYOUT_X16, n, ds.p,
+                                            dw.p, da.p, 0, nr, nc, 0, nr, nullptr, &algo);
+  if (st != TCRV_HIP_OK)
+    return fail(name, st);
+  if (algo != TCRV_HIP_ALGO_REPACK_GEMM) {
+    std::printf("FAIL %s: routed to algorithm %d\n", name, algo);
+    return 1;
+  }
+  HIP_OK(hipMemcpy(got.data(), ds.p, got.size() * 4, hipMemcpyDeviceToHost));
+  for (size_t i = 0; i < got.size(); ++i)
+    if (std::memcmp(&got[i], &want[i], 4) != 0) {
+      std::printf("FAIL %s mismatch at %zu: got %.9g expected %.9g\n", name, i, got[i], want[i]);
+      return 1;
+    }
+  std::printf("%s ok: %zu x %zu x %zu bit-identical to the oracle (algorithm %d)\n", name, nr, nc,
+              n, algo);
+  return 0;
+}
+
 }  // namespace
 
 int main() {
@@ -179,7 +226,8 @@ int main() {
       routed_contraction("routed q8_0 prefill", TCRV_HIP_QUANT_Q8_0, 160, 72, 512,
                          TCRV_HIP_ALGO_MFMA_GEMM) ||
       routed_contraction("routed q4_0 prefill", TCRV_HIP_QUANT_Q4_0, 130, 40, 256,
-                         TCRV_HIP_ALGO_MFMA_GEMM))
+                         TCRV_HIP_ALGO_MFMA_GEMM) ||
+      routed_repack_gemm(272, 44, 352))
     return 1;
   std::printf("harness ok\n");
   return 0;

@@ -24,5 +24,5 @@ def test_harness_runs_on_the_gpu():
     lines = r.stdout.splitlines()
     assert "add proof ok: 1031 elements checked" in lines
     assert sum(1 for ln in lines if ln.startswith("route ")) == 12
-    assert sum(1 for ln in lines if "bit-identical to the oracle" in ln) == 4
+    assert sum(1 for ln in lines if "bit-identical to the oracle" in ln) == 5
     assert lines[-1] == "harness ok"
