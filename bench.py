@@ -704,8 +704,8 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (each config "
-              "shards by rows with no exchange but an all-gather of the output; see the "
-              "sharding design in DESIGN.md).  Run with --gpus 1.", file=sys.stderr)
+              "would shard by output rows, with no exchange but an all-gather of the "
+              "output).  Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
