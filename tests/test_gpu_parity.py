@@ -478,6 +478,28 @@ def test_repack_gemm_q4_0(hip, oracle, dev, nr, nc, nb, bpad):
     assert np.all(got[rows:] == -7.0) and np.all(got[:, cols:] == -7.0)  # unwritten
 
 
+def test_pack_q8_0x4_two_byte_aligned_source(hip, oracle, dev):
+    nr, nb = 8, 3
+    a = synth.q8_0_matrix(nr, nb * 32, 73, 1.0)
+    buf = empty_dev(a.size + 16, torch.uint8, dev)
+    buf[2:2 + a.size] = to_dev(a.reshape(-1), dev)
+    dst = empty_dev(nr // 4 * nb * 136, torch.uint8, dev)
+    hip.pack_q8_0_to_q8_0x4(nr, nb, buf[2:2 + a.size], a.shape[1], dst)
+    assert np.array_equal(from_dev(dst), oracle.pack_q8_0x4(a, nr, nb, a.shape[1]))
+
+
+def test_repack_gemm_argument_checks(hip, dev):
+    """Misaligned operands and null pointers are refused before any launch
+    (fake addresses would fault if one happened); empty groups write nothing."""
+    call = lambda *a: hip.call("tcrv_hip_repack_gemm_q4_0_q8_0", *a, hip._stream(None),
+                               check=False)
+    assert call(64, 0x1000, 0x2002, 0x3000, 4, 16, 16) == hip.ERR_MISALIGNED
+    assert call(64, 0x1000, 0x2000, 0x3002, 4, 16, 16) == hip.ERR_MISALIGNED
+    assert call(64, 0, 0x2000, 0x3000, 4, 16, 16) == hip.ERR_NULL_POINTER
+    assert call(64, 0x1000, 0x2000, 0x3000, 3, 16, 16) == hip.OK   # no full activation group
+    assert call(64, 0x1000, 0x2000, 0x3000, 4, 15, 16) == hip.OK   # no full weight group
+
+
 def test_repack_gemm_rejects_overlapping_rows(hip, dev):
     """Each group writes 4 activation rows at stride bs: a stride shorter than
     the written row is refused before anything runs (fake addresses would fault
