@@ -6,6 +6,9 @@
   rocprof_summary.py counters <pmc-root> <COUNTER> [name-substring ...]
       median KiB per dispatch of each matching kernel in
       <pmc-root>/pmc_<COUNTER>_configs/run_counter_collection.csv
+  rocprof_summary.py multi <run_counter_collection.csv> [name-substring ...]
+      median per dispatch of every counter of one multi-counter pass, per
+      matching kernel
   rocprof_summary.py traffic <pmc-root>
       HBM bytes per dispatch of the GEMV and GEMM kernels from the two
       counter passes (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled by
@@ -86,6 +89,22 @@ def counter_per_dispatch(path, kernel):
     return statistics.median(v), len(v)
 
 
+def multi(path, needles):
+    per = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            if needles and not any(n in name for n in needles):
+                continue
+            key = (name.split("(")[0], r["Counter_Name"])
+            d = per.setdefault(key, {})
+            d[r["Dispatch_Id"]] = d.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+    print("| kernel | counter | dispatches | median per dispatch |")
+    print("|---|---|---|---|")
+    for (kernel, ctr), d in sorted(per.items()):
+        print(f"| {kernel} | {ctr} | {len(d)} | {statistics.median(d.values()):.4e} |")
+
+
 def traffic(root):
     out = {"method": "median KiB per dispatch x 1024, scaled by calib bytes / calib counter"}
     scale = {}
@@ -114,6 +133,8 @@ def main():
         stats(sys.argv[2], sys.argv[3:])
     elif len(sys.argv) == 3 and sys.argv[1] == "traffic":
         traffic(sys.argv[2])
+    elif len(sys.argv) >= 3 and sys.argv[1] == "multi":
+        multi(sys.argv[2], sys.argv[3:])
     elif len(sys.argv) >= 4 and sys.argv[1] == "counters":
         counters(sys.argv[2], sys.argv[3], sys.argv[4:])
     else:
