@@ -2,18 +2,23 @@
 """Benchmark of the quantized hot path on one MI355X.
 
 BASELINE.json metric: "Q4_0 GEMV GB/s (% HBM peak); Q8_0 GEMM int8 TOPS (% MFMA
-peak)".  `value` is the first half: one step = one Q4_0 x Q8_0 decode GEMV,
-W 4096 x 4096, through the C-ABI entry tcrv_hip_gemv_q4_0_q8_0.
-The second half, the Q8_0 x Q8_0 GEMM 4096^3, is timed in the
-same run and reported under "gemm"; configs[0..2] (add, dequant, block dot)
-are reported under "configs".
+peak)".  `value` is the first half: the Q4_0 x Q8_0 decode GEMV, W 4096 x 4096
+(configs[3]), through the C-ABI entry tcrv_hip_gemv_q4_0_q8_0.  One step is one
+decode pass over a stack of LAYERS distinct 4096 x 4096 Q4_0 weight matrices
+(the configs[3] matrix, copied): LAYERS GEMV launches, each reading its own
+matrix, 605 MB per step -- more than the 256 MB Infinity Cache, so every launch
+reads its weights from HBM whatever --steps is.  The second half, the Q8_0 x
+Q8_0 GEMM 4096^3, is timed in the same run and reported under
+"gemm"; configs[0..2] (add, dequant, block dot) and the other kernels are
+reported under "configs".
 
 Timing: inputs are synthetic (tianchen-rv_amd/synth.py seeds) and resident in
-HBM before a timed region starts.  A region is K launches captured in one HIP
-graph and replayed once, bracketed by torch.cuda.synchronize() and HIP events
-recorded on the launch stream; per-launch time = region / K.  Every
-bandwidth-bound config rotates through enough distinct input sets (> 256 MB,
-the Infinity Cache size) that each launch reads its inputs from HBM.
+HBM before a timed region starts.  A region is a HIP graph of launches,
+replayed once untimed and then once between HIP events recorded on the launch
+stream, bracketed by torch.cuda.synchronize(); per-launch time = region /
+launches.  Every bandwidth-bound config rotates through enough distinct input
+sets (> 256 MB, the Infinity Cache size) that each launch reads its inputs
+from HBM, and times at least as many launches as it has sets.
 
 cpu_baseline: the scalar C oracle (oracle/, the CPU restatement of the
 reference emitters) timed on the host cores over a bounded sample of the same
@@ -34,6 +39,7 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published
 N = 4096
 MALL_BYTES = 256 << 20       # Infinity Cache
+LAYERS = 64                  # GEMV launches (distinct weight matrices) per step: 605 MB
 HOST_COPIES = 48             # CPU-baseline GEMV weight copies (453 MB > host last-level cache)
 
 METRIC = "Q4_0 GEMV GB/s (% HBM peak); Q8_0 GEMM int8 TOPS (% MFMA peak)"
@@ -83,15 +89,14 @@ def log(msg: str) -> None:
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000, help="timed GEMV launches")
-    ap.add_argument("--warmup", type=int, default=200, help="untimed GEMV launches")
+    ap.add_argument("--steps", type=int, default=32,
+                    help=f"timed GEMV steps (each {LAYERS} launches over distinct weights)")
+    ap.add_argument("--warmup", type=int, default=4, help="untimed GEMV steps")
     ap.add_argument("--gemm-steps", type=int, default=20, help="GEMM launches per timed region")
     ap.add_argument("--gemm-regions", type=int, default=5,
                     help="timed GEMM regions; the median region is reported")
     ap.add_argument("--config-steps", type=int, default=50,
                     help="timed launches for each of add / dequant / block dot")
-    ap.add_argument("--copies", type=int, default=40,
-                    help="distinct GEMV weight copies rotated over (> 256 MB in total)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall time of the CPU-baseline sample (0 disables it)")
     ap.add_argument("--only", choices=["all", "gemv", "gemv_rows", "gemm", "configs", "calib"],
@@ -114,6 +119,12 @@ class Region:
                 for i in range(steps):
                     launch(i)
         torch.cuda.synchronize()
+
+    def timed(self) -> float:
+        """One untimed replay (first-replay costs stay out of the figure), then
+        the timed one."""
+        self.run()
+        return self.run()
 
     def run(self) -> float:
         torch = self.torch
@@ -156,11 +167,15 @@ def copies_for(nbytes: int, minimum: int = 2) -> int:
 
 
 def bench_gemv(torch, lib, stream, args):
+    """K steps of LAYERS GEMVs each, every launch over its own weight matrix;
+    the graphs hold at most 32 steps (2048 launches) and are replayed back to
+    back between one pair of events."""
     log("GEMV inputs: W 4096x4096 Q4_0 (seed 1006, N(0,0.02)), x Q8_0 (seed 1007, N(0,1))")
     w = inputs("gemv_w")
     x = inputs("gemv_x")
     dev = torch.device("cuda:0")
-    copies = max(args.copies, copies_for(w.size, 2))
+    copies = LAYERS
+    assert copies * w.size > MALL_BYTES
     wd = torch.empty((copies, w.size), dtype=torch.uint8, device=dev)
     wd[:] = torch.from_numpy(w.reshape(-1)).to(dev)
     xd = torch.from_numpy(x).to(dev)
@@ -175,19 +190,38 @@ def bench_gemv(torch, lib, stream, args):
         k = i % copies
         fn(N, yp[k], wp[k], bx, xd.data_ptr(), N, sp)
 
-    warm = Region(torch, stream, launch, max(args.warmup, 1))
-    warm.run()
-    del warm
+    if args.warmup > 0:
+        Region(torch, stream, launch, args.warmup * LAYERS).run()
+    steps = max(args.steps, 1)
+    per_graph = min(steps, 32)
+    full, rest = divmod(steps, per_graph)
+    graphs = [(Region(torch, stream, launch, per_graph * LAYERS), full)]
+    if rest:
+        graphs.append((Region(torch, stream, launch, rest * LAYERS), 1))
+    for g, _ in graphs:  # one untimed replay of each graph
+        g.run()
     yd.zero_()
-    timed = Region(torch, stream, launch, args.steps)
-    ms = timed.run()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for g, reps in graphs:
+            for _ in range(reps):
+                g.graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
     same_as_eager(torch, stream, yd[0], lambda out: fn(N, out, wp[0], bx, xd.data_ptr(), N, sp),
                   "GEMV")
-    us = ms * 1e3 / args.steps
+    launches = steps * LAYERS
+    us = ms * 1e3 / launches
     gbs = GEMV_BYTES / (us * 1e-6) / 1e9
-    log(f"GEMV {us:.2f} us/launch over {args.steps} launches, {copies} weight copies: "
-        f"{gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
-    return {"us": us, "gbs": gbs, "copies": copies, "ms_region": ms}
+    log(f"GEMV {us:.3f} us/launch over {launches} launches ({steps} steps of {LAYERS} "
+        f"weight matrices): {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+    return {"us": us, "gbs": gbs, "copies": copies, "ms_region": ms, "launches": launches,
+            "steps": steps, "ms_per_step": ms / steps,
+            "bytes_touched_per_step": copies * (w.size + N * 4) + x.size}
 
 
 def bench_gemv_rows(torch, lib, stream, args):
@@ -216,7 +250,7 @@ def bench_gemv_rows(torch, lib, stream, args):
             fn(N, yp[k], wp[k], bx, xd.data_ptr(), nr, sp)
 
         Region(torch, stream, launch, max(steps // 4, 4)).run()
-        ms = Region(torch, stream, launch, steps).run()
+        ms = Region(torch, stream, launch, max(steps, copies)).timed()
         same_as_eager(torch, stream, yd[(steps - 1) % copies],
                       lambda o, nr=nr, k=(steps - 1) % copies, wp=wp:
                       fn(N, o, wp[k], bx, xd.data_ptr(), nr, sp), f"GEMV {nr} rows")
@@ -253,6 +287,7 @@ def bench_gemm(torch, lib, stream, args):
     Region(torch, stream, launch, 50).run()
     cd.zero_()
     timed = Region(torch, stream, launch, args.gemm_steps)
+    timed.run()  # untimed first replay
     per = sorted(timed.run() * 1e3 / args.gemm_steps for _ in range(args.gemm_regions))
     same_as_eager(torch, stream, cd,
                   lambda out: fn(N, out, bd.data_ptr(), ad.data_ptr(), rb, N, N, rb, N, sp), "GEMM")
@@ -394,7 +429,7 @@ def bench_configs(torch, lib, stream, args):
     soa = torch.empty(N * nb * 18, dtype=torch.uint8, device=dev)
     checked(lib.tcrv_hip_pack_q4_0_to_soa, "pack_soa")(N, nb, wd.data_ptr(), nb * 18,
                                                       soa.data_ptr(), sp)
-    sets = max(args.copies, copies_for(soa.numel(), 2))
+    sets = max(LAYERS, copies_for(soa.numel(), 2))
     S = torch.empty((sets, soa.numel()), dtype=torch.uint8, device=dev)
     S[:] = soa
     Yv = torch.empty((sets, N), device=dev)
@@ -440,6 +475,7 @@ def bench_configs(torch, lib, stream, args):
 
     Region(torch, stream, q4_gemm, 50).run()  # loaded clocks, as for the Q8_0 GEMM
     reg = Region(torch, stream, q4_gemm, 10)
+    reg.run()
     per = sorted(reg.run() * 1e3 / 10 for _ in range(3))
     us = per[1]
     out["q4_0_q8_0_gemm"] = {"workload": "a7 Q4_0 x Q8_0 GEMM 4096 rows x 4096 tokens x 4096",
@@ -462,6 +498,7 @@ def bench_configs(torch, lib, stream, args):
 
     Region(torch, stream, rp_gemm, 50).run()
     reg = Region(torch, stream, rp_gemm, 10)
+    reg.run()
     per = sorted(reg.run() * 1e3 / 10 for _ in range(3))
     us = per[1]
     out["repack_gemm_q4_0_q8_0"] = {"workload": "a8 repack GEMM: x16 Q4_0 weights 4096 x x4 "
@@ -478,11 +515,45 @@ def bench_configs(torch, lib, stream, args):
     return out
 
 
+ORACLE_BUILD = ("gcc -O3 -march=x86-64-v3 -ffp-contract=off -fopenmp, every fold an explicit "
+                "fmaf in the reference order (the bits -ffp-contract=on gives for the "
+                "reference's one-expression folds)")
+
+
+def host_cpu():
+    """The host's CPU facts and the thread count the baselines use:
+    OMP_NUM_THREADS when set (the GPU box sets it to the host-CPU share of one
+    GPU, 16), else every CPU this process may run on."""
+    aff = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = int(omp) if omp and omp.isdigit() and int(omp) > 0 else aff
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"threads": threads, "nproc": os.cpu_count(), "affinity_cpus": aff,
+            "omp_num_threads": omp, "cpu_model": model, "build": ORACLE_BUILD}
+
+
 def cpu_threads() -> int:
-    env = os.environ.get("OMP_NUM_THREADS")
-    if env and env.isdigit():
-        return max(1, int(env))
-    return max(1, min(os.cpu_count() or 1, 16))
+    return host_cpu()["threads"]
+
+
+def split_run(pool, calls):
+    """Runs the calls (oracle slices: ctypes releases the GIL) on the pool and
+    waits for all of them."""
+    for f in [pool.submit(c) for c in calls]:
+        f.result()
+
+
+def slices(total: int, parts: int):
+    step = -(-total // parts)
+    return [(i, min(i + step, total)) for i in range(0, total, step)]
 
 
 def cpu_baseline(seconds: float):
@@ -514,23 +585,16 @@ def cpu_baseline(seconds: float):
 
     one, reps1 = rate(1, seconds / 4)
     many, reps = rate(threads, seconds)
-    cpu = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    log(f"CPU oracle GEMV: {many:.1f} GB/s on {threads} threads, {one:.2f} GB/s on 1 ({cpu})")
+    cpu = host_cpu()
+    log(f"CPU oracle GEMV: {many:.1f} GB/s on {threads} threads, {one:.2f} GB/s on 1 "
+        f"({cpu['cpu_model']}, nproc {cpu['nproc']}, affinity {cpu['affinity_cpus']})")
     return {
         "value": round(many, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-        "sample": (f"oracle/ scalar C (gcc -O3 -march=x86-64-v3, OpenMP over rows, serial "
-                   f"fmaf fold per row): {reps} whole 4096x4096 Q4_0xQ8_0 GEMVs over "
-                   f"{HOST_COPIES} rotating weight copies in {seconds:.0f} s on {threads} "
-                   f"threads of {cpu}; 1 thread: {one:.3f} GB/s ({reps1} GEMVs)"),
-        "value_1thread": round(one, 4),
+        "sample": (f"oracle/ scalar C, OpenMP over rows with a serial fmaf fold per row: {reps} "
+                   f"whole 4096x4096 Q4_0xQ8_0 GEMVs over {HOST_COPIES} rotating weight copies "
+                   f"in {seconds:.0f} s on {threads} threads of {cpu['cpu_model']}; "
+                   f"1 thread: {one:.3f} GB/s ({reps1} GEMVs)"),
+        "value_1thread": round(one, 4), "host": cpu,
     }
 
 
@@ -557,20 +621,27 @@ def cpu_baseline_gemm(seconds: float):
     tops = 2.0 * rows * N * N * reps / dt / 1e12
     log(f"CPU oracle GEMM: {tops * 1e3:.1f} GOPS on {threads} threads")
     return {"value": round(tops, 5), "unit": "TOPS", "cores": threads, "kind": "port",
+            "host": host_cpu(),
             "sample": (f"oracle/ scalar C, OpenMP over rows: {reps} slices of {rows} weight rows "
                        f"x 4096 tokens x 4096 (1/256 of the GEMM each) in {dt:.1f} s")}
 
 
 def cpu_baseline_configs(seconds: float):
-    """The oracle on the host beside each of configs[0..2], the x16 GEMV and
-    the Q4_0 GEMM, each timed for `seconds` on a bounded sample of its workload
-    (the element-wise oracles are single-threaded C loops; the row-parallel
-    ones use OpenMP over rows with every row's fold serial)."""
+    """The oracle on the host beside each of configs[0..2] and the other
+    kernels, each timed for `seconds` on a bounded sample of its workload, on
+    one thread and on all the baseline's threads (row-parallel oracles use
+    OpenMP over rows with every row's fold serial; element-wise ones run one
+    contiguous slice per thread)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_binding
 
     ora = oracle_binding.load()
     threads = cpu_threads()
+    pool = ThreadPoolExecutor(max_workers=threads)
 
     def timed(call):
         reps, t0 = 0, time.perf_counter()
@@ -581,83 +652,118 @@ def cpu_baseline_configs(seconds: float):
             if dt >= seconds:
                 return reps, dt
 
-    def entry(value, unit, cores, sample):
-        return {"value": round(value, 4), "unit": unit, "cores": cores, "kind": "port",
-                "sample": sample}
+    def entry(work, unit, sample, one, many):
+        """one/many: callables doing one whole sample on 1 / all threads."""
+        r1, d1 = timed(one)
+        rn, dn = timed(many)
+        return {"value": round(work * rn / dn / (1e9 if unit == "GB/s" else 1e12), 4),
+                "unit": unit, "cores": threads, "kind": "port",
+                "value_1thread": round(work * r1 / d1 / (1e9 if unit == "GB/s" else 1e12), 4),
+                "sample": f"{sample}; {rn} on {threads} threads in {dn:.1f} s, {r1} on 1 "
+                          f"thread in {d1:.1f} s"}
 
     out = {}
-    n = 1 << 24  # the whole config: 201 MB per call
     a = inputs("add_a")
     b = inputs("add_b")
-    reps, dt = timed(lambda: ora.add_f32(a, b))
-    out["add_f32"] = entry(ADD_BYTES * reps / dt / 1e9, "GB/s", 1,
-                           f"{reps} whole adds of n = 2^24 in {dt:.1f} s")
+    n = a.size
+    out["add_f32"] = entry(
+        ADD_BYTES, "GB/s", "whole adds of n = 2^24", lambda: ora.add_f32(a, b),
+        lambda: split_run(pool, [lambda i=i, j=j: ora.add_f32(a[i:j], b[i:j])
+                                 for i, j in slices(n, threads)]))
     q = inputs("dequant_q")
-    reps, dt = timed(lambda: ora.dequantize_row_q8_0(q, N * N))
-    out["dequant_q8_0"] = entry(DEQ_BYTES * reps / dt / 1e9, "GB/s", 1,
-                                f"{reps} whole 4096x4096 dequants in {dt:.1f} s")
+    nbq = N * N // 32
+    out["dequant_q8_0"] = entry(
+        DEQ_BYTES, "GB/s", "whole 4096x4096 dequants", lambda: ora.dequantize_row_q8_0(q, N * N),
+        lambda: split_run(pool, [lambda i=i, j=j: ora.dequantize_row_q8_0(q[34 * i:34 * j],
+                                                                         32 * (j - i))
+                                 for i, j in slices(nbq, threads)]))
     xq = inputs("dot_x")
     yq = inputs("dot_y")
     rb = xq.shape[1]
-    reps, dt = timed(lambda: ora.vec_dot_q8_0_rows(N, xq, rb, yq, rb, DOT_ROWS, threads))
-    out["vec_dot_q8_0_q8_0"] = entry(DOT_BYTES * reps / dt / 1e9, "GB/s", threads,
-                                     f"{reps} whole 16384 x 4096 block dots (143 MB each) in "
-                                     f"{dt:.1f} s, OpenMP over rows")
+    out["vec_dot_q8_0_q8_0"] = entry(
+        DOT_BYTES, "GB/s", "whole 16384 x 4096 block dots (143 MB each), OpenMP over rows",
+        lambda: ora.vec_dot_q8_0_rows(N, xq, rb, yq, rb, DOT_ROWS, 1),
+        lambda: ora.vec_dot_q8_0_rows(N, xq, rb, yq, rb, DOT_ROWS, threads))
     w = inputs("gemv_w")
     x = inputs("gemv_x")
     nb = N // 32
-    packed = ora.pack_q4_0x16(
-        w.reshape(N // 16, 16, nb, 18).transpose(0, 2, 1, 3).copy().reshape(-1), N // 16 * nb)
-    import numpy as np
+    src = w.reshape(N // 16, 16, nb, 18).transpose(0, 2, 1, 3).copy().reshape(-1)
+    packed = ora.pack_q4_0x16(src, N // 16 * nb)
     ps = np.ascontiguousarray(np.broadcast_to(packed, (HOST_COPIES,) + packed.shape))
     k = [0]
+    gb = nb * 288  # bytes per 16-row group
 
-    def repack():
+    def repack_one():
         ora.repack_gemv_q4_0(N, ps[k[0] % HOST_COPIES], x, N)
         k[0] += 1
-    reps, dt = timed(repack)
-    out["repack_gemv_q4_0_q8_0"] = entry(GEMV_BYTES * reps / dt / 1e9, "GB/s", 1,
-                                         f"{reps} whole 4096x4096 x16 GEMVs over {HOST_COPIES} "
-                                         f"rotating weight copies in {dt:.1f} s")
+
+    def repack_many():
+        p = ps[k[0] % HOST_COPIES]
+        split_run(pool, [lambda i=i, j=j: ora.repack_gemv_q4_0(N, p[gb * i:gb * j], x, 16 * (j - i))
+                         for i, j in slices(N // 16, threads)])
+        k[0] += 1
+    out["repack_gemv_q4_0_q8_0"] = entry(
+        GEMV_BYTES, "GB/s", f"whole 4096x4096 x16 GEMVs over {HOST_COPIES} rotating weight "
+        "copies (threads split the 16-row groups)", repack_one, repack_many)
+    del ps
     w8 = inputs("gemm_b")
     packed8 = ora.pack_q8_0x16(
         w8.reshape(N // 16, 16, nb, 34).transpose(0, 2, 1, 3).copy().reshape(-1), N // 16 * nb)
     copies8 = HOST_COPIES // 2
     ps8 = np.ascontiguousarray(np.broadcast_to(packed8, (copies8,) + packed8.shape))
     k8 = [0]
+    gb8 = nb * 544
 
-    def repack8():
+    def repack8_one():
         ora.repack_gemv_q8_0(N, ps8[k8[0] % copies8], x, N)
         k8[0] += 1
-    reps, dt = timed(repack8)
-    out["repack_gemv_q8_0_q8_0"] = entry(REPACK8_BYTES * reps / dt / 1e9, "GB/s", 1,
-                                         f"{reps} whole 4096x4096 Q8_0 x16 GEMVs over {copies8} "
-                                         f"rotating weight copies in {dt:.1f} s")
+
+    def repack8_many():
+        p = ps8[k8[0] % copies8]
+        split_run(pool, [lambda i=i, j=j: ora.repack_gemv_q8_0(N, p[gb8 * i:gb8 * j], x,
+                                                               16 * (j - i))
+                         for i, j in slices(N // 16, threads)])
+        k8[0] += 1
+    out["repack_gemv_q8_0_q8_0"] = entry(
+        REPACK8_BYTES, "GB/s", f"whole 4096x4096 Q8_0 x16 GEMVs over {copies8} rotating weight "
+        "copies", repack8_one, repack8_many)
     del ps8
-    src = w.reshape(N // 16, 16, nb, 18).transpose(0, 2, 1, 3).copy().reshape(-1)
-    reps, dt = timed(lambda: ora.pack_q4_0x16(src, N // 16 * nb))
-    out["pack_q4_0_to_q4_0x16"] = entry(PACK_BYTES * reps / dt / 1e9, "GB/s", 1,
-                                        f"{reps} packs of the 4096x4096 Q4_0 weights in {dt:.1f} s")
+    nx16 = N // 16 * nb
+    out["pack_q4_0_to_q4_0x16"] = entry(
+        PACK_BYTES, "GB/s", "packs of the 4096x4096 Q4_0 weights",
+        lambda: ora.pack_q4_0x16(src, nx16),
+        lambda: split_run(pool, [lambda i=i, j=j: ora.pack_q4_0x16(src[288 * i:288 * j], j - i)
+                                 for i, j in slices(nx16, threads)]))
     xf = inputs("gemm_a_f32")
-    reps, dt = timed(lambda: ora.quantize_q8_0(xf))
-    out["quantize_row_q8_0"] = entry(QUANT_BYTES * reps / dt / 1e9, "GB/s", 1,
-                                     f"{reps} quantizations of 4096 x 4096 f32 in {dt:.1f} s")
+    out["quantize_row_q8_0"] = entry(
+        QUANT_BYTES, "GB/s", "quantizations of 4096 x 4096 f32", lambda: ora.quantize_q8_0(xf),
+        lambda: split_run(pool, [lambda i=i, j=j: ora.quantize_q8_0(xf[32 * i:32 * j])
+                                 for i, j in slices(N * N // 32, threads)]))
     a8 = inputs("gemm_a")
     w16 = w[:16].copy()
-    reps, dt = timed(lambda: ora.gemm_q4_0(N, w16, a8, a8.shape[1], 16, N, w16.shape[1], N,
-                                           threads))
-    out["q4_0_q8_0_gemm"] = entry(2.0 * 16 * N * N * reps / dt / 1e12, "TOPS", threads,
-                                  f"{reps} slices of 16 weight rows x 4096 tokens x 4096 "
-                                  f"(1/256 of the GEMM each) in {dt:.1f} s, OpenMP over rows")
-    ax4 = ora.pack_q8_0x4(a8[:16].copy(), 16, N // 32, a8.shape[1])
-    wx16 = ora.pack_q4_0x16(w.reshape(N // 16, 16, N // 32, 18).transpose(0, 2, 1, 3).copy()
-                            .reshape(-1), N // 16 * (N // 32))
-    reps, dt = timed(lambda: ora.repack_gemm_q4_0(N, wx16, ax4, 16, N, N))
-    out["repack_gemm_q4_0_q8_0"] = entry(2.0 * 16 * N * N * reps / dt / 1e12, "TOPS", 1,
-                                         f"{reps} slices of 16 activation rows x 4096 weight rows "
-                                         f"x 4096 (1/256 of the GEMM each) in {dt:.1f} s, "
-                                         f"one thread")
-    log("CPU oracle configs: " + ", ".join(f"{k} {v['value']} {v['unit']}"
+    out["q4_0_q8_0_gemm"] = entry(
+        2.0 * 16 * N * N, "TOPS", "slices of 16 weight rows x 4096 tokens x 4096 (1/256 of the "
+        "GEMM each), OpenMP over the 16 weight rows",
+        lambda: ora.gemm_q4_0(N, w16, a8, a8.shape[1], 16, N, w16.shape[1], N, 1),
+        lambda: ora.gemm_q4_0(N, w16, a8, a8.shape[1], 16, N, w16.shape[1], N, threads))
+    wx16 = ora.pack_q4_0x16(src, nx16)
+    ax4s = [ora.pack_q8_0x4(a8[16 * t:16 * t + 16].copy(), 16, nb, a8.shape[1])
+            for t in range(threads)]
+    out["repack_gemm_q4_0_q8_0"] = entry(
+        2.0 * 16 * N * N, "TOPS", "slices of 16 activation rows x 4096 weight rows x 4096 "
+        "(1/256 of the GEMM), one slice per thread",
+        lambda: ora.repack_gemm_q4_0(N, wx16, ax4s[0], 16, N, N),
+        lambda: split_run(pool, [lambda t=t: ora.repack_gemm_q4_0(N, wx16, ax4s[t], 16, N, N)
+                                 for t in range(threads)]))
+    # the all-thread repack GEMM sample does `threads` slices per call
+    out["repack_gemm_q4_0_q8_0"]["value"] = round(out["repack_gemm_q4_0_q8_0"]["value"] * threads,
+                                                  4)
+    pool.shutdown()
+    host = host_cpu()
+    for v in out.values():
+        v["host"] = host
+    log("CPU oracle configs: " + ", ".join(f"{k} {v['value']} {v['unit']} "
+                                           f"({v['value_1thread']} on 1 thread)"
                                            for k, v in out.items()))
     return out
 
@@ -739,11 +845,12 @@ def main():
                 if args.cpu_seconds > 0 and "gemm" in res else None)
     traffic = load_traffic()
 
+    g = res.get("gemv", {})
     line = {
         "metric": METRIC,
         "higher_is_better": True,
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": g.get("steps", args.steps),
         "warmup": args.warmup,
         "scaling": "weak",
         "vs_baseline": None,
@@ -751,17 +858,24 @@ def main():
         "arith": "int8 block quants (q4_0 / q8_0) -> exact int32 block sums -> fp32 fold in the "
                  "reference order",
         "data": "synthetic: splitmix64 Box-Muller, seeds 1001-1009 (tianchen-rv_amd/synth.py)",
-        "config": {"workload": "gemv_q4_0_q8_0 W 4096x4096 Q4_0 x Q8_0 vector (configs[3])",
-                   "rows": N, "cols": N, "launch": "HIP graph of `steps` launches",
-                   "weight_copies": res.get("gemv", {}).get("copies")},
+        "config": {"workload": f"gemv_q4_0_q8_0 W 4096x4096 Q4_0 x Q8_0 vector (configs[3]); "
+                               f"one step = {LAYERS} GEMVs over {LAYERS} distinct weight "
+                               f"matrices (a decode pass), 605 MB > the 256 MB Infinity Cache",
+                   "rows": N, "cols": N, "launches_per_step": LAYERS,
+                   "launches_timed": g.get("launches"),
+                   "launch": "HIP graphs of up to 32 steps, each replayed once untimed first",
+                   "bytes_touched_per_step": g.get("bytes_touched_per_step")},
     }
+    traffic_src = ("stored figure from profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE and "
+                   "WRITE_SIZE per dispatch, scaled by the add_f32 calibration); not measured "
+                   "in this run")
     if "gemv" in res:
-        g = res["gemv"]
         line.update({
-            "value": round(g["gbs"], 2), "unit": "GB/s", "ms_per_step": g["us"] / 1e3,
+            "value": round(g["gbs"], 2), "unit": "GB/s", "ms_per_step": g["ms_per_step"],
             "roofline": {"bound": "hbm", "achieved": round(g["gbs"], 2), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
                          "traffic": traffic.get("gemv_q4_0_q8_0", {}).get("bytes"),
+                         "traffic_source": traffic_src,
                          "kernel": "gemv_q4_0_q8_0_direct",
                          "bytes_per_launch": GEMV_BYTES,
                          "us_per_launch": round(g["us"], 4)},
@@ -776,6 +890,7 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(m["tops"], 2), "peak": INT8_PEAK_TOPS,
                          "unit": "TOPS", "frac": round(m["tops"] / INT8_PEAK_TOPS, 4),
                          "traffic": traffic.get("q8_0_q8_0_gemm", {}).get("bytes"),
+                         "traffic_source": traffic_src,
                          "kernel": "tcrv::gemm_wide<false>", "ops_per_launch": GEMM_OPS},
         }
         if "gemv" not in res:

@@ -120,6 +120,22 @@ TCRV_HIP_API int tcrv_hip_dequantize_row_q8_0(const uint8_t *vx, float *y, size_
  * 25-27; RVVOps.td:8345-8431).  x 4-byte aligned. */
 TCRV_HIP_API int tcrv_hip_quantize_row_q8_0(size_t n, const float *x, uint8_t *vy, void *stream);
 
+/* ---- a4: the packed-i4 offset-binary x i8 integer core --------------------
+ * Replaces tcrv_emitc_..._integer_core(const int8_t *w, const int8_t *qlo,
+ * const int8_t *qhi, const int32_t *acc, int32_t *out, size_t n)
+ * (test/Conversion/RVV/rvv-to-emitc-packed-i4-offset-binary-x-i8-product-
+ * reduce.mlir:22-27; op tcrv_rvv.packed_i4_offset_binary_x_i8_product,
+ * RVVOps.td:3814-3871):
+ *   out[0] = acc[0] + sum_{i<n} (lo(w[i])*qlo[i] + hi(w[i])*qhi[i])
+ * where lo/hi are the weight byte's low/high offset-binary nibbles minus 8, in
+ * int32 arithmetic that wraps.  acc may alias out; any alignment. */
+TCRV_HIP_API int tcrv_hip_packed_i4_offset_binary_x_i8_product_reduce(const int8_t *w,
+                                                                      const int8_t *qlo,
+                                                                      const int8_t *qhi,
+                                                                      const int32_t *acc,
+                                                                      int32_t *out, size_t n,
+                                                                      void *stream);
+
 /* ---- a5: Q8_0 . Q8_0 block dot ---------------------------------------------
  * Replaces tcrv_emitc_..._q8_0_q8_0_block_dot(size_t n, float *s,
  * const uint8_t *vx, const uint8_t *vy)
@@ -192,6 +208,37 @@ TCRV_HIP_API int tcrv_hip_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx, 
 TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
                             size_t by, size_t nr, size_t nc, size_t bx, size_t bs,
                             void *stream);
+
+/* ---- a9 over the GEMM-tile layout (no reference counterpart) --------------
+ * A GPU layout of the same Q8_0 bytes for the MFMA GEMM: rows in groups of 64;
+ * for group g and block b one 2176-byte record at (g*nb + b)*2176 holding, for
+ * rows 64g..64g+63, quants 0-15 (16 B a row), then quants 16-31, then the 64
+ * fp16 scales.  Rows past nrows in the last group are zero.  The GEMM stages
+ * its operands from this layout by DMA, 16-byte aligned, with no realignment.
+ * Bytes of the layout for nrows rows of nb blocks: */
+TCRV_HIP_API size_t tcrv_hip_gemm_tiles_bytes(size_t nrows, size_t nb);
+/* Plain Q8_0 rows (stride bx, 2-byte aligned) -> the layout at dst (16-byte
+ * aligned, tcrv_hip_gemm_tiles_bytes(nrows, nb) bytes). */
+TCRV_HIP_API int tcrv_hip_pack_q8_0_to_gemm_tiles(size_t nrows, size_t nb, const uint8_t *src,
+                                                  size_t bx, uint8_t *dst, void *stream);
+/* The Q8_0 x Q8_0 GEMM over operands in that layout (tx: nr weight rows, ty: nc
+ * token rows, both 16-byte aligned): s[ir*bs + col] exactly as
+ * tcrv_hip_q8_0_q8_0_gemm computes it from the plain rows.  Weights that are
+ * packed once serve every later call. */
+TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm_tiles(size_t n, float *s, const uint8_t *tx,
+                                               const uint8_t *ty, size_t nr, size_t nc,
+                                               size_t bs, void *stream);
+/* tcrv_hip_q8_0_q8_0_gemm (same ABI and results) with a caller-owned device
+ * workspace: both operands are packed into it (tx then ty) and the tiled GEMM
+ * runs.  Needs tcrv_hip_q8_0_q8_0_gemm_workspace_bytes(n, nr, nc) bytes, 16-byte
+ * aligned; shapes the tiled kernel does not serve (nr < 256, nc < 2) run
+ * tcrv_hip_q8_0_q8_0_gemm and leave the workspace untouched.  Calls that share
+ * a workspace must be ordered (one stream). */
+TCRV_HIP_API size_t tcrv_hip_q8_0_q8_0_gemm_workspace_bytes(size_t n, size_t nr, size_t nc);
+TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm_ws(size_t n, float *s, const uint8_t *vx,
+                                            const uint8_t *vy, size_t by, size_t nr, size_t nc,
+                                            size_t bx, size_t bs, void *workspace,
+                                            size_t workspace_bytes, void *stream);
 
 /* ---- a8: the x16 block-as-lane weight layout ---------------------------
  * Replaces tcrv_emitc_..._pack_q4_0_to_q4_0x16(size_t nblocks, const uint8_t *src,

@@ -56,6 +56,15 @@ TCRV_HIP_API int tcrv_hip_route_select(int weight_quant, int m_regime, int weigh
 /* The M regime a shape implies when the op carries none: nc <= 1 is decode. */
 TCRV_HIP_API int tcrv_hip_route_m_regime(size_t nc);
 
+/* tcrv_rvv.binary from its typed facts: the op's `kind` attribute
+ * (TCRV_HIP_BINARY_*) and its element type (TCRV_HIP_ELEM_*), the two facts
+ * binaryMnemonic (RVVToEmitC.cpp:4976-4993) selects the RVV intrinsic from.
+ * Writes the libtcrv_hip entry ("tcrv_hip_binary", taking (kind, elem, lhs,
+ * rhs, out, n, stream)) and an audit token; returns TCRV_HIP_ERR_UNSUPPORTED
+ * (entry NULL) for a kind or element type outside the grid. */
+TCRV_HIP_API int tcrv_hip_route_binary(int kind, int elem, const char **entry,
+                                       const char **reason);
+
 /* Runs one contraction in the reference GEMM ABI
  * (n, s, vx, vy, by, nr, nc, bx, bs) -- q4_0_q8_0_gemm's parameter order,
  * test/Conversion/RVV/rvv-to-emitc-q4-0-q8-0-gemm.mlir:23-31 -- on the
@@ -91,6 +100,30 @@ TCRV_HIP_API int tcrv_hip_route_param(size_t row, size_t param, const char **c_n
 /* Row of an op identity, or -1 when the table has none. */
 TCRV_HIP_API long tcrv_hip_route_find(const char *op);
 
+/* ---- the host half of the export (lib/Target for this backend) ----------
+ * What a HIP emission driver hands to the artifact export in place of the RVV
+ * C the reference renders with exportMaterializedEmitCModuleToCpp
+ * (lib/Target/TargetArtifactExport.cpp:2040-2052): for one selected variant of
+ * op `op`, the C++ text of
+ *   extern "C" int tcrv_emitc_<kernel>_<variant>(<the op's runtime-ABI
+ *                                                 parameters>, void *stream)
+ * -- the name as the reference derives it (RVVToEmitC.cpp:167-172), the
+ * parameters with the fixtures' names and C types in runtime_abi_value
+ * declaration order (:134-145, :258-268) -- whose body forwards to the op's
+ * libtcrv_hip entry and returns its status.  Op attributes the emitted C bakes
+ * in are typed facts in attrs[]: tcrv_rvv.binary takes {kind, element}
+ * (TCRV_HIP_BINARY_*, TCRV_HIP_ELEM_*), tcrv_rvv.q4_0_q8_0_gemm_tile
+ * {activation_cols}.  form selects the definition or the prototype alone
+ * (for a header).  Writes at most cap bytes, NUL-terminated, and the full size
+ * in *needed (may be NULL).  Returns TCRV_HIP_ERR_UNSUPPORTED for an op outside
+ * the table, TCRV_HIP_ERR_BAD_SIZE for missing or invalid attributes or form. */
+enum { TCRV_HIP_EXPORT_DEFINITION = 0, TCRV_HIP_EXPORT_DECLARATION = 1 };
+TCRV_HIP_API int tcrv_hip_export_function(const char *op, const char *kernel, const char *variant,
+                                          const int64_t *attrs, size_t nattrs, int form,
+                                          char *buf, size_t cap, size_t *needed);
+/* The translation unit's opening text (includes), static storage. */
+TCRV_HIP_API const char *tcrv_hip_export_prologue(void);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 
@@ -119,6 +152,13 @@ struct HipContractionSelection {
 
 HipContractionSelection selectHipContractionAlgorithm(QuantType weight, MRegime mRegime,
                                                       WeightLayout layout);
+
+struct HipBinarySelection {
+  const char *entry;   /* libtcrv_hip symbol, nullptr when declined */
+  const char *reason;  /* stable audit token */
+};
+
+HipBinarySelection selectHipBinary(int kind, int elem);
 
 MRegime deriveMRegime(size_t nc);
 

@@ -167,6 +167,27 @@ void tcrv_oracle_dequantize_row_q8_0(size_t n, float *y, const uint8_t *vx) {
 /* (RVVToEmitCBlockQuantLinear.cpp:160-220; y_hi at +16, RVVOps.td:3893-3897)*/
 /* ------------------------------------------------------------------------ */
 
+/* The same core as the standalone kernel the reference emits for the op      */
+/* (rvv-to-emitc-packed-i4-offset-binary-x-i8-product-reduce.mlir:22-27, its  */
+/* CHECK lines :48-70): out[0] = acc[0] seeded before the strip loop, then   */
+/* each strip's i16 lanes vwredsum'd onto the running int32 cell, which wraps */
+/* modulo 2^32 like the RVV integer add.                                       */
+void tcrv_oracle_packed_i4_offset_binary_x_i8_product_reduce(const int8_t *w, const int8_t *qlo,
+                                                             const int8_t *qhi,
+                                                             const int32_t *acc, int32_t *out,
+                                                             size_t n) {
+  uint32_t cell = (uint32_t)acc[0];
+  for (size_t i = 0; i < n; ++i) {
+    uint8_t v = (uint8_t)((uint8_t)w[i] ^ 0x88u);
+    int8_t lo = (int8_t)((int8_t)(uint8_t)(v << 4) >> 4);
+    int8_t hi = (int8_t)((int8_t)v >> 4);
+    int16_t lane = (int16_t)((int16_t)lo * (int16_t)qlo[i]);       /* vwmul  */
+    lane = (int16_t)(lane + (int16_t)hi * (int16_t)qhi[i]);          /* vwmacc */
+    cell += (uint32_t)(int32_t)lane;                                  /* vwredsum */
+  }
+  out[0] = (int32_t)cell;
+}
+
 int32_t tcrv_oracle_q4_0_q8_0_block_sumi(const uint8_t *xb, const uint8_t *yb) {
   const uint8_t *w = xb + 2;
   const int8_t *ylo = (const int8_t *)(yb + 2);

@@ -58,6 +58,13 @@ void tcrv_oracle_dequantize_row_q8_0(size_t n, float *y, const uint8_t *vx);
 /* a4: the packed-i4 offset-binary x i8 integer core for one Q4_0 block against
  * one Q8_0 block (RVVToEmitC.cpp:2524-2589). */
 int32_t tcrv_oracle_q4_0_q8_0_block_sumi(const uint8_t *xb, const uint8_t *yb);
+/* a4 as its standalone kernel: out[0] = acc[0] + sum over i < n of the
+ * decoded weight byte w[i]'s low nibble x qlo[i] + high nibble x qhi[i]
+ * (int32, wrapping). */
+void tcrv_oracle_packed_i4_offset_binary_x_i8_product_reduce(const int8_t *w, const int8_t *qlo,
+                                                             const int8_t *qhi,
+                                                             const int32_t *acc, int32_t *out,
+                                                             size_t n);
 /* a5's integer core for one block pair. */
 int32_t tcrv_oracle_q8_0_q8_0_block_sumi(const uint8_t *xb, const uint8_t *yb);
 

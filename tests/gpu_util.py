@@ -32,3 +32,20 @@ def assert_f32_parity(got: np.ndarray, want: np.ndarray, rtol: float = 1e-5, wha
     diff = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
     assert diff.size == 0, (f"{what}: {diff.size} elements not bit-identical; first at "
                             f"{diff[0]}: got {got[diff[0]]!r} want {want[diff[0]]!r}")
+
+
+def assert_f32_parity_nan(got: np.ndarray, want: np.ndarray, what: str = ""):
+    """Bit-identical outside NaNs; NaN exactly where the oracle has NaN.  The
+    payload of a NaN is not part of the contract: a RISC-V FPU returns the
+    canonical NaN where x86 and the GPU propagate an input's payload."""
+    got = np.asarray(got, dtype=np.float32).reshape(-1)
+    want = np.asarray(want, dtype=np.float32).reshape(-1)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    gn, wn = np.isnan(got), np.isnan(want)
+    bad = np.flatnonzero(gn != wn)
+    assert bad.size == 0, (f"{what}: NaN pattern differs at {bad.size} elements; first at "
+                           f"{bad[0]}: got {got[bad[0]]!r} want {want[bad[0]]!r}")
+    ok = ~wn
+    diff = np.flatnonzero(got[ok].view(np.uint32) != want[ok].view(np.uint32))
+    assert diff.size == 0, (f"{what}: {diff.size} elements not bit-identical; first: got "
+                            f"{got[ok][diff[0]]!r} want {want[ok][diff[0]]!r}")

@@ -29,6 +29,7 @@ _SIGS = {
     "tcrv_oracle_dequantize_row_q8_0": ([_sz, _p, _p], None),
     "tcrv_oracle_q4_0_q8_0_block_sumi": ([_p, _p], _i32),
     "tcrv_oracle_q8_0_q8_0_block_sumi": ([_p, _p], _i32),
+    "tcrv_oracle_packed_i4_offset_binary_x_i8_product_reduce": ([_p, _p, _p, _p, _p, _sz], None),
     "tcrv_oracle_block_sums_q8_0_q8_0": ([_sz, _p, _p, _p], None),
     "tcrv_oracle_block_sums_q4_0_q8_0": ([_sz, _p, _p, _p], None),
     "tcrv_oracle_vec_dot_q8_0_q8_0": ([_sz, _p, _p, _p], None),
@@ -97,6 +98,14 @@ class Oracle:
     # -- a4/a5/a6 ----------------------------------------------------------
     def q4_block_sumi(self, xb: np.ndarray, yb: np.ndarray) -> int:
         return self.lib.tcrv_oracle_q4_0_q8_0_block_sumi(_a(xb), _a(yb))
+
+    def int_core_reduce(self, w: np.ndarray, qlo: np.ndarray, qhi: np.ndarray,
+                        acc: int) -> int:
+        a = np.array([acc], dtype=np.int32)
+        out = np.zeros(1, dtype=np.int32)
+        self.lib.tcrv_oracle_packed_i4_offset_binary_x_i8_product_reduce(
+            _a(w), _a(qlo), _a(qhi), _a(a), _a(out), w.size)
+        return int(out[0])
 
     def q8_block_sumi(self, xb: np.ndarray, yb: np.ndarray) -> int:
         return self.lib.tcrv_oracle_q8_0_q8_0_block_sumi(_a(xb), _a(yb))

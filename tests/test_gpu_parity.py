@@ -82,6 +82,49 @@ def test_quantize_q8_0(hip, oracle, dev, nb):
     assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} bytes differ"
 
 
+# ------------------------------------------------- a4 standalone integer core ---
+
+@pytest.mark.parametrize("n,off", [(0, 0), (1, 0), (16, 0), (4095, 0), (1 << 20, 0), (1000, 3),
+                                   ((1 << 20) + 7, 1)])
+def test_int_core_reduce(hip, oracle, dev, n, off):
+    """tcrv_hip_packed_i4_offset_binary_x_i8_product_reduce against the oracle:
+    16-byte aligned operands take the v_dot4 path, others the byte path; every
+    weight byte value appears."""
+    rng = np.random.default_rng(n + off)
+    w = rng.integers(0, 256, n + off).astype(np.uint8)
+    w[off:off + min(n, 256)] = np.arange(min(n, 256))
+    qlo = rng.integers(-128, 128, n + off).astype(np.int8)
+    qhi = rng.integers(-128, 128, n + off).astype(np.int8)
+    acc = np.array([-12345], np.int32)
+    want = oracle.int_core_reduce(w[off:].view(np.int8).copy(), qlo[off:].copy(), qhi[off:].copy(),
+                                  int(acc[0]))
+    dw, dl, dh = to_dev(w, dev), to_dev(qlo, dev), to_dev(qhi, dev)
+    out = to_dev(np.array([7], np.int32), dev)
+    hip.packed_i4_offset_binary_x_i8_product_reduce(dw[off:], dl[off:], dh[off:],
+                                                    to_dev(acc, dev), out, n)
+    assert int(from_dev(out)[0]) == want
+    # the accumulator cell may be the output cell
+    cell = to_dev(acc.copy(), dev)
+    hip.packed_i4_offset_binary_x_i8_product_reduce(dw[off:], dl[off:], dh[off:], cell, cell, n)
+    assert int(from_dev(cell)[0]) == want
+
+
+def test_int_core_reduce_wraps_int32(hip, oracle, dev):
+    """n large enough that the sum leaves int32: the cell wraps as the RVV
+    integer add does."""
+    n = 1 << 21
+    w = np.zeros(n, np.uint8)            # every nibble 0 -> -8
+    qlo = np.full(n, -128, np.int8)       # -8 * -128 = 1024 per element
+    qhi = np.full(n, -128, np.int8)
+    acc = np.array([2**31 - 5], np.int32)
+    want = oracle.int_core_reduce(w.view(np.int8), qlo, qhi, int(acc[0]))
+    assert want == ((2**31 - 5 + 2048 * n + 2**31) % 2**32) - 2**31
+    out = empty_dev(1, torch.int32, dev)
+    hip.packed_i4_offset_binary_x_i8_product_reduce(to_dev(w, dev), to_dev(qlo, dev),
+                                                    to_dev(qhi, dev), to_dev(acc, dev), out, n)
+    assert int(from_dev(out)[0]) == want
+
+
 # ------------------------------------------------------------ block sums a4/a5 ---
 
 @pytest.mark.parametrize("nb,rows", [(1, 3), (2, 5), (128, 64), (131, 7), (300, 2)])
@@ -488,27 +531,6 @@ def test_pack_q8_0x4_two_byte_aligned_source(hip, oracle, dev):
     assert np.array_equal(from_dev(dst), oracle.pack_q8_0x4(a, nr, nb, a.shape[1]))
 
 
-def test_repack_gemm_argument_checks(hip, dev):
-    """Misaligned operands and null pointers are refused before any launch
-    (fake addresses would fault if one happened); empty groups write nothing."""
-    call = lambda *a: hip.call("tcrv_hip_repack_gemm_q4_0_q8_0", *a, hip._stream(None),
-                               check=False)
-    assert call(64, 0x1000, 0x2002, 0x3000, 4, 16, 16) == hip.ERR_MISALIGNED
-    assert call(64, 0x1000, 0x2000, 0x3002, 4, 16, 16) == hip.ERR_MISALIGNED
-    assert call(64, 0, 0x2000, 0x3000, 4, 16, 16) == hip.ERR_NULL_POINTER
-    assert call(64, 0x1000, 0x2000, 0x3000, 3, 16, 16) == hip.OK   # no full activation group
-    assert call(64, 0x1000, 0x2000, 0x3000, 4, 15, 16) == hip.OK   # no full weight group
-
-
-def test_repack_gemm_rejects_overlapping_rows(hip, dev):
-    """Each group writes 4 activation rows at stride bs: a stride shorter than
-    the written row is refused before anything runs (fake addresses would fault
-    if a launch happened)."""
-    st = hip.call("tcrv_hip_repack_gemm_q4_0_q8_0", 64, 0x1000, 0x2000, 0x3000, 4, 32, 31,
-                  hip._stream(None), check=False)
-    assert st == hip.ERR_BAD_SIZE
-
-
 def test_repack_gemm_full_size_sampled_tokens(hip, oracle, dev):
     """4096 weight rows x 4096 tokens x K 4096 on the GPU; the oracle checks three
     4-token groups (first, middle, last) against all 4096 weight rows."""
@@ -576,8 +598,8 @@ def _binary_inputs(dtype, n, seed):
         info = np.iinfo(dtype)
         a = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
         b = rng.integers(info.min, info.max, n, dtype=dtype, endpoint=True)
-        a[:3] = [info.min, info.max, info.max]
-        b[:3] = [info.min, 1, info.max]
+        a[:4] = [info.min, info.max, info.max, -1 if info.min < 0 else info.max]
+        b[:4] = [info.min, 1, info.max, -1 if info.min < 0 else info.max]  # all-ones x all-ones
     else:
         a = (rng.standard_normal(n) * 1e3).astype(dtype)
         b = rng.standard_normal(n).astype(dtype)
@@ -751,3 +773,116 @@ def test_graph_replays_match_the_oracle(hip, oracle, dev):
             assert_f32_parity(from_dev(out[k]), want[k], what=f"graph replay {rep} {k}")
         assert np.array_equal(from_dev(out["quant"]), want["quant"]), f"graph replay {rep} quant"
     assert_f32_parity(from_dev(side), want["gemv"], what="eager GEMV between replays")
+
+
+# ------------------------------------ a9 over the GEMM-tile layout (DMA staged) ---
+
+def tiles_reference(a, nrows, nb):
+    """The documented GEMM-tile layout, built independently in numpy from plain
+    Q8_0 rows: per 64-row group and block, 64 x 16 quant bytes (elements 0-15),
+    64 x 16 (elements 16-31), 64 fp16 scales; rows past nrows zero."""
+    ng = -(-nrows // 64)
+    blocks = np.zeros((ng * 64, nb, 34), np.uint8)
+    blocks[:nrows] = a[:nrows, :nb * 34].reshape(nrows, nb, 34)
+    blocks = blocks.reshape(ng, 64, nb, 34).transpose(0, 2, 1, 3)  # g, b, row, byte
+    rec = np.concatenate([blocks[..., 2:18].reshape(ng, nb, 1024),
+                          blocks[..., 18:34].reshape(ng, nb, 1024),
+                          blocks[..., 0:2].reshape(ng, nb, 128)], axis=2)
+    return rec.reshape(-1)
+
+
+@pytest.mark.parametrize("nrows,nb,pad,off", [(64, 1, 0, 0), (100, 9, 16, 0), (130, 7, 0, 2),
+                                              (5, 4, 2, 2)])
+def test_pack_q8_0_to_gemm_tiles(hip, dev, nrows, nb, pad, off):
+    a = np.pad(synth.q8_0_matrix(nrows, nb * 32, 80, 1.0), ((0, 0), (0, pad)))
+    want = tiles_reference(a, nrows, nb)
+    assert hip.gemm_tiles_bytes(nrows, nb) == want.size
+    buf = empty_dev(a.size + 16, torch.uint8, dev)
+    buf[off:off + a.size] = to_dev(a.reshape(-1), dev)  # off 2: 2-byte aligned rows
+    dst = to_dev(np.full(want.size, 0xEE, np.uint8), dev)
+    hip.pack_q8_0_to_gemm_tiles(nrows, nb, buf[off:off + a.size], a.shape[1], dst)
+    assert np.array_equal(from_dev(dst), want)
+
+
+@pytest.mark.parametrize("nr,nc,nb,xpad,ypad", [
+    (256, 128, 4, 0, 0),      # one tile, one chunk
+    (256, 128, 8, 0, 0),      # two chunks
+    (300, 130, 9, 16, 32),    # partial tiles both ways, 2 chunks + 1 block, padded strides
+    (520, 257, 13, 0, 4),     # three tile rows, 3 chunks + 1 block
+    (256, 2, 1, 0, 0),        # one block: only the partial chunk
+    (640, 384, 130, 0, 0),    # 32 chunks + 2 blocks, groups past the last one re-read
+])
+def test_q8_0_gemm_tiles_and_ws(hip, oracle, dev, nr, nc, nb, xpad, ypad):
+    n = nb * 32
+    w = np.pad(synth.q8_0_matrix(nr, n, 1009, 0.02), ((0, 0), (0, xpad)))
+    a = np.pad(synth.q8_0_matrix(nc, n, 1008, 1.0), ((0, 0), (0, ypad)))
+    w[0, 2:34] = 0x80
+    a[0, 2:34] = 0x80  # -128 x -128 block sums
+    bs = nc + 3
+    want = oracle.gemm_q8_0(n, w, a, a.shape[1], nr, nc, w.shape[1], bs, 8).reshape(nr, bs)
+    dw, da = to_dev(w, dev), to_dev(a, dev)
+    # pre-packed operands
+    tx = empty_dev(hip.gemm_tiles_bytes(nr, nb), torch.uint8, dev)
+    ty = empty_dev(hip.gemm_tiles_bytes(nc, nb), torch.uint8, dev)
+    hip.pack_q8_0_to_gemm_tiles(nr, nb, dw, w.shape[1], tx)
+    hip.pack_q8_0_to_gemm_tiles(nc, nb, da, a.shape[1], ty)
+    s = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+    hip.q8_0_q8_0_gemm_tiles(n, s, tx, ty, nr, nc, bs)
+    got = from_dev(s).reshape(nr, bs)
+    assert_f32_parity(got[:, :nc], want[:, :nc], what=f"tiles gemm {nr}x{nc}x{n}")
+    assert np.all(got[:, nc:] == -7.0)
+    # the reference ABI with a workspace
+    wsb = hip.q8_0_q8_0_gemm_workspace_bytes(n, nr, nc)
+    ws = empty_dev(wsb, torch.uint8, dev)
+    s2 = empty_dev(nr * bs, torch.float32, dev)
+    hip.q8_0_q8_0_gemm_ws(n, s2, dw, da, a.shape[1], nr, nc, w.shape[1], bs, ws, wsb)
+    assert_f32_parity(from_dev(s2).reshape(nr, bs)[:, :nc], want[:, :nc], what="gemm_ws")
+
+
+def test_q8_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
+    """Shapes the tiled kernel does not serve run the plain entry and leave the
+    workspace alone; a workspace that is too small or misaligned is refused."""
+    n, nb = 256, 8
+    for nr, nc in ((100, 70), (300, 1), (1, 40)):
+        w = synth.q8_0_matrix(nr, n, 81, 0.02)
+        a = synth.q8_0_matrix(nc, n, 82, 1.0)
+        ws = to_dev(np.full(64, 0x5A, np.uint8), dev)
+        s = empty_dev(nr * nc, torch.float32, dev)
+        hip.q8_0_q8_0_gemm_ws(n, s, to_dev(w, dev), to_dev(a, dev), a.shape[1], nr, nc,
+                              w.shape[1], nc, ws, 64)
+        assert_f32_parity(from_dev(s), oracle.gemm_q8_0(n, w, a, a.shape[1], nr, nc, w.shape[1],
+                                                        nc, 8))
+        assert np.all(from_dev(ws) == 0x5A)
+    w = synth.q8_0_matrix(256, n, 83, 0.02)
+    a = synth.q8_0_matrix(16, n, 84, 1.0)
+    need = hip.q8_0_q8_0_gemm_workspace_bytes(n, 256, 16)
+    ws = empty_dev(need + 16, torch.uint8, dev)
+    s = empty_dev(256 * 16, torch.float32, dev)
+    call = lambda *args: hip.call("tcrv_hip_q8_0_q8_0_gemm_ws", n, s, to_dev(w, dev),
+                                  to_dev(a, dev), a.shape[1], 256, 16, w.shape[1], 16, *args, 0,
+                                  check=False)
+    assert call(ws, need - 1) == hip.ERR_BAD_SIZE
+    assert call(ws[8:], need) == hip.ERR_MISALIGNED
+    torch.cuda.synchronize()
+
+
+def test_q8_0_gemm_ws_full_size_sampled(hip, oracle, dev):
+    """4096 x 4096 x 4096 through the workspace entry; 64 rows and 64 columns
+    checked against the oracle."""
+    n = nr = nc = 4096
+    w = synth.q8_0_matrix(nr, n, 1009, 0.02)
+    a = synth.q8_0_matrix(nc, n, 1008, 1.0)
+    wsb = hip.q8_0_q8_0_gemm_workspace_bytes(n, nr, nc)
+    ws = empty_dev(wsb, torch.uint8, dev)
+    s = empty_dev(nr * nc, torch.float32, dev)
+    hip.q8_0_q8_0_gemm_ws(n, s, to_dev(w, dev), to_dev(a, dev), a.shape[1], nr, nc, w.shape[1],
+                          nc, ws, wsb)
+    got = from_dev(s).reshape(nr, nc)
+    rng = np.random.default_rng(11)
+    for r in np.sort(rng.choice(nr, 64, replace=False)):
+        want = oracle.gemm_q8_0(n, w[r].copy(), a, a.shape[1], 1, nc, w.shape[1], nc, 8)
+        assert_f32_parity(got[r], want, what=f"row {r}")
+    cols = np.sort(rng.choice(nc, 64, replace=False))
+    sub = np.ascontiguousarray(a[cols])
+    want = oracle.gemm_q8_0(n, w, sub, sub.shape[1], nr, len(cols), w.shape[1], len(cols), 8)
+    assert_f32_parity(got[:, cols], want.reshape(nr, len(cols)), what="sampled cols")

@@ -36,7 +36,7 @@ def test_exports_exactly_the_header():
 
 
 def test_binding_covers_the_header():
-    bound = set(tcrv_hip.SIGNATURES) | set(tcrv_hip.STRING_FUNCS)
+    bound = set(tcrv_hip.SIGNATURES) | set(tcrv_hip.STRING_FUNCS) | set(tcrv_hip.SIZE_FUNCS)
     assert bound == set(declared_symbols())
 
 
@@ -78,3 +78,22 @@ def test_argument_errors_before_launch(name, args, want):
 ])
 def test_empty_problems_are_no_ops(name, args):
     assert tcrv_hip.call(name, *args, check=False) == tcrv_hip.OK
+
+
+def test_repack_gemm_argument_checks():
+    """Misaligned operands and null pointers are refused before any launch
+    (the addresses are fake: nothing may run); empty groups write nothing."""
+    call = lambda *a: tcrv_hip.call("tcrv_hip_repack_gemm_q4_0_q8_0", *a, 0, check=False)
+    assert call(64, 0x1000, 0x2002, 0x3000, 4, 16, 16) == tcrv_hip.ERR_MISALIGNED
+    assert call(64, 0x1000, 0x2000, 0x3002, 4, 16, 16) == tcrv_hip.ERR_MISALIGNED
+    assert call(64, 0, 0x2000, 0x3000, 4, 16, 16) == tcrv_hip.ERR_NULL_POINTER
+    assert call(64, 0x1000, 0x2000, 0x3000, 3, 16, 16) == tcrv_hip.OK   # no full activation group
+    assert call(64, 0x1000, 0x2000, 0x3000, 4, 15, 16) == tcrv_hip.OK   # no full weight group
+
+
+def test_repack_gemm_rejects_overlapping_rows():
+    """Each group writes 4 activation rows at stride bs: a stride shorter than
+    the written row is refused before anything runs."""
+    st = tcrv_hip.call("tcrv_hip_repack_gemm_q4_0_q8_0", 64, 0x1000, 0x2000, 0x3000, 4, 32, 31, 0,
+                       check=False)
+    assert st == tcrv_hip.ERR_BAD_SIZE

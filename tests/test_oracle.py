@@ -589,3 +589,40 @@ def test_pack_q4_0_soa_matches_an_independent_gather_and_round_trips(oracle):
     assert np.array_equal(soa[:nrows * nb * 16].reshape(-1, 16), blocks[:, 2:])
     assert np.array_equal(soa[nrows * nb * 16:].reshape(-1, 2), blocks[:, :2])
     assert np.array_equal(oracle.unpack_q4_0_soa(soa, nrows, nb), plain.reshape(-1))
+
+
+# ------------------------------------- a4 standalone kernel (integer core) ---
+
+def test_int_core_reduce_equals_block_sums(oracle):
+    """The standalone a4 kernel over the 16 weight bytes of a Q4_0 block and the
+    two halves of a Q8_0 block is the block's integer core (already pinned by
+    brute force above): out = acc + block_sumi, for every block of a matrix."""
+    import synth
+    rng = np.random.default_rng(41)
+    x = synth.q4_0_matrix(4, 32 * 64, 42, 0.02).reshape(-1, 18)
+    y = synth.q8_0_matrix(4, 32 * 64, 43, 1.0).reshape(-1, 34)
+    for k in range(x.shape[0]):
+        w = np.ascontiguousarray(x[k, 2:]).view(np.int8)
+        qlo = np.ascontiguousarray(y[k, 2:18]).view(np.int8)
+        qhi = np.ascontiguousarray(y[k, 18:]).view(np.int8)
+        acc = int(rng.integers(-1000, 1000))
+        assert oracle.int_core_reduce(w, qlo, qhi, acc) == \
+            acc + oracle.q4_block_sumi(np.ascontiguousarray(x[k]), np.ascontiguousarray(y[k]))
+
+
+def test_int_core_reduce_brute_force_every_weight_byte(oracle):
+    """All 256 weight bytes against the (nibble - 8) definition (RVVOps.td:
+    3837-3840) with extreme activations, summed in int64 and wrapped to int32."""
+    rng = np.random.default_rng(44)
+    w = np.resize(np.arange(256, dtype=np.uint8), 4096)
+    qlo = rng.integers(-128, 128, w.size).astype(np.int8)
+    qhi = rng.integers(-128, 128, w.size).astype(np.int8)
+    qlo[:256] = -128
+    qhi[:256] = 127
+    lo = (w & 0xF).astype(np.int64) - 8
+    hi = (w >> 4).astype(np.int64) - 8
+    for acc in (0, -7, 2**31 - 1 - 10):
+        want = acc + int(np.sum(lo * qlo.astype(np.int64) + hi * qhi.astype(np.int64)))
+        want = (want + 2**31) % 2**32 - 2**31  # the int32 cell wraps
+        assert oracle.int_core_reduce(w.view(np.int8), qlo, qhi, acc) == want
+    assert oracle.int_core_reduce(w.view(np.int8)[:0], qlo[:0], qhi[:0], 123) == 123

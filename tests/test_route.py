@@ -19,8 +19,13 @@ ROUTE_HEADER = os.path.join(ROOT, "include", "tcrv_hip_route.h")
 REFERENCE_ROLES = {
     "lhs-input-buffer", "rhs-input-buffer", "output-buffer", "runtime-element-count",
     "lhs-input-stride", "rhs-input-stride", "output-stride", "source-byte-stride",
-    "destination-byte-stride", "rhs-scalar-value",
+    "destination-byte-stride", "rhs-scalar-value", "accumulator-input-buffer",
 }
+# Values that are not runtime-ABI parameters in the reference but arguments of
+# the HIP entry: op attributes and the element type.
+NON_ABI = {("tcrv_rvv.q4_0_q8_0_gemm_tile", "m"): "op-attribute",
+           ("tcrv_rvv.binary", "kind"): "op-attribute",
+           ("tcrv_rvv.binary", "elem"): "element-type"}
 
 
 def header_params(entry):
@@ -42,7 +47,7 @@ def test_route_library_exports_its_header():
                          check=True).stdout
     exported = sorted({ln.split()[-1] for ln in out.splitlines()
                        if ln.split() and ln.split()[-1].startswith("tcrv_")})
-    declared = sorted(set(re.findall(r"TCRV_HIP_API\s+[\w\s\*]*?\b(tcrv_hip_route_\w+)\s*\(",
+    declared = sorted(set(re.findall(r"TCRV_HIP_API\s+[\w\s\*]*?\b(tcrv_hip_(?:route|export)_\w+)\s*\(",
                                      open(ROUTE_HEADER).read())))
     assert exported == declared
     assert set(tcrv_hip.ROUTE_SIGNATURES) == set(declared)
@@ -94,6 +99,21 @@ def test_selection_rejects_values_outside_the_enums():
         assert a.value == -7  # untouched
 
 
+@pytest.mark.parametrize("kind", [tcrv_hip.BINARY_ADD, tcrv_hip.BINARY_SUB, tcrv_hip.BINARY_MUL])
+@pytest.mark.parametrize("elem", list(tcrv_hip.ELEM))
+def test_route_binary_typed_facts(kind, elem):
+    st, entry, reason = tcrv_hip.route_binary(kind, elem)
+    assert st == tcrv_hip.OK and entry == "tcrv_hip_binary"
+    assert reason == ("hip-binary-float-ieee" if elem in ("f32", "f64")
+                      else "hip-binary-integer-wrapping")
+
+
+@pytest.mark.parametrize("kind,elem", [(3, 0), (-1, 0), (0, 9), (0, -1)])
+def test_route_binary_declines_outside_the_grid(kind, elem):
+    st, entry, reason = tcrv_hip.route_binary(kind, elem)
+    assert st == tcrv_hip.ERR_UNSUPPORTED and entry is None and reason.startswith("hip-decline")
+
+
 @pytest.mark.parametrize("nc,regime", [(0, 0), (1, 0), (2, 1), (4096, 1)])
 def test_m_regime_from_shape(nc, regime):
     assert tcrv_hip.load_route().tcrv_hip_route_m_regime(nc) == regime
@@ -111,10 +131,11 @@ def test_route_table_matches_the_c_abi():
         # the entry takes the op's runtime-ABI parameters in order, then the stream
         assert header_params(row["entry"]) == names + ["stream"], row["entry"]
         for c_name, c_type, role in row["params"]:
-            # the gemm tile's column count is an op attribute in the reference
-            # (activation_cols, RVVOps.td:4048-4133), an argument here
-            if role == "op-attribute":
-                assert (row["op"], c_name) == ("tcrv_rvv.q4_0_q8_0_gemm_tile", "m")
+            # the gemm tile's column count and the binary op's kind are op
+            # attributes in the reference (activation_cols, RVVOps.td:4048-4133;
+            # kind, :3217-3243), arguments here, as is the element type
+            if (row["op"], c_name) in NON_ABI:
+                assert role == NON_ABI[(row["op"], c_name)]
                 continue
             assert role in REFERENCE_ROLES, (row["op"], c_name, role)
             assert c_type in ("size_t", "int32_t") or c_type.endswith("*")
@@ -132,6 +153,14 @@ def test_route_table_keeps_the_reference_gemm_abi():
     rgemm = rows["tcrv_rvv.repack_gemm_q4_0_q8_0"]["params"]
     # rvv-to-emitc-repack-gemm-q4-0-q8-0.mlir:22-28
     assert [p[0] for p in rgemm] == ["n", "s", "vx", "vy", "nr", "nc", "bs"]
+    core = rows["tcrv_rvv.packed_i4_offset_binary_x_i8_product"]["params"]
+    # rvv-to-emitc-packed-i4-offset-binary-x-i8-product-reduce.mlir:22-27
+    assert [p[0] for p in core] == ["w", "qlo", "qhi", "acc", "out", "n"]
+    assert core[3] == ("acc", "const int32_t *", "accumulator-input-buffer")
+    binary = rows["tcrv_rvv.binary"]["params"]
+    # the reference's (lhs, rhs, out, n) after the two typed facts
+    assert [p[0] for p in binary] == ["kind", "elem", "lhs", "rhs", "out", "n"]
+    assert not any(op.startswith("tcrv_rvv.binary.") for op in rows)  # no names with facts in them
     dot = rows["tcrv_rvv.q4_0_q8_0_block_dot"]["params"]
     # the ggml vec_dot ABI, rvv-to-emitc-q4-0-q8-0-block-dot.mlir:24-31
     assert [p[0] for p in dot] == ["n", "s", "bs", "vx", "bx", "vy", "by", "nrc"]

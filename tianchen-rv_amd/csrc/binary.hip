@@ -7,6 +7,8 @@
 // operations (the library is built with -ffp-contract=off).  Each thread moves
 // kUnroll 16-byte vectors per operand, all loads issued before the arithmetic;
 // a scalar kernel covers the tail and pointers that are not 16-byte aligned.
+#include <type_traits>
+
 #include "tcrv_hip_internal.h"
 
 namespace {
@@ -14,14 +16,23 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kUnroll = 2;  // as add_f32: two 16-byte vectors per operand measured fastest
 
+// Integer elements narrower than 32 bits would be promoted to (signed) int by
+// C++, where 0xFFFF * 0xFFFF overflows; they are computed in uint32_t, whose
+// arithmetic wraps by definition, and narrowed back (the low bits are the RVV
+// result).
+template <typename T>
+using wide_t = typename std::conditional<std::is_integral<T>::value && (sizeof(T) < 4),
+                                         uint32_t, T>::type;
+
 template <typename T, int kKind>
 __device__ __forceinline__ T apply(T a, T b) {
+  const wide_t<T> x = static_cast<wide_t<T>>(a), y = static_cast<wide_t<T>>(b);
   if constexpr (kKind == TCRV_HIP_BINARY_ADD)
-    return a + b;
+    return static_cast<T>(x + y);
   else if constexpr (kKind == TCRV_HIP_BINARY_SUB)
-    return a - b;
+    return static_cast<T>(x - y);
   else
-    return a * b;
+    return static_cast<T>(x * y);
 }
 
 template <typename T, int kKind>

@@ -176,8 +176,11 @@ __global__ __launch_bounds__(kQzThreads) void quantize_q8_0(const float *x, uint
 #pragma unroll
   for (int k = 0; k < kQzPer; ++k) {
     const int lb = (threadIdx.x >> 3) + k * (kQzThreads / 8);
-    const float amax = max8(fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)),
-                                  fmaxf(fabsf(v[k].z), fabsf(v[k].w))));
+    // seeded with 0.0f as the reference's reduction is: NaN elements are
+    // skipped, and an all-NaN block has amax = 0 (d = 0, id = 0)
+    const float amax = fmaxf(max8(fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)),
+                                        fmaxf(fabsf(v[k].z), fabsf(v[k].w)))),
+                             0.0f);
     const float d = __fdiv_rn(amax, 127.0f);
     const float id = d != 0.0f ? __frcp_rn(d) : 0.0f;
     if (lb < nblk) {

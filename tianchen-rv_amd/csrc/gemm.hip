@@ -18,6 +18,7 @@
 //   gemm_q8_0_q8_0_kernel  any 2-byte aligned rows: 4 waves, 2x2 tiles each,
 //                          raw block bytes through LDS, scalar scale epilogue.
 #include "tcrv_hip_internal.h"
+#include "mfma_fold.h"
 
 namespace tcrv {
 
@@ -206,26 +207,6 @@ constexpr int kFbKB = 8;                   // blocks per K chunk
 constexpr int kFbQRow = kFbKB * kQK + 16;  // 272: quant bytes per staged row (+16 pad: 16-byte
                                            // reads of 32 consecutive rows hit distinct banks)
 
-// XCD-aware tile order: work-groups are dispatched round-robin over the 8
-// XCDs (id % 8), so id is first remapped so that each XCD owns one contiguous
-// range of tiles, and that range is walked in groups of kGroupM tile rows so
-// that concurrently running work-groups share weight and activation panels in
-// their XCD's L2.
-__device__ __forceinline__ void tile_of(unsigned id, unsigned tiles_m, unsigned tiles_n,
-                                        unsigned &tm, unsigned &tn) {
-  constexpr unsigned kXcds = 8, kGroupM = 8;
-  const unsigned total = tiles_m * tiles_n;
-  if (total % kXcds == 0)
-    id = (id % kXcds) * (total / kXcds) + id / kXcds;
-  const unsigned per_group = kGroupM * tiles_n;
-  const unsigned group = id / per_group;
-  const unsigned first_m = group * kGroupM;
-  const unsigned gm = min(tiles_m - first_m, kGroupM);
-  const unsigned in_group = id - group * per_group;
-  tm = first_m + in_group % gm;
-  tn = in_group / gm;
-}
-
 // Work-group: 16 waves, each owning one 32x32 tile of a 128x128 output tile
 // (four waves per SIMD hide LDS and MFMA latency; at most 128 VGPRs).  K chunks
 // of 8 blocks are staged split -- each 34-byte block into its 32 quants
@@ -260,20 +241,35 @@ __device__ __forceinline__ void load_pair(PairRegs &p, const uint8_t *q, bool tw
   }
 }
 
-__device__ __forceinline__ void store_pair(const PairRegs &p, bool two, int8_t *qrow,
-                                           float *d0, float *d1) {
+__device__ __forceinline__ void store_pair_quants(const PairRegs &p, bool two, int8_t *qrow) {
   const uint32_t *r = p.r;
   uint4 *dst = reinterpret_cast<uint4 *>(qrow);
   dst[0] = make_uint4(funnel16(r[0], r[1]), funnel16(r[1], r[2]), funnel16(r[2], r[3]),
                       funnel16(r[3], r[4]));
   dst[1] = make_uint4(funnel16(r[4], r[5]), funnel16(r[5], r[6]), funnel16(r[6], r[7]),
                       funnel16(r[7], r[8]));
-  *d0 = fp16_bits_to_f32(r[0] & 0xffffu);
   if (two) {
     dst[2] = make_uint4(r[9], r[10], r[11], r[12]);
     dst[3] = make_uint4(r[13], r[14], r[15], r[16]);
-    *d1 = fp16_bits_to_f32(r[8] >> 16);
   }
+}
+
+__device__ __forceinline__ void store_pair(const PairRegs &p, bool two, int8_t *qrow,
+                                           float *d0, float *d1) {
+  store_pair_quants(p, two, qrow);
+  *d0 = fp16_bits_to_f32(p.r[0] & 0xffffu);
+  if (two)
+    *d1 = fp16_bits_to_f32(p.r[8] >> 16);
+}
+
+// The same with the scales kept as their fp16 bit patterns (the operands of
+// the f16 scale MFMA below).
+__device__ __forceinline__ void store_pair_h(const PairRegs &p, bool two, int8_t *qrow,
+                                             uint16_t *h0, uint16_t *h1) {
+  store_pair_quants(p, two, qrow);
+  *h0 = static_cast<uint16_t>(p.r[0] & 0xffffu);
+  if (two)
+    *h1 = static_cast<uint16_t>(p.r[8] >> 16);
 }
 
 // A Q4_0 weight block pair task (36 bytes, or 18 when only block 2m exists),
@@ -513,12 +509,42 @@ constexpr int kWRows = kWBM + kWBN;               // 384 staged rows per chunk
 constexpr int kWStage = kWRows * kWQRow;
 constexpr int kWTasks = kWRows * (kWKB / 2);      // 768 block-pair tasks per chunk
 
+// ---------------------------------------------------------------------------
+// The Q8_0 fold of the wide tile, software-pipelined.  Per 32x32 tile and block:
+//   v_mfma_i32_32x32x32_i8  -> sumi(row, col) (exact int32 block sums)
+//   v_mfma_f32_32x32x8_f16  -> d_x(row) * d_y(col): k-slot 0 carries the two
+//                              fp16 scales, every other k-slot is zero, so each
+//                              output is one product of two fp16 values, exact
+//                              in fp32 (16 matrix cycles, half the 2-block f32
+//                              outer product's per-block cost)
+//   VALU: acc = fma((float)sumi, dxy, acc) -- the reference fold, in order.
+// The MFMAs of step s+1 (tile, block) are issued before the fold of step s, so
+// the matrix core works while the VALU folds (on this part one wave issues a
+// VALU instruction about every 6 cycles; the matrix core fills the gaps).
+// Scales are staged as fp16 bit patterns, [stage][block][row], with 32 zero
+// rows after the 384 panel rows: lanes 32-63 (k-slots 4-7 of the f16 MFMA)
+// point there, so building an operand costs one 16-bit LDS read and no VALU.
+// ---------------------------------------------------------------------------
+constexpr int kHRow = kWRows + 32;     // fp16 scales per block row (+32 zero rows)
+constexpr int kHStage = kWKB * kHRow;  // per stage
+#ifndef TCRV_GEMM_Q8_PIPE
+#define TCRV_GEMM_Q8_PIPE 0
+#endif
+constexpr bool kGemmQ8Pipe = TCRV_GEMM_Q8_PIPE;
+// the step after which a wave stores its staged part of the next chunk (a
+// sweep over steps 1, 3, 5 and 7 measured within run-to-run noise)
+constexpr int kGemmStageStep = 2 * kWKB - 1;
+
 template <bool kQ4>
 __global__ __launch_bounds__(kOcThreads, 1) void gemm_wide(
     size_t nb, float *s, const uint8_t *vx, const uint8_t *vy, size_t by, size_t nr,
     size_t nc, size_t bx, size_t bs) {
   __shared__ __align__(16) int8_t q[2][kWStage];
-  __shared__ __align__(16) float dsc[2][kWKB][kWRows];  // [stage][block][row]
+  // scales: f32 [stage][block][row] for the Q4_0 fold, fp16 bit patterns with
+  // 32 zero rows for the Q8_0 fold (only the one the instantiation uses is
+  // allocated)
+  __shared__ __align__(16) float dsc[2][kWKB][kWRows];
+  __shared__ __align__(16) uint16_t dsh[2][kWKB][kHRow];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -555,13 +581,24 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_wide(
     active = stager && 2 * sm < nbc;
     two = 2 * sm + 1 < nbc;
   };
+  auto stage = [&](int st, bool two) {
+    if constexpr (kQ4)
+      store_task(pr, two, q4_task, q[st] + sr * kWQRow + 64 * sm, &dsc[st][2 * sm][sr],
+                 &dsc[st][2 * sm + 1][sr]);
+    else
+      store_pair_h(pr, two, q[st] + sr * kWQRow + 64 * sm, &dsh[st][2 * sm][sr],
+                   &dsh[st][2 * sm + 1][sr]);
+  };
+  if constexpr (!kQ4) {
+    if (tid < 2 * kWKB * 32)  // the zero rows of both stages
+      dsh[tid >> 7][(tid >> 5) & 3][kWRows + (tid & 31)] = 0;
+  }
   bool act, two;
   chunk_task(0, act, two);
   if (act)
     load_task(pr, sbase + 2 * sm * sblk, two, q4_task);
   if (act)
-    store_task(pr, two, q4_task, q[0] + sr * kWQRow + 64 * sm, &dsc[0][2 * sm][sr],
-               &dsc[0][2 * sm + 1][sr]);
+    stage(0, two);
   __syncthreads();
 
   // this lane's operand addresses in stage 0 for the wave's first tile (the
@@ -572,6 +609,9 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_wide(
   const float *syh0 = &dsc[0][h][kWBM + wn * 32 + li];
   const float *syc0 = &dsc[0][0][kWBM + wn * 32 + li];
   constexpr int kDscStage = kWKB * kWRows;
+  const uint16_t *hx0 = h ? &dsh[0][0][kWRows + li] : &dsh[0][0][wm * 64 + li];
+  const uint16_t *hx1 = h ? &dsh[0][0][kWRows + li] : &dsh[0][0][wm * 64 + 32 + li];
+  const uint16_t *hy = h ? &dsh[0][0][kWRows + li] : &dsh[0][0][kWBM + wn * 32 + li];
 
   const size_t nfull = nb / kWKB;
   for (size_t c = 0; c < nfull; ++c) {
@@ -582,39 +622,55 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_wide(
       if (act1)
         load_task(pr, sbase + ((c + 1) * kWKB + 2 * sm) * sblk, two1, q4_task);
     }
+    if constexpr (kQ4) {
 #pragma unroll
-    for (int b = 0; b < kWKB; b += 2) {
+      for (int b = 0; b < kWKB; b += 2) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        fold_pair<kQ4, true, kWRows>(acc[i], qa0 + i * 32 * kWQRow + st * kWStage,
-                                     qb0 + st * kWStage, sxh0 + i * 32 + st * kDscStage,
-                                     syh0 + st * kDscStage, syc0 + st * kDscStage, b);
+        for (int i = 0; i < 2; ++i) {
+          fold_pair<kQ4, true, kWRows>(acc[i], qa0 + i * 32 * kWQRow + st * kWStage,
+                                       qb0 + st * kWStage, sxh0 + i * 32 + st * kDscStage,
+                                       syh0 + st * kDscStage, syc0 + st * kDscStage, b);
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          asm volatile("" : "+v"(acc[i][e]));
-        __builtin_amdgcn_sched_barrier(0);
+          for (int e = 0; e < 16; ++e)
+            asm volatile("" : "+v"(acc[i][e]));
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
+    } else {
+      fold_chunk_q8<kGemmQ8Pipe, kWKB, kQK, 32 * kWQRow, kHRow>(
+          acc, qa0 + st * kWStage, qb0 + st * kWStage, hx0 + st * kHStage, hx1 + st * kHStage,
+          hy + st * kHStage, [&](int step) {
+            if (step == kGemmStageStep && act1)
+              stage(st ^ 1, two1);
+          });
     }
-    if (act1)
-      store_task(pr, two1, q4_task, q[st ^ 1] + sr * kWQRow + 64 * sm,
-                 &dsc[st ^ 1][2 * sm][sr], &dsc[st ^ 1][2 * sm + 1][sr]);
+    if constexpr (kQ4) {
+      if (act1)
+        stage(st ^ 1, two1);
+    }
     __syncthreads();
   }
   const int nbc = static_cast<int>(nb - nfull * kWKB);
   if (nbc > 0) {
     const int st = static_cast<int>(nfull & 1);
+    if constexpr (kQ4) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int8_t *qa = qa0 + i * 32 * kWQRow + st * kWStage;
-      const int8_t *qb = qb0 + st * kWStage;
-      const float *sxh = sxh0 + i * 32 + st * kDscStage;
-      const float *syh = syh0 + st * kDscStage;
-      const float *syc = syc0 + st * kDscStage;
-      int b = 0;
-      for (; b + 1 < nbc; b += 2)
-        fold_pair<kQ4, true, kWRows>(acc[i], qa, qb, sxh, syh, syc, b);
-      if (b < nbc)
-        fold_pair<kQ4, false, kWRows>(acc[i], qa, qb, sxh, syh, syc, b);
+      for (int i = 0; i < 2; ++i) {
+        const int8_t *qa = qa0 + i * 32 * kWQRow + st * kWStage;
+        const int8_t *qb = qb0 + st * kWStage;
+        const float *sxh = sxh0 + i * 32 + st * kDscStage;
+        const float *syh = syh0 + st * kDscStage;
+        const float *syc = syc0 + st * kDscStage;
+        int b = 0;
+        for (; b + 1 < nbc; b += 2)
+          fold_pair<kQ4, true, kWRows>(acc[i], qa, qb, sxh, syh, syc, b);
+        if (b < nbc)
+          fold_pair<kQ4, false, kWRows>(acc[i], qa, qb, sxh, syh, syc, b);
+      }
+    } else {
+      fold_tail_q8<kQK, 32 * kWQRow, kHRow>(acc, qa0 + st * kWStage, qb0 + st * kWStage,
+                                            hx0 + st * kHStage, hx1 + st * kHStage,
+                                            hy + st * kHStage, nbc);
     }
   }
 
@@ -669,8 +725,8 @@ __device__ __forceinline__ void rg_load(RgRegs &p, const uint8_t *quant, const u
 }
 
 // -> rows 16g + 0..15, quants 32j + 4q.. (low nibbles) and 32j + 16 + 4q..
-// (high nibbles) as int8, scales dsc_j[16g + 4q .. +3]
-__device__ __forceinline__ void rg_store_w(const RgRegs &p, int8_t *stage, float *dsc_j, int g,
+// (high nibbles) as int8, fp16 scales dsh_j[16g + 4q .. +3]
+__device__ __forceinline__ void rg_store_w(const RgRegs &p, int8_t *stage, uint16_t *dsh_j, int g,
                                            int j, int q) {
 #pragma unroll
   for (int rq = 0; rq < 4; ++rq) {
@@ -685,13 +741,11 @@ __device__ __forceinline__ void rg_store_w(const RgRegs &p, int8_t *stage, float
       *reinterpret_cast<uint32_t *>(dst + 16) = nibbles_to_i8x4(raw >> 4);
     }
   }
-  *reinterpret_cast<float4 *>(dsc_j + 16 * g + 4 * q) =
-      make_float4(fp16_bits_to_f32(p.r[16] & 0xffffu), fp16_bits_to_f32(p.r[16] >> 16),
-                  fp16_bits_to_f32(p.r[17] & 0xffffu), fp16_bits_to_f32(p.r[17] >> 16));
+  *reinterpret_cast<uint2 *>(dsh_j + 16 * g + 4 * q) = make_uint2(p.r[16], p.r[17]);
 }
 
-// -> rows kWBM + 4t + 0..3, quants 32j + 16hf + 0..15, scales dsc_j[kWBM + 4t ..]
-__device__ __forceinline__ void rg_store_a(const RgRegs &p, int8_t *stage, float *dsc_j, int t,
+// -> rows kWBM + 4t + 0..3, quants 32j + 16hf + 0..15, fp16 scales dsh_j[kWBM + 4t ..]
+__device__ __forceinline__ void rg_store_a(const RgRegs &p, int8_t *stage, uint16_t *dsh_j, int t,
                                            int j, int hf) {
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
@@ -703,16 +757,14 @@ __device__ __forceinline__ void rg_store_a(const RgRegs &p, int8_t *stage, float
                                     4 * m) = rows[c];
   }
   if (hf == 0)
-    *reinterpret_cast<float4 *>(dsc_j + kWBM + 4 * t) =
-        make_float4(fp16_bits_to_f32(p.r[16] & 0xffffu), fp16_bits_to_f32(p.r[16] >> 16),
-                    fp16_bits_to_f32(p.r[17] & 0xffffu), fp16_bits_to_f32(p.r[17] >> 16));
+    *reinterpret_cast<uint2 *>(dsh_j + kWBM + 4 * t) = make_uint2(p.r[16], p.r[17]);
 }
 
 __global__ __launch_bounds__(kOcThreads, 1) void gemm_repack_q4_0(
     size_t nb, float *s, const uint8_t *vx, const uint8_t *vy, size_t ngw, size_t nga,
     size_t bs, bool vec_out) {
   __shared__ __align__(16) int8_t q[2][kWStage];
-  __shared__ __align__(16) float dsc[2][kWKB][kWRows];  // [stage][block][row]
+  __shared__ __align__(16) uint16_t dsh[2][kWKB][kHRow];  // fp16 scales + 32 zero rows
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -751,20 +803,22 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_repack_q4_0(
 
   const size_t nchunks = (nb + kWKB - 1) / kWKB;
   RgRegs pr;
+  if (tid < 2 * kWKB * 32)  // the zero rows of both stages
+    dsh[tid >> 7][(tid >> 5) & 3][kWRows + (tid & 31)] = 0;
   if ((wtask || atask) && sj < static_cast<int>(min(static_cast<size_t>(kWKB), nb))) {
     rg_load(pr, squant, sscale);
     if (wtask)
-      rg_store_w(pr, q[0], dsc[0][sj], sg, sj, sq);
+      rg_store_w(pr, q[0], dsh[0][sj], sg, sj, sq);
     else
-      rg_store_a(pr, q[0], dsc[0][sj], sg, sj, sq);
+      rg_store_a(pr, q[0], dsh[0][sj], sg, sj, sq);
   }
   __syncthreads();
 
   const int8_t *qa0 = q[0] + (wm * 64 + li) * kWQRow + 16 * h;
   const int8_t *qb0 = q[0] + (kWBM + wn * 32 + li) * kWQRow + 16 * h;
-  const float *sxh0 = &dsc[0][h][wm * 64 + li];
-  const float *syh0 = &dsc[0][h][kWBM + wn * 32 + li];
-  constexpr int kDscStage = kWKB * kWRows;
+  const uint16_t *hx0 = h ? &dsh[0][0][kWRows + li] : &dsh[0][0][wm * 64 + li];
+  const uint16_t *hx1 = h ? &dsh[0][0][kWRows + li] : &dsh[0][0][wm * 64 + 32 + li];
+  const uint16_t *hy = h ? &dsh[0][0][kWRows + li] : &dsh[0][0][kWBM + wn * 32 + li];
 
   const size_t nfull = nb / kWKB;
   for (size_t c = 0; c < nfull; ++c) {
@@ -773,42 +827,24 @@ __global__ __launch_bounds__(kOcThreads, 1) void gemm_repack_q4_0(
                       static_cast<size_t>(sj) < min(static_cast<size_t>(kWKB), nb - (c + 1) * kWKB);
     if (act1)
       rg_load(pr, squant + (c + 1) * cstride, sscale + (c + 1) * cstride);
-#pragma unroll
-    for (int b = 0; b < kWKB; b += 2) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        fold_pair<false, true, kWRows>(acc[i], qa0 + i * 32 * kWQRow + st * kWStage,
-                                       qb0 + st * kWStage, sxh0 + i * 32 + st * kDscStage,
-                                       syh0 + st * kDscStage, nullptr, b);
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          asm volatile("" : "+v"(acc[i][e]));
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    if (act1) {
-      if (wtask)
-        rg_store_w(pr, q[st ^ 1], dsc[st ^ 1][sj], sg, sj, sq);
-      else
-        rg_store_a(pr, q[st ^ 1], dsc[st ^ 1][sj], sg, sj, sq);
-    }
+    fold_chunk_q8<kGemmQ8Pipe, kWKB, kQK, 32 * kWQRow, kHRow>(
+        acc, qa0 + st * kWStage, qb0 + st * kWStage, hx0 + st * kHStage, hx1 + st * kHStage,
+        hy + st * kHStage, [&](int step) {
+          if (step == kGemmStageStep && act1) {
+            if (wtask)
+              rg_store_w(pr, q[st ^ 1], dsh[st ^ 1][sj], sg, sj, sq);
+            else
+              rg_store_a(pr, q[st ^ 1], dsh[st ^ 1][sj], sg, sj, sq);
+          }
+        });
     __syncthreads();
   }
   const int nbc = static_cast<int>(nb - nfull * kWKB);
   if (nbc > 0) {
     const int st = static_cast<int>(nfull & 1);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int8_t *qa = qa0 + i * 32 * kWQRow + st * kWStage;
-      const int8_t *qb = qb0 + st * kWStage;
-      const float *sxh = sxh0 + i * 32 + st * kDscStage;
-      const float *syh = syh0 + st * kDscStage;
-      int b = 0;
-      for (; b + 1 < nbc; b += 2)
-        fold_pair<false, true, kWRows>(acc[i], qa, qb, sxh, syh, nullptr, b);
-      if (b < nbc)
-        fold_pair<false, false, kWRows>(acc[i], qa, qb, sxh, syh, nullptr, b);
-    }
+    fold_tail_q8<kQK, 32 * kWQRow, kHRow>(acc, qa0 + st * kWStage, qb0 + st * kWStage,
+                                          hx0 + st * kHStage, hx1 + st * kHStage,
+                                          hy + st * kHStage, nbc);
   }
 
   // a lane holds 4 consecutive weight rows per group of 4 elements: one

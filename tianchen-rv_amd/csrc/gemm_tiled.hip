@@ -1,0 +1,365 @@
+// gemm_tiled.hip -- a9 Q8_0 x Q8_0 GEMM over operands in the GEMM-tile layout,
+// staged into LDS by DMA (global_load_lds_dwordx4): no staging registers and
+// no staging VALU, so every VGPR and VALU cycle goes to the fold.
+//
+// GEMM-tile layout of a Q8_0 matrix of nrows rows x nb blocks (the same bytes
+// as the plain rows, regrouped): rows in groups of 64; for group g and block b
+// one 2176-byte record at (g*nb + b)*2176:
+//   bytes    0..1023  quants 0..15 of the block for rows 64g+0..63, 16 B a row
+//   bytes 1024..2047  quants 16..31, the same way
+//   bytes 2048..2175  the 64 fp16 scales
+// Rows past nrows in the last group are zero.  A record's halves are the
+// operand of one v_mfma_i32_32x32x32_i8 lane (16 quants), already 16-byte
+// aligned, so a wave moves one half of 64 rows with one 1 KB DMA instruction.
+//
+// Semantics are those of tcrv_hip_q8_0_q8_0_gemm (gemm.hip): every output is
+// the a5 block dot, folded in ascending block order (mfma_fold.h).
+#include "mfma_fold.h"
+
+namespace tcrv {
+
+constexpr int kTG = 64;                        // rows per tile group
+constexpr int kTRec = 2 * kTG * 16 + kTG * 2;  // 2176 bytes per (group, block) record
+constexpr int kDBM = 256, kDBN = 128, kDKB = 4;   // work-group tile, blocks per K chunk
+constexpr int kDRows = kDBM + kDBN;               // 384 staged rows
+constexpr int kDHalf = kDRows * 16;               // 6144: one half of one block, all rows
+constexpr int kDBlock = 2 * kDHalf;               // 12288: both halves of one block
+constexpr int kDStage = kDKB * kDBlock;           // 49152 quant bytes per stage
+constexpr int kDHRow = kDRows + 32;               // fp16 scales per block row (+32 zero rows)
+constexpr int kDThreads = 1024;
+constexpr int kDQuantDma = kDKB * 2 * (kDRows / kTG);  // 48 quant DMA instructions per chunk
+constexpr int kDDma = kDQuantDma + kDKB;               // + one scale instruction per block
+constexpr int kDStages = 3;  // chunks c+1 and c+2 in flight while chunk c is folded
+
+// ---------------------------------------------------------------- pack ---
+// One wave per (group, block) record, lane r = row 64g + r.  kAligned: the
+// rows are 4-byte aligned (dword loads, realigned with v_alignbyte for even
+// blocks); otherwise 16-bit loads.
+template <bool kAligned>
+__global__ __launch_bounds__(256) void pack_gemm_tiles(size_t nrows, size_t nb,
+                                                       const uint8_t *src, size_t bx,
+                                                       uint8_t *dst, size_t nrec) {
+  const size_t t = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  const size_t rec = t >> 6;
+  if (rec >= nrec)
+    return;
+  const int r = static_cast<int>(t & 63);
+  const size_t g = rec / nb, b = rec - g * nb;
+  const size_t row = g * kTG + r;
+  uint32_t q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  uint32_t d = 0;
+  if (row < nrows) {
+    const uint8_t *blk = src + row * bx + b * kQ8Bytes;
+    if constexpr (kAligned) {
+      if ((b & 1) == 0) {  // block 4-byte aligned: scale, then quants at +2
+        const uint32_t *w = reinterpret_cast<const uint32_t *>(blk);
+        uint32_t v[9];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          v[k] = w[k];
+        v[8] = *reinterpret_cast<const uint16_t *>(blk + 32);
+        d = v[0] & 0xffffu;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          q[k] = funnel16(v[k], v[k + 1]);
+      } else {  // quants 4-byte aligned, the scale in the dword before them
+        const uint32_t *w = reinterpret_cast<const uint32_t *>(blk - 2);
+        d = w[0] >> 16;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          q[k] = w[k + 1];
+      }
+    } else {
+      const uint16_t *h = reinterpret_cast<const uint16_t *>(blk);
+      d = h[0];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        q[k] = static_cast<uint32_t>(h[1 + 2 * k]) | (static_cast<uint32_t>(h[2 + 2 * k]) << 16);
+    }
+  }
+  uint8_t *o = dst + rec * kTRec;
+  reinterpret_cast<uint4 *>(o)[r] = make_uint4(q[0], q[1], q[2], q[3]);
+  reinterpret_cast<uint4 *>(o + 1024)[r] = make_uint4(q[4], q[5], q[6], q[7]);
+  reinterpret_cast<uint16_t *>(o + 2048)[r] = static_cast<uint16_t>(d);
+}
+
+// ---------------------------------------------------------------- GEMM ---
+typedef __attribute__((address_space(3))) void lds_void;
+
+// The DMA of one K chunk is kDDma wave instructions: j < 48 moves half h of
+// block b of one 64-row group (A groups 0-3, B groups 4-5) -- 1 KB, lane l its
+// 16 bytes of row l; j >= 48 the scales of block j-48 of all six groups (48
+// lanes, 16 bytes each).  Wave w issues j = w, w+16, w+32, w+48: its "slots",
+// whose source addresses (chunk 0) and LDS offsets (stage 0) are computed once;
+// chunk c adds c*kDKB records, stage st a fixed offset.  Groups past the
+// operand's last one re-read the last (their outputs are not stored).
+struct DmaSlots {
+  const uint8_t *src[4];  // this lane's 16 source bytes, chunk 0
+  lds_void *dst[4];       // the slot's LDS destination, stage 0 (wave-uniform)
+  int stage_bytes[4];     // LDS bytes from stage 0 to stage 1
+  int blk[4];             // block of the chunk the slot moves
+  bool on[4];             // this lane takes part (scale slots use 48 lanes)
+};
+
+__device__ __forceinline__ void dma_slots(DmaSlots &d, int8_t *qs, uint16_t *dsh,
+                                          const uint8_t *tx, const uint8_t *ty, size_t gx0,
+                                          size_t ngx, size_t gy0, size_t ngy, size_t nb,
+                                          int wave, int lane) {
+  auto record = [&](int g, int b) {
+    return g < 4 ? tx + (min(gx0 + g, ngx - 1) * nb + b) * kTRec
+                 : ty + (min(gy0 + (g - 4), ngy - 1) * nb + b) * kTRec;
+  };
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int j = min(wave + 16 * k, kDDma - 1);  // slots past kDDma are never issued
+    if (j < kDQuantDma) {
+      const int b = j / 12, h = (j / 6) & 1, g = j % 6;
+      d.src[k] = record(g, b) + h * 1024 + lane * 16;
+      // a generic pointer into LDS -> the LDS address space (what the DMA takes)
+      d.dst[k] = (lds_void *)(qs + b * kDBlock + h * kDHalf + g * kTG * 16);
+      d.stage_bytes[k] = kDStage;
+      d.blk[k] = b;
+      d.on[k] = true;
+    } else {
+      const int b = j - kDQuantDma;
+      d.src[k] = record(min(lane >> 3, 5), b) + 2048 + (lane & 7) * 16;
+      d.dst[k] = (lds_void *)(dsh + b * kDHRow);
+      d.stage_bytes[k] = kDKB * kDHRow * 2;
+      d.blk[k] = b;
+      d.on[k] = lane < 48;
+    }
+  }
+}
+
+// Issues this wave's DMA of K chunk c (nbc blocks) into stage st; returns
+// how many DMA instructions it issued.
+__device__ __forceinline__ int dma_chunk(const DmaSlots &d, size_t c, int nbc, int st,
+                                         int wave) {
+  const size_t coff = c * kDKB * kTRec;
+  int issued = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    if (wave + 16 * k < kDDma && d.blk[k] < nbc) {
+      if (d.on[k])
+        __builtin_amdgcn_global_load_lds(d.src[k] + coff,
+                                         (lds_void *)((char __attribute__((address_space(3))) *)
+                                                          d.dst[k] + st * d.stage_bytes[k]),
+                                         16, 0, 0);
+      ++issued;
+    }
+  }
+  return issued;
+}
+
+// Waits until at most `pending` of this wave's memory loads are outstanding
+// (the DMA of the newest chunk; every older chunk has landed in LDS) and all
+// its LDS reads are done, then meets the other waves at a barrier: after it,
+// every wave's DMA of the older chunks is visible and no wave still reads the
+// stage the next DMA overwrites.  s_waitcnt takes an immediate, hence the
+// switch (gfx9 encoding: vmcnt in bits 3:0, expcnt 6:4 = 7 (no wait), lgkmcnt
+// 11:8 = 0).
+__device__ __forceinline__ void wait_dma_barrier(int pending) {
+  switch (__builtin_amdgcn_readfirstlane(pending)) {  // the same in every lane
+  case 0: __builtin_amdgcn_s_waitcnt(0x070); break;
+  case 1: __builtin_amdgcn_s_waitcnt(0x071); break;
+  case 2: __builtin_amdgcn_s_waitcnt(0x072); break;
+  case 3: __builtin_amdgcn_s_waitcnt(0x073); break;
+  default: __builtin_amdgcn_s_waitcnt(0x074); break;
+  }
+  __builtin_amdgcn_s_barrier();
+}
+
+// Work-group: 256 weight rows x 128 tokens, 16 waves, each wave two 32x32
+// tiles stacked in M (64 weight rows x 32 tokens); K chunks of 4 blocks in
+// three LDS stages: the DMA of chunks c+1 and c+2 is in flight while chunk c
+// is folded, and the barrier after chunk c waits only for chunk c+1's.
+template <bool kPipe>
+__global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q8(size_t nb, float *s,
+                                                              const uint8_t *tx,
+                                                              const uint8_t *ty, size_t nr,
+                                                              size_t nc, size_t bs) {
+  __shared__ __align__(16) int8_t qs[kDStages * kDStage];
+  __shared__ __align__(16) uint16_t dsh[kDStages * kDKB * kDHRow];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wm = wave >> 2, wn = wave & 3;  // 64 weight rows x 32 tokens per wave
+  const int li = lane & 31, h = lane >> 5;
+  const unsigned tiles_m = static_cast<unsigned>((nr + kDBM - 1) / kDBM);
+  const unsigned tiles_n = static_cast<unsigned>((nc + kDBN - 1) / kDBN);
+  unsigned tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const size_t m0 = static_cast<size_t>(tm) * kDBM;
+  const size_t n0 = static_cast<size_t>(tn) * kDBN;
+  const size_t ngx = (nr + kTG - 1) / kTG, ngy = (nc + kTG - 1) / kTG;
+  const size_t gx0 = m0 / kTG, gy0 = n0 / kTG;
+
+  float acc[2][16];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      acc[i][e] = 0.0f;
+
+  if (tid < kDStages * kDKB * 32)  // the zero rows of every stage
+    dsh[(tid >> 5) * kDHRow + kDRows + (tid & 31)] = 0;
+  const size_t nchunks = (nb + kDKB - 1) / kDKB;
+  const size_t nfull = nb / kDKB;
+  auto blocks_of = [&](size_t c) {
+    return static_cast<int>(min(static_cast<size_t>(kDKB), nb - c * kDKB));
+  };
+  DmaSlots slots;
+  dma_slots(slots, qs, dsh, tx, ty, gx0, ngx, gy0, ngy, nb, wave, lane);
+  dma_chunk(slots, 0, blocks_of(0), 0, wave);
+  int pending = nchunks > 1 ? dma_chunk(slots, 1, blocks_of(1), 1, wave) : 0;
+  wait_dma_barrier(pending);  // chunk 0 is in LDS, the zero rows written
+
+  // this lane's operands in stage 0, block 0, for the wave's first tile
+  const int8_t *qa0 = qs + (h * kDRows + wm * 64 + li) * 16;
+  const int8_t *qb0 = qs + (h * kDRows + kDBM + wn * 32 + li) * 16;
+  const uint16_t *hx0 = dsh + (h ? kDRows + li : wm * 64 + li);
+  const uint16_t *hx1 = dsh + (h ? kDRows + li : wm * 64 + 32 + li);
+  const uint16_t *hy = dsh + (h ? kDRows + li : kDBM + wn * 32 + li);
+  constexpr int kHStage = kDKB * kDHRow;
+
+  int st = 0;  // stage of chunk c
+  for (size_t c = 0; c < nfull; ++c) {
+    const int st2 = st == 0 ? 2 : st - 1;  // (c + 2) % 3
+    pending = c + 2 < nchunks ? dma_chunk(slots, c + 2, blocks_of(c + 2), st2, wave) : 0;
+    fold_chunk_q8<kPipe, kDKB, kDBlock, 32 * 16, kDHRow>(
+        acc, qa0 + st * kDStage, qb0 + st * kDStage, hx0 + st * kHStage, hx1 + st * kHStage,
+        hy + st * kHStage, [](int) {});
+    wait_dma_barrier(pending);  // chunk c+1 is in LDS
+    st = st == 2 ? 0 : st + 1;
+  }
+  const int nbc = static_cast<int>(nb - nfull * kDKB);
+  if (nbc > 0)
+    fold_tail_q8<kDBlock, 32 * 16, kDHRow>(acc, qa0 + st * kDStage, qb0 + st * kDStage,
+                                           hx0 + st * kHStage, hx1 + st * kHStage,
+                                           hy + st * kHStage, nbc);
+
+  const size_t col = n0 + wn * 32 + li;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const size_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (row < nr && col < nc)
+        s[row * bs + col] = acc[i][e];
+    }
+}
+
+}  // namespace tcrv
+
+namespace {
+
+constexpr bool kTiledPipe = true;
+
+size_t tile_bytes(size_t nrows, size_t nb) {
+  return (nrows + tcrv::kTG - 1) / tcrv::kTG * nb * tcrv::kTRec;
+}
+
+int pack_tiles(size_t nrows, size_t nb, const uint8_t *src, size_t bx, uint8_t *dst,
+               hipStream_t st) {
+  using namespace tcrv_host;
+  const size_t nrec = (nrows + tcrv::kTG - 1) / tcrv::kTG * nb;
+  const size_t grid = (nrec * 64 + 255) / 256;
+  if (grid > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  if (aligned4(src) && (nrows == 1 || bx % 4 == 0))
+    tcrv::pack_gemm_tiles<true><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(
+        nrows, nb, src, bx, dst, nrec);
+  else
+    tcrv::pack_gemm_tiles<false><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(
+        nrows, nb, src, bx, dst, nrec);
+  return launch_status();
+}
+
+int gemm_tiles(size_t nb, float *s, const uint8_t *tx, const uint8_t *ty, size_t nr, size_t nc,
+               size_t bs, hipStream_t st) {
+  using namespace tcrv_host;
+  const size_t tiles = ((nr + tcrv::kDBM - 1) / tcrv::kDBM) * ((nc + tcrv::kDBN - 1) / tcrv::kDBN);
+  if (tiles > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  tcrv::gemm_tiles_q8<kTiledPipe><<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kDThreads), 0,
+                                    st>>>(nb, s, tx, ty, nr, nc, bs);
+  return launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t tcrv_hip_gemm_tiles_bytes(size_t nrows, size_t nb) { return tile_bytes(nrows, nb); }
+
+int tcrv_hip_pack_q8_0_to_gemm_tiles(size_t nrows, size_t nb, const uint8_t *src, size_t bx,
+                                     uint8_t *dst, void *stream) {
+  using namespace tcrv_host;
+  if (nrows == 0 || nb == 0)
+    return TCRV_HIP_OK;
+  if (!src || !dst)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned2(src) || (nrows > 1 && (bx & 1u)) || !aligned16(dst))
+    return TCRV_HIP_ERR_MISALIGNED;
+  if (nrows > 1 && bx < nb * tcrv::kQ8Bytes)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  return pack_tiles(nrows, nb, src, bx, dst, as_stream(stream));
+}
+
+int tcrv_hip_q8_0_q8_0_gemm_tiles(size_t n, float *s, const uint8_t *tx, const uint8_t *ty,
+                                  size_t nr, size_t nc, size_t bs, void *stream) {
+  using namespace tcrv_host;
+  const size_t nb = n / tcrv::kQK;
+  if (nr == 0 || nc == 0)
+    return TCRV_HIP_OK;
+  if (nr > 1 && bs < nc)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  if (nb == 0)
+    return zero_outputs(s, nr * nc, bs, nc, stream);
+  if (!s || !tx || !ty)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned16(tx) || !aligned16(ty))
+    return TCRV_HIP_ERR_MISALIGNED;
+  return gemm_tiles(nb, s, tx, ty, nr, nc, bs, as_stream(stream));
+}
+
+size_t tcrv_hip_q8_0_q8_0_gemm_workspace_bytes(size_t n, size_t nr, size_t nc) {
+  const size_t nb = n / tcrv::kQK;
+  return tile_bytes(nr, nb) + tile_bytes(nc, nb);
+}
+
+int tcrv_hip_q8_0_q8_0_gemm_ws(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
+                               size_t by, size_t nr, size_t nc, size_t bx, size_t bs,
+                               void *workspace, size_t workspace_bytes, void *stream) {
+  using namespace tcrv_host;
+  const size_t nb = n / tcrv::kQK;
+  // shapes the tiled kernel does not serve run as tcrv_hip_q8_0_q8_0_gemm,
+  // without the workspace: fewer weight rows than one 256-row tile, a single
+  // token (decode), or no blocks
+  if (nr < static_cast<size_t>(tcrv::kDBM) || nc < 2 || nb == 0)
+    return tcrv_hip_q8_0_q8_0_gemm(n, s, vx, vy, by, nr, nc, bx, bs, stream);
+  if (bs < nc)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  if (!s || !vx || !vy || !workspace)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned2(vx) || !aligned2(vy) || (bx & 1u) || (by & 1u) || !aligned16(workspace))
+    return TCRV_HIP_ERR_MISALIGNED;
+  const size_t rowbytes = nb * tcrv::kQ8Bytes;
+  if (bx < rowbytes || by < rowbytes)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  const size_t tx_bytes = tile_bytes(nr, nb), ty_bytes = tile_bytes(nc, nb);
+  if (workspace_bytes < tx_bytes + ty_bytes)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  uint8_t *tx = static_cast<uint8_t *>(workspace);
+  uint8_t *ty = tx + tx_bytes;  // tx_bytes is a multiple of 2176 = 16 * 136
+  hipStream_t st = as_stream(stream);
+  int rc = pack_tiles(nr, nb, vx, bx, tx, st);
+  if (rc != TCRV_HIP_OK)
+    return rc;
+  rc = pack_tiles(nc, nb, vy, by, ty, st);
+  if (rc != TCRV_HIP_OK)
+    return rc;
+  return gemm_tiles(nb, s, tx, ty, nr, nc, bs, st);
+}
+
+}  // extern "C"

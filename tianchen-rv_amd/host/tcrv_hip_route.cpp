@@ -4,8 +4,11 @@
 // every launch goes through the C-ABI of libtcrv_hip.
 #include "tcrv_hip_route.h"
 
+#include <algorithm>
+#include <cstdio>
 #include <cstring>
 #include <iterator>
+#include <string>
 
 namespace tianchenrv::plugin::hip {
 namespace {
@@ -75,6 +78,20 @@ HipContractionSelection selectHipContractionAlgorithm(QuantType weight, MRegime 
 
 MRegime deriveMRegime(size_t nc) { return nc <= 1 ? MRegime::Decode : MRegime::Prefill; }
 
+HipBinarySelection selectHipBinary(int kind, int elem) {
+  // kind: the verifier's set, "add" | "sub" | "mul"
+  // (RVVDialectArithmeticOps.cpp:58-61), the intrinsic family chosen by
+  // binaryMnemonic (RVVToEmitC.cpp:4976-4993); elem: every element type the
+  // kernel is built for (signed and unsigned integers of 8-64 bits wrap alike,
+  // f32/f64 are single IEEE operations)
+  if (kind < TCRV_HIP_BINARY_ADD || kind > TCRV_HIP_BINARY_MUL)
+    return {nullptr, "hip-decline-binary-kind-outside-add-sub-mul"};
+  if (elem < TCRV_HIP_ELEM_I8 || elem > TCRV_HIP_ELEM_F64)
+    return {nullptr, "hip-decline-binary-element-type"};
+  const bool fp = elem == TCRV_HIP_ELEM_F32 || elem == TCRV_HIP_ELEM_F64;
+  return {"tcrv_hip_binary", fp ? "hip-binary-float-ieee" : "hip-binary-integer-wrapping"};
+}
+
 namespace {
 
 struct AbiParam {
@@ -92,7 +109,8 @@ struct HipKernelRoute {
 
 // Parameter names, C types and roles as the reference's fixtures declare them
 // (test/Conversion/RVV/...):
-//   add:            rvv-to-emitc-add-cpp-golden.mlir (i32 there; f32 entry here)
+//   binary:         rvv-to-emitc-add-cpp-golden.mlir:15-18 (lhs, rhs, out, n)
+//   integer core:   rvv-to-emitc-packed-i4-offset-binary-x-i8-product-reduce.mlir:22-27
 //   q8_0 block dot: rvv-to-emitc-q8-0-q8-0-block-dot.mlir:16-19
 //   q4_0 block dot: rvv-to-emitc-q4-0-q8-0-block-dot.mlir:24-31
 //   q4_0 gemm:      rvv-to-emitc-q4-0-q8-0-gemm.mlir:23-31
@@ -103,25 +121,32 @@ struct HipKernelRoute {
 //   pack:           rvv-to-emitc-pack-q4-0-to-q4-0x16.mlir:19-21
 //   quantize:       rvv-to-emitc-ggml-quantize-row-q8-0.mlir
 // The Q8_0 GEMM has no reference op; it takes the q4_0 GEMM's ABI with Q8_0
-// weights.  A row is found by its exact op identity: the op name, and for
-// tcrv_rvv.binary also its kind and element type (".add.f32").
+// weights.  A row is found by its exact op identity (the op name); nothing is
+// read from a name beyond that.
 constexpr const char *kN = "runtime-element-count";
 constexpr const char *kOut = "output-buffer";
 constexpr const char *kLhs = "lhs-input-buffer";
 constexpr const char *kRhs = "rhs-input-buffer";
-// Not a runtime-ABI value in the reference: an op attribute the emitted C bakes
-// in (q4_0_q8_0_gemm_tile's activation_cols), passed at run time here.
+// Not runtime-ABI values in the reference: an op attribute the emitted C bakes
+// in (q4_0_q8_0_gemm_tile's activation_cols, tcrv_rvv.binary's kind) and the
+// element type of the op's vectors, passed at run time here.
 constexpr const char *kOpAttr = "op-attribute";
+constexpr const char *kElemType = "element-type";
 
 const HipKernelRoute kHipKernelRoutes[] = {
-    {"tcrv_rvv.binary.add.f32", "tcrv_hip_add_f32",
-     {{"lhs", "const float *", kLhs}, {"rhs", "const float *", kRhs}, {"out", "float *", kOut},
-      {"n", "size_t", kN}},
-     4},
-    {"tcrv_rvv.binary.add.i32", "tcrv_hip_add_i32",
-     {{"lhs", "const int32_t *", kLhs}, {"rhs", "const int32_t *", kRhs},
+    // tcrv_rvv.binary: the op's kind attribute and element type are typed
+    // facts (tcrv_hip_route_binary validates them); the entry takes them as its
+    // first two arguments, then the reference's (lhs, rhs, out, n)
+    {"tcrv_rvv.binary", "tcrv_hip_binary",
+     {{"kind", "int", kOpAttr}, {"elem", "int", kElemType}, {"lhs", "const void *", kLhs},
+      {"rhs", "const void *", kRhs}, {"out", "void *", kOut}, {"n", "size_t", kN}},
+     6},
+    {"tcrv_rvv.packed_i4_offset_binary_x_i8_product",
+     "tcrv_hip_packed_i4_offset_binary_x_i8_product_reduce",
+     {{"w", "const int8_t *", kLhs}, {"qlo", "const int8_t *", kRhs},
+      {"qhi", "const int8_t *", kRhs}, {"acc", "const int32_t *", "accumulator-input-buffer"},
       {"out", "int32_t *", kOut}, {"n", "size_t", kN}},
-     4},
+     6},
     {"tcrv_rvv.q4_0_q8_0_block_dot", "tcrv_hip_q4_0_q8_0_block_dot",
      {{"n", "size_t", kN}, {"s", "float *", kOut}, {"bs", "size_t", "output-stride"},
       {"vx", "const uint8_t *", kLhs}, {"bx", "size_t", "lhs-input-stride"},
@@ -171,6 +196,94 @@ const HipKernelRoute kHipKernelRoutes[] = {
 };
 constexpr size_t kNumRoutes = std::size(kHipKernelRoutes);
 
+// The C element type a tcrv_rvv.binary of element `elem` reads and writes.
+const char *binaryCType(int elem) {
+  switch (elem) {
+  case TCRV_HIP_ELEM_I8: return "int8_t";
+  case TCRV_HIP_ELEM_U8: return "uint8_t";
+  case TCRV_HIP_ELEM_I16: return "int16_t";
+  case TCRV_HIP_ELEM_U16: return "uint16_t";
+  case TCRV_HIP_ELEM_I32: return "int32_t";
+  case TCRV_HIP_ELEM_U32: return "uint32_t";
+  case TCRV_HIP_ELEM_I64: return "int64_t";
+  case TCRV_HIP_ELEM_F32: return "float";
+  case TCRV_HIP_ELEM_F64: return "double";
+  default: return nullptr;
+  }
+}
+
+const char *binaryKindName(int kind) {
+  switch (kind) {
+  case TCRV_HIP_BINARY_ADD: return "TCRV_HIP_BINARY_ADD";
+  case TCRV_HIP_BINARY_SUB: return "TCRV_HIP_BINARY_SUB";
+  case TCRV_HIP_BINARY_MUL: return "TCRV_HIP_BINARY_MUL";
+  default: return nullptr;
+  }
+}
+
+const char *binaryElemName(int elem) {
+  static const char *const names[] = {"TCRV_HIP_ELEM_I8",  "TCRV_HIP_ELEM_U8",  "TCRV_HIP_ELEM_I16",
+                                      "TCRV_HIP_ELEM_U16", "TCRV_HIP_ELEM_I32", "TCRV_HIP_ELEM_U32",
+                                      "TCRV_HIP_ELEM_I64", "TCRV_HIP_ELEM_F32", "TCRV_HIP_ELEM_F64"};
+  return elem >= TCRV_HIP_ELEM_I8 && elem <= TCRV_HIP_ELEM_F64 ? names[elem] : nullptr;
+}
+
+// The exported function of one route row: its parameters are the row's
+// runtime-ABI parameters (op attributes and the element type excluded: the
+// emitted C bakes those in, so they come from `attrs`) plus the stream; its
+// body forwards to the row's libtcrv_hip entry.  `declaration` emits the
+// prototype alone.  Returns false for missing or invalid attributes.
+bool exportFunction(const HipKernelRoute &r, const std::string &name, const int64_t *attrs,
+                    size_t nattrs, bool declaration, std::string &out) {
+  const bool binary = std::strcmp(r.op, "tcrv_rvv.binary") == 0;
+  const bool tile = std::strcmp(r.op, "tcrv_rvv.q4_0_q8_0_gemm_tile") == 0;
+  const size_t need = binary ? 2 : tile ? 1 : 0;
+  if (nattrs < need || (need && !attrs))
+    return false;
+  const char *elemType = nullptr;
+  if (binary) {
+    elemType = binaryCType(static_cast<int>(attrs[1]));
+    if (!binaryKindName(static_cast<int>(attrs[0])) || !elemType)
+      return false;
+  }
+  if (tile && attrs[0] < 1)
+    return false;
+  std::string sig, call;
+  for (size_t i = 0; i < r.nparams; ++i) {
+    const AbiParam &p = r.params[i];
+    if (!call.empty())
+      call += ", ";
+    if (std::strcmp(p.role, kOpAttr) == 0 || std::strcmp(p.role, kElemType) == 0) {
+      if (binary)
+        call += std::strcmp(p.cName, "kind") == 0 ? binaryKindName(static_cast<int>(attrs[0]))
+                                                  : binaryElemName(static_cast<int>(attrs[1]));
+      else
+        call += std::to_string(attrs[0]) + " /* " + p.cName + " */";
+      continue;
+    }
+    std::string ctype = p.cType;
+    if (binary && ctype.find("void") != std::string::npos)  // the element's C type
+      ctype = (ctype.rfind("const ", 0) == 0 ? std::string("const ") : std::string()) +
+              elemType + " *";
+    if (!sig.empty())
+      sig += ", ";
+    sig += ctype + (ctype.back() == '*' ? "" : " ") + p.cName;
+    call += p.cName;
+  }
+  const std::string proto =
+      "extern \"C\" int " + name + "(" + sig + (sig.empty() ? "" : ", ") + "void *stream)";
+  if (declaration) {
+    out += proto + ";\n";
+    return true;
+  }
+  out += "// ";
+  out += r.op;
+  out += " -> libtcrv_hip ";
+  out += r.entry;
+  out += "\n" + proto + " {\n  return " + r.entry + "(" + call + ", stream);\n}\n";
+  return true;
+}
+
 bool validFacts(int quant, int regime, int layout) {
   return quant >= TCRV_HIP_QUANT_Q4_0 && quant <= TCRV_HIP_QUANT_Q4_K &&
          (regime == TCRV_HIP_M_DECODE || regime == TCRV_HIP_M_PREFILL) &&
@@ -201,6 +314,15 @@ int tcrv_hip_route_select(int weight_quant, int m_regime, int weight_layout, int
 }
 
 int tcrv_hip_route_m_regime(size_t nc) { return static_cast<int>(deriveMRegime(nc)); }
+
+int tcrv_hip_route_binary(int kind, int elem, const char **entry, const char **reason) {
+  const HipBinarySelection sel = selectHipBinary(kind, elem);
+  if (entry)
+    *entry = sel.entry;
+  if (reason)
+    *reason = sel.reason;
+  return sel.entry ? TCRV_HIP_OK : TCRV_HIP_ERR_UNSUPPORTED;
+}
 
 int tcrv_hip_route_contraction(int weight_quant, int weight_layout, size_t n, float *s,
                                const uint8_t *vx, const uint8_t *vy, size_t by, size_t nr,
@@ -265,6 +387,39 @@ int tcrv_hip_route_param(size_t row, size_t param, const char **c_name, const ch
     *c_type = p.cType;
   if (role)
     *role = p.role;
+  return TCRV_HIP_OK;
+}
+
+const char *tcrv_hip_export_prologue(void) {
+  return "// Generated by the TianChen-RV HIP target export (libtcrv_hip_route): one\n"
+         "// tcrv_emitc_<kernel>_<variant> per selected variant, forwarding to libtcrv_hip.\n"
+         "#include <stddef.h>\n#include <stdint.h>\n\n#include \"tcrv_hip.h\"\n";
+}
+
+int tcrv_hip_export_function(const char *op, const char *kernel, const char *variant,
+                             const int64_t *attrs, size_t nattrs, int form, char *buf, size_t cap,
+                             size_t *needed) {
+  if (!op || !kernel || !variant)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (form != TCRV_HIP_EXPORT_DEFINITION && form != TCRV_HIP_EXPORT_DECLARATION)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  const long row = tcrv_hip_route_find(op);
+  if (row < 0)
+    return TCRV_HIP_ERR_UNSUPPORTED;
+  // the name the reference derives: tcrv_emitc_<kernel>_<variant>
+  // (RVVToEmitC.cpp:167-172)
+  const std::string name = std::string("tcrv_emitc_") + kernel + "_" + variant;
+  std::string text;
+  if (!exportFunction(kHipKernelRoutes[row], name, attrs, nattrs,
+                      form == TCRV_HIP_EXPORT_DECLARATION, text))
+    return TCRV_HIP_ERR_BAD_SIZE;
+  if (needed)
+    *needed = text.size() + 1;
+  if (buf && cap > 0) {
+    const size_t n = std::min(cap - 1, text.size());
+    std::memcpy(buf, text.data(), n);
+    buf[n] = '\0';
+  }
   return TCRV_HIP_OK;
 }
 

@@ -74,7 +74,14 @@ SIGNATURES = {
     "tcrv_hip_pack_q8_0_to_q8_0x4": [_sz, _sz, _p, _sz, _p, _p],
     "tcrv_hip_pack_q4_0_to_soa": [_sz, _sz, _p, _sz, _p, _p],
     "tcrv_hip_gemv_q4_0_soa_q8_0": [_sz, _p, _p, _p, _sz, _p],
+    "tcrv_hip_packed_i4_offset_binary_x_i8_product_reduce": [_p, _p, _p, _p, _p, _sz, _p],
+    "tcrv_hip_pack_q8_0_to_gemm_tiles": [_sz, _sz, _p, _sz, _p, _p],
+    "tcrv_hip_q8_0_q8_0_gemm_tiles": [_sz, _p, _p, _p, _sz, _sz, _sz, _p],
+    "tcrv_hip_q8_0_q8_0_gemm_ws": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p, _sz, _p],
 }
+# size queries (return size_t)
+SIZE_FUNCS = {"tcrv_hip_gemm_tiles_bytes": [_sz, _sz],
+              "tcrv_hip_q8_0_q8_0_gemm_workspace_bytes": [_sz, _sz, _sz]}
 STRING_FUNCS = {"tcrv_hip_status_string": [_int], "tcrv_hip_version": []}
 
 _lib: Optional[ctypes.CDLL] = None
@@ -108,6 +115,10 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = argtypes
         fn.restype = ctypes.c_char_p
+    for name, argtypes in SIZE_FUNCS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = _sz
     _lib = lib
     return lib
 
@@ -182,6 +193,11 @@ def dequantize_row_q8_0(vx, y, n: int, stream=None):
 
 def quantize_row_q8_0(n: int, x, vy, stream=None):
     return call("tcrv_hip_quantize_row_q8_0", n, x, vy, _stream(stream))
+
+
+def packed_i4_offset_binary_x_i8_product_reduce(w, qlo, qhi, acc, out, n: int, stream=None):
+    return call("tcrv_hip_packed_i4_offset_binary_x_i8_product_reduce", w, qlo, qhi, acc, out, n,
+                _stream(stream))
 
 
 def q8_0_q8_0_block_dot(n: int, s, vx, vy, stream=None):
@@ -263,6 +279,28 @@ def gemv_q4_0_soa_q8_0(n: int, s, vx, vy, nr: int, stream=None):
     return call("tcrv_hip_gemv_q4_0_soa_q8_0", n, s, vx, vy, nr, _stream(stream))
 
 
+def gemm_tiles_bytes(nrows: int, nb: int) -> int:
+    return load().tcrv_hip_gemm_tiles_bytes(nrows, nb)
+
+
+def pack_q8_0_to_gemm_tiles(nrows: int, nb: int, src, bx: int, dst, stream=None):
+    return call("tcrv_hip_pack_q8_0_to_gemm_tiles", nrows, nb, src, bx, dst, _stream(stream))
+
+
+def q8_0_q8_0_gemm_tiles(n: int, s, tx, ty, nr: int, nc: int, bs: int, stream=None):
+    return call("tcrv_hip_q8_0_q8_0_gemm_tiles", n, s, tx, ty, nr, nc, bs, _stream(stream))
+
+
+def q8_0_q8_0_gemm_workspace_bytes(n: int, nr: int, nc: int) -> int:
+    return load().tcrv_hip_q8_0_q8_0_gemm_workspace_bytes(n, nr, nc)
+
+
+def q8_0_q8_0_gemm_ws(n: int, s, vx, vy, by: int, nr: int, nc: int, bx: int, bs: int, ws,
+                      ws_bytes: int, stream=None):
+    return call("tcrv_hip_q8_0_q8_0_gemm_ws", n, s, vx, vy, by, nr, nc, bx, bs, ws, ws_bytes,
+                _stream(stream))
+
+
 def synchronize(stream=None):
     return call("tcrv_hip_stream_synchronize", _stream(stream))
 
@@ -282,6 +320,7 @@ ROUTE_SIGNATURES = {
     "tcrv_hip_route_select": ([_int, _int, _int, ctypes.POINTER(_int), ctypes.POINTER(_cs),
                                ctypes.POINTER(_cs)], _int),
     "tcrv_hip_route_m_regime": ([_sz], _int),
+    "tcrv_hip_route_binary": ([_int, _int, ctypes.POINTER(_cs), ctypes.POINTER(_cs)], _int),
     "tcrv_hip_route_contraction": ([_int, _int, _sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p,
                                     ctypes.POINTER(_int)], _int),
     "tcrv_hip_route_count": ([], _sz),
@@ -291,7 +330,12 @@ ROUTE_SIGNATURES = {
     "tcrv_hip_route_param": ([_sz, _sz, ctypes.POINTER(_cs), ctypes.POINTER(_cs),
                               ctypes.POINTER(_cs)], _int),
     "tcrv_hip_route_find": ([_cs], ctypes.c_long),
+    "tcrv_hip_export_function": ([_cs, _cs, _cs, ctypes.POINTER(ctypes.c_int64), _sz, _int,
+                                  ctypes.c_char_p, _sz, ctypes.POINTER(_sz)], _int),
+    "tcrv_hip_export_prologue": ([], _cs),
 }
+
+EXPORT_DEFINITION, EXPORT_DECLARATION = 0, 1
 
 _route: Optional[ctypes.CDLL] = None
 
@@ -325,6 +369,16 @@ def route_select(quant: str, m_regime: int, layout: str):
     return ALGO[algo.value], reason.value.decode(), entry.value.decode() if entry.value else None
 
 
+def route_binary(kind: int, elem: str):
+    """(status, entry symbol or None, audit token) for tcrv_rvv.binary's typed
+    facts: kind BINARY_ADD/SUB/MUL, elem a key of ELEM."""
+    lib = load_route()
+    entry, reason = _cs(), _cs()
+    st = lib.tcrv_hip_route_binary(kind, ELEM[elem] if isinstance(elem, str) else elem,
+                                   ctypes.byref(entry), ctypes.byref(reason))
+    return st, entry.value.decode() if entry.value else None, reason.value.decode()
+
+
 def route_table():
     """The op-identity route table: [{op, entry, params: [(c_name, c_type, role)]}]."""
     lib = load_route()
@@ -339,6 +393,27 @@ def route_table():
         rows.append({"op": lib.tcrv_hip_route_op(i).decode(),
                      "entry": lib.tcrv_hip_route_entry(i).decode(), "params": params})
     return rows
+
+
+def export_function(op: str, kernel: str, variant: str, attrs=(), form: int = EXPORT_DEFINITION):
+    """(status, C++ text) of the exported tcrv_emitc_<kernel>_<variant> for
+    one selected variant of `op`; attrs are the baked-in op facts ({kind,
+    element} for tcrv_rvv.binary, {activation_cols} for the GEMM tile)."""
+    lib = load_route()
+    arr = (ctypes.c_int64 * max(1, len(attrs)))(*attrs)
+    need = _sz()
+    st = lib.tcrv_hip_export_function(op.encode(), kernel.encode(), variant.encode(), arr,
+                                      len(attrs), form, None, 0, ctypes.byref(need))
+    if st != OK:
+        return st, None
+    buf = ctypes.create_string_buffer(need.value)
+    st = lib.tcrv_hip_export_function(op.encode(), kernel.encode(), variant.encode(), arr,
+                                      len(attrs), form, buf, need.value, None)
+    return st, buf.value.decode()
+
+
+def export_prologue() -> str:
+    return load_route().tcrv_hip_export_prologue().decode()
 
 
 def route_contraction(quant: str, layout: str, n: int, s, vx, vy, by: int, nr: int, nc: int,
