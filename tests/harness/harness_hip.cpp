@@ -5,9 +5,14 @@
 // the scalar references here are the oracle library (oracle/tcrv_oracle.h).
 //
 //   1. the reference's own add proof (i32, n = 1031, lhs = 3i - 17,
-//      rhs = 41 - 2i) through tcrv_hip_add_i32;
-//   2. the route provider's selection for every combination of typed facts;
-//   3. routed decode GEMVs and prefill GEMMs (Q4_0 and Q8_0 weights, and the
+//      rhs = 41 - 2i) through the exported fixture function
+//      tcrv_emitc_explicit_selected_body_add_kernel_explicit_selected_body_rvv_i32_add;
+//   2. every other exported fixture function (_gen/tcrv_emitc_fixtures.cpp,
+//      generated from emitc_fixtures.manifest by the package's export tool),
+//      called by its name on synthetic inputs, each output compared bit for bit
+//      with the oracle;
+//   3. the route provider's selection for every combination of typed facts;
+//   4. routed decode GEMVs and prefill GEMMs (Q4_0 and Q8_0 weights, and the
 //      repack GEMM over x16 Q4_0 weights) on
 //      quantized synthetic rows, each output compared bit for bit with the
 //      oracle.
@@ -24,6 +29,10 @@
 #include "tcrv_hip.h"
 #include "tcrv_hip_route.h"
 #include "tcrv_oracle.h"
+// the generated prototypes, then the fixtures' own: g++ rejects the build if
+// any two differ
+#include "tcrv_emitc_fixtures.h"
+#include "emitc_fixture_prototypes.h"
 
 namespace {
 
@@ -81,16 +90,17 @@ int add_proof() {
   }
   HIP_OK(hipMemcpy(dl.p, lhs.data(), n * 4, hipMemcpyHostToDevice));
   HIP_OK(hipMemcpy(dr.p, rhs.data(), n * 4, hipMemcpyHostToDevice));
-  const int st = tcrv_hip_add_i32(dl.p, dr.p, dout.p, n, nullptr);
+  const int st = tcrv_emitc_explicit_selected_body_add_kernel_explicit_selected_body_rvv_i32_add(
+      dl.p, dr.p, dout.p, n, nullptr);
   if (st != TCRV_HIP_OK)
-    return fail("tcrv_hip_add_i32", st);
+    return fail("exported add", st);
   HIP_OK(hipMemcpy(out.data(), dout.p, n * 4, hipMemcpyDeviceToHost));
   for (size_t i = 0; i < n; ++i)
     if (out[i] != want[i] || out[i] != lhs[i] + rhs[i]) {
       std::printf("FAIL add mismatch at %zu: got %d expected %d\n", i, out[i], want[i]);
       return 1;
     }
-  std::printf("add proof ok: %zu elements checked\n", n);
+  std::printf("add proof ok: %zu elements checked (exported add)\n", n);
   return 0;
 }
 
@@ -127,6 +137,229 @@ std::vector<uint8_t> quantized_rows(size_t nrows, size_t n, uint64_t seed, float
       tcrv_oracle_quantize_row_q4_0(n, x.data(), out.data() + r * rb);
   }
   return out;
+}
+
+// ---- the exported fixture functions -------------------------------------
+
+template <typename T>
+bool upload(DeviceBuffer<T> &d, const std::vector<T> &h) {
+  return d.p && hipMemcpy(d.p, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice) == hipSuccess;
+}
+
+template <typename T>
+bool download(std::vector<T> &h, const DeviceBuffer<T> &d) {
+  return hipMemcpy(h.data(), d.p, h.size() * sizeof(T), hipMemcpyDeviceToHost) == hipSuccess;
+}
+
+// Compares got with want byte for byte and prints the step's line.
+template <typename T>
+int same(const char *name, const std::vector<T> &got, const std::vector<T> &want,
+         const char *shape) {
+  for (size_t i = 0; i < got.size(); ++i)
+    if (std::memcmp(&got[i], &want[i], sizeof(T)) != 0) {
+      std::printf("FAIL exported %s mismatch at element %zu\n", name, i);
+      return 1;
+    }
+  std::printf("exported %s ok: %s bit-identical to the oracle\n", name, shape);
+  return 0;
+}
+
+std::vector<uint8_t> random_bytes(size_t n, uint64_t seed) {
+  Rng rng{seed};
+  std::vector<uint8_t> v(n);
+  for (auto &b : v)
+    b = static_cast<uint8_t>(rng.next() >> 56);
+  return v;
+}
+
+// x16 source order of nrows plain rows (nb blocks of `bytes` each): group x,
+// block b holds block b of rows 16x .. 16x+15.
+std::vector<uint8_t> x16_source(const std::vector<uint8_t> &w, size_t nrows, size_t nb,
+                                size_t bytes) {
+  std::vector<uint8_t> src(w.size());
+  for (size_t x = 0; x < nrows / 16; ++x)
+    for (size_t b = 0; b < nb; ++b)
+      for (size_t r = 0; r < 16; ++r)
+        std::memcpy(&src[((x * nb + b) * 16 + r) * bytes], &w[(16 * x + r) * nb * bytes + b * bytes],
+                    bytes);
+  return src;
+}
+
+#define EXPORTED_OK(name, call)              \
+  do {                                       \
+    const int st_ = (call);                  \
+    if (st_ != TCRV_HIP_OK)                  \
+      return fail("exported " name, st_);    \
+  } while (0)
+
+int exported_variants() {
+  const size_t n = 1024, nb = n / 32;
+  // Q8_0 . Q8_0 and Q4_0 . Q8_0 block dots (one row pair each)
+  {
+    const std::vector<uint8_t> x8 = quantized_rows(1, n, 2001, 0.5f, true);
+    const std::vector<uint8_t> x4 = quantized_rows(1, n, 2002, 0.5f, false);
+    const std::vector<uint8_t> y8 = quantized_rows(1, n, 2003, 1.0f, true);
+    DeviceBuffer<uint8_t> dx8(x8.size()), dx4(x4.size()), dy8(y8.size());
+    DeviceBuffer<float> ds(1);
+    if (!upload(dx8, x8) || !upload(dx4, x4) || !upload(dy8, y8) || !ds.p)
+      return fail("upload", -1);
+    std::vector<float> got(1), want(1);
+    EXPORTED_OK("q8_0 block dot", tcrv_emitc_ggml_vec_dot_q8_0_q8_0_kernel_ggml_vec_dot_q8_0_q8_0(
+                                      n, ds.p, dx8.p, dy8.p, nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    if (!download(got, ds))
+      return fail("download", -1);
+    tcrv_oracle_vec_dot_q8_0_q8_0(n, want.data(), x8.data(), y8.data());
+    if (same("q8_0 block dot", got, want, "K 1024"))
+      return 1;
+    EXPORTED_OK("q4_0 block dot", tcrv_emitc_ggml_vec_dot_q4_0_q8_0_kernel_ggml_vec_dot_q4_0_q8_0(
+                                      n, ds.p, 0, dx4.p, 0, dy8.p, 0, 1, nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    if (!download(got, ds))
+      return fail("download", -1);
+    tcrv_oracle_vec_dot_q4_0_q8_0(n, want.data(), 0, x4.data(), 0, y8.data(), 0, 1);
+    if (same("q4_0 block dot", got, want, "K 1024"))
+      return 1;
+  }
+  // the Q4_0 GEMM (ragged 37 x 11) and its one-row tile (activation_cols = 4)
+  {
+    const size_t nr = 37, nc = 11, wb = nb * 18, ab = nb * 34;
+    const std::vector<uint8_t> w = quantized_rows(nr, n, 2004, 0.02f, false);
+    const std::vector<uint8_t> a = quantized_rows(nc, n, 2005, 1.0f, true);
+    DeviceBuffer<uint8_t> dw(w.size()), da(a.size());
+    DeviceBuffer<float> ds(nr * nc);
+    if (!upload(dw, w) || !upload(da, a) || !ds.p)
+      return fail("upload", -1);
+    std::vector<float> got(nr * nc), want(nr * nc);
+    EXPORTED_OK("q4_0 gemm", tcrv_emitc_ggml_q4_0_q8_0_gemm_kernel_ggml_q4_0_q8_0_gemm(
+                                 n, ds.p, dw.p, da.p, ab, nr, nc, wb, nc, nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    if (!download(got, ds))
+      return fail("download", -1);
+    tcrv_oracle_gemm_q4_0_q8_0(n, want.data(), w.data(), a.data(), ab, nr, nc, wb, nc, 1);
+    if (same("q4_0 gemm", got, want, "37 x 11 x 1024"))
+      return 1;
+    std::vector<float> tile(4), tile_want(4);
+    EXPORTED_OK("q4_0 gemm tile", tcrv_emitc_ggml_q4_0_q8_0_gemm_tile_kernel_ggml_q4_0_q8_0_gemm_tile(
+                                      n, ds.p, dw.p, da.p, ab, nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    if (!download(tile, ds))
+      return fail("download", -1);
+    tcrv_oracle_gemm_q4_0_q8_0(n, tile_want.data(), w.data(), a.data(), ab, 1, 4, wb, 4, 1);
+    if (same("q4_0 gemm tile", tile, tile_want, "1 x 4 x 1024"))
+      return 1;
+  }
+  // x16 pack and the repack GEMVs (64 weight rows)
+  {
+    const size_t rows = 64, groups = rows / 16;
+    const std::vector<uint8_t> w4 = quantized_rows(rows, n, 2006, 0.02f, false);
+    const std::vector<uint8_t> w8 = quantized_rows(rows, n, 2007, 0.02f, true);
+    const std::vector<uint8_t> a = quantized_rows(1, n, 2008, 1.0f, true);
+    const std::vector<uint8_t> src4 = x16_source(w4, rows, nb, 18);
+    const std::vector<uint8_t> src8 = x16_source(w8, rows, nb, 34);
+    std::vector<uint8_t> p4(groups * nb * 288), p4_want(p4.size()), p8(groups * nb * 544);
+    tcrv_oracle_pack_q4_0_to_q4_0x16(groups * nb, src4.data(), p4_want.data());
+    tcrv_oracle_pack_q8_0_to_q8_0x16(groups * nb, src8.data(), p8.data());
+    DeviceBuffer<uint8_t> dsrc(src4.size()), dp4(p4.size()), dp8(p8.size()), da(a.size());
+    DeviceBuffer<float> ds(rows);
+    if (!upload(dsrc, src4) || !upload(dp8, p8) || !upload(da, a) || !dp4.p || !ds.p)
+      return fail("upload", -1);
+    EXPORTED_OK("x16 pack", tcrv_emitc_ggml_pack_q4_0_to_q4_0x16_kernel_ggml_pack_q4_0_to_q4_0x16(
+                                groups * nb, dsrc.p, dp4.p, nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    if (!download(p4, dp4))
+      return fail("download", -1);
+    if (same("x16 pack", p4, p4_want, "128 block_q4_0x16"))
+      return 1;
+    std::vector<float> got(rows), want(rows);
+    EXPORTED_OK("q4_0 repack gemv",
+                tcrv_emitc_ggml_repack_gemv_q4_0_q8_0_kernel_ggml_repack_gemv_q4_0_q8_0(
+                    n, ds.p, dp4.p, da.p, rows, nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    if (!download(got, ds))
+      return fail("download", -1);
+    tcrv_oracle_repack_gemv_q4_0_q8_0(n, want.data(), p4_want.data(), a.data(), rows);
+    if (same("q4_0 repack gemv", got, want, "64 x 1024"))
+      return 1;
+    EXPORTED_OK("q8_0 repack gemv",
+                tcrv_emitc_ggml_repack_gemv_q8_0_q8_0_kernel_ggml_repack_gemv_q8_0_q8_0(
+                    n, ds.p, dp8.p, da.p, rows, nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    if (!download(got, ds))
+      return fail("download", -1);
+    tcrv_oracle_repack_gemv_q8_0_q8_0(n, want.data(), p8.data(), a.data(), rows);
+    if (same("q8_0 repack gemv", got, want, "64 x 1024"))
+      return 1;
+  }
+  // the repack GEMM: 48 x16 weight rows x 12 x4 activation rows
+  {
+    const size_t wrows = 48, arows = 12;
+    const std::vector<uint8_t> w = quantized_rows(wrows, n, 2009, 0.02f, false);
+    const std::vector<uint8_t> a = quantized_rows(arows, n, 2010, 1.0f, true);
+    const std::vector<uint8_t> src = x16_source(w, wrows, nb, 18);
+    std::vector<uint8_t> wx16(wrows / 16 * nb * 288), ax4(arows / 4 * nb * 136);
+    tcrv_oracle_pack_q4_0_to_q4_0x16(wrows / 16 * nb, src.data(), wx16.data());
+    tcrv_oracle_pack_q8_0_to_q8_0x4(arows, nb, a.data(), nb * 34, ax4.data());
+    DeviceBuffer<uint8_t> dw(wx16.size()), da(ax4.size());
+    DeviceBuffer<float> ds(wrows * arows);
+    if (!upload(dw, wx16) || !upload(da, ax4) || !ds.p)
+      return fail("upload", -1);
+    std::vector<float> got(wrows * arows), want(wrows * arows);
+    EXPORTED_OK("repack gemm",
+                tcrv_emitc_ggml_repack_gemm_q4_0_q8_0_kernel_ggml_repack_gemm_q4_0_q8_0(
+                    n, ds.p, dw.p, da.p, arows, wrows, wrows, nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    if (!download(got, ds))
+      return fail("download", -1);
+    tcrv_oracle_repack_gemm_q4_0_q8_0(n, want.data(), wx16.data(), ax4.data(), arows, wrows, wrows);
+    if (same("repack gemm", got, want, "48 x 12 x 1024"))
+      return 1;
+  }
+  // quantize_row_q8_0 over 97 blocks
+  {
+    const size_t nq = 97 * 32;
+    Rng rng{2011};
+    std::vector<float> x(nq);
+    for (auto &v : x)
+      v = 3.0f * rng.uniform();
+    std::vector<uint8_t> got(97 * 34), want(97 * 34);
+    tcrv_oracle_quantize_row_q8_0(nq, x.data(), want.data());
+    DeviceBuffer<float> dx(nq);
+    DeviceBuffer<uint8_t> dy(got.size());
+    if (!upload(dx, x) || !dy.p)
+      return fail("upload", -1);
+    EXPORTED_OK("quantize", tcrv_emitc_quantize_row_q8_0_kernel_quantize_row_q8_0(nq, dx.p, dy.p,
+                                                                               nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    if (!download(got, dy))
+      return fail("download", -1);
+    if (same("quantize", got, want, "97 blocks"))
+      return 1;
+  }
+  // the integer core over 1003 bytes (the vector and the tail paths)
+  {
+    const size_t ni = 1003;
+    const std::vector<uint8_t> wb = random_bytes(ni, 2012), lb = random_bytes(ni, 2013),
+                               hb = random_bytes(ni, 2014);
+    std::vector<int8_t> w(wb.begin(), wb.end()), lo(lb.begin(), lb.end()), hi(hb.begin(), hb.end());
+    const std::vector<int32_t> acc = {12345};
+    std::vector<int32_t> got(1), want(1);
+    tcrv_oracle_packed_i4_offset_binary_x_i8_product_reduce(w.data(), lo.data(), hi.data(),
+                                                            acc.data(), want.data(), ni);
+    DeviceBuffer<int8_t> dw(ni), dlo(ni), dhi(ni);
+    DeviceBuffer<int32_t> dacc(1), dout(1);
+    if (!upload(dw, w) || !upload(dlo, lo) || !upload(dhi, hi) || !upload(dacc, acc) || !dout.p)
+      return fail("upload", -1);
+    EXPORTED_OK("integer core",
+                tcrv_emitc_rvv_q4_0_q8_0_integer_core_kernel_rvv_q4_0_q8_0_integer_core(
+                    dw.p, dlo.p, dhi.p, dacc.p, dout.p, ni, nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    if (!download(got, dout))
+      return fail("download", -1);
+    if (same("integer core", got, want, "1003 bytes"))
+      return 1;
+  }
+  return 0;
 }
 
 int routed_contraction(const char *name, int quant, size_t nr, size_t nc, size_t n,
@@ -218,7 +451,7 @@ int routed_repack_gemm(size_t nr, size_t nc, size_t n) {
 
 int main() {
   std::printf("%s\n", tcrv_hip_version());
-  if (add_proof() || route_matrix() ||
+  if (add_proof() || exported_variants() || route_matrix() ||
       routed_contraction("routed q4_0 decode", TCRV_HIP_QUANT_Q4_0, 256, 1, 1024,
                          TCRV_HIP_ALGO_DECODE_GEMV) ||
       routed_contraction("routed q8_0 decode", TCRV_HIP_QUANT_Q8_0, 96, 1, 512,
