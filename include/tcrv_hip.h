@@ -52,7 +52,8 @@ enum {
   TCRV_HIP_ERR_BAD_SIZE = -2,       /* a size/stride violates the kernel's contract */
   TCRV_HIP_ERR_MISALIGNED = -3,     /* a pointer/stride is not aligned as documented */
   TCRV_HIP_ERR_TOO_LARGE = -4,      /* a size exceeds the kernel's index range */
-  TCRV_HIP_ERR_UNSUPPORTED = -5     /* argument combination not implemented */
+  TCRV_HIP_ERR_UNSUPPORTED = -5,    /* argument combination not implemented */
+  TCRV_HIP_ERR_SCRATCH_LIMIT = -6   /* the call needs more than the fixed device scratch */
 };
 
 /* Human-readable name of a status value (static storage, never NULL). */
@@ -239,6 +240,20 @@ TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm_ws(size_t n, float *s, const uint8_t *v
                                             const uint8_t *vy, size_t by, size_t nr, size_t nc,
                                             size_t bx, size_t bs, void *workspace,
                                             size_t workspace_bytes, void *stream);
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid hipMalloc).
+ * tcrv_hip_q8_0_q8_0_gemm_ws (same ABI and results) with its workspace in a
+ * fixed device array of tcrv_hip_q8_0_q8_0_gemm_noalloc_max_bytes() (64 MiB)
+ * per GPU, held until the process ends; calls no allocating routine.  A shape
+ * whose workspace exceeds it returns TCRV_HIP_ERR_SCRATCH_LIMIT before
+ * launching anything (4096 x 4096 x K 4096 needs 35.7 MB).  Every call on one
+ * GPU shares that GPU's array: calls that overlap in time on one GPU race and
+ * must be ordered by the caller (one stream).  The first call on a device
+ * looks up the array's address (not capturable; make it outside a capture). */
+TCRV_HIP_API size_t tcrv_hip_q8_0_q8_0_gemm_noalloc_max_bytes(void);
+TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm_noalloc(size_t n, float *s, const uint8_t *vx,
+                                                 const uint8_t *vy, size_t by, size_t nr,
+                                                 size_t nc, size_t bx, size_t bs, void *stream);
 
 /* ---- a8: the x16 block-as-lane weight layout ---------------------------
  * Replaces tcrv_emitc_..._pack_q4_0_to_q4_0x16(size_t nblocks, const uint8_t *src,

@@ -80,6 +80,16 @@ def test_empty_problems_are_no_ops(name, args):
     assert tcrv_hip.call(name, *args, check=False) == tcrv_hip.OK
 
 
+def test_noalloc_gemm_refuses_shapes_beyond_its_scratch():
+    """Checked before any HIP call (fake addresses: nothing may run)."""
+    assert tcrv_hip.q8_0_q8_0_gemm_noalloc_max_bytes() == 64 << 20
+    nb = 241  # 4096 x 4096 x K 7712: 67.1 MB of GEMM tiles
+    st = tcrv_hip.call("tcrv_hip_q8_0_q8_0_gemm_noalloc", nb * 32, 0x1000, 0x2000, 0x3000,
+                       nb * 34, 4096, 4096, nb * 34, 4096, 0, check=False)
+    assert st == tcrv_hip.ERR_SCRATCH_LIMIT
+    assert "scratch" in tcrv_hip.status_string(st)
+
+
 def test_repack_gemm_argument_checks():
     """Misaligned operands and null pointers are refused before any launch
     (the addresses are fake: nothing may run); empty groups write nothing."""

@@ -215,6 +215,8 @@ const char *tcrv_hip_status_string(int status) {
     return "size exceeds the kernel's index range";
   case TCRV_HIP_ERR_UNSUPPORTED:
     return "argument combination not supported";
+  case TCRV_HIP_ERR_SCRATCH_LIMIT:
+    return "the call needs more than the entry's fixed device scratch";
   default:
     break;
   }

@@ -323,6 +323,21 @@ int tcrv_hip_q8_0_q8_0_gemm_tiles(size_t n, float *s, const uint8_t *tx, const u
   return gemm_tiles(nb, s, tx, ty, nr, nc, bs, as_stream(stream));
 }
 
+}  // extern "C"
+
+namespace tcrv_host {
+
+// Shapes the tiled kernel does not serve run as tcrv_hip_q8_0_q8_0_gemm,
+// without the workspace: fewer weight rows than one 256-row tile, a single
+// token (decode), or no blocks.
+bool gemm_ws_uses_workspace(size_t n, size_t nr, size_t nc) {
+  return nr >= static_cast<size_t>(tcrv::kDBM) && nc >= 2 && n / tcrv::kQK > 0;
+}
+
+}  // namespace tcrv_host
+
+extern "C" {
+
 size_t tcrv_hip_q8_0_q8_0_gemm_workspace_bytes(size_t n, size_t nr, size_t nc) {
   const size_t nb = n / tcrv::kQK;
   return tile_bytes(nr, nb) + tile_bytes(nc, nb);
@@ -333,10 +348,7 @@ int tcrv_hip_q8_0_q8_0_gemm_ws(size_t n, float *s, const uint8_t *vx, const uint
                                void *workspace, size_t workspace_bytes, void *stream) {
   using namespace tcrv_host;
   const size_t nb = n / tcrv::kQK;
-  // shapes the tiled kernel does not serve run as tcrv_hip_q8_0_q8_0_gemm,
-  // without the workspace: fewer weight rows than one 256-row tile, a single
-  // token (decode), or no blocks
-  if (nr < static_cast<size_t>(tcrv::kDBM) || nc < 2 || nb == 0)
+  if (!gemm_ws_uses_workspace(n, nr, nc))
     return tcrv_hip_q8_0_q8_0_gemm(n, s, vx, vy, by, nr, nc, bx, bs, stream);
   if (bs < nc)
     return TCRV_HIP_ERR_BAD_SIZE;

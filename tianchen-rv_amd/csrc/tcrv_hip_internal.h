@@ -190,4 +190,9 @@ int q4_0_rows_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t b
 int q4_0_grid(size_t n, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by,
               size_t nr, size_t nc, size_t bs, void *stream);
 
+// tcrv_hip_q8_0_q8_0_gemm_ws packs into its workspace and runs the tiled
+// kernel for this shape (otherwise it runs the plain GEMM and reads no
+// workspace); gemm_tiled.hip.
+bool gemm_ws_uses_workspace(size_t n, size_t nr, size_t nc);
+
 }  // namespace tcrv_host

@@ -30,6 +30,7 @@ ERR_BAD_SIZE = -2
 ERR_MISALIGNED = -3
 ERR_TOO_LARGE = -4
 ERR_UNSUPPORTED = -5
+ERR_SCRATCH_LIMIT = -6
 
 BINARY_ADD, BINARY_SUB, BINARY_MUL = 0, 1, 2
 ELEM = {"i8": 0, "u8": 1, "i16": 2, "u16": 3, "i32": 4, "u32": 5, "i64": 6, "f32": 7, "f64": 8}
@@ -78,10 +79,12 @@ SIGNATURES = {
     "tcrv_hip_pack_q8_0_to_gemm_tiles": [_sz, _sz, _p, _sz, _p, _p],
     "tcrv_hip_q8_0_q8_0_gemm_tiles": [_sz, _p, _p, _p, _sz, _sz, _sz, _p],
     "tcrv_hip_q8_0_q8_0_gemm_ws": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p, _sz, _p],
+    "tcrv_hip_q8_0_q8_0_gemm_noalloc": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p],
 }
 # size queries (return size_t)
 SIZE_FUNCS = {"tcrv_hip_gemm_tiles_bytes": [_sz, _sz],
-              "tcrv_hip_q8_0_q8_0_gemm_workspace_bytes": [_sz, _sz, _sz]}
+              "tcrv_hip_q8_0_q8_0_gemm_workspace_bytes": [_sz, _sz, _sz],
+              "tcrv_hip_q8_0_q8_0_gemm_noalloc_max_bytes": []}
 STRING_FUNCS = {"tcrv_hip_status_string": [_int], "tcrv_hip_version": []}
 
 _lib: Optional[ctypes.CDLL] = None
@@ -299,6 +302,18 @@ def q8_0_q8_0_gemm_ws(n: int, s, vx, vy, by: int, nr: int, nc: int, bx: int, bs:
                       ws_bytes: int, stream=None):
     return call("tcrv_hip_q8_0_q8_0_gemm_ws", n, s, vx, vy, by, nr, nc, bx, bs, ws, ws_bytes,
                 _stream(stream))
+
+
+def q8_0_q8_0_gemm_noalloc_max_bytes() -> int:
+    return load().tcrv_hip_q8_0_q8_0_gemm_noalloc_max_bytes()
+
+
+def q8_0_q8_0_gemm_noalloc(n: int, s, vx, vy, by: int, nr: int, nc: int, bx: int, bs: int,
+                           stream=None, check: bool = True):
+    """tcrv_hip_q8_0_q8_0_gemm_ws with the library's fixed device scratch as the
+    workspace (no allocation); returns the status when check is False."""
+    return call("tcrv_hip_q8_0_q8_0_gemm_noalloc", n, s, vx, vy, by, nr, nc, bx, bs,
+                _stream(stream), check=check)
 
 
 def synchronize(stream=None):
