@@ -373,6 +373,55 @@ def test_quantize_q8_0_rne_ties(oracle):
     assert list(q[:9]) == [127, 0, 2, 2, 0, -2, -2, 4, 126]
 
 
+# The reference quantizer converts with vfncvt_x_f_w_i16m4 then vncvt_x_x_w_i8m2
+# (RVVOps.td:8376-8377).  RVV 1.0 specifies the first as a narrowing
+# float-to-signed-integer conversion under the dynamic rounding mode (frm = RNE),
+# with the F extension's invalid-input results (RISC-V unprivileged spec, "Single-
+# Precision Floating-Point Conversion": NaN and +inf or any positive value above
+# the range give the largest integer, -inf or any negative value below it the
+# smallest), and the second as vnsrl.wx with shift 0 (the low SEW bits).  Each row:
+# the product x*id the quantizer forms, the i16 the rule gives, the byte stored.
+RVV_VFNCVT_RULE = [
+    ("NaN", np.nan, 32767, 0xFF),
+    ("+inf", np.inf, 32767, 0xFF),
+    ("-inf", -np.inf, -32768, 0x00),
+    ("RNE tie to even, 2.5", 2.5, 2, 0x02),
+    ("RNE tie to even, 3.5", 3.5, 4, 0x04),
+    ("RNE tie to even, -2.5", -2.5, -2, 0xFE),
+    ("in range, -127", -127.0, -127, 0x81),
+]
+
+
+def test_quantize_conversion_follows_the_rvv_vfncvt_rule(oracle):
+    """The oracle's bytes for products that hit each row of the rule table."""
+    rows = {name: (i16, byte) for name, _, i16, byte in RVV_VFNCVT_RULE}
+    for name, v, i16, byte in RVV_VFNCVT_RULE:  # the table is self-consistent
+        assert (i16 & 0xFF) == byte, name
+    # amax = 127 -> d = 1, id = 1: the products are the inputs themselves
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1:4] = [2.5, 3.5, -2.5]
+    x[4] = -127.0
+    x[5] = np.nan  # skipped by amax (0.0-seeded max), NaN*1 = NaN
+    q = oracle.quantize_q8_0(x)[2:]
+    assert q[1] == rows["RNE tie to even, 2.5"][1]
+    assert q[2] == rows["RNE tie to even, 3.5"][1]
+    assert q[3] == rows["RNE tie to even, -2.5"][1]
+    assert q[4] == rows["in range, -127"][1]
+    assert q[5] == rows["NaN"][1]
+    # subnormal amax: d = amax/127 is so small that id = 1/d overflows to +inf,
+    # so a positive input's product is +inf, a negative one's -inf, 0*inf = NaN
+    x = np.zeros(32, np.float32)
+    x[0] = 1e-40
+    x[1] = -1e-40
+    q = oracle.quantize_q8_0(x)[2:]
+    with np.errstate(over="ignore"):
+        assert np.isinf(np.float32(1.0) / (np.float32(1e-40) / np.float32(127.0)))
+    assert q[0] == rows["+inf"][1]
+    assert q[1] == rows["-inf"][1]
+    assert q[2] == rows["NaN"][1]
+
+
 def test_quantize_q4_0_matches_host_quantizer(oracle):
     x = synth.normal_f32(1006, 32 * 500, 0.0, 0.02)
     x[:32] = 0.0
