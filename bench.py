@@ -267,6 +267,11 @@ def bench_gemv_rows(torch, lib, stream, args):
 
 
 def bench_gemm(torch, lib, stream, args):
+    """The 4096^3 Q8_0 GEMM in the reference ABI through the workspace entry
+    (both operands packed into the GEMM-tile layout, then the DMA-staged tiled
+    kernel), beside the plain entry, the path with weights packed once (only
+    the activations packed per call) and the tiled kernel alone (the roofline
+    kernel).  Median of --gemm-regions regions of --gemm-steps launches each."""
     log("GEMM inputs: A 4096 tokens x 4096 Q8_0 (seed 1008, N(0,1)), "
         "B 4096x4096 Q8_0 (seed 1009, N(0,0.02))")
     a = inputs("gemm_a")
@@ -275,28 +280,53 @@ def bench_gemm(torch, lib, stream, args):
     ad = torch.from_numpy(a).to(dev)
     bd = torch.from_numpy(b).to(dev)
     cd = torch.empty(N * N, dtype=torch.float32, device=dev)
-    fn = checked(lib.tcrv_hip_q8_0_q8_0_gemm, "gemm")
     rb, sp = a.shape[1], stream.cuda_stream
+    nb = N // 32
+    plain = checked(lib.tcrv_hip_q8_0_q8_0_gemm, "gemm")
+    ws_fn = checked(lib.tcrv_hip_q8_0_q8_0_gemm_ws, "gemm_ws")
+    pack = checked(lib.tcrv_hip_pack_q8_0_to_gemm_tiles, "pack_q8_0_to_gemm_tiles")
+    tiles = checked(lib.tcrv_hip_q8_0_q8_0_gemm_tiles, "gemm_tiles")
+    wsb = lib.tcrv_hip_q8_0_q8_0_gemm_workspace_bytes(N, N, N)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    txb = lib.tcrv_hip_gemm_tiles_bytes(N, nb)
+    tx = torch.empty(txb, dtype=torch.uint8, device=dev)       # weights, packed once
+    ty = torch.empty(wsb - txb, dtype=torch.uint8, device=dev)  # activations, per call
+    with torch.cuda.stream(stream):
+        pack(N, nb, bd.data_ptr(), rb, tx.data_ptr(), sp)
+        pack(N, nb, ad.data_ptr(), rb, ty.data_ptr(), sp)
+    torch.cuda.synchronize()
 
-    def launch(i):
-        # s[ir*bs + col]: ir = weight row (B), col = token (A)
-        fn(N, cd.data_ptr(), bd.data_ptr(), ad.data_ptr(), rb, N, N, rb, N, sp)
-
-    # ~50 launches (~10 ms of dense MFMA work) bring the clocks to their
-    # loaded state before anything is timed
-    Region(torch, stream, launch, 50).run()
-    cd.zero_()
-    timed = Region(torch, stream, launch, args.gemm_steps)
-    timed.run()  # untimed first replay
-    per = sorted(timed.run() * 1e3 / args.gemm_steps for _ in range(args.gemm_regions))
-    same_as_eager(torch, stream, cd,
-                  lambda out: fn(N, out, bd.data_ptr(), ad.data_ptr(), rb, N, N, rb, N, sp), "GEMM")
-    us = per[len(per) // 2]
-    tops = GEMM_OPS / (us * 1e-6) / 1e12
-    log(f"GEMM {us:.1f} us/launch (median of {len(per)} regions of {args.gemm_steps}; "
-        f"min {per[0]:.1f}, max {per[-1]:.1f}): {tops:.0f} TOPS "
-        f"({100 * tops / INT8_PEAK_TOPS:.1f}% of dense int8 peak)")
-    return {"us": us, "tops": tops, "us_min": per[0], "us_max": per[-1], "regions": len(per)}
+    # s[ir*bs + col]: ir = weight row (B), col = token (A)
+    paths = {
+        "gemm_ws": lambda out: ws_fn(N, out, bd.data_ptr(), ad.data_ptr(), rb, N, N, rb, N,
+                                     ws.data_ptr(), wsb, sp),
+        "plain": lambda out: plain(N, out, bd.data_ptr(), ad.data_ptr(), rb, N, N, rb, N, sp),
+        "prepacked_weights": lambda out: (pack(N, nb, ad.data_ptr(), rb, ty.data_ptr(), sp),
+                                          tiles(N, out, tx.data_ptr(), ty.data_ptr(), N, N, N,
+                                                sp)),
+        "tiles_kernel": lambda out: tiles(N, out, tx.data_ptr(), ty.data_ptr(), N, N, N, sp),
+    }
+    # ~50 launches (~10 ms of dense MFMA work) bring the clocks to their loaded
+    # state before anything is timed
+    Region(torch, stream, lambda i: paths["gemm_ws"](cd.data_ptr()), 50).run()
+    res = {}
+    for name, fn in paths.items():
+        cd.zero_()
+        timed = Region(torch, stream, lambda i, fn=fn: fn(cd.data_ptr()), args.gemm_steps)
+        timed.run()  # untimed first replay
+        per = sorted(timed.run() * 1e3 / args.gemm_steps for _ in range(args.gemm_regions))
+        # the graph really ran, and every path writes what the plain entry writes
+        same_as_eager(torch, stream, cd, paths["plain"], f"GEMM {name}")
+        us = per[len(per) // 2]
+        res[name] = {"us": us, "tops": GEMM_OPS / (us * 1e-6) / 1e12, "us_min": per[0],
+                     "us_max": per[-1]}
+        log(f"GEMM {name}: {us:.1f} us/launch (median of {len(per)} regions of "
+            f"{args.gemm_steps}; min {per[0]:.1f}, max {per[-1]:.1f}): "
+            f"{res[name]['tops']:.0f} TOPS ({100 * res[name]['tops'] / INT8_PEAK_TOPS:.1f}% of "
+            f"dense int8 peak)")
+    m = res["gemm_ws"]
+    return {"us": m["us"], "tops": m["tops"], "us_min": m["us_min"], "us_max": m["us_max"],
+            "regions": args.gemm_regions, "paths": res}
 
 
 def bench_configs(torch, lib, stream, args):
@@ -882,16 +912,27 @@ def main():
         })
     if "gemm" in res:
         m = res["gemm"]
+        k = m["paths"]["tiles_kernel"]
         line["gemm"] = {
-            "workload": "q8_0_q8_0_gemm 4096 weight rows x 4096 tokens x 4096 (configs[4])",
+            "workload": "q8_0_q8_0_gemm 4096 weight rows x 4096 tokens x 4096 (configs[4]) in "
+                        "the reference ABI through tcrv_hip_q8_0_q8_0_gemm_ws: both operands "
+                        "packed into the GEMM-tile layout, then the tiled kernel, every launch",
             "value": round(m["tops"], 2), "unit": "TOPS", "ms_per_step": m["us"] / 1e3,
             "steps": args.gemm_steps, "regions": m["regions"], "cpu_baseline": cpu_gemm,
             "us_min": round(m["us_min"], 2), "us_max": round(m["us_max"], 2),
-            "roofline": {"bound": "mfma", "achieved": round(m["tops"], 2), "peak": INT8_PEAK_TOPS,
-                         "unit": "TOPS", "frac": round(m["tops"] / INT8_PEAK_TOPS, 4),
-                         "traffic": traffic.get("q8_0_q8_0_gemm", {}).get("bytes"),
+            "paths": {name: {"us": round(v["us"], 2), "TOPS": round(v["tops"], 2),
+                             "us_min": round(v["us_min"], 2), "us_max": round(v["us_max"], 2)}
+                      for name, v in m["paths"].items()},
+            "paths_note": "gemm_ws = the value; plain = tcrv_hip_q8_0_q8_0_gemm (no workspace); "
+                          "prepacked_weights = weights packed once, activations packed per "
+                          "call; tiles_kernel = the tiled kernel alone on packed operands",
+            "roofline": {"bound": "mfma", "achieved": round(k["tops"], 2),
+                         "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                         "frac": round(k["tops"] / INT8_PEAK_TOPS, 4),
+                         "traffic": traffic.get("q8_0_q8_0_gemm_tiles", {}).get("bytes"),
                          "traffic_source": traffic_src,
-                         "kernel": "tcrv::gemm_wide<false>", "ops_per_launch": GEMM_OPS},
+                         "kernel": "tcrv::gemm_tiles_q8<true>", "ops_per_launch": GEMM_OPS,
+                         "us_per_launch": round(k["us"], 2)},
         }
         if "gemv" not in res:
             line.update({"value": line["gemm"]["value"], "unit": "TOPS",

@@ -67,18 +67,19 @@ TCRV_HIP_API int tcrv_hip_route_binary(int kind, int elem, const char **entry,
 
 /* Runs one contraction in the reference GEMM ABI
  * (n, s, vx, vy, by, nr, nc, bx, bs) -- q4_0_q8_0_gemm's parameter order,
- * test/Conversion/RVV/rvv-to-emitc-q4-0-q8-0-gemm.mlir:23-31 -- on the
- * algorithm tcrv_hip_route_select picks for (weight_quant, the regime of nc,
- * weight_layout).  Plain weights: the activation is plain Q8_0 rows.  x16
- * weights: vx holds nr/16 groups of 16 rows in the x16 layout, bx and by are
- * ignored, and nr % 16 == 0.  Decode (nc == 1) runs the repacked GEMV on one
- * plain Q8_0 activation row and needs bs == 1 (or nr == 1): it writes s[ir].
- * Prefill runs the repack GEMM in that op's contract
- * (tcrv_hip_repack_gemm_q4_0_q8_0): vy holds nc/4 groups of block_q8_0x4,
- * nc % 4 == 0, and the output is activation-row major, s[col*bs + ir].  A
- * declined request, or an x16 shape outside these, returns
- * TCRV_HIP_ERR_UNSUPPORTED before touching anything.  *algorithm (may be
- * NULL) receives the algorithm used. */
+ * test/Conversion/RVV/rvv-to-emitc-q4-0-q8-0-gemm.mlir:23-31 -- with that ABI's
+ * meaning (activation column col at vy + col*by as plain Q8_0 rows, output
+ * s[ir*bs + col]) on the algorithm tcrv_hip_route_select picks for
+ * (weight_quant, the regime of nc, weight_layout).  x16 weights (vx holds nr/16
+ * groups of 16 rows in the x16 layout, bx ignored, nr % 16 == 0) are served in
+ * decode only: the repacked GEMV on one plain Q8_0 activation row, needing
+ * bs == 1 (or nr == 1), writes s[ir].  An x16 prefill selects the repack GEMM
+ * (tcrv_hip_repack_gemm_q4_0_q8_0), whose contract is not this ABI's
+ * (block_q8_0x4 activations, output s[col*bs + ir]): this call refuses it, and
+ * the caller runs that entry in its own ABI.  A declined or refused request, or
+ * an x16 decode shape outside the above, returns TCRV_HIP_ERR_UNSUPPORTED before
+ * touching anything.  *algorithm (may be NULL) receives the algorithm
+ * selected. */
 TCRV_HIP_API int tcrv_hip_route_contraction(int weight_quant, int weight_layout, size_t n,
                                             float *s, const uint8_t *vx, const uint8_t *vy,
                                             size_t by, size_t nr, size_t nc, size_t bx,

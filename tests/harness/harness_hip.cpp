@@ -12,10 +12,10 @@
 //      called by its name on synthetic inputs, each output compared bit for bit
 //      with the oracle;
 //   3. the route provider's selection for every combination of typed facts;
-//   4. routed decode GEMVs and prefill GEMMs (Q4_0 and Q8_0 weights, and the
-//      repack GEMM over x16 Q4_0 weights) on
-//      quantized synthetic rows, each output compared bit for bit with the
-//      oracle.
+//   4. routed decode GEMVs and prefill GEMMs (Q4_0 and Q8_0 weights) on
+//      quantized synthetic rows, and the x16 Q4_0 prefill, whose selected
+//      repack GEMM runs in its own ABI, each output compared bit for bit with
+//      the oracle.
 // Prints one line per step and "harness ok" last; exits non-zero on any
 // mismatch or failed call.
 #include <hip/hip_runtime_api.h>
@@ -401,9 +401,11 @@ int routed_contraction(const char *name, int quant, size_t nr, size_t nc, size_t
   return 0;
 }
 
-// Prefill over x16 Q4_0 weights: the route runs the repack GEMM in its own
-// contract (activations in block_q8_0x4, output activation-row major); both
-// layouts are built here with the oracle's packs.
+// Prefill over x16 Q4_0 weights: the selection names the repack GEMM, whose
+// contract (activations in block_q8_0x4, output activation-row major) is not
+// the reference GEMM ABI, so the routed GEMM-ABI call refuses it untouched and
+// the caller runs the selected entry in its own ABI; both layouts are built
+// here with the oracle's packs.
 int routed_repack_gemm(size_t nr, size_t nc, size_t n) {
   const char *name = "routed q4_0 x16 prefill";
   const size_t nb = n / 32;
@@ -417,7 +419,7 @@ int routed_repack_gemm(size_t nr, size_t nc, size_t n) {
         std::memcpy(&src[((x * nb + b) * 16 + r) * 18], &w[(16 * x + r) * nb * 18 + b * 18], 18);
   tcrv_oracle_pack_q4_0_to_q4_0x16(nr / 16 * nb, src.data(), wx16.data());
   tcrv_oracle_pack_q8_0_to_q8_0x4(nc, nb, a.data(), nb * 34, ax4.data());
-  std::vector<float> got(nc * nr), want(nc * nr);
+  std::vector<float> got(nc * nr, -5.0f), want(nc * nr);
   tcrv_oracle_repack_gemm_q4_0_q8_0(n, want.data(), wx16.data(), ax4.data(), nc, nr, nr);
   DeviceBuffer<uint8_t> dw(wx16.size()), da(ax4.size());
   DeviceBuffer<float> ds(got.size());
@@ -427,23 +429,37 @@ int routed_repack_gemm(size_t nr, size_t nc, size_t n) {
   }
   HIP_OK(hipMemcpy(dw.p, wx16.data(), wx16.size(), hipMemcpyHostToDevice));
   HIP_OK(hipMemcpy(da.p, ax4.data(), ax4.size(), hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(ds.p, got.data(), got.size() * 4, hipMemcpyHostToDevice));
   int algo = -1;
-  const int st = tcrv_hip_route_contraction(TCRV_HIP_QUANT_Q4_0, TCRV_HIP_LAYOUT_X16, n, ds.p,
-                                            dw.p, da.p, 0, nr, nc, 0, nr, nullptr, &algo);
-  if (st != TCRV_HIP_OK)
-    return fail(name, st);
-  if (algo != TCRV_HIP_ALGO_REPACK_GEMM) {
-    std::printf("FAIL %s: routed to algorithm %d\n", name, algo);
+  int st = tcrv_hip_route_contraction(TCRV_HIP_QUANT_Q4_0, TCRV_HIP_LAYOUT_X16, n, ds.p, dw.p,
+                                      da.p, 0, nr, nc, 0, nr, nullptr, &algo);
+  if (st != TCRV_HIP_ERR_UNSUPPORTED || algo != TCRV_HIP_ALGO_REPACK_GEMM) {
+    std::printf("FAIL %s: the GEMM-ABI call returned %d (algorithm %d), expected a refusal\n",
+                name, st, algo);
     return 1;
   }
+  const char *reason = nullptr, *entry = nullptr;
+  st = tcrv_hip_route_select(TCRV_HIP_QUANT_Q4_0, TCRV_HIP_M_PREFILL, TCRV_HIP_LAYOUT_X16, &algo,
+                             &reason, &entry);
+  if (st != TCRV_HIP_OK || !entry || std::strcmp(entry, "tcrv_hip_repack_gemm_q4_0_q8_0") != 0)
+    return fail("tcrv_hip_route_select (x16 prefill)", st);
+  HIP_OK(hipMemcpy(got.data(), ds.p, got.size() * 4, hipMemcpyDeviceToHost));
+  for (float v : got)
+    if (v != -5.0f) {
+      std::printf("FAIL %s: the refused call wrote its output\n", name);
+      return 1;
+    }
+  st = tcrv_hip_repack_gemm_q4_0_q8_0(n, ds.p, dw.p, da.p, nc, nr, nr, nullptr);
+  if (st != TCRV_HIP_OK)
+    return fail(entry, st);
   HIP_OK(hipMemcpy(got.data(), ds.p, got.size() * 4, hipMemcpyDeviceToHost));
   for (size_t i = 0; i < got.size(); ++i)
     if (std::memcmp(&got[i], &want[i], 4) != 0) {
       std::printf("FAIL %s mismatch at %zu: got %.9g expected %.9g\n", name, i, got[i], want[i]);
       return 1;
     }
-  std::printf("%s ok: %zu x %zu x %zu bit-identical to the oracle (algorithm %d)\n", name, nr, nc,
-              n, algo);
+  std::printf("%s ok: %zu x %zu x %zu bit-identical to the oracle (selected entry %s, %s)\n",
+              name, nr, nc, n, entry, reason);
   return 0;
 }
 

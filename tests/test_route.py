@@ -170,8 +170,8 @@ def test_route_table_keeps_the_reference_gemm_abi():
 @pytest.mark.parametrize("quant,layout,nr,nc,bs", [
     ("q4_K", "plain", 16, 1, 1),   # no kernel for the format
     ("q8_0", "x16", 32, 8, 8),     # Q8_0 x16 prefill: no repack GEMM in the reference
-    ("q4_0", "x16", 32, 6, 8),     # Q4_0 x16 prefill with a partial 4-row activation group
-    ("q4_0", "x16", 24, 8, 8),     # Q4_0 x16 prefill with a partial 16-row weight group
+    ("q4_0", "x16", 32, 8, 8),     # Q4_0 x16 prefill: the repack GEMM's own ABI differs
+    ("q4_0", "x16", 32, 6, 8),     # ... with a partial 4-row activation group
     ("q4_0", "x16", 24, 1, 1),     # x16 decode with a partial 16-row group
     ("q8_0", "x16", 32, 1, 4),     # x16 decode into a strided output
 ])
@@ -230,17 +230,22 @@ def test_routed_contractions_match_the_oracle(oracle, dev):
         assert packed.size == nr // 16 * nb * xbytes
         assert_f32_parity(from_dev(s), ref(n, packed, x, nr), what=f"routed {quant} x16")
 
-    # prefill over x16 Q4_0 weights -> the repack GEMM (x4 activations, output
-    # activation-row major)
+    # prefill over x16 Q4_0 weights: the selection names the repack GEMM, which
+    # the caller runs in its own ABI (x4 activations, output activation-row
+    # major); the GEMM-ABI call refuses it and writes nothing
     nc = 8
     plain = synth.q4_0_matrix(nr, n, 1006, 0.02)
     src = plain.reshape(nr // 16, 16, nb, 18).transpose(0, 2, 1, 3).reshape(-1)
     packed = oracle.pack_q4_0x16(np.ascontiguousarray(src), nr // 16 * nb)
     a8 = synth.q8_0_matrix(nc, n, 1008, 1.0)
     ax4 = oracle.pack_q8_0x4(a8, nc, nb, a8.shape[1])
-    s = empty_dev(nc * nr, torch.float32, dev)
-    _, algo = tcrv_hip.route_contraction("q4_0", "x16", n, s, to_dev(packed, dev),
-                                         to_dev(ax4, dev), 0, nr, nc, 0, nr)
-    assert algo == "repack_gemm"
+    s = to_dev(np.full(nc * nr, -5.0, np.float32), dev)
+    st, algo = tcrv_hip.route_contraction("q4_0", "x16", n, s, to_dev(packed, dev),
+                                          to_dev(ax4, dev), 0, nr, nc, 0, nr, check=False)
+    assert (st, algo) == (tcrv_hip.ERR_UNSUPPORTED, "repack_gemm")
+    assert np.all(from_dev(s) == -5.0)
+    algo, _, entry = tcrv_hip.route_select("q4_0", tcrv_hip.M_PREFILL, "x16")
+    assert (algo, entry) == ("repack_gemm", "tcrv_hip_repack_gemm_q4_0_q8_0")
+    tcrv_hip.repack_gemm_q4_0_q8_0(n, s, to_dev(packed, dev), to_dev(ax4, dev), nc, nr, nr)
     assert_f32_parity(from_dev(s), oracle.repack_gemm_q4_0(n, packed, ax4, nc, nr, nr),
-                      what="routed q4_0 x16 prefill")
+                      what="selected q4_0 x16 prefill entry")

@@ -347,13 +347,10 @@ int tcrv_hip_route_contraction(int weight_quant, int weight_layout, size_t n, fl
     return q4 ? tcrv_hip_repack_gemv_q4_0_q8_0(n, s, vx, vy, nr, stream)
               : tcrv_hip_repack_gemv_q8_0_q8_0(n, s, vx, vy, nr, stream);
   case HipContractionAlgorithm::RepackGemm:
-    // the op's own contract: nc activation rows in nc/4 block_q8_0x4 groups,
-    // output s[col*bs + ir]; shapes that would leave groups unwritten are refused
-    if (nr == 0 || nc == 0)
-      return TCRV_HIP_OK;
-    if (nr % 16 != 0 || nc % 4 != 0)
-      return TCRV_HIP_ERR_UNSUPPORTED;
-    return tcrv_hip_repack_gemm_q4_0_q8_0(n, s, vx, vy, nc, nr, bs, stream);
+    // the selected kernel has a different contract from this call's GEMM ABI
+    // (block_q8_0x4 activations, activation-row-major output s[col*bs + ir]):
+    // refused here, the caller runs sel.entry in its own ABI
+    return TCRV_HIP_ERR_UNSUPPORTED;
   case HipContractionAlgorithm::DecodeGemv:
   case HipContractionAlgorithm::MfmaGemm:
     return q4 ? tcrv_hip_q4_0_q8_0_gemm(n, s, vx, vy, by, nr, nc, bx, bs, stream)

@@ -10,7 +10,8 @@
       median per dispatch of every counter of one multi-counter pass, per
       matching kernel
   rocprof_summary.py traffic <pmc-root>
-      HBM bytes per dispatch of the GEMV and GEMM kernels from the two
+      HBM bytes per dispatch of the GEMV and GEMM kernels (plain and tiled
+      GEMM, and the GEMM-tile pack) from the two
       counter passes (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled by
       what the same counter reads for the known-size calibration kernel
       (add_f32 over n = 2^24: 128 MiB read, 64 MiB written per launch).
@@ -29,6 +30,8 @@ import sys
 KERNELS = {
     "gemv_q4_0_q8_0": "gemv_q4_0_q8_0_direct",
     "q8_0_q8_0_gemm": "gemm_wide<false>",
+    "q8_0_q8_0_gemm_tiles": "gemm_tiles_q8<true>",
+    "pack_q8_0_to_gemm_tiles": "pack_gemm_tiles<true>",
     "calib": "add_f32_vec4",
 }
 CALIB_BYTES = {"FETCH_SIZE": 8 << 24, "WRITE_SIZE": 4 << 24}  # per add_f32 launch, n = 2^24
@@ -114,7 +117,8 @@ def traffic(root):
         scale[ctr] = known / (kib * 1024.0)
         out[f"calib_{ctr}"] = {"KiB_per_dispatch": kib, "dispatches": n, "known_bytes": known,
                                "scale": scale[ctr]}
-    for key, tag in (("gemv_q4_0_q8_0", "gemv"), ("q8_0_q8_0_gemm", "gemm")):
+    for key, tag in (("gemv_q4_0_q8_0", "gemv"), ("q8_0_q8_0_gemm", "gemm"),
+                     ("q8_0_q8_0_gemm_tiles", "gemm"), ("pack_q8_0_to_gemm_tiles", "gemm")):
         total = 0.0
         entry = {"kernel": KERNELS[key]}
         for ctr in CALIB_BYTES:
