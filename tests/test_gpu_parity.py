@@ -791,8 +791,13 @@ def tiles_reference(a, nrows, nb):
     return rec.reshape(-1)
 
 
-@pytest.mark.parametrize("nrows,nb,pad,off", [(64, 1, 0, 0), (100, 9, 16, 0), (130, 7, 0, 2),
-                                              (5, 4, 2, 2)])
+@pytest.mark.parametrize("nrows,nb,pad,off", [
+    (64, 1, 0, 0), (100, 9, 16, 0), (130, 7, 0, 2), (5, 4, 2, 2),  # the per-record kernel
+    (128, 16, 0, 0),   # 16-byte aligned rows: the 8-block span kernel only
+    (70, 11, 10, 0),   # spans for blocks 0-7, the per-record kernel for 8-10, partial group
+    (200, 24, 16, 0),  # padded 16-byte stride, 3 spans, partial last group
+    (1, 8, 0, 0),      # one row
+])
 def test_pack_q8_0_to_gemm_tiles(hip, dev, nrows, nb, pad, off):
     a = np.pad(synth.q8_0_matrix(nrows, nb * 32, 80, 1.0), ((0, 0), (0, pad)))
     want = tiles_reference(a, nrows, nb)
@@ -811,6 +816,7 @@ def test_pack_q8_0_to_gemm_tiles(hip, dev, nrows, nb, pad, off):
     (520, 257, 13, 0, 4),     # three tile rows, 3 chunks + 1 block
     (256, 2, 1, 0, 0),        # one block: only the partial chunk
     (640, 384, 130, 0, 0),    # 32 chunks + 2 blocks, groups past the last one re-read
+    (512, 200, 128, 0, 0),    # 16-byte aligned rows: both operands packed by 8-block spans
 ])
 def test_q8_0_gemm_tiles_and_ws(hip, oracle, dev, nr, nc, nb, xpad, ypad):
     n = nb * 32
