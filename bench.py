@@ -7,10 +7,14 @@ peak)".  `value` is the first half: the Q4_0 x Q8_0 decode GEMV, W 4096 x 4096
 decode pass over a stack of LAYERS distinct 4096 x 4096 Q4_0 weight matrices
 (the configs[3] matrix, copied): LAYERS GEMV launches, each reading its own
 matrix, 605 MB per step -- more than the 256 MB Infinity Cache, so every launch
-reads its weights from HBM whatever --steps is.  The second half, the Q8_0 x
-Q8_0 GEMM 4096^3, is timed in the same run and reported under
-"gemm"; configs[0..2] (add, dequant, block dot) and the other kernels are
-reported under "configs".
+reads its weights from HBM whatever --steps is; the steps run in HIP graphs of
+at most 32 steps, and the median of GEMV_REGIONS timed regions of --steps steps
+is reported with its min and max.  The second half, the Q8_0 x Q8_0 GEMM 4096^3
+(configs[4]) in the reference ABI through the workspace entry
+tcrv_hip_q8_0_q8_0_gemm_ws, is timed in the same run and reported under "gemm"
+beside the plain entry, pre-packed weights and the tiled kernel alone;
+configs[0..2] (add, dequant, block dot) and the other kernels are reported
+under "configs".
 
 Timing: inputs are synthetic (tianchen-rv_amd/synth.py seeds) and resident in
 HBM before a timed region starts.  A region is a HIP graph of launches,
@@ -22,7 +26,7 @@ from HBM, and times at least as many launches as it has sets.
 
 cpu_baseline: the scalar C oracle (oracle/, the CPU restatement of the
 reference emitters) timed on the host cores over a bounded sample of the same
-GEMV workload.
+GEMV workload, on all host threads and on one, with the host recorded.
 """
 from __future__ import annotations
 
@@ -40,6 +44,7 @@ INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published
 N = 4096
 MALL_BYTES = 256 << 20       # Infinity Cache
 LAYERS = 64                  # GEMV launches (distinct weight matrices) per step: 605 MB
+GEMV_REGIONS = 3             # timed regions of --steps steps each; the median is reported
 HOST_COPIES = 48             # CPU-baseline GEMV weight copies (453 MB > host last-level cache)
 
 METRIC = "Q4_0 GEMV GB/s (% HBM peak); Q8_0 GEMM int8 TOPS (% MFMA peak)"
@@ -201,26 +206,33 @@ def bench_gemv(torch, lib, stream, args):
     for g, _ in graphs:  # one untimed replay of each graph
         g.run()
     yd.zero_()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        e0.record(stream)
-        for g, reps in graphs:
-            for _ in range(reps):
-                g.graph.replay()
-        e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1)
+    region_ms = []
+    for _ in range(GEMV_REGIONS):  # each region replays every graph once
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            for g, reps in graphs:
+                for _ in range(reps):
+                    g.graph.replay()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        region_ms.append(e0.elapsed_time(e1))
     same_as_eager(torch, stream, yd[0], lambda out: fn(N, out, wp[0], bx, xd.data_ptr(), N, sp),
                   "GEMV")
+    region_ms.sort()
+    ms = region_ms[len(region_ms) // 2]
     launches = steps * LAYERS
     us = ms * 1e3 / launches
     gbs = GEMV_BYTES / (us * 1e-6) / 1e9
     log(f"GEMV {us:.3f} us/launch over {launches} launches ({steps} steps of {LAYERS} "
-        f"weight matrices): {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+        f"weight matrices; median of {GEMV_REGIONS} regions, min "
+        f"{region_ms[0] * 1e3 / launches:.3f}, max {region_ms[-1] * 1e3 / launches:.3f}): "
+        f"{gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
     return {"us": us, "gbs": gbs, "copies": copies, "ms_region": ms, "launches": launches,
-            "steps": steps, "ms_per_step": ms / steps,
+            "steps": steps, "ms_per_step": ms / steps, "regions": GEMV_REGIONS,
+            "us_min": region_ms[0] * 1e3 / launches, "us_max": region_ms[-1] * 1e3 / launches,
             "bytes_touched_per_step": copies * (w.size + N * 4) + x.size}
 
 
@@ -893,7 +905,10 @@ def main():
                                f"matrices (a decode pass), 605 MB > the 256 MB Infinity Cache",
                    "rows": N, "cols": N, "launches_per_step": LAYERS,
                    "launches_timed": g.get("launches"),
-                   "launch": "HIP graphs of up to 32 steps, each replayed once untimed first",
+                   "launch": "HIP graphs of up to 32 steps, each replayed once untimed first; "
+                             "the median of 3 timed regions, each replaying every graph once",
+                   "us_min": round(g["us_min"], 4) if "us_min" in g else None,
+                   "us_max": round(g["us_max"], 4) if "us_max" in g else None,
                    "bytes_touched_per_step": g.get("bytes_touched_per_step")},
     }
     traffic_src = ("stored figure from profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE and "

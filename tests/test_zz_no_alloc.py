@@ -67,3 +67,36 @@ def test_noalloc_refuses_a_workspace_beyond_its_scratch(hip, dev):
     assert "scratch" in hip.status_string(st)
     torch.cuda.synchronize()
     assert bool(torch.all(s == -3.0))  # nothing was launched
+
+
+def test_noalloc_under_graph_capture(hip, oracle, dev):
+    """The callers it is for: a HIP graph captures the entry (after one eager
+    call on the device, which looks up the scratch address); every replay,
+    with eager work and synchronizations between replays, equals the eager
+    result bit for bit."""
+    nr, nc, nb = 300, 70, 9
+    n = nb * 32
+    w = synth.q8_0_matrix(nr, n, 1207, 0.02)
+    a = synth.q8_0_matrix(nc, n, 1208, 1.0)
+    dw, da = to_dev(w, dev), to_dev(a, dev)
+    eager = empty_dev(nr * nc, torch.float32, dev)
+    hip.q8_0_q8_0_gemm_noalloc(n, eager, dw, da, a.shape[1], nr, nc, w.shape[1], nc)
+    torch.cuda.synchronize()
+    want = oracle.gemm_q8_0(n, w, a, a.shape[1], nr, nc, w.shape[1], nc, 8)
+    assert_f32_parity(from_dev(eager), want, what="noalloc eager")
+    out = torch.full((nr * nc,), -3.0, dtype=torch.float32, device=dev)
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            hip.q8_0_q8_0_gemm_noalloc(n, out, dw, da, a.shape[1], nr, nc, w.shape[1], nc,
+                                       stream=stream)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        out.fill_(-3.0)
+        # eager work between replays, on the same device's scratch
+        hip.q8_0_q8_0_gemm_noalloc(n, eager, dw, da, a.shape[1], nr, nc, w.shape[1], nc)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), eager.view(torch.int32)), f"replay {rep}"
