@@ -20,16 +20,24 @@ namespace tcrv {
 
 constexpr int kTG = 64;                        // rows per tile group
 constexpr int kTRec = 2 * kTG * 16 + kTG * 2;  // 2176 bytes per (group, block) record
-constexpr int kDBM = 256, kDBN = 128, kDKB = 4;   // work-group tile, blocks per K chunk
+// K chunk and LDS stages, 4096^3 on one box (us): 6 blocks x 2 stages 163.7-164.4,
+// 5 x 2 163.5, 4 x 3 169.7-170.5, 3 x 3 174.9: one chunk in flight covers the DMA
+// latency, and longer chunks meet at fewer barriers.
+constexpr int kDBM = 256, kDBN = 128, kDKB = 6;  // work-group tile, blocks per K chunk
 constexpr int kDRows = kDBM + kDBN;               // 384 staged rows
 constexpr int kDHalf = kDRows * 16;               // 6144: one half of one block, all rows
 constexpr int kDBlock = 2 * kDHalf;               // 12288: both halves of one block
-constexpr int kDStage = kDKB * kDBlock;           // 49152 quant bytes per stage
+constexpr int kDStage = kDKB * kDBlock;           // 73728 quant bytes per stage
 constexpr int kDHRow = kDRows + 32;               // fp16 scales per block row (+32 zero rows)
 constexpr int kDThreads = 1024;
-constexpr int kDQuantDma = kDKB * 2 * (kDRows / kTG);  // 48 quant DMA instructions per chunk
+constexpr int kDQuantDma = kDKB * 2 * (kDRows / kTG);  // 72 quant DMA instructions per chunk
 constexpr int kDDma = kDQuantDma + kDKB;               // + one scale instruction per block
-constexpr int kDStages = 3;  // chunks c+1 and c+2 in flight while chunk c is folded
+constexpr int kDStages = 2;  // chunks c+1 .. c+kDStages-1 in flight while chunk c is
+                             // folded (2 or 3)
+constexpr int kDSlots = (kDDma + 15) / 16;   // DMA instructions per wave and chunk
+static_assert(kDStages == 2 || kDStages == 3, "prefetch distance 1 or 2");
+static_assert(kDStages * (kDKB * 12288 + kDKB * (kDBM + kDBN + 32) * 2) <= 160 * 1024,
+              "the stages fit the 160 KB of LDS");
 
 // ---------------------------------------------------------------- pack ---
 // Rows 16-byte aligned (and bx % 16 == 0): one wave per (group, 8-block range),
@@ -147,19 +155,20 @@ __global__ __launch_bounds__(256) void pack_gemm_tiles(size_t nrows, size_t nb,
 // ---------------------------------------------------------------- GEMM ---
 typedef __attribute__((address_space(3))) void lds_void;
 
-// The DMA of one K chunk is kDDma wave instructions: j < 48 moves half h of
-// block b of one 64-row group (A groups 0-3, B groups 4-5) -- 1 KB, lane l its
-// 16 bytes of row l; j >= 48 the scales of block j-48 of all six groups (48
-// lanes, 16 bytes each).  Wave w issues j = w, w+16, w+32, w+48: its "slots",
-// whose source addresses (chunk 0) and LDS offsets (stage 0) are computed once;
+// The DMA of one K chunk is kDDma wave instructions: j < kDQuantDma moves
+// half h of block b of one 64-row group (A groups 0-3, B groups 4-5) -- 1 KB,
+// lane l its 16 bytes of row l; j >= kDQuantDma the scales of block
+// j - kDQuantDma of all six groups (48 lanes, 16 bytes each).  Wave w issues
+// j = w, w+16, w+32, ... (kDSlots of them): its "slots", whose source
+// addresses (chunk 0) and LDS offsets (stage 0) are computed once;
 // chunk c adds c*kDKB records, stage st a fixed offset.  Groups past the
 // operand's last one re-read the last (their outputs are not stored).
 struct DmaSlots {
-  const uint8_t *src[4];  // this lane's 16 source bytes, chunk 0
-  lds_void *dst[4];       // the slot's LDS destination, stage 0 (wave-uniform)
-  int stage_bytes[4];     // LDS bytes from stage 0 to stage 1
-  int blk[4];             // block of the chunk the slot moves
-  bool on[4];             // this lane takes part (scale slots use 48 lanes)
+  const uint8_t *src[kDSlots];  // this lane's 16 source bytes, chunk 0
+  lds_void *dst[kDSlots];       // the slot's LDS destination, stage 0 (wave-uniform)
+  int stage_bytes[kDSlots];     // LDS bytes from stage 0 to stage 1
+  int blk[kDSlots];             // block of the chunk the slot moves
+  bool on[kDSlots];             // this lane takes part (scale slots use 48 lanes)
 };
 
 __device__ __forceinline__ void dma_slots(DmaSlots &d, int8_t *qs, uint16_t *dsh,
@@ -171,7 +180,7 @@ __device__ __forceinline__ void dma_slots(DmaSlots &d, int8_t *qs, uint16_t *dsh
                  : ty + (min(gy0 + (g - 4), ngy - 1) * nb + b) * kTRec;
   };
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < kDSlots; ++k) {
     const int j = min(wave + 16 * k, kDDma - 1);  // slots past kDDma are never issued
     if (j < kDQuantDma) {
       const int b = j / 12, h = (j / 6) & 1, g = j % 6;
@@ -199,7 +208,7 @@ __device__ __forceinline__ int dma_chunk(const DmaSlots &d, size_t c, int nbc, i
   const size_t coff = c * kDKB * kTRec;
   int issued = 0;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < kDSlots; ++k) {
     if (wave + 16 * k < kDDma && d.blk[k] < nbc) {
       if (d.on[k])
         __builtin_amdgcn_global_load_lds(d.src[k] + coff,
@@ -225,15 +234,18 @@ __device__ __forceinline__ void wait_dma_barrier(int pending) {
   case 1: __builtin_amdgcn_s_waitcnt(0x071); break;
   case 2: __builtin_amdgcn_s_waitcnt(0x072); break;
   case 3: __builtin_amdgcn_s_waitcnt(0x073); break;
-  default: __builtin_amdgcn_s_waitcnt(0x074); break;
+  case 4: __builtin_amdgcn_s_waitcnt(0x074); break;
+  case 5: __builtin_amdgcn_s_waitcnt(0x075); break;
+  case 6: __builtin_amdgcn_s_waitcnt(0x076); break;
+  default: __builtin_amdgcn_s_waitcnt(0x077); break;
   }
   __builtin_amdgcn_s_barrier();
 }
 
 // Work-group: 256 weight rows x 128 tokens, 16 waves, each wave two 32x32
-// tiles stacked in M (64 weight rows x 32 tokens); K chunks of 4 blocks in
-// three LDS stages: the DMA of chunks c+1 and c+2 is in flight while chunk c
-// is folded, and the barrier after chunk c waits only for chunk c+1's.
+// tiles stacked in M (64 weight rows x 32 tokens); K chunks of kDKB blocks in
+// kDStages LDS stages: the DMA of the next kDStages-1 chunks is in flight while
+// chunk c is folded, and the barrier after chunk c waits for chunk c+1's.
 template <bool kPipe>
 __global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q8(size_t nb, float *s,
                                                               const uint8_t *tx,
@@ -271,8 +283,9 @@ __global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q8(size_t nb, float *
   };
   DmaSlots slots;
   dma_slots(slots, qs, dsh, tx, ty, gx0, ngx, gy0, ngy, nb, wave, lane);
+  constexpr int kAhead = kDStages - 1;  // chunks in flight beyond the one folded
   dma_chunk(slots, 0, blocks_of(0), 0, wave);
-  int pending = nchunks > 1 ? dma_chunk(slots, 1, blocks_of(1), 1, wave) : 0;
+  int pending = kAhead > 1 && nchunks > 1 ? dma_chunk(slots, 1, blocks_of(1), 1, wave) : 0;
   wait_dma_barrier(pending);  // chunk 0 is in LDS, the zero rows written
 
   // this lane's operands in stage 0, block 0, for the wave's first tile
@@ -285,13 +298,16 @@ __global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q8(size_t nb, float *
 
   int st = 0;  // stage of chunk c
   for (size_t c = 0; c < nfull; ++c) {
-    const int st2 = st == 0 ? 2 : st - 1;  // (c + 2) % 3
-    pending = c + 2 < nchunks ? dma_chunk(slots, c + 2, blocks_of(c + 2), st2, wave) : 0;
+    const int sta = st + kAhead >= kDStages ? st + kAhead - kDStages : st + kAhead;
+    pending = c + kAhead < nchunks
+                  ? dma_chunk(slots, c + kAhead, blocks_of(c + kAhead), sta, wave)
+                  : 0;
     fold_chunk_q8<kPipe, kDKB, kDBlock, 32 * 16, kDHRow>(
         acc, qa0 + st * kDStage, qb0 + st * kDStage, hx0 + st * kHStage, hx1 + st * kHStage,
         hy + st * kHStage, [](int) {});
-    wait_dma_barrier(pending);  // chunk c+1 is in LDS
-    st = st == 2 ? 0 : st + 1;
+    // chunk c+1 is in LDS: with one chunk ahead it is the newest DMA
+    wait_dma_barrier(kAhead > 1 ? pending : 0);
+    st = st + 1 == kDStages ? 0 : st + 1;
   }
   const int nbc = static_cast<int>(nb - nfull * kDKB);
   if (nbc > 0)
