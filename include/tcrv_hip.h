@@ -255,6 +255,23 @@ TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm_noalloc(size_t n, float *s, const uint8
                                                  const uint8_t *vy, size_t by, size_t nr,
                                                  size_t nc, size_t bx, size_t bs, void *stream);
 
+/* ---- a7 over the GEMM-tile layout (no reference counterpart) --------------
+ * Q4_0 weight rows in the same 2176-byte records, their nibbles decoded to the
+ * signed quants (q - 8) in element order: quants 0-15 are the low nibbles of a
+ * block's 16 bytes, quants 16-31 the high ones; the fp16 scale is copied.
+ * tcrv_hip_gemm_tiles_bytes gives the size.  Plain Q4_0 rows (stride bx, 2-byte
+ * aligned) -> dst (16-byte aligned): */
+TCRV_HIP_API int tcrv_hip_pack_q4_0_to_gemm_tiles(size_t nrows, size_t nb, const uint8_t *src,
+                                                  size_t bx, uint8_t *dst, void *stream);
+/* The Q4_0 x Q8_0 GEMM over tx (Q4_0 weights packed as above) and ty (Q8_0
+ * tokens packed by tcrv_hip_pack_q8_0_to_gemm_tiles): s[ir*bs + col] exactly as
+ * tcrv_hip_q4_0_q8_0_gemm computes it from the plain rows.  For weights packed
+ * once; there is no workspace form, since packing both operands per call costs
+ * more than the tiled kernel saves over tcrv_hip_q4_0_q8_0_gemm. */
+TCRV_HIP_API int tcrv_hip_q4_0_q8_0_gemm_tiles(size_t n, float *s, const uint8_t *tx,
+                                               const uint8_t *ty, size_t nr, size_t nc,
+                                               size_t bs, void *stream);
+
 /* ---- a8: the x16 block-as-lane weight layout ---------------------------
  * Replaces tcrv_emitc_..._pack_q4_0_to_q4_0x16(size_t nblocks, const uint8_t *src,
  * uint8_t *dst) (test/Conversion/RVV/rvv-to-emitc-pack-q4-0-to-q4-0x16.mlir:

@@ -49,3 +49,17 @@ def assert_f32_parity_nan(got: np.ndarray, want: np.ndarray, what: str = ""):
     diff = np.flatnonzero(got[ok].view(np.uint32) != want[ok].view(np.uint32))
     assert diff.size == 0, (f"{what}: {diff.size} elements not bit-identical; first: got "
                             f"{got[ok][diff[0]]!r} want {want[ok][diff[0]]!r}")
+
+
+def q4_tiles_gemm(hip, dev, n, w, a, nr, nc, bs, s):
+    """The Q4_0 x Q8_0 GEMM through the GEMM-tile layout: both operands packed
+    (tcrv_hip_pack_q4_0_to_gemm_tiles, tcrv_hip_pack_q8_0_to_gemm_tiles), then
+    tcrv_hip_q4_0_q8_0_gemm_tiles into the device buffer s."""
+    import torch
+    nb = n // 32
+    tx = empty_dev(hip.gemm_tiles_bytes(nr, nb), torch.uint8, dev)
+    ty = empty_dev(hip.gemm_tiles_bytes(nc, nb), torch.uint8, dev)
+    hip.pack_q4_0_to_gemm_tiles(nr, nb, to_dev(w, dev), w.shape[1], tx)
+    hip.pack_q8_0_to_gemm_tiles(nc, nb, to_dev(a, dev), a.shape[1], ty)
+    hip.q4_0_q8_0_gemm_tiles(n, s, tx, ty, nr, nc, bs)
+    return s

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 import synth
-from gpu_util import assert_f32_parity, empty_dev, from_dev, to_dev
+from gpu_util import assert_f32_parity, empty_dev, from_dev, q4_tiles_gemm, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -891,4 +891,96 @@ def test_q8_0_gemm_ws_full_size_sampled(hip, oracle, dev):
     cols = np.sort(rng.choice(nc, 64, replace=False))
     sub = np.ascontiguousarray(a[cols])
     want = oracle.gemm_q8_0(n, w, sub, sub.shape[1], nr, len(cols), w.shape[1], len(cols), 8)
+    assert_f32_parity(got[:, cols], want.reshape(nr, len(cols)), what="sampled cols")
+
+
+# ------------------------------------ a7 Q4_0 x Q8_0 over the GEMM-tile layout ---
+
+def q4_tiles_reference(w, nrows, nb):
+    """The Q4_0 records of the GEMM-tile layout built in numpy from plain Q4_0
+    rows: each nibble decoded to (q - 8) as an int8 byte, element j < 16 from the
+    low nibble of quant byte j, element 16 + j from its high nibble; the fp16
+    scale bytes copied; rows past nrows zero."""
+    blocks = w[:nrows, :nb * 18].reshape(nrows, nb, 18)
+    q = blocks[..., 2:18].astype(np.int16)
+    q8 = np.zeros((nrows, nb, 34), np.uint8)
+    q8[..., 0:2] = blocks[..., 0:2]
+    q8[..., 2:18] = ((q & 0x0F) - 8).astype(np.int8).view(np.uint8)
+    q8[..., 18:34] = ((q >> 4) - 8).astype(np.int8).view(np.uint8)
+    return tiles_reference(q8.reshape(nrows, nb * 34), nrows, nb)
+
+
+@pytest.mark.parametrize("nrows,nb,pad,off", [
+    (64, 1, 0, 0), (100, 9, 14, 0), (130, 7, 0, 2), (5, 4, 2, 2),
+    (128, 16, 0, 0),   # 4096-wide-style rows: 16-byte aligned every 8 blocks
+    (70, 11, 10, 0), (200, 24, 16, 0), (1, 8, 0, 0),
+])
+def test_pack_q4_0_to_gemm_tiles(hip, dev, nrows, nb, pad, off):
+    w = np.pad(synth.q4_0_matrix(nrows, nb * 32, 90, 1.0), ((0, 0), (0, pad)))
+    w[0, 2:18] = np.arange(16, dtype=np.uint8) * 0x11  # every nibble value, both halves
+    want = q4_tiles_reference(w, nrows, nb)
+    assert hip.gemm_tiles_bytes(nrows, nb) == want.size
+    buf = empty_dev(w.size + 16, torch.uint8, dev)
+    buf[off:off + w.size] = to_dev(w.reshape(-1), dev)
+    dst = to_dev(np.full(want.size, 0xEE, np.uint8), dev)
+    hip.pack_q4_0_to_gemm_tiles(nrows, nb, buf[off:off + w.size], w.shape[1], dst)
+    assert np.array_equal(from_dev(dst), want)
+
+
+@pytest.mark.parametrize("nr,nc,nb,xpad,ypad", [
+    (256, 128, 6, 0, 0),      # one tile, one chunk
+    (256, 128, 12, 0, 0),     # two chunks
+    (300, 130, 9, 14, 32),    # partial tiles both ways, 1 chunk + 3 blocks, padded strides
+    (520, 257, 13, 0, 4),     # three tile rows, 2 chunks + 1 block
+    (256, 2, 1, 0, 0),        # one block: only the partial chunk
+    (640, 384, 130, 0, 0),    # 21 chunks + 4 blocks
+    (512, 200, 128, 0, 0),    # 16-byte aligned rows: both operands packed by 8-block spans
+    (100, 70, 9, 0, 0),       # fewer weight rows and tokens than one work-group tile
+    (300, 1, 8, 0, 0),        # one token
+    (1, 40, 8, 0, 0),         # one weight row
+])
+def test_q4_0_gemm_tiles(hip, oracle, dev, nr, nc, nb, xpad, ypad):
+    n = nb * 32
+    w = np.pad(synth.q4_0_matrix(nr, n, 1019, 0.02), ((0, 0), (0, xpad)))
+    a = np.pad(synth.q8_0_matrix(nc, n, 1018, 1.0), ((0, 0), (0, ypad)))
+    w[0, 2:18] = 0x00
+    a[0, 2:34] = 0x80  # -8 x -128 block sums
+    bs = nc + 3
+    want = oracle.gemm_q4_0(n, w, a, a.shape[1], nr, nc, w.shape[1], bs, 8).reshape(nr, bs)
+    s = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+    got = from_dev(q4_tiles_gemm(hip, dev, n, w, a, nr, nc, bs, s)).reshape(nr, bs)
+    assert_f32_parity(got[:, :nc], want[:, :nc], what=f"q4 tiles gemm {nr}x{nc}x{n}")
+    assert np.all(got[:, nc:] == -7.0)
+
+
+def test_q4_0_gemm_tiles_checks(hip, dev):
+    """No blocks: zero outputs; misaligned tiles or a short output stride are
+    refused before anything launches."""
+    nr, nc, nb = 256, 16, 8
+    tx = empty_dev(hip.gemm_tiles_bytes(nr, nb) + 16, torch.uint8, dev)
+    ty = empty_dev(hip.gemm_tiles_bytes(nc, nb), torch.uint8, dev)
+    s = to_dev(np.full(nr * nc, 3.0, np.float32), dev)
+    hip.q4_0_q8_0_gemm_tiles(31, s, tx, ty, nr, nc, nc)  # n < 32: no blocks
+    assert np.all(from_dev(s) == 0.0)
+    call = lambda *args: hip.call("tcrv_hip_q4_0_q8_0_gemm_tiles", *args, 0, check=False)
+    assert call(nb * 32, s, tx[8:], ty, nr, nc, nc) == hip.ERR_MISALIGNED
+    assert call(nb * 32, s, tx, ty, nr, nc, nc - 1) == hip.ERR_BAD_SIZE
+    torch.cuda.synchronize()
+
+
+def test_q4_0_gemm_tiles_full_size_sampled(hip, oracle, dev):
+    """4096 x 4096 x 4096 Q4_0 x Q8_0 through the GEMM-tile layout; 64 rows
+    and 64 columns checked against the oracle."""
+    n = nr = nc = 4096
+    w = synth.q4_0_matrix(nr, n, 1006, 0.02)
+    a = synth.q8_0_matrix(nc, n, 1008, 1.0)
+    s = empty_dev(nr * nc, torch.float32, dev)
+    got = from_dev(q4_tiles_gemm(hip, dev, n, w, a, nr, nc, nc, s)).reshape(nr, nc)
+    rng = np.random.default_rng(13)
+    for r in np.sort(rng.choice(nr, 64, replace=False)):
+        want = oracle.gemm_q4_0(n, w[r].copy(), a, a.shape[1], 1, nc, w.shape[1], nc, 8)
+        assert_f32_parity(got[r], want, what=f"row {r}")
+    cols = np.sort(rng.choice(nc, 64, replace=False))
+    sub = np.ascontiguousarray(a[cols])
+    want = oracle.gemm_q4_0(n, w, sub, sub.shape[1], nr, len(cols), w.shape[1], len(cols), 8)
     assert_f32_parity(got[:, cols], want.reshape(nr, len(cols)), what="sampled cols")

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import synth
-from gpu_util import assert_f32_parity_nan, empty_dev, from_dev, to_dev
+from gpu_util import assert_f32_parity_nan, empty_dev, from_dev, q4_tiles_gemm, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -98,6 +98,39 @@ def test_q4_0_gemm_special_scales(hip, oracle, dev, nr, nc, nb):
     hip.q4_0_q8_0_gemm(n, s, to_dev(w, dev), to_dev(a, dev), a.shape[1], nr, nc, w.shape[1], nc)
     want = oracle.gemm_q4_0(n, w, a, a.shape[1], nr, nc, w.shape[1], nc, 8)
     assert_f32_parity_nan(from_dev(s), want, what=f"q4 gemm {nr}x{nc}x{n}")
+
+
+def test_q4_0_gemm_tiles_special_scales(hip, oracle, dev):
+    """The DMA-staged tiled Q4_0 GEMM over the GEMM-tile layout."""
+    nr, nc, nb = 300, 130, 9
+    n = nb * 32
+    w = q4(nr, nb, 33, nonfinite_every=16)
+    a = q8(nc, nb, 34, 1.0, nonfinite_every=23)
+    s = q4_tiles_gemm(hip, dev, n, w, a, nr, nc, nc, empty_dev(nr * nc, torch.float32, dev))
+    want = oracle.gemm_q4_0(n, w, a, a.shape[1], nr, nc, w.shape[1], nc, 8)
+    assert_f32_parity_nan(from_dev(s), want, what="q4 gemm tiles")
+
+
+def test_q4_0_gemm_tiles_nonfinite_dx_mid_k(hip, oracle, dev):
+    """The tiled Q4_0 GEMM folds each 6-block chunk in a fast form that is exact
+    only for finite d_x, switching a wave to the exact form from the first chunk
+    whose d_x holds a non-finite value: +-Inf planted at the first chunk, in
+    the middle of K, in the last full chunk and in the partial tail, NaN, and an
+    infinite d_x over a zero block sum (0 * Inf = NaN)."""
+    nr, nc, nb = 512, 256, 40  # 6 full chunks + 4 tail blocks
+    n = nb * 32
+    w = q4(nr, nb, 41)
+    a = q8(nc, nb, 42, 1.0, nonfinite_every=37)
+    for r, b, bits in ((70, 20, 0x7C00), (130, 0, 0xFC00), (200, 37, 0x7E00),
+                       (330, 35, 0x7C00), (400, 10, 0xFC00), (450, 29, 0x7C00)):
+        _set_scale(w, r, b, 18, bits)
+    w[400, 10 * 18 + 2:10 * 18 + 18] = 0x88  # every quant q - 8 = 0: block sums 0
+    s = q4_tiles_gemm(hip, dev, n, w, a, nr, nc, nc, empty_dev(nr * nc, torch.float32, dev))
+    want = oracle.gemm_q4_0(n, w, a, a.shape[1], nr, nc, w.shape[1], nc, 8)
+    got = from_dev(s)
+    assert_f32_parity_nan(got, want, what="q4 tiles, non-finite d_x")
+    g = got.reshape(nr, nc)
+    assert np.isinf(g[70]).any() and np.isnan(g[400]).all()  # the planted cases took effect
 
 
 def _x16_source(w, nb, k):

@@ -152,6 +152,108 @@ __global__ __launch_bounds__(256) void pack_gemm_tiles(size_t nrows, size_t nb,
   reinterpret_cast<uint16_t *>(o + 2048)[r] = static_cast<uint16_t>(d);
 }
 
+// Q4_0 rows into the same layout with every nibble decoded to the int8 it
+// stands for (n - 8): quants 0-15 are the low nibbles of the 16 quant bytes,
+// 16-31 the high nibbles.  The subtraction is bytewise and carry-free:
+// n + 0x78 stays below 0x100, and flipping bit 7 maps it to n - 8.
+__device__ __forceinline__ void decode_q4_quants(const uint32_t w[4], uint32_t q[8]) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    q[m] = ((w[m] & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+    q[4 + m] = (((w[m] >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+  }
+}
+
+// Rows 16-byte aligned (bx % 16 == 0): one wave per (group, 8-block span),
+// lane r = row 64g + r; the span is 144 contiguous bytes (9 aligned 128-bit
+// loads), block k at byte 18k.
+__global__ __launch_bounds__(256) void pack_q4_tiles_span(size_t nrows, size_t nb,
+                                                          const uint8_t *src, size_t bx,
+                                                          uint8_t *dst, size_t nspans) {
+  const size_t wave = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
+  const size_t spans_per_group = nb / kPackSpan;
+  if (wave >= nspans)
+    return;
+  const int r = static_cast<int>(threadIdx.x & 63);
+  const size_t g = wave / spans_per_group, c = wave - g * spans_per_group;
+  const size_t row = g * kTG + r;
+  uint32_t v[4 * 9];
+  if (row < nrows) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(src + row * bx + c * kPackSpan * kQ4Bytes);
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+      const uint4 x = p[k];
+      v[4 * k] = x.x; v[4 * k + 1] = x.y; v[4 * k + 2] = x.z; v[4 * k + 3] = x.w;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kPackSpan; ++k) {
+    // even k: the scale is the low half of dword 9k/2, the quants 2 bytes in;
+    // odd k: the high half of dword (18k-2)/4, the quants the next 4 dwords
+    uint32_t w[4] = {0, 0, 0, 0}, d = 0;
+    if (row < nrows) {
+      if ((k & 1) == 0) {
+        const int w0 = 9 * k / 2;
+        d = v[w0] & 0xffffu;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          w[j] = funnel16(v[w0 + j], v[w0 + j + 1]);
+      } else {
+        const int w0 = (18 * k - 2) / 4;
+        d = v[w0] >> 16;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          w[j] = v[w0 + 1 + j];
+      }
+    }
+    uint32_t q[8];
+    decode_q4_quants(w, q);
+    if (row >= nrows) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        q[j] = 0;  // rows past nrows in the last group are zero
+    }
+    uint8_t *o = dst + (g * nb + c * kPackSpan + k) * kTRec;
+    reinterpret_cast<uint4 *>(o)[r] = make_uint4(q[0], q[1], q[2], q[3]);
+    reinterpret_cast<uint4 *>(o + 1024)[r] = make_uint4(q[4], q[5], q[6], q[7]);
+    reinterpret_cast<uint16_t *>(o + 2048)[r] = static_cast<uint16_t>(d);
+  }
+}
+
+// One wave per (group, block) record for blocks b0.. of every group (rows
+// 2-byte aligned: 16-bit loads).
+__global__ __launch_bounds__(256) void pack_q4_tiles(size_t nrows, size_t nb, const uint8_t *src,
+                                                     size_t bx, uint8_t *dst, size_t b0,
+                                                     size_t nrec) {
+  const size_t t = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  const size_t rec = t >> 6;
+  if (rec >= nrec)
+    return;
+  const int r = static_cast<int>(t & 63);
+  const size_t per_group = nb - b0;
+  const size_t g = rec / per_group, b = b0 + (rec - g * per_group);
+  const size_t row = g * kTG + r;
+  uint32_t w[4] = {0, 0, 0, 0}, d = 0;
+  if (row < nrows) {
+    const uint16_t *hp = reinterpret_cast<const uint16_t *>(src + row * bx + b * kQ4Bytes);
+    d = hp[0];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = static_cast<uint32_t>(hp[1 + 2 * j]) | (static_cast<uint32_t>(hp[2 + 2 * j]) << 16);
+  }
+  uint32_t q[8];
+  decode_q4_quants(w, q);
+  if (row >= nrows) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      q[j] = 0;
+  }
+  uint8_t *o = dst + (g * nb + b) * kTRec;
+  reinterpret_cast<uint4 *>(o)[r] = make_uint4(q[0], q[1], q[2], q[3]);
+  reinterpret_cast<uint4 *>(o + 1024)[r] = make_uint4(q[4], q[5], q[6], q[7]);
+  reinterpret_cast<uint16_t *>(o + 2048)[r] = static_cast<uint16_t>(d);
+}
+
 // ---------------------------------------------------------------- GEMM ---
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -159,16 +261,21 @@ typedef __attribute__((address_space(3))) void lds_void;
 // half h of block b of one 64-row group (A groups 0-3, B groups 4-5) -- 1 KB,
 // lane l its 16 bytes of row l; j >= kDQuantDma the scales of block
 // j - kDQuantDma of all six groups (48 lanes, 16 bytes each).  Wave w issues
-// j = w, w+16, w+32, ... (kDSlots of them): its "slots", whose source
-// addresses (chunk 0) and LDS offsets (stage 0) are computed once;
-// chunk c adds c*kDKB records, stage st a fixed offset.  Groups past the
-// operand's last one re-read the last (their outputs are not stored).
+// j = w, w+16, w+32, ... (kDSlots of them): its "slots", whose sources (chunk
+// 0) and LDS offsets (stage 0) are computed once; chunk c adds c*kDKB records,
+// stage st a fixed offset.  Every slot but the last is a quant slot for every
+// wave, so its source is a wave-uniform record half (scalar registers) plus
+// the lane's 16-byte offset; the last slot, a scale slot on some waves, keeps
+// a per-lane address.  Groups past the operand's last one re-read the last
+// (their outputs are not stored).
+static_assert(16 * (kDSlots - 2) + 15 < kDQuantDma, "slots before the last are quant slots");
 struct DmaSlots {
-  const uint8_t *src[kDSlots];  // this lane's 16 source bytes, chunk 0
-  lds_void *dst[kDSlots];       // the slot's LDS destination, stage 0 (wave-uniform)
-  int stage_bytes[kDSlots];     // LDS bytes from stage 0 to stage 1
-  int blk[kDSlots];             // block of the chunk the slot moves
-  bool on[kDSlots];             // this lane takes part (scale slots use 48 lanes)
+  const uint8_t *base[kDSlots - 1];  // quant slots: the record half of chunk 0 (wave-uniform)
+  const uint8_t *last;               // the last slot: this lane's 16 source bytes, chunk 0
+  lds_void *dst[kDSlots];            // the slot's LDS destination, stage 0 (wave-uniform)
+  int stage_bytes[kDSlots];          // LDS bytes from stage 0 to stage 1
+  int blk[kDSlots];                  // block of the chunk the slot moves
+  bool on_last;                      // this lane takes part in the last slot
 };
 
 __device__ __forceinline__ void dma_slots(DmaSlots &d, int8_t *qs, uint16_t *dsh,
@@ -184,19 +291,23 @@ __device__ __forceinline__ void dma_slots(DmaSlots &d, int8_t *qs, uint16_t *dsh
     const int j = min(wave + 16 * k, kDDma - 1);  // slots past kDDma are never issued
     if (j < kDQuantDma) {
       const int b = j / 12, h = (j / 6) & 1, g = j % 6;
-      d.src[k] = record(g, b) + h * 1024 + lane * 16;
+      if (k + 1 < kDSlots)
+        d.base[k] = record(g, b) + h * 1024;
+      else
+        d.last = record(g, b) + h * 1024 + lane * 16;
       // a generic pointer into LDS -> the LDS address space (what the DMA takes)
       d.dst[k] = (lds_void *)(qs + b * kDBlock + h * kDHalf + g * kTG * 16);
       d.stage_bytes[k] = kDStage;
       d.blk[k] = b;
-      d.on[k] = true;
+      if (k + 1 == kDSlots)
+        d.on_last = true;
     } else {
       const int b = j - kDQuantDma;
-      d.src[k] = record(min(lane >> 3, 5), b) + 2048 + (lane & 7) * 16;
+      d.last = record(min(lane >> 3, 5), b) + 2048 + (lane & 7) * 16;
       d.dst[k] = (lds_void *)(dsh + b * kDHRow);
       d.stage_bytes[k] = kDKB * kDHRow * 2;
       d.blk[k] = b;
-      d.on[k] = lane < 48;
+      d.on_last = lane < 48;
     }
   }
 }
@@ -204,17 +315,18 @@ __device__ __forceinline__ void dma_slots(DmaSlots &d, int8_t *qs, uint16_t *dsh
 // Issues this wave's DMA of K chunk c (nbc blocks) into stage st; returns
 // how many DMA instructions it issued.
 __device__ __forceinline__ int dma_chunk(const DmaSlots &d, size_t c, int nbc, int st,
-                                         int wave) {
+                                         int wave, int lane) {
   const size_t coff = c * kDKB * kTRec;
   int issued = 0;
 #pragma unroll
   for (int k = 0; k < kDSlots; ++k) {
     if (wave + 16 * k < kDDma && d.blk[k] < nbc) {
-      if (d.on[k])
-        __builtin_amdgcn_global_load_lds(d.src[k] + coff,
-                                         (lds_void *)((char __attribute__((address_space(3))) *)
-                                                          d.dst[k] + st * d.stage_bytes[k]),
-                                         16, 0, 0);
+      lds_void *to = (lds_void *)((char __attribute__((address_space(3))) *)d.dst[k] +
+                                  st * d.stage_bytes[k]);
+      if (k + 1 < kDSlots)
+        __builtin_amdgcn_global_load_lds(d.base[k] + coff + lane * 16, to, 16, 0, 0);
+      else if (d.on_last)
+        __builtin_amdgcn_global_load_lds(d.last + coff, to, 16, 0, 0);
       ++issued;
     }
   }
@@ -246,13 +358,14 @@ __device__ __forceinline__ void wait_dma_barrier(int pending) {
 // tiles stacked in M (64 weight rows x 32 tokens); K chunks of kDKB blocks in
 // kDStages LDS stages: the DMA of the next kDStages-1 chunks is in flight while
 // chunk c is folded, and the barrier after chunk c waits for chunk c+1's.
-template <bool kPipe>
-__global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q8(size_t nb, float *s,
-                                                              const uint8_t *tx,
-                                                              const uint8_t *ty, size_t nr,
-                                                              size_t nc, size_t bs) {
-  __shared__ __align__(16) int8_t qs[kDStages * kDStage];
-  __shared__ __align__(16) uint16_t dsh[kDStages * kDKB * kDHRow];
+// kQ4: the weight tiles (tx) hold Q4_0 rows decoded to int8 (nibble - 8) and
+// the fold is the Q4_0 one, fma(fl((float)sumi * d_x), d_y, acc), on
+// transposed 32x32 tiles (tokens x weights; fold_chunk_q4); otherwise both
+// sides are Q8_0 and the fold is fma((float)sumi, d_x * d_y, acc).
+template <bool kPipe, bool kQ4>
+__device__ __forceinline__ void gemm_tiles_body(size_t nb, float *s, const uint8_t *tx,
+                                                const uint8_t *ty, size_t nr, size_t nc,
+                                                size_t bs, int8_t *qs, uint16_t *dsh) {
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -284,8 +397,8 @@ __global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q8(size_t nb, float *
   DmaSlots slots;
   dma_slots(slots, qs, dsh, tx, ty, gx0, ngx, gy0, ngy, nb, wave, lane);
   constexpr int kAhead = kDStages - 1;  // chunks in flight beyond the one folded
-  dma_chunk(slots, 0, blocks_of(0), 0, wave);
-  int pending = kAhead > 1 && nchunks > 1 ? dma_chunk(slots, 1, blocks_of(1), 1, wave) : 0;
+  dma_chunk(slots, 0, blocks_of(0), 0, wave, lane);
+  int pending = kAhead > 1 && nchunks > 1 ? dma_chunk(slots, 1, blocks_of(1), 1, wave, lane) : 0;
   wait_dma_barrier(pending);  // chunk 0 is in LDS, the zero rows written
 
   // this lane's operands in stage 0, block 0, for the wave's first tile
@@ -296,34 +409,117 @@ __global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q8(size_t nb, float *
   const uint16_t *hy = dsh + (h ? kDRows + li : kDBM + wn * 32 + li);
   constexpr int kHStage = kDKB * kDHRow;
 
+  // the Q4_0 fold (transposed tiles): d_x of the lane's weight row of tile 0,
+  // d_y of its tokens 4h.. (4 of every 8)
+  const uint16_t *qx = dsh + wm * 64 + li;
+  const uint16_t *qy = dsh + kDBM + wn * 32 + 4 * h;
+
   int st = 0;  // stage of chunk c
-  for (size_t c = 0; c < nfull; ++c) {
+  size_t c = 0;
+  // One full chunk: the DMA of chunk c + kAhead is issued, chunk c folded, and
+  // the barrier passed once chunk c + 1 is in LDS (with one chunk ahead it is
+  // the newest DMA).
+  auto chunk = [&](auto fold) {
     const int sta = st + kAhead >= kDStages ? st + kAhead - kDStages : st + kAhead;
     pending = c + kAhead < nchunks
-                  ? dma_chunk(slots, c + kAhead, blocks_of(c + kAhead), sta, wave)
+                  ? dma_chunk(slots, c + kAhead, blocks_of(c + kAhead), sta, wave, lane)
                   : 0;
-    fold_chunk_q8<kPipe, kDKB, kDBlock, 32 * 16, kDHRow>(
-        acc, qa0 + st * kDStage, qb0 + st * kDStage, hx0 + st * kHStage, hx1 + st * kHStage,
-        hy + st * kHStage, [](int) {});
-    // chunk c+1 is in LDS: with one chunk ahead it is the newest DMA
+    fold();
     wait_dma_barrier(kAhead > 1 ? pending : 0);
     st = st + 1 == kDStages ? 0 : st + 1;
-  }
+  };
   const int nbc = static_cast<int>(nb - nfull * kDKB);
-  if (nbc > 0)
-    fold_tail_q8<kDBlock, 32 * 16, kDHRow>(acc, qa0 + st * kDStage, qb0 + st * kDStage,
-                                           hx0 + st * kHStage, hx1 + st * kHStage,
-                                           hy + st * kHStage, nbc);
-
-  const size_t col = n0 + wn * 32 + li;
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const size_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-      if (row < nr && col < nc)
-        s[row * bs + col] = acc[i][e];
+  if constexpr (kQ4) {
+    // the fast fold until a chunk holds a non-finite d_x among the wave's rows,
+    // the exact one from there on (and for the partial tail, always)
+    for (; c < nfull; ++c) {
+      if (q4_chunk_nonfinite<kDHRow>(dsh + st * kHStage + wm * 64, kDKB, lane))
+        break;
+      chunk([&] {
+        fold_chunk_q4<false, kDKB, kDBlock, 32 * 16, kDHRow>(
+            acc, qa0 + st * kDStage, qb0 + st * kDStage, qx + st * kHStage, qy + st * kHStage,
+            [](int) {});
+      });
     }
+    for (; c < nfull; ++c)
+      chunk([&] {
+        fold_chunk_q4<true, kDKB, kDBlock, 32 * 16, kDHRow>(
+            acc, qa0 + st * kDStage, qb0 + st * kDStage, qx + st * kHStage, qy + st * kHStage,
+            [](int) {});
+      });
+    if (nbc > 0)
+      fold_tail_q4<true, kDBlock, 32 * 16, kDHRow>(acc, qa0 + st * kDStage, qb0 + st * kDStage,
+                                                   qx + st * kHStage, qy + st * kHStage, nbc);
+  } else {
+    for (; c < nfull; ++c)
+      chunk([&] {
+        fold_chunk_q8<kPipe, kDKB, kDBlock, 32 * 16, kDHRow>(
+            acc, qa0 + st * kDStage, qb0 + st * kDStage, hx0 + st * kHStage,
+            hx1 + st * kHStage, hy + st * kHStage, [](int) {});
+      });
+    if (nbc > 0)
+      fold_tail_q8<kDBlock, 32 * 16, kDHRow>(acc, qa0 + st * kDStage, qb0 + st * kDStage,
+                                             hx0 + st * kHStage, hx1 + st * kHStage,
+                                             hy + st * kHStage, nbc);
+  }
+
+  if constexpr (kQ4) {
+    // Lane (li, h) holds weight row li of each tile and tokens 8g + 4h + j:
+    // stored directly, every store would scatter over 32 rows.  Each tile goes
+    // through a wave-private 32x32 fp32 buffer in LDS instead (row-major,
+    // padded to 33 floats a row: no bank conflicts either way), read back as
+    // 32 consecutive tokens of one row per half-wave.  The buffers lie in the
+    // quant stage the last full chunk used: no wave reads it after that
+    // chunk's barrier (the tail, if any, reads the other stage) and no DMA
+    // targets it.
+    float *tb = reinterpret_cast<float *>(qs + (nbc > 0 ? 1 - st : st) * kDStage) + wave * 32 * 33;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        tb[li * 33 + 8 * (e >> 2) + 4 * h + (e & 3)] = acc[i][e];
+      __builtin_amdgcn_wave_barrier();
+      const size_t col = n0 + wn * 32 + li;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int r = 2 * k + h;  // this half-wave's weight row of the tile
+        const size_t row = m0 + wm * 64 + i * 32 + r;
+        const float v = tb[r * 33 + li];
+        if (row < nr && col < nc)
+          s[row * bs + col] = v;
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  } else {
+    const size_t col = n0 + wn * 32 + li;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const size_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (row < nr && col < nc)
+          s[row * bs + col] = acc[i][e];
+      }
+  }
+}
+
+template <bool kPipe>
+__global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q8(size_t nb, float *s,
+                                                              const uint8_t *tx,
+                                                              const uint8_t *ty, size_t nr,
+                                                              size_t nc, size_t bs) {
+  __shared__ __align__(16) int8_t qs[kDStages * kDStage];
+  __shared__ __align__(16) uint16_t dsh[kDStages * kDKB * kDHRow];
+  gemm_tiles_body<kPipe, false>(nb, s, tx, ty, nr, nc, bs, qs, dsh);
+}
+
+__global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q4(size_t nb, float *s,
+                                                              const uint8_t *tx,
+                                                              const uint8_t *ty, size_t nr,
+                                                              size_t nc, size_t bs) {
+  __shared__ __align__(16) int8_t qs[kDStages * kDStage];
+  __shared__ __align__(16) uint16_t dsh[kDStages * kDKB * kDHRow];
+  gemm_tiles_body<true, true>(nb, s, tx, ty, nr, nc, bs, qs, dsh);
 }
 
 }  // namespace tcrv
@@ -365,14 +561,43 @@ int pack_tiles(size_t nrows, size_t nb, const uint8_t *src, size_t bx, uint8_t *
   return launch_status();
 }
 
+int pack_tiles_q4(size_t nrows, size_t nb, const uint8_t *src, size_t bx, uint8_t *dst,
+                  hipStream_t st) {
+  using namespace tcrv_host;
+  const size_t ngroups = (nrows + tcrv::kTG - 1) / tcrv::kTG;
+  size_t b0 = 0;  // blocks below b0 are packed by the span kernel
+  if (aligned16(src) && (nrows == 1 || bx % 16 == 0) && nb >= tcrv::kPackSpan) {
+    const size_t nspans = ngroups * (nb / tcrv::kPackSpan);
+    const size_t grid = (nspans * 64 + 255) / 256;
+    if (grid > 0x7fffffffu)
+      return TCRV_HIP_ERR_TOO_LARGE;
+    tcrv::pack_q4_tiles_span<<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(
+        nrows, nb, src, bx, dst, nspans);
+    b0 = nb / tcrv::kPackSpan * tcrv::kPackSpan;
+  }
+  if (b0 < nb) {
+    const size_t nrec = ngroups * (nb - b0);
+    const size_t grid = (nrec * 64 + 255) / 256;
+    if (grid > 0x7fffffffu)
+      return TCRV_HIP_ERR_TOO_LARGE;
+    tcrv::pack_q4_tiles<<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(
+        nrows, nb, src, bx, dst, b0, nrec);
+  }
+  return launch_status();
+}
+
 int gemm_tiles(size_t nb, float *s, const uint8_t *tx, const uint8_t *ty, size_t nr, size_t nc,
-               size_t bs, hipStream_t st) {
+               size_t bs, hipStream_t st, bool q4 = false) {
   using namespace tcrv_host;
   const size_t tiles = ((nr + tcrv::kDBM - 1) / tcrv::kDBM) * ((nc + tcrv::kDBN - 1) / tcrv::kDBN);
   if (tiles > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
-  tcrv::gemm_tiles_q8<kTiledPipe><<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kDThreads), 0,
-                                    st>>>(nb, s, tx, ty, nr, nc, bs);
+  if (q4)
+    tcrv::gemm_tiles_q4<<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kDThreads), 0, st>>>(
+        nb, s, tx, ty, nr, nc, bs);
+  else
+    tcrv::gemm_tiles_q8<kTiledPipe><<<dim3(static_cast<unsigned>(tiles)),
+                                      dim3(tcrv::kDThreads), 0, st>>>(nb, s, tx, ty, nr, nc, bs);
   return launch_status();
 }
 
@@ -462,6 +687,37 @@ int tcrv_hip_q8_0_q8_0_gemm_ws(size_t n, float *s, const uint8_t *vx, const uint
   if (rc != TCRV_HIP_OK)
     return rc;
   return gemm_tiles(nb, s, tx, ty, nr, nc, bs, st);
+}
+
+int tcrv_hip_pack_q4_0_to_gemm_tiles(size_t nrows, size_t nb, const uint8_t *src, size_t bx,
+                                     uint8_t *dst, void *stream) {
+  using namespace tcrv_host;
+  if (nrows == 0 || nb == 0)
+    return TCRV_HIP_OK;
+  if (!src || !dst)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned2(src) || (nrows > 1 && (bx & 1u)) || !aligned16(dst))
+    return TCRV_HIP_ERR_MISALIGNED;
+  if (nrows > 1 && bx < nb * tcrv::kQ4Bytes)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  return pack_tiles_q4(nrows, nb, src, bx, dst, as_stream(stream));
+}
+
+int tcrv_hip_q4_0_q8_0_gemm_tiles(size_t n, float *s, const uint8_t *tx, const uint8_t *ty,
+                                  size_t nr, size_t nc, size_t bs, void *stream) {
+  using namespace tcrv_host;
+  const size_t nb = n / tcrv::kQK;
+  if (nr == 0 || nc == 0)
+    return TCRV_HIP_OK;
+  if (nr > 1 && bs < nc)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  if (nb == 0)
+    return zero_outputs(s, nr * nc, bs, nc, stream);
+  if (!s || !tx || !ty)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned16(tx) || !aligned16(ty))
+    return TCRV_HIP_ERR_MISALIGNED;
+  return gemm_tiles(nb, s, tx, ty, nr, nc, bs, as_stream(stream), true);
 }
 
 }  // extern "C"

@@ -1,6 +1,7 @@
 // mfma_fold.h -- pieces shared by the MFMA GEMMs (gemm.hip, gemm_tiled.hip):
-// the XCD-aware tile order and the Q8_0 fold of tcrv::gemm_wide<false>, the
-// repack GEMM and the tiled GEMM, parametrized by their staging layouts.
+// the XCD-aware tile order, the Q8_0 fold of tcrv::gemm_wide<false>, the
+// repack GEMM and the tiled GEMM, and the Q4_0 fold of the tiled Q4_0 GEMM,
+// parametrized by their staging layouts.
 //
 // Per 32x32 output tile and Q8_0 block b, the reference fold is
 //   acc = fma((float)sumi, d_x * d_y, acc)
@@ -169,6 +170,147 @@ __device__ __forceinline__ void fold_tail_q8(float (&acc)[2][16], const int8_t *
       const v16f dxy = q8_dxy(q8_scale<kScaleRow>(i ? hx1 : hx0, b), uy);
       q8_fold(acc[i], sumi, dxy);
     }
+  }
+}
+
+// ---- the Q4_0 x Q8_0 fold ----------------------------------------------
+// Per tile and block the reference folds acc = fma(fl((float)sumi * d_x), d_y,
+// acc) (RVVToEmitCBlockQuantLinear.cpp:322-356): the product with d_x is
+// rounded first, so the scales cannot be multiplied ahead.
+//
+// The tile is computed transposed: the block-sum MFMA takes the tokens as its
+// A operand and the weights as B, so lane (c = lane % 32, h = lane / 32) holds
+// weight row c and tokens 8g + 4h + j (g, j < 4) of the tile.  d_x is then one
+// value per lane and tile-block (a 16-bit LDS read) and d_y one per element
+// (a 64-bit LDS read gives four; both tiles of a wave share them).
+//
+// The MFMA's accumulator input is the integer bit pattern of M = 1.5 * 2^23
+// (0x4B400000) in every element, so its results read as floats are
+// F = M + sumi exactly: |sumi| <= 32 * 8 * 128 < 2^22 keeps F in M's binade,
+// whose spacing is 1.  Then fma(F, d_x, -M * d_x) = fl(sumi * d_x): the exact
+// F * d_x - M * d_x = sumi * d_x is rounded once, and -M * d_x is itself exact
+// (an fp16 significand times 1.5).  That fma and fma(t, d_y, acc), both with
+// the fp16 scale read in place (v_fma_mix_f32), are the fold's two VALU
+// instructions per element; -M * d_x is one per lane and tile-block.
+// An infinite d_x makes -M * d_x infinite, and the fast form NaN where the
+// reference has +-inf: a chunk with a non-finite d_x among the wave's weight
+// rows (q4_chunk_nonfinite, one test per chunk) is folded in the exact
+// three-instruction form instead (sumi = F - M, exact; fl(sumi * d_x); the
+// fma), so the steps themselves carry no branch.
+constexpr int kSeedBits = 0x4B400000;
+constexpr float kSeed = 12582912.0f;
+
+// The seeded block-sum MFMA of one tile and block: F = M + sumi.  The whole
+// vector is bit-cast: __builtin_bit_cast of one subscripted element of an
+// int vector reads element 0 with this compiler.
+__device__ __forceinline__ v16f q4_seeded_sums(const v4i &tokens, const v4i &weights) {
+  v16i seed;
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    seed[e] = kSeedBits;
+  return __builtin_bit_cast(v16f,
+                            __builtin_amdgcn_mfma_i32_32x32x32_i8(tokens, weights, seed, 0, 0, 0));
+}
+
+// fp16 bit pattern (low 16 bits of u) -> fp32, exact.
+__device__ __forceinline__ float f16_bits(uint32_t u) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u)));
+}
+
+// Whether any d_x of the wave's 64 weight rows in the chunk's nbc blocks is
+// non-finite (exponent field all ones; NaN is included, which only costs the
+// exact form): lane 8b + k reads rows 8k..8k+7 of block b as one 128-bit LDS
+// read, and (h & 0x7C00) + 0x0400 reaches bit 15 exactly when h's exponent is
+// 0x1F (no carry crosses into the other half).  hx: the wave's row 0, block 0.
+template <int kScaleRow>
+__device__ __forceinline__ bool q4_chunk_nonfinite(const uint16_t *hx, int nbc, int lane) {
+  const int b = lane >> 3, k = lane & 7;
+  uint32_t top = 0;
+  if (b < nbc) {
+    const uint4 w = *reinterpret_cast<const uint4 *>(hx + b * kScaleRow + 8 * k);
+    top = ((w.x & 0x7C007C00u) + 0x04000400u) | ((w.y & 0x7C007C00u) + 0x04000400u) |
+          ((w.z & 0x7C007C00u) + 0x04000400u) | ((w.w & 0x7C007C00u) + 0x04000400u);
+  }
+  return __builtin_amdgcn_ballot_w64((top & 0x80008000u) != 0) != 0;
+}
+
+// The fold of one tile and block: F the seeded sums, ux the lane's d_x bits,
+// hy d_y of its tokens 4h.. of the block (rows 8g + 4h + 0..3 as fp16 pairs,
+// read per g); kExact: the three-instruction form.
+template <bool kExact>
+__device__ __forceinline__ void q4_fold(float (&acc)[16], const v16f &F, uint32_t ux,
+                                        const uint16_t *hy) {
+  // Plain fp32 arithmetic on widened fp16 values: the compiler selects
+  // v_fma_mix_f32 (the fp16 operand read in place) and inserts the wait states
+  // a VALU read of a matrix-core result needs.
+  const float dx = f16_bits(ux);
+  const float c = -kSeed * dx;  // -M * d_x, exact (unused by the exact form)
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const uint2 dy = *reinterpret_cast<const uint2 *>(hy + 8 * g);
+    // fl(sumi * d_x) of four rows, from F directly or from sumi = F - M
+    // (exact), all four before the fmas that take them: a VALU result read by
+    // the next instruction stalls the wave.
+    float t[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      t[j] = kExact ? (F[4 * g + j] - kSeed) * dx : fmaf(F[4 * g + j], dx, c);
+    asm volatile("" : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t w = j < 2 ? dy.x : dy.y;
+      acc[4 * g + j] = fmaf(t[j], f16_bits((j & 1) ? w >> 16 : w), acc[4 * g + j]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    asm volatile("" : "+v"(acc[e]));
+}
+
+// One chunk of kBlocks blocks for a wave's two tiles with the Q4_0 fold, steps
+// s = 2b + i in ascending block order, the seeded MFMA of step s+1 issued in
+// step s (as fold_chunk_q8 with kPipe).  qw: this lane's weight quants of tile
+// 0, block 0 (tile 1 kTileStride bytes on); qt: its token quants; hx: its
+// weight row's d_x slot of tile 0, block 0 (tile 1 is 32 rows on); hy: d_y of
+// its tokens' first row (q4_token_scales).
+template <bool kExact, int kBlocks, int kBlockStride, int kTileStride, int kScaleRow,
+          typename AfterStep>
+__device__ __forceinline__ void fold_chunk_q4(float (&acc)[2][16], const int8_t *qw,
+                                              const int8_t *qt, const uint16_t *hx,
+                                              const uint16_t *hy, AfterStep &&after_step) {
+  v4i tq = q8_frag<kBlockStride>(qt, 0);
+  v16f cur = q4_seeded_sums(tq, q8_frag<kBlockStride>(qw, 0));
+#pragma unroll
+  for (int s = 0; s < 2 * kBlocks; ++s) {
+    const int i = s & 1, b = s >> 1;
+    v16f nxt;
+    if (s + 1 < 2 * kBlocks) {
+      const int i1 = (s + 1) & 1, b1 = (s + 1) >> 1;
+      if (i1 == 0)  // a new block: its token operand
+        tq = q8_frag<kBlockStride>(qt, b1);
+      nxt = q4_seeded_sums(tq, q8_frag<kBlockStride>(qw + i1 * kTileStride, b1));
+    }
+    q4_fold<kExact>(acc[i], cur, q8_scale<kScaleRow>(hx + 32 * i, b), hy + b * kScaleRow);
+    if (s + 1 < 2 * kBlocks) {
+      asm volatile("" : "+v"(nxt));
+      cur = nxt;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    after_step(s);
+  }
+}
+
+// A trailing partial chunk of nbc blocks with the Q4_0 fold.
+template <bool kExact, int kBlockStride, int kTileStride, int kScaleRow>
+__device__ __forceinline__ void fold_tail_q4(float (&acc)[2][16], const int8_t *qw,
+                                             const int8_t *qt, const uint16_t *hx,
+                                             const uint16_t *hy, int nbc) {
+  for (int b = 0; b < nbc; ++b) {
+    const v4i tq = q8_frag<kBlockStride>(qt, b);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      q4_fold<kExact>(acc[i], q4_seeded_sums(tq, q8_frag<kBlockStride>(qw + i * kTileStride, b)),
+                      q8_scale<kScaleRow>(hx + 32 * i, b), hy + b * kScaleRow);
   }
 }
 

@@ -31,7 +31,7 @@ KERNELS = {
     "gemv_q4_0_q8_0": "gemv_q4_0_q8_0_direct",
     "q8_0_q8_0_gemm": "gemm_wide<false>",
     "q8_0_q8_0_gemm_tiles": "gemm_tiles_q8<true>",
-    "pack_q8_0_to_gemm_tiles": "pack_gemm_tiles<true>",
+    "pack_q8_0_to_gemm_tiles": "pack_gemm_tiles_span",
     "calib": "add_f32_vec4",
 }
 CALIB_BYTES = {"FETCH_SIZE": 8 << 24, "WRITE_SIZE": 4 << 24}  # per add_f32 launch, n = 2^24

@@ -80,6 +80,8 @@ SIGNATURES = {
     "tcrv_hip_q8_0_q8_0_gemm_tiles": [_sz, _p, _p, _p, _sz, _sz, _sz, _p],
     "tcrv_hip_q8_0_q8_0_gemm_ws": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p, _sz, _p],
     "tcrv_hip_q8_0_q8_0_gemm_noalloc": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p],
+    "tcrv_hip_pack_q4_0_to_gemm_tiles": [_sz, _sz, _p, _sz, _p, _p],
+    "tcrv_hip_q4_0_q8_0_gemm_tiles": [_sz, _p, _p, _p, _sz, _sz, _sz, _p],
 }
 # size queries (return size_t)
 SIZE_FUNCS = {"tcrv_hip_gemm_tiles_bytes": [_sz, _sz],
@@ -314,6 +316,14 @@ def q8_0_q8_0_gemm_noalloc(n: int, s, vx, vy, by: int, nr: int, nc: int, bx: int
     workspace (no allocation); returns the status when check is False."""
     return call("tcrv_hip_q8_0_q8_0_gemm_noalloc", n, s, vx, vy, by, nr, nc, bx, bs,
                 _stream(stream), check=check)
+
+
+def pack_q4_0_to_gemm_tiles(nrows: int, nb: int, src, bx: int, dst, stream=None):
+    return call("tcrv_hip_pack_q4_0_to_gemm_tiles", nrows, nb, src, bx, dst, _stream(stream))
+
+
+def q4_0_q8_0_gemm_tiles(n: int, s, tx, ty, nr: int, nc: int, bs: int, stream=None):
+    return call("tcrv_hip_q4_0_q8_0_gemm_tiles", n, s, tx, ty, nr, nc, bs, _stream(stream))
 
 
 def synchronize(stream=None):
