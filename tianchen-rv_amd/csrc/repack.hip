@@ -22,38 +22,62 @@ constexpr int kQ4x16Bytes = 288;
 constexpr int kQ8x16Bytes = 544;
 
 // ---------------------------------------------------------------------------
-// Packs, spans that are only 2-byte aligned: one thread per output dword (8
-// scale dwords + 64 or 128 quant dwords).
+// Packs.  The output's quant bytes are a 16 x 16 (Q4_0) or 16 x 32 (Q8_0)
+// byte transpose of the 16 source blocks' quants: out[32 + 16i + r] = quant
+// byte i of source block r.  One lane per source block: lane r of a 16-lane group loads its block's
+// quant bytes into registers (2-byte aligned source: the aligned dwords over
+// them, realigned with v_perm; no load leaves the block), as dwords X_k =
+// quant bytes 4k..4k+3.
+// Within each lane quad (rows 4q..4q+3, j = r % 4) a 4x4 byte transpose of X_k
+// -- two DPP quad moves and two v_perm -- leaves lane r holding bytes 4k+j of
+// rows 4q..4q+3, i.e. output dword 8 + 4(4k+j) + q; for each k the group's 16
+// lanes store 16 consecutive dwords.  The scale d of source block r is the
+// output's fp16 d[r]: one 16-bit store per lane, 32 contiguous bytes per group.
 // ---------------------------------------------------------------------------
 template <bool kQ4>
-__global__ __launch_bounds__(256) void pack_x16(size_t nblocks, const uint8_t *src,
-                                                uint8_t *dst) {
+__global__ __launch_bounds__(256) void pack_x16_quad(size_t nblocks, const uint8_t *src,
+                                                     uint8_t *dst) {
   constexpr int kSrc = kQ4 ? kQ4Bytes : kQ8Bytes;
   constexpr int kDst = kQ4 ? kQ4x16Bytes : kQ8x16Bytes;
-  constexpr int kDwords = kDst / 4;
+  constexpr int kQw = (kSrc - 2) / 4;  // quant dwords per source block: 4 or 8
   const size_t t = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (t >= nblocks * kDwords)
+  const size_t o = t >> 4;  // output block; its 16 lanes are a whole DPP row
+  if (o >= nblocks)
     return;
-  const size_t o = t / kDwords;
-  const int k = static_cast<int>(t - o * kDwords);
-  const uint8_t *in = src + o * 16 * kSrc;
-  uint32_t v;
-  if (k < 8) {  // scales d[2k], d[2k+1]
-    const uint32_t d0 = *reinterpret_cast<const uint16_t *>(in + (2 * k) * kSrc);
-    const uint32_t d1 = *reinterpret_cast<const uint16_t *>(in + (2 * k + 1) * kSrc);
-    v = d0 | (d1 << 16);
-  } else {  // qs bytes 4q .. 4q+3: byte i -> source block i % 16, offset i / 16
-    const int q = k - 8;
-    const int off = 2 + q / 4;
-    const int r0 = 4 * (q % 4);
-    v = 0;
+  const int r = static_cast<int>(t & 15), j = r & 3, q = r >> 2;
+  const uint8_t *in = src + o * kDst + r * kSrc;  // source block r (16 blocks = kDst bytes)
+  const uint8_t *qs = in + 2;
+  const int sh = static_cast<int>(reinterpret_cast<uintptr_t>(qs) & 2u);  // 0 or 2
+  const uint32_t *w = reinterpret_cast<const uint32_t *>(qs - sh);
+  uint32_t raw[kQw + 1];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      v |= static_cast<uint32_t>(in[(r0 + j) * kSrc + off]) << (8 * j);
+  for (int k = 0; k < kQw; ++k)
+    raw[k] = w[k];  // ends at the block's last byte (sh = 0) or 2 bytes before it
+  // the quants' last 2 bytes, read on their own (the dword holding them when
+  // sh = 2 would run 2 bytes past the block); unused when sh = 0
+  raw[kQw] = *reinterpret_cast<const uint16_t *>(qs + 4 * kQw - 2);
+  const uint32_t d = *reinterpret_cast<const uint16_t *>(in);
+  // X_k = quant bytes 4k..4k+3: {raw[k+1]:raw[k]} >> 8*sh
+  const uint32_t sel_align = sh ? 0x05040302u : 0x03020100u;
+  // 4x4 byte transpose within the quad: stage 1 pairs lanes j, j^1, stage 2
+  // j, j^2 (v_perm: selector bytes 0-3 pick the lane's own dword, 4-7 the
+  // partner's)
+  const uint32_t sel1 = (j & 1) ? 0x03070105u : 0x06020400u;
+  const uint32_t sel2 = (j & 2) ? 0x03020706u : 0x05040100u;
+  uint32_t *out = reinterpret_cast<uint32_t *>(dst + o * kDst);
+#pragma unroll
+  for (int k = 0; k < kQw; ++k) {
+    uint32_t x = __builtin_amdgcn_perm(raw[k + 1], raw[k], sel_align);
     if constexpr (kQ4)
-      v ^= 0x88888888u;
+      x ^= 0x88888888u;  // both nibbles offset-binary biased
+    const uint32_t p1 = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+        0, static_cast<int>(x), 0xB1 /* quad_perm:[1,0,3,2] */, 0xf, 0xf, false));
+    const uint32_t tq = __builtin_amdgcn_perm(p1, x, sel1);
+    const uint32_t p2 = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+        0, static_cast<int>(tq), 0x4E /* quad_perm:[2,3,0,1] */, 0xf, 0xf, false));
+    out[8 + 4 * (4 * k + j) + q] = __builtin_amdgcn_perm(p2, tq, sel2);
   }
-  reinterpret_cast<uint32_t *>(dst + o * kDst)[k] = v;
+  reinterpret_cast<uint16_t *>(out)[r] = static_cast<uint16_t>(d);
 }
 
 // Quant bytes 4k..4k+3 of activation block b staged raw (34-byte blocks) in
@@ -228,55 +252,6 @@ __global__ __launch_bounds__(64 * kRwWaves) void repack_gemv_waves(size_t nb, fl
     s[static_cast<size_t>(blockIdx.x) * 16 + 4 * w + fr] = acc;
 }
 
-// ---------------------------------------------------------------------------
-// Packs, 16-byte aligned spans.  The 16 source blocks of an x16 block are
-// contiguous and as long as it (16 x 18 = 288, 16 x 34 = 544 bytes), so a
-// work-group copies kPkBlocks of them into LDS with consecutive 128-bit loads
-// (all issued before the first store), gathers each output dword from LDS and
-// writes the output span with consecutive dword stores.
-// ---------------------------------------------------------------------------
-constexpr int kPkBlocks = 16;  // x16 blocks per work-group (4/8/16/32: 8.4/6.5/6.0/6.6 us)
-
-template <bool kQ4>
-__global__ __launch_bounds__(256) void pack_x16_lds(size_t nblocks, const uint8_t *src,
-                                                    uint8_t *dst) {
-  constexpr int kSrc = kQ4 ? kQ4Bytes : kQ8Bytes;
-  constexpr int kDst = kQ4 ? kQ4x16Bytes : kQ8x16Bytes;
-  constexpr int kDwords = kDst / 4;
-  constexpr int kPieces = kPkBlocks * kDst / 16;
-  constexpr int kPer = (kPieces + 255) / 256;
-  __shared__ __align__(16) uint8_t in[kPkBlocks * kDst];
-  const size_t o0 = static_cast<size_t>(blockIdx.x) * kPkBlocks;
-  const int nblk = static_cast<int>(min(static_cast<size_t>(kPkBlocks), nblocks - o0));
-  const int np = nblk * (kDst / 16);
-  uint4 v[kPer];
-  load_pieces<kPer, 256>(v, src + o0 * kDst, np, threadIdx.x);
-  store_pieces<kPer, 256, kPieces, 16 * kPieces>(v, in, np, threadIdx.x);
-  __syncthreads();
-  uint32_t *d = reinterpret_cast<uint32_t *>(dst + o0 * kDst);
-  for (int t = threadIdx.x; t < nblk * kDwords; t += 256) {
-    const int o = t / kDwords, k = t - o * kDwords;
-    const uint8_t *b = in + o * kDst;  // the output block's 16 source blocks
-    uint32_t w;
-    if (k < 8) {  // scales d[2k], d[2k+1]
-      const uint32_t d0 = *reinterpret_cast<const uint16_t *>(b + (2 * k) * kSrc);
-      const uint32_t d1 = *reinterpret_cast<const uint16_t *>(b + (2 * k + 1) * kSrc);
-      w = d0 | (d1 << 16);
-    } else {  // qs bytes 4q .. 4q+3: byte i -> source block i % 16, offset i / 16
-      const int q = k - 8;
-      const int off = 2 + q / 4;
-      const int r0 = 4 * (q % 4);
-      w = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        w |= static_cast<uint32_t>(b[(r0 + j) * kSrc + off]) << (8 * j);
-      if constexpr (kQ4)
-        w ^= 0x88888888u;
-    }
-    d[t] = w;
-  }
-}
-
 }  // namespace tcrv
 
 namespace {
@@ -290,20 +265,11 @@ int launch_pack(size_t nblocks, const uint8_t *src, uint8_t *dst, void *stream) 
     return TCRV_HIP_ERR_NULL_POINTER;
   if (!aligned2(src) || !aligned4(dst))
     return TCRV_HIP_ERR_MISALIGNED;
-  if (aligned16(src) && aligned16(dst)) {
-    const size_t grid = (nblocks + tcrv::kPkBlocks - 1) / tcrv::kPkBlocks;
-    if (grid > 0x7fffffffu)
-      return TCRV_HIP_ERR_TOO_LARGE;
-    tcrv::pack_x16_lds<kQ4><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0,
-                              as_stream(stream)>>>(nblocks, src, dst);
-    return launch_status();
-  }
-  const size_t dwords = nblocks * ((kQ4 ? tcrv::kQ4x16Bytes : tcrv::kQ8x16Bytes) / 4);
-  const size_t grid = (dwords + 255) / 256;
+  const size_t grid = (nblocks * 16 + 255) / 256;
   if (grid > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
-  tcrv::pack_x16<kQ4><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, as_stream(stream)>>>(
-      nblocks, src, dst);
+  tcrv::pack_x16_quad<kQ4><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                             as_stream(stream)>>>(nblocks, src, dst);
   return launch_status();
 }
 
