@@ -51,14 +51,11 @@ constexpr int kPackSpan = 8;  // blocks per lane (4096 rows x 128 blocks: 7.3 us
                               // per-record kernel 9.3 us; two waves per 8-block span
                               // with 9 loads each 12.2 us)
 
-__global__ __launch_bounds__(256) void pack_gemm_tiles_span(size_t nrows, size_t nb,
-                                                            const uint8_t *src, size_t bx,
-                                                            uint8_t *dst, size_t nspans) {
-  const size_t wave = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
+// Span `wave` of one operand (64-row group g, 8-block span c), lane r = row
+// 64g + r.
+__device__ __forceinline__ void pack_span(size_t nrows, size_t nb, const uint8_t *src,
+                                          size_t bx, uint8_t *dst, size_t wave, int r) {
   const size_t spans_per_group = nb / kPackSpan;
-  if (wave >= nspans)
-    return;
-  const int r = static_cast<int>(threadIdx.x & 63);
   const size_t g = wave / spans_per_group, c = wave - g * spans_per_group;
   const size_t row = g * kTG + r;
   uint32_t v[4 * 17];
@@ -98,6 +95,36 @@ __global__ __launch_bounds__(256) void pack_gemm_tiles_span(size_t nrows, size_t
     reinterpret_cast<uint4 *>(o + 1024)[r] = make_uint4(q[4], q[5], q[6], q[7]);
     reinterpret_cast<uint16_t *>(o + 2048)[r] = static_cast<uint16_t>(d);
   }
+}
+
+__global__ __launch_bounds__(256) void pack_gemm_tiles_span(size_t nrows, size_t nb,
+                                                            const uint8_t *src, size_t bx,
+                                                            uint8_t *dst, size_t nspans) {
+  const size_t wave = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
+  if (wave >= nspans)
+    return;
+  pack_span(nrows, nb, src, bx, dst, wave, static_cast<int>(threadIdx.x & 63));
+}
+
+// Both operands of one GEMM in one launch (their spans back to back in the
+// grid): one launch instead of two, and twice the loads in flight.
+struct SpanOperand {
+  const uint8_t *src;
+  size_t bx, nrows, nspans;
+  uint8_t *dst;
+};
+
+__global__ __launch_bounds__(256) void pack_gemm_tiles_span2(size_t nb, SpanOperand x,
+                                                             SpanOperand y) {
+  size_t wave = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
+  const int r = static_cast<int>(threadIdx.x & 63);
+  if (wave < x.nspans) {
+    pack_span(x.nrows, nb, x.src, x.bx, x.dst, wave, r);
+    return;
+  }
+  wave -= x.nspans;
+  if (wave < y.nspans)
+    pack_span(y.nrows, nb, y.src, y.bx, y.dst, wave, r);
 }
 
 // One wave per (group, block) record for blocks b0.. of every group, lane
@@ -561,6 +588,28 @@ int pack_tiles(size_t nrows, size_t nb, const uint8_t *src, size_t bx, uint8_t *
   return launch_status();
 }
 
+// Both Q8_0 operands of a GEMM: one launch of the span kernel when every block
+// of both is in an 8-block span of 16-byte aligned rows, else pack_tiles each.
+int pack_tiles_both(size_t nb, const uint8_t *vx, size_t bx, size_t nr, uint8_t *tx,
+                    const uint8_t *vy, size_t by, size_t nc, uint8_t *ty, hipStream_t st) {
+  using namespace tcrv_host;
+  auto spans_only = [&](const uint8_t *src, size_t stride, size_t nrows) {
+    return aligned16(src) && (nrows == 1 || stride % 16 == 0) && nb % tcrv::kPackSpan == 0;
+  };
+  if (nb == 0 || !spans_only(vx, bx, nr) || !spans_only(vy, by, nc)) {
+    const int rc = pack_tiles(nr, nb, vx, bx, tx, st);
+    return rc != TCRV_HIP_OK ? rc : pack_tiles(nc, nb, vy, by, ty, st);
+  }
+  const size_t per_group = nb / tcrv::kPackSpan;
+  const tcrv::SpanOperand x{vx, bx, nr, (nr + tcrv::kTG - 1) / tcrv::kTG * per_group, tx};
+  const tcrv::SpanOperand y{vy, by, nc, (nc + tcrv::kTG - 1) / tcrv::kTG * per_group, ty};
+  const size_t grid = ((x.nspans + y.nspans) * 64 + 255) / 256;
+  if (grid > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  tcrv::pack_gemm_tiles_span2<<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(nb, x, y);
+  return launch_status();
+}
+
 int pack_tiles_q4(size_t nrows, size_t nb, const uint8_t *src, size_t bx, uint8_t *dst,
                   hipStream_t st) {
   using namespace tcrv_host;
@@ -680,10 +729,7 @@ int tcrv_hip_q8_0_q8_0_gemm_ws(size_t n, float *s, const uint8_t *vx, const uint
   uint8_t *tx = static_cast<uint8_t *>(workspace);
   uint8_t *ty = tx + tx_bytes;  // tx_bytes is a multiple of 2176 = 16 * 136
   hipStream_t st = as_stream(stream);
-  int rc = pack_tiles(nr, nb, vx, bx, tx, st);
-  if (rc != TCRV_HIP_OK)
-    return rc;
-  rc = pack_tiles(nc, nb, vy, by, ty, st);
+  const int rc = pack_tiles_both(nb, vx, bx, nr, tx, vy, by, nc, ty, st);
   if (rc != TCRV_HIP_OK)
     return rc;
   return gemm_tiles(nb, s, tx, ty, nr, nc, bs, st);
