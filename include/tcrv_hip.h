@@ -198,6 +198,18 @@ TCRV_HIP_API int tcrv_hip_q4_0_q8_0_gemm_tile(size_t n, float *s, const uint8_t 
 /* The decode GEMV (the q4_0 GEMM with nc = 1): s[ir] for ir < nr. */
 TCRV_HIP_API int tcrv_hip_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx, size_t bx,
                             const uint8_t *vy, size_t nr, void *stream);
+/* The decode GEMV with its schedule knob set by the caller, as the reference's
+ * block-dot ops carry bounded schedule attributes (integer_core_lmul,
+ * multi_block_factor, strip_elision: RVVOps.td:3912-3972) that change how the
+ * kernel runs and never what it computes.  rows_per_wave (2, 4 or 8; the plain
+ * entry uses 4, tcrv_hip_route_schedule lists the candidates) sets how many
+ * weight rows one wave of the register-direct kernel owns; the results are
+ * bit-identical for every value.  Shapes served by the LDS-staged kernel (odd
+ * n/32, rows not 4-byte aligned) ignore it.  Any other value returns
+ * TCRV_HIP_ERR_BAD_SIZE. */
+TCRV_HIP_API int tcrv_hip_gemv_q4_0_q8_0_shaped(size_t n, float *s, const uint8_t *vx, size_t bx,
+                                                const uint8_t *vy, size_t nr, int rows_per_wave,
+                                                void *stream);
 
 /* ---- a9: Q8_0 x Q8_0 GEMM (prefill) ---------------------------------------
  * Same ABI as the q4_0 GEMM above; elements are the a5 block dot:

@@ -101,6 +101,36 @@ TCRV_HIP_API int tcrv_hip_route_param(size_t row, size_t param, const char **c_n
 /* Row of an op identity, or -1 when the table has none. */
 TCRV_HIP_API long tcrv_hip_route_find(const char *op);
 
+/* ---- schedule descriptors ------------------------------------------------
+ * The reference looks a kernel's bounded schedule knobs up in a registry of
+ * descriptors (lookupRVVScheduleDescriptor,
+ * lib/Plugin/RVV/RVVScheduleDescriptorRegistry.cpp:151-190): the legal
+ * candidate shapes, each with its knobs, and the default with the reason it
+ * was chosen (measured-fastest, or a static cost); the knobs change how a
+ * kernel runs, never what it computes (RVVOps.td:3912-3972).  This is the same
+ * registry for the gfx950 kernels: one row per (op, regime, knob, candidate
+ * value).  A row with a non-NULL `entry` names the libtcrv_hip entry that takes
+ * the knob as an argument (every value bit-identical); the others are
+ * build-time shapes, listed with the measurement that chose among them. */
+typedef struct {
+  const char *op;      /* op identity of the route table */
+  int m_regime;        /* TCRV_HIP_M_DECODE or TCRV_HIP_M_PREFILL; -1: not regime-specific */
+  const char *kernel;  /* the device kernel */
+  const char *knob;    /* knob name */
+  int64_t value;       /* the candidate's value */
+  int is_default;      /* 1: the value the op's own entry runs */
+  const char *entry;   /* entry taking the knob, or NULL (fixed at build time) */
+  double measured_us;  /* per launch at the op's reference shape (4096 rows), or -1 */
+  const char *reason;  /* why the default is the default, or how the candidate compares */
+} tcrv_hip_schedule;
+/* Number of rows, and row `index` (TCRV_HIP_ERR_BAD_SIZE past the end). */
+TCRV_HIP_API size_t tcrv_hip_route_schedule_count(void);
+TCRV_HIP_API int tcrv_hip_route_schedule(size_t index, tcrv_hip_schedule *out);
+/* The default value of `knob` for (op, m_regime) (a row with m_regime -1
+ * matches either regime); TCRV_HIP_ERR_UNSUPPORTED when the registry has none. */
+TCRV_HIP_API int tcrv_hip_route_schedule_default(const char *op, int m_regime, const char *knob,
+                                                 int64_t *value);
+
 /* ---- the host half of the export (lib/Target for this backend) ----------
  * What a HIP emission driver hands to the artifact export in place of the RVV
  * C the reference renders with exportMaterializedEmitCModuleToCpp

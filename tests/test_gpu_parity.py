@@ -231,6 +231,31 @@ def test_gemv_q4_0_q8_0(hip, oracle, dev, nr, nb):
     assert_f32_parity(from_dev(s), want, what=f"gemv nr={nr} nb={nb}")
 
 
+@pytest.mark.parametrize("nr,nb", [(1000, 128), (333, 40), (129, 200), (70, 9)])
+def test_gemv_shapes_are_bit_identical(hip, oracle, dev, nr, nb):
+    """The decode GEMV's schedule knob (rows per wave 2, 4, 8) changes how it
+    runs, never what it computes: every shape equals the oracle and the plain
+    entry bit for bit (one 128-block chunk, one partial chunk, two chunks, and
+    odd nb, which the LDS-staged kernel serves whatever the knob)."""
+    n = nb * 32
+    w = synth.q4_0_matrix(nr, n, 2201, 0.02)
+    x = synth.q8_0_matrix(1, n, 2202, 1.0)[0]
+    want = oracle.gemm_q4_0(n, w, x, 0, nr, 1, w.shape[1], 1, 8)[:nr]
+    dw, dx = to_dev(w, dev), to_dev(x, dev)
+    plain = empty_dev(nr, torch.float32, dev)
+    hip.gemv_q4_0_q8_0(n, plain, dw, w.shape[1], dx, nr)
+    assert_f32_parity(from_dev(plain), want, what="plain")
+    for rpw in (2, 4, 8):
+        s = empty_dev(nr, torch.float32, dev)
+        hip.gemv_q4_0_q8_0_shaped(n, s, dw, w.shape[1], dx, nr, rpw)
+        assert_f32_parity(from_dev(s), want, what=f"rows_per_wave {rpw}")
+    s = empty_dev(nr, torch.float32, dev)
+    for bad in (0, 1, 3, 16):
+        assert hip.gemv_q4_0_q8_0_shaped(n, s, dw, w.shape[1], dx, nr, bad,
+                                         check=False) == hip.ERR_BAD_SIZE
+    torch.cuda.synchronize()
+
+
 def test_q4_0_gemm_entry_nc1_strided_output(hip, oracle, dev):
     n, nr, bs = 32 * 40, 77, 3
     w = np.pad(synth.q4_0_matrix(nr, n, 5, 0.02), ((0, 0), (0, 48)))

@@ -53,6 +53,49 @@ def test_route_library_exports_its_header():
     assert set(tcrv_hip.ROUTE_SIGNATURES) == set(declared)
 
 
+def test_schedule_registry_is_consistent():
+    """Every registry row names an op of the route table; each (op, regime,
+    knob) has distinct candidate values and exactly one default, which is
+    within 1 % of the fastest measured candidate; a selectable row names an
+    entry the C-ABI header declares and libtcrv_hip exports."""
+    ops = {r["op"] for r in tcrv_hip.route_table()}
+    rows = tcrv_hip.route_schedules()
+    assert rows
+    hip_text = open(HIP_HEADER).read()
+    exported = subprocess.run(["nm", "-D", "--defined-only", tcrv_hip.LIB_PATH],
+                              capture_output=True, text=True, check=True).stdout
+    groups = {}
+    for r in rows:
+        assert r["op"] in ops, r
+        assert r["m_regime"] in (-1, tcrv_hip.M_DECODE, tcrv_hip.M_PREFILL), r
+        assert r["measured_us"] > 0 and r["reason"], r
+        if r["entry"]:
+            assert re.search(r"TCRV_HIP_API\s+int\s+" + r["entry"] + r"\s*\(", hip_text), r
+            assert re.search(r"\b" + r["entry"] + r"\b", exported), r
+        groups.setdefault((r["op"], r["m_regime"], r["knob"]), []).append(r)
+    for key, cands in groups.items():
+        values = [c["value"] for c in cands]
+        assert len(set(values)) == len(values), key
+        defaults = [c for c in cands if c["is_default"]]
+        assert len(defaults) == 1, key
+        assert defaults[0]["measured_us"] <= 1.01 * min(c["measured_us"] for c in cands), key
+        assert len({c["entry"] for c in cands}) == 1, key  # a knob is selectable or not
+
+
+def test_schedule_default_lookup():
+    d = tcrv_hip.route_schedule_default
+    assert d("tcrv_rvv.q4_0_q8_0_gemm", tcrv_hip.M_DECODE, "rows_per_wave") == (tcrv_hip.OK, 4)
+    assert d("tcrv_rvv.q8_0_q8_0_gemm", tcrv_hip.M_PREFILL, "k_chunk_blocks") == (tcrv_hip.OK, 6)
+    for regime in (tcrv_hip.M_DECODE, tcrv_hip.M_PREFILL):  # not regime-specific
+        assert d("tcrv_rvv.quantize_row_q8_0", regime, "blocks_per_lane_group") == (tcrv_hip.OK, 2)
+    assert d("tcrv_rvv.q4_0_q8_0_gemm", tcrv_hip.M_PREFILL, "rows_per_wave")[0] == \
+        tcrv_hip.ERR_UNSUPPORTED
+    assert d("tcrv_rvv.q4_0_q8_0_gemm", tcrv_hip.M_DECODE, "no_such_knob")[0] == \
+        tcrv_hip.ERR_UNSUPPORTED
+    assert d("tcrv_rvv.no_such_op", tcrv_hip.M_DECODE, "rows_per_wave")[0] == \
+        tcrv_hip.ERR_UNSUPPORTED
+
+
 @pytest.mark.parametrize("quant,regime,layout,algo,entry", [
     ("q4_0", tcrv_hip.M_DECODE, "plain", "decode_gemv", "tcrv_hip_q4_0_q8_0_gemm"),
     ("q8_0", tcrv_hip.M_DECODE, "plain", "decode_gemv", "tcrv_hip_q8_0_q8_0_gemm"),

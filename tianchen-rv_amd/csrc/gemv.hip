@@ -322,8 +322,27 @@ constexpr int kGemvRows = 2;
 constexpr int kDirectWaves = 4;
 constexpr int kDirectRows = 4;
 
+// The register-direct GEMV with kR rows per wave (kDirectWaves waves per
+// work-group); every shape computes the same per-row fold, bit for bit.
+template <int kR>
+int launch_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
+                  const uint8_t *vy, size_t nr, hipStream_t st) {
+  constexpr int kW = kDirectWaves;
+  const size_t rows_per_wg = static_cast<size_t>(kW) * kR;
+  const size_t grid = (nr + rows_per_wg - 1) / rows_per_wg;
+  if (grid > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  if (nb == static_cast<size_t>(tcrv::kGvChunk))
+    tcrv::gemv_q4_0_q8_0_direct<kW, kR, true>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(nb, s, os, vx, bx, vy, nr);
+  else
+    tcrv::gemv_q4_0_q8_0_direct<kW, kR, false>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(nb, s, os, vx, bx, vy, nr);
+  return launch_status();
+}
+
 int gemv_q4_0_q8_0(size_t n, float *s, size_t os, const uint8_t *vx, size_t bx,
-                   const uint8_t *vy, size_t nr, void *stream) {
+                   const uint8_t *vy, size_t nr, void *stream, int rows_per_wave) {
   const size_t nb = n / tcrv::kQK;
   if (nr == 0)
     return TCRV_HIP_OK;
@@ -337,18 +356,11 @@ int gemv_q4_0_q8_0(size_t n, float *s, size_t os, const uint8_t *vx, size_t bx,
     return TCRV_HIP_ERR_BAD_SIZE;
   hipStream_t st = as_stream(stream);
   if (nb % 2 == 0 && aligned4(vx) && aligned4(vy) && (nr == 1 || bx % 4 == 0)) {
-    constexpr int kW = kDirectWaves, kR = kDirectRows;
-    const size_t rows_per_wg = static_cast<size_t>(kW) * kR;
-    const size_t grid = (nr + rows_per_wg - 1) / rows_per_wg;
-    if (grid > 0x7fffffffu)
-      return TCRV_HIP_ERR_TOO_LARGE;
-    if (nb == static_cast<size_t>(tcrv::kGvChunk))
-      tcrv::gemv_q4_0_q8_0_direct<kW, kR, true>
-          <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(nb, s, os, vx, bx, vy, nr);
-    else
-      tcrv::gemv_q4_0_q8_0_direct<kW, kR, false>
-          <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(nb, s, os, vx, bx, vy, nr);
-    return launch_status();
+    switch (rows_per_wave) {
+    case 2: return launch_direct<2>(nb, s, os, vx, bx, vy, nr, st);
+    case 8: return launch_direct<8>(nb, s, os, vx, bx, vy, nr, st);
+    default: return launch_direct<kDirectRows>(nb, s, os, vx, bx, vy, nr, st);
+    }
   }
   const size_t rows_per_wg = static_cast<size_t>(tcrv::kGvWaves) * kGemvRows;
   const size_t grid = (nr + rows_per_wg - 1) / rows_per_wg;
@@ -442,7 +454,19 @@ int tcrv_hip_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx, size_t bx,
     return TCRV_HIP_OK;
   if (n / tcrv::kQK == 0)
     return tcrv_host::zero_outputs(s, nr, 1, 1, stream);
-  return tcrv_host::gemv_q4_0_q8_0(n, s, 1, vx, bx, vy, nr, stream);
+  return tcrv_host::gemv_q4_0_q8_0(n, s, 1, vx, bx, vy, nr, stream, tcrv_host::kDirectRows);
+}
+
+int tcrv_hip_gemv_q4_0_q8_0_shaped(size_t n, float *s, const uint8_t *vx, size_t bx,
+                                   const uint8_t *vy, size_t nr, int rows_per_wave,
+                                   void *stream) {
+  if (rows_per_wave != 2 && rows_per_wave != 4 && rows_per_wave != 8)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  if (nr == 0)
+    return TCRV_HIP_OK;
+  if (n / tcrv::kQK == 0)
+    return tcrv_host::zero_outputs(s, nr, 1, 1, stream);
+  return tcrv_host::gemv_q4_0_q8_0(n, s, 1, vx, bx, vy, nr, stream, rows_per_wave);
 }
 
 int tcrv_hip_q4_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
@@ -455,7 +479,7 @@ int tcrv_hip_q4_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t
   if (n / tcrv::kQK == 0)
     return tcrv_host::zero_outputs(s, nr * nc, bs, nc, stream);
   if (nc == 1)
-    return tcrv_host::gemv_q4_0_q8_0(n, s, bs, vx, bx, vy, nr, stream);
+    return tcrv_host::gemv_q4_0_q8_0(n, s, bs, vx, bx, vy, nr, stream, tcrv_host::kDirectRows);
   if (!s || !vx || !vy)
     return TCRV_HIP_ERR_NULL_POINTER;
   if (!tcrv_host::aligned2(vx) || !tcrv_host::aligned2(vy) || (nr > 1 && (bx & 1u)) || (by & 1u))

@@ -196,6 +196,55 @@ const HipKernelRoute kHipKernelRoutes[] = {
 };
 constexpr size_t kNumRoutes = std::size(kHipKernelRoutes);
 
+// The schedule registry (tcrv_hip_route_schedule): for each knob of a kernel
+// the legal candidates, the default and the measurement that chose it -- per
+// launch at the op's reference shape (the 4096-row configs), on one MI355X, in
+// the same bench as the shipped figure.  Rows with an entry can be chosen per
+// call; the rest are template constants of the library build.
+const tcrv_hip_schedule kSchedules[] = {
+    // the decode GEMV (q4_0 GEMM, nc = 1): rows per wave of the register-direct
+    // kernel, 4 waves per work-group; the fold runs on 8 lanes per row for 4 or
+    // 8 rows per wave, on 16 for 2
+    {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_DECODE, "gemv_q4_0_q8_0_direct", "rows_per_wave", 2,
+     0, "tcrv_hip_gemv_q4_0_q8_0_shaped", 4.173,
+     "2048 waves: two per SIMD share the read; the per-row fold chain is 15 lane hops"},
+    {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_DECODE, "gemv_q4_0_q8_0_direct", "rows_per_wave", 4,
+     1, "tcrv_hip_gemv_q4_0_q8_0_shaped", 3.911,
+     "measured fastest: one wave per SIMD, every lane busy in the decode and 32 fold lanes"},
+    {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_DECODE, "gemv_q4_0_q8_0_direct", "rows_per_wave", 8,
+     0, "tcrv_hip_gemv_q4_0_q8_0_shaped", 5.070,
+     "512 waves leave half the SIMDs idle during the read"},
+    // the tiled Q8_0 GEMM: blocks per K chunk (measured with two LDS stages for
+    // 5-6 blocks, three for 3-4)
+    {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles_q8", "k_chunk_blocks", 3, 0,
+     nullptr, 174.9, "three stages; more barriers per K"},
+    {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles_q8", "k_chunk_blocks", 4, 0,
+     nullptr, 170.1, "three stages"},
+    {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles_q8", "k_chunk_blocks", 5, 0,
+     nullptr, 163.5, "two stages; within the run-to-run spread of 6"},
+    {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles_q8", "k_chunk_blocks", 6, 1,
+     nullptr, 164.0,
+     "measured fastest with 5 (two stages, 154 KB of LDS: one chunk in flight covers the DMA "
+     "latency); 6 divides the 128 blocks of K = 4096 more evenly"},
+    // quantize_row_q8_0: 32-float blocks per 8-lane group
+    {"tcrv_rvv.quantize_row_q8_0", -1, "quantize_q8_0", "blocks_per_lane_group", 1, 0, nullptr,
+     18.3, "fewer loads in flight per thread"},
+    {"tcrv_rvv.quantize_row_q8_0", -1, "quantize_q8_0", "blocks_per_lane_group", 2, 1, nullptr,
+     16.5, "measured fastest"},
+    {"tcrv_rvv.quantize_row_q8_0", -1, "quantize_q8_0", "blocks_per_lane_group", 4, 0, nullptr,
+     17.3, "more registers, fewer waves"},
+    // tcrv_rvv.binary (add f32, n = 2^24): 16-byte vectors per operand and thread
+    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 1, 0, nullptr, 28.4,
+     "loads of one vector in flight"},
+    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 2, 1, nullptr, 28.1,
+     "measured fastest"},
+    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 4, 0, nullptr, 28.8,
+     "fewer work-groups in flight"},
+    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 8, 0, nullptr, 29.3,
+     "fewer work-groups in flight"},
+};
+constexpr size_t kNumSchedules = std::size(kSchedules);
+
 // The C element type a tcrv_rvv.binary of element `elem` reads and writes.
 const char *binaryCType(int elem) {
   switch (elem) {
@@ -418,6 +467,29 @@ int tcrv_hip_export_function(const char *op, const char *kernel, const char *var
     buf[n] = '\0';
   }
   return TCRV_HIP_OK;
+}
+
+size_t tcrv_hip_route_schedule_count(void) { return kNumSchedules; }
+
+int tcrv_hip_route_schedule(size_t index, tcrv_hip_schedule *out) {
+  if (index >= kNumSchedules || !out)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  *out = kSchedules[index];
+  return TCRV_HIP_OK;
+}
+
+int tcrv_hip_route_schedule_default(const char *op, int m_regime, const char *knob,
+                                    int64_t *value) {
+  if (!op || !knob)
+    return TCRV_HIP_ERR_UNSUPPORTED;
+  for (const tcrv_hip_schedule &r : kSchedules)
+    if (r.is_default && std::strcmp(r.op, op) == 0 && std::strcmp(r.knob, knob) == 0 &&
+        (r.m_regime == -1 || r.m_regime == m_regime)) {
+      if (value)
+        *value = r.value;
+      return TCRV_HIP_OK;
+    }
+  return TCRV_HIP_ERR_UNSUPPORTED;
 }
 
 long tcrv_hip_route_find(const char *op) {

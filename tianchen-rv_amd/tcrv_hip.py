@@ -66,6 +66,7 @@ SIGNATURES = {
     "tcrv_hip_q4_0_q8_0_gemm": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p],
     "tcrv_hip_q4_0_q8_0_gemm_tile": [_sz, _p, _p, _p, _sz, _sz, _p],
     "tcrv_hip_gemv_q4_0_q8_0": [_sz, _p, _p, _sz, _p, _sz, _p],
+    "tcrv_hip_gemv_q4_0_q8_0_shaped": [_sz, _p, _p, _sz, _p, _sz, _i32, _p],
     "tcrv_hip_q8_0_q8_0_gemm": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p],
     "tcrv_hip_pack_q4_0_to_q4_0x16": [_sz, _p, _p, _p],
     "tcrv_hip_pack_q8_0_to_q8_0x16": [_sz, _p, _p, _p],
@@ -247,6 +248,12 @@ def gemv_q4_0_q8_0(n: int, s, vx, bx: int, vy, nr: int, stream=None):
     return call("tcrv_hip_gemv_q4_0_q8_0", n, s, vx, bx, vy, nr, _stream(stream))
 
 
+def gemv_q4_0_q8_0_shaped(n: int, s, vx, bx: int, vy, nr: int, rows_per_wave: int, stream=None,
+                          check: bool = True):
+    return call("tcrv_hip_gemv_q4_0_q8_0_shaped", n, s, vx, bx, vy, nr, rows_per_wave,
+                _stream(stream), check=check)
+
+
 def q8_0_q8_0_gemm(n: int, s, vx, vy, by: int, nr: int, nc: int, bx: int, bs: int,
                    stream=None):
     return call("tcrv_hip_q8_0_q8_0_gemm", n, s, vx, vy, by, nr, nc, bx, bs, _stream(stream))
@@ -341,6 +348,15 @@ LAYOUT = {"plain": 0, "x16": 1}
 ALGO = {0: "decline", 1: "decode_gemv", 2: "repack_gemv", 3: "mfma_gemm", 4: "repack_gemm"}
 
 _cs = ctypes.c_char_p
+
+
+class Schedule(ctypes.Structure):
+    """tcrv_hip_schedule (include/tcrv_hip_route.h)."""
+    _fields_ = [("op", _cs), ("m_regime", _int), ("kernel", _cs), ("knob", _cs),
+                ("value", ctypes.c_int64), ("is_default", _int), ("entry", _cs),
+                ("measured_us", ctypes.c_double), ("reason", _cs)]
+
+
 ROUTE_SIGNATURES = {
     "tcrv_hip_route_select": ([_int, _int, _int, ctypes.POINTER(_int), ctypes.POINTER(_cs),
                                ctypes.POINTER(_cs)], _int),
@@ -355,6 +371,9 @@ ROUTE_SIGNATURES = {
     "tcrv_hip_route_param": ([_sz, _sz, ctypes.POINTER(_cs), ctypes.POINTER(_cs),
                               ctypes.POINTER(_cs)], _int),
     "tcrv_hip_route_find": ([_cs], ctypes.c_long),
+    "tcrv_hip_route_schedule_count": ([], _sz),
+    "tcrv_hip_route_schedule": ([_sz, ctypes.POINTER(Schedule)], _int),
+    "tcrv_hip_route_schedule_default": ([_cs, _int, _cs, ctypes.POINTER(ctypes.c_int64)], _int),
     "tcrv_hip_export_function": ([_cs, _cs, _cs, ctypes.POINTER(ctypes.c_int64), _sz, _int,
                                   ctypes.c_char_p, _sz, ctypes.POINTER(_sz)], _int),
     "tcrv_hip_export_prologue": ([], _cs),
@@ -418,6 +437,28 @@ def route_table():
         rows.append({"op": lib.tcrv_hip_route_op(i).decode(),
                      "entry": lib.tcrv_hip_route_entry(i).decode(), "params": params})
     return rows
+
+
+def route_schedules():
+    """The schedule registry: one dict per (op, regime, knob, candidate value)."""
+    lib = load_route()
+    rows = []
+    for i in range(lib.tcrv_hip_route_schedule_count()):
+        r = Schedule()
+        _check("tcrv_hip_route_schedule", lib.tcrv_hip_route_schedule(i, ctypes.byref(r)))
+        rows.append({"op": r.op.decode(), "m_regime": r.m_regime, "kernel": r.kernel.decode(),
+                     "knob": r.knob.decode(), "value": r.value, "is_default": bool(r.is_default),
+                     "entry": r.entry.decode() if r.entry else None,
+                     "measured_us": r.measured_us, "reason": r.reason.decode()})
+    return rows
+
+
+def route_schedule_default(op: str, m_regime: int, knob: str):
+    """(status, the default value of `knob` for (op, m_regime) or None)."""
+    v = ctypes.c_int64()
+    st = load_route().tcrv_hip_route_schedule_default(op.encode(), m_regime, knob.encode(),
+                                                      ctypes.byref(v))
+    return st, (v.value if st == OK else None)
 
 
 def export_function(op: str, kernel: str, variant: str, attrs=(), form: int = EXPORT_DEFINITION):
