@@ -31,7 +31,7 @@ KERNELS = {
     "gemv_q4_0_q8_0": "gemv_q4_0_q8_0_direct",
     "q8_0_q8_0_gemm": "gemm_wide<false>",
     "q8_0_q8_0_gemm_tiles": "gemm_tiles_q8<true>",
-    "pack_q8_0_to_gemm_tiles": "pack_gemm_tiles_span",
+    "pack_both_to_gemm_tiles": "pack_gemm_tiles_span2",
     "calib": "add_f32_vec4",
 }
 CALIB_BYTES = {"FETCH_SIZE": 8 << 24, "WRITE_SIZE": 4 << 24}  # per add_f32 launch, n = 2^24
@@ -118,7 +118,7 @@ def traffic(root):
         out[f"calib_{ctr}"] = {"KiB_per_dispatch": kib, "dispatches": n, "known_bytes": known,
                                "scale": scale[ctr]}
     for key, tag in (("gemv_q4_0_q8_0", "gemv"), ("q8_0_q8_0_gemm", "gemm"),
-                     ("q8_0_q8_0_gemm_tiles", "gemm"), ("pack_q8_0_to_gemm_tiles", "gemm")):
+                     ("q8_0_q8_0_gemm_tiles", "gemm"), ("pack_both_to_gemm_tiles", "gemm")):
         total = 0.0
         entry = {"kernel": KERNELS[key]}
         for ctr in CALIB_BYTES:
