@@ -29,6 +29,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 // XCD-aware tile order: work-groups are dispatched round-robin over the 8
 // XCDs (id % 8), so id is first remapped so that each XCD owns one contiguous
@@ -73,9 +74,13 @@ __device__ __forceinline__ v16i q8_sumi(const v4i &a, const v4i &bq) {
 // The scale MFMA: d_x * d_y of one tile and block, from the lane's two fp16
 // scale bit patterns (k-slot 0; the zero k-slots of lanes 32-63 come from the
 // zero rows).
+// The operands are the zero-extended 16-bit reads taken whole as the low two
+// halves (k-slots 0, 1 = the scale, 0): built half by half, the compiler masks
+// each read again (one VALU instruction and a hazard wait before the MFMA).
 __device__ __forceinline__ v16f q8_dxy(uint32_t ux, uint32_t uy) {
-  const v4h ax = __builtin_bit_cast(v4h, make_uint2(ux, 0u));
-  const v4h by = __builtin_bit_cast(v4h, make_uint2(uy, 0u));
+  const v2h z = {};
+  const v4h ax = __builtin_shufflevector(__builtin_bit_cast(v2h, ux), z, 0, 1, 2, 3);
+  const v4h by = __builtin_shufflevector(__builtin_bit_cast(v2h, uy), z, 0, 1, 2, 3);
   return __builtin_amdgcn_mfma_f32_32x32x8f16(ax, by, v16f{}, 0, 0, 0);
 }
 
