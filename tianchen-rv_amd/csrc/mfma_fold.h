@@ -245,10 +245,13 @@ __device__ __forceinline__ bool q4_chunk_nonfinite(const uint16_t *hx, int nbc, 
 template <bool kExact>
 __device__ __forceinline__ void q4_fold(float (&acc)[16], const v16f &F, uint32_t ux,
                                         const uint16_t *hy) {
-  // Plain fp32 arithmetic on widened fp16 values: the compiler selects
-  // v_fma_mix_f32 (the fp16 operand read in place) and inserts the wait states
-  // a VALU read of a matrix-core result needs.
-  const float dx = f16_bits(ux);
+  // Plain fp32 arithmetic on widened fp16 values (the compiler inserts the
+  // wait states a VALU read of a matrix-core result needs).  d_x is widened
+  // once and hidden from instruction selection, which would otherwise re-read
+  // it as fp16 in every product (v_fma_mix_f32 issues slower than v_fma_f32);
+  // d_y, one per element, is read in place by v_fma_mix_f32.
+  float dx = f16_bits(ux);
+  asm volatile("" : "+v"(dx));
   const float c = -kSeed * dx;  // -M * d_x, exact (unused by the exact form)
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
