@@ -187,16 +187,17 @@ __device__ __forceinline__ void fold_tail_q8(float (&acc)[2][16], const int8_t *
 // A operand and the weights as B, so lane (c = lane % 32, h = lane / 32) holds
 // weight row c and tokens 8g + 4h + j (g, j < 4) of the tile.  d_x is then one
 // value per lane and tile-block (a 16-bit LDS read) and d_y one per element
-// (a 64-bit LDS read gives four; both tiles of a wave share them).
+// (a 64-bit LDS read gives four).
 //
 // The MFMA's accumulator input is the integer bit pattern of M = 1.5 * 2^23
 // (0x4B400000) in every element, so its results read as floats are
 // F = M + sumi exactly: |sumi| <= 32 * 8 * 128 < 2^22 keeps F in M's binade,
 // whose spacing is 1.  Then fma(F, d_x, -M * d_x) = fl(sumi * d_x): the exact
 // F * d_x - M * d_x = sumi * d_x is rounded once, and -M * d_x is itself exact
-// (an fp16 significand times 1.5).  That fma and fma(t, d_y, acc), both with
-// the fp16 scale read in place (v_fma_mix_f32), are the fold's two VALU
-// instructions per element; -M * d_x is one per lane and tile-block.
+// (an fp16 significand times 1.5).  That fma (v_fma_f32) and fma(t, d_y, acc)
+// (v_fma_mix_f32, the fp16 d_y read in place) are the fold's two VALU
+// instructions per element; d_x and -M * d_x are one each per lane and
+// tile-block.
 // An infinite d_x makes -M * d_x infinite, and the fast form NaN where the
 // reference has +-inf: a chunk with a non-finite d_x among the wave's weight
 // rows (q4_chunk_nonfinite, one test per chunk) is folded in the exact
@@ -257,8 +258,8 @@ __device__ __forceinline__ void q4_fold(float (&acc)[16], const v16f &F, uint32_
   for (int g = 0; g < 4; ++g) {
     const uint2 dy = *reinterpret_cast<const uint2 *>(hy + 8 * g);
     // fl(sumi * d_x) of four rows, from F directly or from sumi = F - M
-    // (exact), all four before the fmas that take them: a VALU result read by
-    // the next instruction stalls the wave.
+    // (exact), all four before the fmas that take them (each product a few
+    // instructions ahead of its use).
     float t[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -280,7 +281,7 @@ __device__ __forceinline__ void q4_fold(float (&acc)[16], const v16f &F, uint32_
 // step s (as fold_chunk_q8 with kPipe).  qw: this lane's weight quants of tile
 // 0, block 0 (tile 1 kTileStride bytes on); qt: its token quants; hx: its
 // weight row's d_x slot of tile 0, block 0 (tile 1 is 32 rows on); hy: d_y of
-// its tokens' first row (q4_token_scales).
+// its tokens 4h.. of block 0 (q4_fold).
 template <bool kExact, int kBlocks, int kBlockStride, int kTileStride, int kScaleRow,
           typename AfterStep>
 __device__ __forceinline__ void fold_chunk_q4(float (&acc)[2][16], const int8_t *qw,
