@@ -1,6 +1,7 @@
-// gemm_tiled.hip -- a9 Q8_0 x Q8_0 GEMM over operands in the GEMM-tile layout,
-// staged into LDS by DMA (global_load_lds_dwordx4): no staging registers and
-// no staging VALU, so every VGPR and VALU cycle goes to the fold.
+// gemm_tiled.hip -- the a9 Q8_0 x Q8_0 and a7 Q4_0 x Q8_0 GEMMs over operands
+// in the GEMM-tile layout, staged into LDS by DMA (global_load_lds_dwordx4): no
+// staging registers and no staging VALU, so every VGPR and VALU cycle goes to
+// the fold.
 //
 // GEMM-tile layout of a Q8_0 matrix of nrows rows x nb blocks (the same bytes
 // as the plain rows, regrouped): rows in groups of 64; for group g and block b
@@ -12,8 +13,13 @@
 // operand of one v_mfma_i32_32x32x32_i8 lane (16 quants), already 16-byte
 // aligned, so a wave moves one half of 64 rows with one 1 KB DMA instruction.
 //
-// Semantics are those of tcrv_hip_q8_0_q8_0_gemm (gemm.hip): every output is
-// the a5 block dot, folded in ascending block order (mfma_fold.h).
+// Q4_0 weights take the same records with each nibble decoded to its signed
+// quant q - 8 (element j < 16 from the low nibble of quant byte j, 16 + j from
+// its high nibble) and the fp16 scale copied.
+//
+// Semantics are those of tcrv_hip_q8_0_q8_0_gemm and tcrv_hip_q4_0_q8_0_gemm
+// (gemm.hip): every output is the a5 / a6 block dot, folded in ascending block
+// order (mfma_fold.h).
 #include "mfma_fold.h"
 
 namespace tcrv {
