@@ -523,20 +523,29 @@ def bench_configs(torch, lib, stream, args):
     out["q4_0_q8_0_gemm"] = {"workload": "a7 Q4_0 x Q8_0 GEMM 4096 rows x 4096 tokens x 4096",
                              "us": round(us, 1), "TOPS": round(GEMM_OPS / us / 1e6, 1),
                              "regions": 3}
-    # the same GEMM over the GEMM-tile layout: Q4_0 weights packed once (outside
-    # the timed region), the activations packed per call, and the tiled kernel
+    # the same GEMM over the GEMM-tile layout: the reference ABI with a workspace
+    # (both operands packed per call), Q4_0 weights packed once (outside the
+    # timed region) with the activations packed per call, and the tiled kernel
     # alone; each checked against one eager launch of the plain entry
     nb = N // 32
     tx4 = torch.empty(lib.tcrv_hip_gemm_tiles_bytes(N, nb), dtype=torch.uint8, device=dev)
     ty4 = torch.empty(lib.tcrv_hip_gemm_tiles_bytes(N, nb), dtype=torch.uint8, device=dev)
+    wsb4 = lib.tcrv_hip_q4_0_q8_0_gemm_workspace_bytes(N, N, N)
+    ws4 = torch.empty(wsb4, dtype=torch.uint8, device=dev)
     pack_w = checked(lib.tcrv_hip_pack_q4_0_to_gemm_tiles, "pack_q4_0_to_gemm_tiles")
     pack_a = checked(lib.tcrv_hip_pack_q8_0_to_gemm_tiles, "pack_q8_0_to_gemm_tiles")
     tiles4 = checked(lib.tcrv_hip_q4_0_q8_0_gemm_tiles, "q4_0_q8_0_gemm_tiles")
+    ws_fn4 = checked(lib.tcrv_hip_q4_0_q8_0_gemm_ws, "q4_0_q8_0_gemm_ws")
     with torch.cuda.stream(stream):
         pack_w(N, nb, wd.data_ptr(), w.shape[1], tx4.data_ptr(), sp)
         pack_a(N, nb, ad.data_ptr(), a.shape[1], ty4.data_ptr(), sp)
     torch.cuda.synchronize()
     q4_paths = {
+        "q4_0_q8_0_gemm_ws": (
+            "a7 Q4_0 x Q8_0 GEMM 4096^3 through tcrv_hip_q4_0_q8_0_gemm_ws (the reference ABI): "
+            "per call both operands packed into the workspace (one launch) + the tiled kernel",
+            lambda i: ws_fn4(N, cd.data_ptr(), wd.data_ptr(), ad.data_ptr(), a.shape[1], N, N,
+                             w.shape[1], N, ws4.data_ptr(), wsb4, sp)),
         "q4_0_q8_0_gemm_prepacked_weights": (
             "a7 Q4_0 x Q8_0 GEMM 4096^3, Q4_0 weights pre-packed into the GEMM-tile layout; "
             "per call: pack the Q8_0 activations + the tiled kernel",
@@ -556,7 +565,7 @@ def bench_configs(torch, lib, stream, args):
                       name)
         out[name] = {"workload": what, "us": round(per[1], 1),
                      "TOPS": round(GEMM_OPS / per[1] / 1e6, 1), "regions": 3}
-    del tx4, ty4
+    del tx4, ty4, ws4
     # the repack GEMM over the same weights (x16) and activations (x4), 4096^3
     nb = N // 32
     srcw = torch.from_numpy(w.reshape(N // 16, 16, nb, 18).transpose(0, 2, 1, 3).copy()).to(dev)

@@ -277,12 +277,23 @@ TCRV_HIP_API int tcrv_hip_pack_q4_0_to_gemm_tiles(size_t nrows, size_t nb, const
                                                   size_t bx, uint8_t *dst, void *stream);
 /* The Q4_0 x Q8_0 GEMM over tx (Q4_0 weights packed as above) and ty (Q8_0
  * tokens packed by tcrv_hip_pack_q8_0_to_gemm_tiles): s[ir*bs + col] exactly as
- * tcrv_hip_q4_0_q8_0_gemm computes it from the plain rows.  For weights packed
- * once; there is no workspace form, since packing both operands per call costs
- * more than the tiled kernel saves over tcrv_hip_q4_0_q8_0_gemm. */
+ * tcrv_hip_q4_0_q8_0_gemm computes it from the plain rows.  Weights that are
+ * packed once serve every later call. */
 TCRV_HIP_API int tcrv_hip_q4_0_q8_0_gemm_tiles(size_t n, float *s, const uint8_t *tx,
                                                const uint8_t *ty, size_t nr, size_t nc,
                                                size_t bs, void *stream);
+/* tcrv_hip_q4_0_q8_0_gemm (same ABI and results) with a caller-owned device
+ * workspace: the Q4_0 weights and the Q8_0 tokens are packed into it (tx then
+ * ty, one launch) and the tiled GEMM runs.  Needs
+ * tcrv_hip_q4_0_q8_0_gemm_workspace_bytes(n, nr, nc) bytes, 16-byte aligned;
+ * shapes the tiled kernel does not serve (nr < 256, nc < 2) run
+ * tcrv_hip_q4_0_q8_0_gemm and leave the workspace untouched.  Calls that share
+ * a workspace must be ordered (one stream). */
+TCRV_HIP_API size_t tcrv_hip_q4_0_q8_0_gemm_workspace_bytes(size_t n, size_t nr, size_t nc);
+TCRV_HIP_API int tcrv_hip_q4_0_q8_0_gemm_ws(size_t n, float *s, const uint8_t *vx,
+                                            const uint8_t *vy, size_t by, size_t nr, size_t nc,
+                                            size_t bx, size_t bs, void *workspace,
+                                            size_t workspace_bytes, void *stream);
 
 /* ---- a8: the x16 block-as-lane weight layout ---------------------------
  * Replaces tcrv_emitc_..._pack_q4_0_to_q4_0x16(size_t nblocks, const uint8_t *src,

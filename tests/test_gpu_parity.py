@@ -976,6 +976,16 @@ def test_q4_0_gemm_tiles(hip, oracle, dev, nr, nc, nb, xpad, ypad):
     got = from_dev(q4_tiles_gemm(hip, dev, n, w, a, nr, nc, bs, s)).reshape(nr, bs)
     assert_f32_parity(got[:, :nc], want[:, :nc], what=f"q4 tiles gemm {nr}x{nc}x{n}")
     assert np.all(got[:, nc:] == -7.0)
+    # the reference ABI with a workspace (shapes below 256 weight rows or with
+    # one token run the plain entry)
+    wsb = hip.q4_0_q8_0_gemm_workspace_bytes(n, nr, nc)
+    ws = empty_dev(max(wsb, 16), torch.uint8, dev)
+    s2 = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+    hip.q4_0_q8_0_gemm_ws(n, s2, to_dev(w, dev), to_dev(a, dev), a.shape[1], nr, nc, w.shape[1],
+                          bs, ws, wsb)
+    got2 = from_dev(s2).reshape(nr, bs)
+    assert_f32_parity(got2[:, :nc], want[:, :nc], what=f"q4 gemm_ws {nr}x{nc}x{n}")
+    assert np.all(got2[:, nc:] == -7.0)
 
 
 def test_q4_0_gemm_tiles_checks(hip, dev):
@@ -993,14 +1003,49 @@ def test_q4_0_gemm_tiles_checks(hip, dev):
     torch.cuda.synchronize()
 
 
+def test_q4_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
+    """Shapes the tiled kernel does not serve run the plain entry and leave the
+    workspace alone; a workspace that is too small or misaligned is refused."""
+    n, nb = 256, 8
+    for nr, nc in ((100, 70), (300, 1), (1, 40)):
+        w = synth.q4_0_matrix(nr, n, 85, 0.02)
+        a = synth.q8_0_matrix(nc, n, 86, 1.0)
+        ws = to_dev(np.full(64, 0x5A, np.uint8), dev)
+        s = empty_dev(nr * nc, torch.float32, dev)
+        hip.q4_0_q8_0_gemm_ws(n, s, to_dev(w, dev), to_dev(a, dev), a.shape[1], nr, nc,
+                              w.shape[1], nc, ws, 64)
+        assert_f32_parity(from_dev(s), oracle.gemm_q4_0(n, w, a, a.shape[1], nr, nc, w.shape[1],
+                                                        nc, 8))
+        assert np.all(from_dev(ws) == 0x5A)
+    w = synth.q4_0_matrix(256, n, 87, 0.02)
+    a = synth.q8_0_matrix(16, n, 88, 1.0)
+    need = hip.q4_0_q8_0_gemm_workspace_bytes(n, 256, 16)
+    assert need == hip.gemm_tiles_bytes(256, nb) + hip.gemm_tiles_bytes(16, nb)
+    ws = empty_dev(need + 16, torch.uint8, dev)
+    s = empty_dev(256 * 16, torch.float32, dev)
+    call = lambda *args: hip.call("tcrv_hip_q4_0_q8_0_gemm_ws", n, s, to_dev(w, dev),
+                                  to_dev(a, dev), a.shape[1], 256, 16, w.shape[1], 16, *args, 0,
+                                  check=False)
+    assert call(ws, need - 1) == hip.ERR_BAD_SIZE
+    assert call(ws[8:], need) == hip.ERR_MISALIGNED
+    torch.cuda.synchronize()
+
+
 def test_q4_0_gemm_tiles_full_size_sampled(hip, oracle, dev):
-    """4096 x 4096 x 4096 Q4_0 x Q8_0 through the GEMM-tile layout; 64 rows
-    and 64 columns checked against the oracle."""
+    """4096 x 4096 x 4096 Q4_0 x Q8_0 through the GEMM-tile layout and through
+    the workspace entry (the two bit-identical everywhere); 64 rows and 64
+    columns checked against the oracle."""
     n = nr = nc = 4096
     w = synth.q4_0_matrix(nr, n, 1006, 0.02)
     a = synth.q8_0_matrix(nc, n, 1008, 1.0)
     s = empty_dev(nr * nc, torch.float32, dev)
     got = from_dev(q4_tiles_gemm(hip, dev, n, w, a, nr, nc, nc, s)).reshape(nr, nc)
+    wsb = hip.q4_0_q8_0_gemm_workspace_bytes(n, nr, nc)
+    ws = empty_dev(wsb, torch.uint8, dev)
+    s2 = empty_dev(nr * nc, torch.float32, dev)
+    hip.q4_0_q8_0_gemm_ws(n, s2, to_dev(w, dev), to_dev(a, dev), a.shape[1], nr, nc, w.shape[1],
+                          nc, ws, wsb)
+    assert np.array_equal(from_dev(s2).reshape(nr, nc).view(np.uint32), got.view(np.uint32))
     rng = np.random.default_rng(13)
     for r in np.sort(rng.choice(nr, 64, replace=False)):
         want = oracle.gemm_q4_0(n, w[r].copy(), a, a.shape[1], 1, nc, w.shape[1], nc, 8)

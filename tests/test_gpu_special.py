@@ -111,6 +111,22 @@ def test_q4_0_gemm_tiles_special_scales(hip, oracle, dev):
     assert_f32_parity_nan(from_dev(s), want, what="q4 gemm tiles")
 
 
+def test_q4_0_gemm_ws_special_scales(hip, oracle, dev):
+    """The workspace entry: both operands packed in one launch (16-byte aligned
+    rows, 8-block spans), then the tiled Q4_0 GEMM."""
+    nr, nc, nb = 320, 96, 16
+    n = nb * 32
+    w = q4(nr, nb, 35, nonfinite_every=16)
+    a = q8(nc, nb, 36, 1.0, nonfinite_every=23)
+    wsb = hip.q4_0_q8_0_gemm_workspace_bytes(n, nr, nc)
+    ws = empty_dev(wsb, torch.uint8, dev)
+    s = empty_dev(nr * nc, torch.float32, dev)
+    hip.q4_0_q8_0_gemm_ws(n, s, to_dev(w, dev), to_dev(a, dev), a.shape[1], nr, nc, w.shape[1],
+                          nc, ws, wsb)
+    want = oracle.gemm_q4_0(n, w, a, a.shape[1], nr, nc, w.shape[1], nc, 8)
+    assert_f32_parity_nan(from_dev(s), want, what="q4 gemm_ws")
+
+
 def test_q4_0_gemm_tiles_nonfinite_dx_mid_k(hip, oracle, dev):
     """The tiled Q4_0 GEMM folds each 6-block chunk in a fast form that is exact
     only for finite d_x, switching a wave to the exact form from the first chunk

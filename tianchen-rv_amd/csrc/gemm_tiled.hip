@@ -112,27 +112,6 @@ __global__ __launch_bounds__(256) void pack_gemm_tiles_span(size_t nrows, size_t
   pack_span(nrows, nb, src, bx, dst, wave, static_cast<int>(threadIdx.x & 63));
 }
 
-// Both operands of one GEMM in one launch (their spans back to back in the
-// grid): one launch instead of two, and twice the loads in flight.
-struct SpanOperand {
-  const uint8_t *src;
-  size_t bx, nrows, nspans;
-  uint8_t *dst;
-};
-
-__global__ __launch_bounds__(256) void pack_gemm_tiles_span2(size_t nb, SpanOperand x,
-                                                             SpanOperand y) {
-  size_t wave = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
-  const int r = static_cast<int>(threadIdx.x & 63);
-  if (wave < x.nspans) {
-    pack_span(x.nrows, nb, x.src, x.bx, x.dst, wave, r);
-    return;
-  }
-  wave -= x.nspans;
-  if (wave < y.nspans)
-    pack_span(y.nrows, nb, y.src, y.bx, y.dst, wave, r);
-}
-
 // One wave per (group, block) record for blocks b0.. of every group, lane
 // r = row 64g + r.  kAligned: the rows are 4-byte aligned (dword loads,
 // realigned with v_alignbyte for even blocks); otherwise 16-bit loads.
@@ -197,17 +176,12 @@ __device__ __forceinline__ void decode_q4_quants(const uint32_t w[4], uint32_t q
   }
 }
 
-// Rows 16-byte aligned (bx % 16 == 0): one wave per (group, 8-block span),
-// lane r = row 64g + r; the span is 144 contiguous bytes (9 aligned 128-bit
-// loads), block k at byte 18k.
-__global__ __launch_bounds__(256) void pack_q4_tiles_span(size_t nrows, size_t nb,
-                                                          const uint8_t *src, size_t bx,
-                                                          uint8_t *dst, size_t nspans) {
-  const size_t wave = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
+// Span `wave` of one Q4_0 operand with 16-byte aligned rows (bx % 16 == 0):
+// 64-row group g, 8-block span c, lane r = row 64g + r; the span is 144
+// contiguous bytes (9 aligned 128-bit loads), block k at byte 18k.
+__device__ __forceinline__ void pack_q4_span(size_t nrows, size_t nb, const uint8_t *src,
+                                             size_t bx, uint8_t *dst, size_t wave, int r) {
   const size_t spans_per_group = nb / kPackSpan;
-  if (wave >= nspans)
-    return;
-  const int r = static_cast<int>(threadIdx.x & 63);
   const size_t g = wave / spans_per_group, c = wave - g * spans_per_group;
   const size_t row = g * kTG + r;
   uint32_t v[4 * 9];
@@ -253,6 +227,16 @@ __global__ __launch_bounds__(256) void pack_q4_tiles_span(size_t nrows, size_t n
   }
 }
 
+// One wave per (group, span) of one Q4_0 operand.
+__global__ __launch_bounds__(256) void pack_q4_tiles_span(size_t nrows, size_t nb,
+                                                          const uint8_t *src, size_t bx,
+                                                          uint8_t *dst, size_t nspans) {
+  const size_t wave = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
+  if (wave >= nspans)
+    return;
+  pack_q4_span(nrows, nb, src, bx, dst, wave, static_cast<int>(threadIdx.x & 63));
+}
+
 // One wave per (group, block) record for blocks b0.. of every group (rows
 // 2-byte aligned: 16-bit loads).
 __global__ __launch_bounds__(256) void pack_q4_tiles(size_t nrows, size_t nb, const uint8_t *src,
@@ -285,6 +269,32 @@ __global__ __launch_bounds__(256) void pack_q4_tiles(size_t nrows, size_t nb, co
   reinterpret_cast<uint4 *>(o)[r] = make_uint4(q[0], q[1], q[2], q[3]);
   reinterpret_cast<uint4 *>(o + 1024)[r] = make_uint4(q[4], q[5], q[6], q[7]);
   reinterpret_cast<uint16_t *>(o + 2048)[r] = static_cast<uint16_t>(d);
+}
+
+// Both operands of one GEMM in one launch (their spans back to back in the
+// grid): one launch instead of two, and twice the loads in flight.  kXQ4: the
+// first operand is Q4_0 weights.
+struct SpanOperand {
+  const uint8_t *src;
+  size_t bx, nrows, nspans;
+  uint8_t *dst;
+};
+
+template <bool kXQ4>
+__global__ __launch_bounds__(256) void pack_gemm_tiles_span2(size_t nb, SpanOperand x,
+                                                             SpanOperand y) {
+  size_t wave = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
+  const int r = static_cast<int>(threadIdx.x & 63);
+  if (wave < x.nspans) {
+    if constexpr (kXQ4)
+      pack_q4_span(x.nrows, nb, x.src, x.bx, x.dst, wave, r);
+    else
+      pack_span(x.nrows, nb, x.src, x.bx, x.dst, wave, r);
+    return;
+  }
+  wave -= x.nspans;
+  if (wave < y.nspans)
+    pack_span(y.nrows, nb, y.src, y.bx, y.dst, wave, r);
 }
 
 // ---------------------------------------------------------------- GEMM ---
@@ -594,28 +604,6 @@ int pack_tiles(size_t nrows, size_t nb, const uint8_t *src, size_t bx, uint8_t *
   return launch_status();
 }
 
-// Both Q8_0 operands of a GEMM: one launch of the span kernel when every block
-// of both is in an 8-block span of 16-byte aligned rows, else pack_tiles each.
-int pack_tiles_both(size_t nb, const uint8_t *vx, size_t bx, size_t nr, uint8_t *tx,
-                    const uint8_t *vy, size_t by, size_t nc, uint8_t *ty, hipStream_t st) {
-  using namespace tcrv_host;
-  auto spans_only = [&](const uint8_t *src, size_t stride, size_t nrows) {
-    return aligned16(src) && (nrows == 1 || stride % 16 == 0) && nb % tcrv::kPackSpan == 0;
-  };
-  if (nb == 0 || !spans_only(vx, bx, nr) || !spans_only(vy, by, nc)) {
-    const int rc = pack_tiles(nr, nb, vx, bx, tx, st);
-    return rc != TCRV_HIP_OK ? rc : pack_tiles(nc, nb, vy, by, ty, st);
-  }
-  const size_t per_group = nb / tcrv::kPackSpan;
-  const tcrv::SpanOperand x{vx, bx, nr, (nr + tcrv::kTG - 1) / tcrv::kTG * per_group, tx};
-  const tcrv::SpanOperand y{vy, by, nc, (nc + tcrv::kTG - 1) / tcrv::kTG * per_group, ty};
-  const size_t grid = ((x.nspans + y.nspans) * 64 + 255) / 256;
-  if (grid > 0x7fffffffu)
-    return TCRV_HIP_ERR_TOO_LARGE;
-  tcrv::pack_gemm_tiles_span2<<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(nb, x, y);
-  return launch_status();
-}
-
 int pack_tiles_q4(size_t nrows, size_t nb, const uint8_t *src, size_t bx, uint8_t *dst,
                   hipStream_t st) {
   using namespace tcrv_host;
@@ -638,6 +626,35 @@ int pack_tiles_q4(size_t nrows, size_t nb, const uint8_t *src, size_t bx, uint8_
     tcrv::pack_q4_tiles<<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(
         nrows, nb, src, bx, dst, b0, nrec);
   }
+  return launch_status();
+}
+
+// Both operands of a GEMM (xq4: the weights vx are Q4_0): one launch of the span
+// kernel when every block of both is in an 8-block span of 16-byte aligned rows,
+// else one pack per operand.
+int pack_tiles_both(size_t nb, const uint8_t *vx, size_t bx, size_t nr, uint8_t *tx,
+                    const uint8_t *vy, size_t by, size_t nc, uint8_t *ty, hipStream_t st,
+                    bool xq4 = false) {
+  using namespace tcrv_host;
+  auto spans_only = [&](const uint8_t *src, size_t stride, size_t nrows) {
+    return aligned16(src) && (nrows == 1 || stride % 16 == 0) && nb % tcrv::kPackSpan == 0;
+  };
+  if (nb == 0 || !spans_only(vx, bx, nr) || !spans_only(vy, by, nc)) {
+    const int rc = xq4 ? pack_tiles_q4(nr, nb, vx, bx, tx, st) : pack_tiles(nr, nb, vx, bx, tx, st);
+    return rc != TCRV_HIP_OK ? rc : pack_tiles(nc, nb, vy, by, ty, st);
+  }
+  const size_t per_group = nb / tcrv::kPackSpan;
+  const tcrv::SpanOperand x{vx, bx, nr, (nr + tcrv::kTG - 1) / tcrv::kTG * per_group, tx};
+  const tcrv::SpanOperand y{vy, by, nc, (nc + tcrv::kTG - 1) / tcrv::kTG * per_group, ty};
+  const size_t grid = ((x.nspans + y.nspans) * 64 + 255) / 256;
+  if (grid > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  if (xq4)
+    tcrv::pack_gemm_tiles_span2<true>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(nb, x, y);
+  else
+    tcrv::pack_gemm_tiles_span2<false>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(nb, x, y);
   return launch_status();
 }
 
@@ -770,6 +787,38 @@ int tcrv_hip_q4_0_q8_0_gemm_tiles(size_t n, float *s, const uint8_t *tx, const u
   if (!aligned16(tx) || !aligned16(ty))
     return TCRV_HIP_ERR_MISALIGNED;
   return gemm_tiles(nb, s, tx, ty, nr, nc, bs, as_stream(stream), true);
+}
+
+size_t tcrv_hip_q4_0_q8_0_gemm_workspace_bytes(size_t n, size_t nr, size_t nc) {
+  const size_t nb = n / tcrv::kQK;
+  return tile_bytes(nr, nb) + tile_bytes(nc, nb);
+}
+
+int tcrv_hip_q4_0_q8_0_gemm_ws(size_t n, float *s, const uint8_t *vx, const uint8_t *vy,
+                               size_t by, size_t nr, size_t nc, size_t bx, size_t bs,
+                               void *workspace, size_t workspace_bytes, void *stream) {
+  using namespace tcrv_host;
+  const size_t nb = n / tcrv::kQK;
+  if (!gemm_ws_uses_workspace(n, nr, nc))
+    return tcrv_hip_q4_0_q8_0_gemm(n, s, vx, vy, by, nr, nc, bx, bs, stream);
+  if (bs < nc)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  if (!s || !vx || !vy || !workspace)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned2(vx) || !aligned2(vy) || (bx & 1u) || (by & 1u) || !aligned16(workspace))
+    return TCRV_HIP_ERR_MISALIGNED;
+  if (bx < nb * tcrv::kQ4Bytes || by < nb * tcrv::kQ8Bytes)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  const size_t tx_bytes = tile_bytes(nr, nb), ty_bytes = tile_bytes(nc, nb);
+  if (workspace_bytes < tx_bytes + ty_bytes)
+    return TCRV_HIP_ERR_BAD_SIZE;
+  uint8_t *tx = static_cast<uint8_t *>(workspace);
+  uint8_t *ty = tx + tx_bytes;  // tx_bytes is a multiple of 2176 = 16 * 136
+  hipStream_t st = as_stream(stream);
+  const int rc = pack_tiles_both(nb, vx, bx, nr, tx, vy, by, nc, ty, st, true);
+  if (rc != TCRV_HIP_OK)
+    return rc;
+  return gemm_tiles(nb, s, tx, ty, nr, nc, bs, st, true);
 }
 
 }  // extern "C"

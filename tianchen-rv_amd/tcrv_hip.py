@@ -83,10 +83,12 @@ SIGNATURES = {
     "tcrv_hip_q8_0_q8_0_gemm_noalloc": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p],
     "tcrv_hip_pack_q4_0_to_gemm_tiles": [_sz, _sz, _p, _sz, _p, _p],
     "tcrv_hip_q4_0_q8_0_gemm_tiles": [_sz, _p, _p, _p, _sz, _sz, _sz, _p],
+    "tcrv_hip_q4_0_q8_0_gemm_ws": [_sz, _p, _p, _p, _sz, _sz, _sz, _sz, _sz, _p, _sz, _p],
 }
 # size queries (return size_t)
 SIZE_FUNCS = {"tcrv_hip_gemm_tiles_bytes": [_sz, _sz],
               "tcrv_hip_q8_0_q8_0_gemm_workspace_bytes": [_sz, _sz, _sz],
+              "tcrv_hip_q4_0_q8_0_gemm_workspace_bytes": [_sz, _sz, _sz],
               "tcrv_hip_q8_0_q8_0_gemm_noalloc_max_bytes": []}
 STRING_FUNCS = {"tcrv_hip_status_string": [_int], "tcrv_hip_version": []}
 
@@ -331,6 +333,16 @@ def pack_q4_0_to_gemm_tiles(nrows: int, nb: int, src, bx: int, dst, stream=None)
 
 def q4_0_q8_0_gemm_tiles(n: int, s, tx, ty, nr: int, nc: int, bs: int, stream=None):
     return call("tcrv_hip_q4_0_q8_0_gemm_tiles", n, s, tx, ty, nr, nc, bs, _stream(stream))
+
+
+def q4_0_q8_0_gemm_workspace_bytes(n: int, nr: int, nc: int) -> int:
+    return load().tcrv_hip_q4_0_q8_0_gemm_workspace_bytes(n, nr, nc)
+
+
+def q4_0_q8_0_gemm_ws(n: int, s, vx, vy, by: int, nr: int, nc: int, bx: int, bs: int, ws,
+                      ws_bytes: int, stream=None):
+    return call("tcrv_hip_q4_0_q8_0_gemm_ws", n, s, vx, vy, by, nr, nc, bx, bs, ws, ws_bytes,
+                _stream(stream))
 
 
 def synchronize(stream=None):
