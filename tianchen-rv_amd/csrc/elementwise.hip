@@ -21,8 +21,8 @@ __device__ __forceinline__ void store_stream(float4 v, float4 *p) {
 // a1: out[i] = lhs[i] + rhs[i].  The reference emits a VL strip loop of
 // vle32/vfadd/vse32 (lib/Conversion/RVV/RVVToEmitC.cpp:605, :1873-1911); here
 // each thread moves kAddUnroll 128-bit vectors per operand, all loads issued
-// before the adds (2 measured fastest for n = 2^24: 28.1 us against 28.4, 28.8
-// and 29.3 us for 1, 4 and 8).  IEEE binary32 addition is correctly rounded,
+// before the adds (2 measured fastest for n = 2^24: 27.8 us against 28.0, 28.7
+// and 29.1 us for 1, 4 and 8).  IEEE binary32 addition is correctly rounded,
 // so the result is bit-identical to the scalar loop.
 // ---------------------------------------------------------------------------
 constexpr int kAddThreads = 256;
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(kDqThreads) void dequantize_q8_0(const uint8_t *vx,
 // and writes them with 128-bit stores.
 // ---------------------------------------------------------------------------
 constexpr int kQzThreads = 256;
-constexpr int kQzPer = 2;  // blocks per 8-lane group (1/2/4: 18.3/16.5/17.3 us at 4096^2)
+constexpr int kQzPer = 2;  // blocks per 8-lane group (1/2/4: 18.1/16.2/17.1 us at 4096^2)
 constexpr int kQzBlocks = kQzPer * kQzThreads / 8;
 
 __device__ __forceinline__ uint32_t quant_byte(float x, float id) {

@@ -206,13 +206,13 @@ const tcrv_hip_schedule kSchedules[] = {
     // kernel, 4 waves per work-group; the fold runs on 8 lanes per row for 4 or
     // 8 rows per wave, on 16 for 2
     {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_DECODE, "gemv_q4_0_q8_0_direct", "rows_per_wave", 2,
-     0, "tcrv_hip_gemv_q4_0_q8_0_shaped", 4.173,
+     0, "tcrv_hip_gemv_q4_0_q8_0_shaped", 3.836,
      "2048 waves: two per SIMD share the read; the per-row fold chain is 15 lane hops"},
     {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_DECODE, "gemv_q4_0_q8_0_direct", "rows_per_wave", 4,
-     1, "tcrv_hip_gemv_q4_0_q8_0_shaped", 3.911,
+     1, "tcrv_hip_gemv_q4_0_q8_0_shaped", 3.565,
      "measured fastest: one wave per SIMD, every lane busy in the decode and 32 fold lanes"},
     {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_DECODE, "gemv_q4_0_q8_0_direct", "rows_per_wave", 8,
-     0, "tcrv_hip_gemv_q4_0_q8_0_shaped", 5.070,
+     0, "tcrv_hip_gemv_q4_0_q8_0_shaped", 4.695,
      "512 waves leave half the SIMDs idle during the read"},
     // the tiled Q8_0 GEMM: blocks per K chunk (measured with two LDS stages for
     // 5-6 blocks, three for 3-4)
@@ -228,19 +228,19 @@ const tcrv_hip_schedule kSchedules[] = {
      "latency); 6 divides the 128 blocks of K = 4096 more evenly"},
     // quantize_row_q8_0: 32-float blocks per 8-lane group
     {"tcrv_rvv.quantize_row_q8_0", -1, "quantize_q8_0", "blocks_per_lane_group", 1, 0, nullptr,
-     18.3, "fewer loads in flight per thread"},
+     18.1, "fewer loads in flight per thread"},
     {"tcrv_rvv.quantize_row_q8_0", -1, "quantize_q8_0", "blocks_per_lane_group", 2, 1, nullptr,
-     16.5, "measured fastest"},
+     16.2, "measured fastest"},
     {"tcrv_rvv.quantize_row_q8_0", -1, "quantize_q8_0", "blocks_per_lane_group", 4, 0, nullptr,
-     17.3, "more registers, fewer waves"},
+     17.1, "more registers, fewer waves"},
     // tcrv_rvv.binary (add f32, n = 2^24): 16-byte vectors per operand and thread
-    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 1, 0, nullptr, 28.4,
+    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 1, 0, nullptr, 28.0,
      "loads of one vector in flight"},
-    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 2, 1, nullptr, 28.1,
+    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 2, 1, nullptr, 27.8,
      "measured fastest"},
-    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 4, 0, nullptr, 28.8,
+    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 4, 0, nullptr, 28.7,
      "fewer work-groups in flight"},
-    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 8, 0, nullptr, 29.3,
+    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 8, 0, nullptr, 29.1,
      "fewer work-groups in flight"},
 };
 constexpr size_t kNumSchedules = std::size(kSchedules);
