@@ -125,18 +125,15 @@ constexpr int kQzThreads = 256;
 constexpr int kQzPer = 2;  // blocks per 8-lane group (1/2/4: 18.1/16.2/17.1 us at 4096^2)
 constexpr int kQzBlocks = kQzPer * kQzThreads / 8;
 
+// Branch-free: the clamp to the i16 range (v_med3_f32) commutes with the
+// rounding, as both bounds are integers; NaN is selected afterwards, since the
+// clamp would map it to a bound.  (Written with branches the compiler gave
+// every element its own exec-mask block: 340 instructions against 271.)
 __device__ __forceinline__ uint32_t quant_byte(float x, float id) {
   const float v = x * id;
-  float r = __builtin_rintf(v);  // v_rndne_f32: nearest-even
-  int w;
-  if (v != v)
-    w = 32767;  // RVV float->int conversion of NaN gives the largest value
-  else if (r >= 32767.0f)
-    w = 32767;
-  else if (r <= -32768.0f)
-    w = -32768;
-  else
-    w = static_cast<int>(r);
+  const float r = fminf(fmaxf(__builtin_rintf(v), -32768.0f), 32767.0f);  // rint: nearest-even
+  // RVV float->int conversion of NaN gives the largest value
+  const int w = v != v ? 32767 : static_cast<int>(r);
   return static_cast<uint32_t>(w) & 0xffu;  // narrowing keeps the low byte
 }
 
