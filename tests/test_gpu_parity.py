@@ -870,6 +870,33 @@ def test_q8_0_gemm_tiles_and_ws(hip, oracle, dev, nr, nc, nb, xpad, ypad):
     assert_f32_parity(from_dev(s2).reshape(nr, bs)[:, :nc], want[:, :nc], what="gemm_ws")
 
 
+@pytest.mark.parametrize("nb", [12, 13, 5])
+def test_q8_0_gemm_tiles_more_tiles_than_cus(hip, oracle, dev, nb):
+    """17 x 17 = 289 work-group tiles of the tiled kernel, partial ones on both
+    edges: more tiles than the part has CUs, so a second round of work-groups
+    runs.  K with no partial chunk (12 blocks), with one (13) and with only one
+    (5).  The whole output equals the plain entry's bit for bit; sampled rows
+    match the oracle."""
+    nr, nc, n = 16 * 256 + 100, 16 * 128 + 70, nb * 32
+    w = synth.q8_0_matrix(nr, n, 1031, 0.02)
+    a = synth.q8_0_matrix(nc, n, 1032, 1.0)
+    dw, da = to_dev(w, dev), to_dev(a, dev)
+    bs = nc + 1
+    wsb = hip.q8_0_q8_0_gemm_workspace_bytes(n, nr, nc)
+    ws = empty_dev(wsb, torch.uint8, dev)
+    s = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+    hip.q8_0_q8_0_gemm_ws(n, s, dw, da, a.shape[1], nr, nc, w.shape[1], bs, ws, wsb)
+    ref = empty_dev(nr * bs, torch.float32, dev)
+    hip.q8_0_q8_0_gemm(n, ref, dw, da, a.shape[1], nr, nc, w.shape[1], bs)
+    got, want = from_dev(s).reshape(nr, bs), from_dev(ref).reshape(nr, bs)
+    assert np.array_equal(got[:, :nc].view(np.uint32), want[:, :nc].view(np.uint32))
+    assert np.all(got[:, nc:] == -7.0)
+    rng = np.random.default_rng(17)
+    for r in np.sort(rng.choice(nr, 16, replace=False)).tolist() + [nr - 1]:
+        row = oracle.gemm_q8_0(n, w[r].copy(), a, a.shape[1], 1, nc, w.shape[1], nc, 8)
+        assert_f32_parity(got[r, :nc], row, what=f"row {r}")
+
+
 def test_q8_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
     """Shapes the tiled kernel does not serve run the plain entry and leave the
     workspace alone; a workspace that is too small or misaligned is refused."""
