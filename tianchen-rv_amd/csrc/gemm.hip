@@ -191,10 +191,13 @@ __global__ __launch_bounds__(kGmThreads) void gemm_q8_0_q8_0_kernel(
 //                                   product of two fp16 values, exact in fp32
 //                                   -- no per-element VALU multiply
 //   VALU: acc = fma((float)sumi, dxy, acc)   -- the reference fold, in order.
-// On this part the matrix core and the VALU do not overlap (a microbenchmark
-// of this loop runs in the sum of the two alone), so the loop is built to
-// issue the fewest VALU instructions: 32 per tile and block, no selects or
-// address arithmetic.
+// The matrix core and the VALU overlap while the VALU issue port has room, but
+// at four waves per SIMD, the occupancy that issues this fold fastest, the
+// MFMAs' issue shares that port and the two add up (placement-controlled
+// microbenchmark: two MFMA-only and two VALU-only waves per SIMD take 0.307 ms
+// against 0.317 ms for the two alone), so the loop is built to issue the
+// fewest VALU instructions: 32 per tile and block, no selects or address
+// arithmetic.
 // ---------------------------------------------------------------------------
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
