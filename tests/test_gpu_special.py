@@ -149,6 +149,29 @@ def test_q4_0_gemm_tiles_nonfinite_dx_mid_k(hip, oracle, dev):
     assert np.isinf(g[70]).any() and np.isnan(g[400]).all()  # the planted cases took effect
 
 
+@pytest.mark.parametrize("nb", [40, 42])
+def test_q4_0_gemm_nonfinite_dx_mid_k(hip, oracle, dev, nb):
+    """The plain Q4_0 entry's 256 x 128 wide kernel with non-finite d_x planted
+    across K: +-Inf in the first chunk of one wave's rows, in the middle of K,
+    in the last block and (nb = 42) in the partial tail, NaN, and an infinite
+    d_x over a zero block sum (0 * Inf = NaN)."""
+    nr, nc = 512, 256
+    n = nb * 32
+    w = q4(nr, nb, 43)
+    a = q8(nc, nb, 44, 1.0, nonfinite_every=37)
+    for r, b, bits in ((70, 20, 0x7C00), (130, 0, 0xFC00), (200, 37, 0x7E00),
+                       (330, nb - 1, 0x7C00), (400, 10, 0xFC00), (450, 29, 0x7C00)):
+        _set_scale(w, r, b, 18, bits)
+    w[400, 10 * 18 + 2:10 * 18 + 18] = 0x88  # every quant q - 8 = 0: block sums 0
+    s = empty_dev(nr * nc, torch.float32, dev)
+    hip.q4_0_q8_0_gemm(n, s, to_dev(w, dev), to_dev(a, dev), a.shape[1], nr, nc, w.shape[1], nc)
+    want = oracle.gemm_q4_0(n, w, a, a.shape[1], nr, nc, w.shape[1], nc, 8)
+    got = from_dev(s)
+    assert_f32_parity_nan(got, want, what=f"q4 gemm, non-finite d_x, nb {nb}")
+    g = got.reshape(nr, nc)
+    assert np.isinf(g[70]).any() and np.isnan(g[400]).all()  # the planted cases took effect
+
+
 def _x16_source(w, nb, k):
     nc = w.shape[0]
     return np.ascontiguousarray(np.concatenate(
