@@ -293,6 +293,32 @@ def test_q4_0_gemm_multi_column(hip, oracle, dev, nr, nc, nb):
     assert_f32_parity(got[:, :nc], want.reshape(nr, bs)[:, :nc], what="q4 gemm")
 
 
+@pytest.mark.parametrize("nr,nc,nb,ypad", [
+    (4096, 2, 128, 0),   # one chunk, two columns
+    (4096, 3, 128, 0),   # a four-column group with three present
+    (100, 7, 130, 16),   # partial work-group, two chunks (the second of 2 blocks), 4 + 3
+    (300, 6, 258, 4),    # three chunks, 4 + 2 columns
+    (64, 9, 64, 0),      # nb < 128, 4 + 4 + 1 (the last column through the GEMV)
+    (48, 64, 8, 0),      # the largest token count of the multi-column path
+    (40, 5, 7, 0),       # odd nb: the MFMA GEMM instead
+])
+def test_q4_0_gemm_few_tokens(hip, oracle, dev, nr, nc, nb, ypad):
+    """The a7 GEMM with a few tokens (batched decode) runs as GEMVs over groups
+    of up to four activation columns, the weights read once per group: every
+    output equals the oracle's, and the output row padding stays untouched."""
+    n = nb * 32
+    w = synth.q4_0_matrix(nr, n, 1017, 0.02)
+    a = np.pad(synth.q8_0_matrix(nc, n, 1016, 1.0), ((0, 0), (0, ypad)))
+    a[0, 2:34] = 0x80
+    bs = nc + 5
+    s = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+    hip.q4_0_q8_0_gemm(n, s, to_dev(w, dev), to_dev(a, dev), a.shape[1], nr, nc, w.shape[1], bs)
+    want = oracle.gemm_q4_0(n, w, a, a.shape[1], nr, nc, w.shape[1], bs, 8).reshape(nr, bs)
+    got = from_dev(s).reshape(nr, bs)
+    assert_f32_parity(got[:, :nc], want[:, :nc], what=f"q4 gemm {nr}x{nc}x{n}")
+    assert np.all(got[:, nc:] == -7.0)
+
+
 # ------------------------------------------------------------------ a9 GEMM ---
 
 @pytest.mark.parametrize("nr,nc,nb,xpad,ypad", [

@@ -89,7 +89,8 @@ def test_q8_0_gemm_ws_special_scales(hip, oracle, dev):
     assert_f32_parity_nan(from_dev(s), want, what="q8 gemm_ws")
 
 
-@pytest.mark.parametrize("nr,nc,nb", [(300, 130, 9), (100, 70, 9), (64, 1, 8), (1, 40, 8)])
+@pytest.mark.parametrize("nr,nc,nb", [(300, 130, 9), (100, 70, 9), (64, 1, 8), (1, 40, 8),
+                                      (200, 4, 8), (64, 3, 10)])  # the last two: multi-column GEMVs
 def test_q4_0_gemm_special_scales(hip, oracle, dev, nr, nc, nb):
     n = nb * 32
     w = q4(nr, nb, 13, nonfinite_every=16)

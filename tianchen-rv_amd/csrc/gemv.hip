@@ -311,6 +311,105 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
     s[(row0 + fr) * os] = sumf;
 }
 
+// Multi-column form of the register-direct GEMV, for the a7 GEMM with a few
+// tokens (batched decode, nc = 2..kGemvColsMax): each wave loads its 4 weight
+// rows' block pairs once and dots them with kCols activation columns (ncols of
+// them present; absent ones re-read the last and are not stored).  Per (row,
+// column) the terms fl((float)sumi * d_x) and the column's d_y go through the
+// wave's LDS and fold on 64 / (4 kCols) lanes -- one chain per row and column,
+// 128 fmas in ascending block order, as the GEMV's.
+template <int kCols, bool kOneChunk>
+__global__ __launch_bounds__(256) void gemv_q4_0_q8_0_cols(size_t nb_arg, float *s, size_t bs,
+                                                           const uint8_t *vx, size_t bx,
+                                                           const uint8_t *vy, size_t by,
+                                                           size_t nr, int ncols) {
+  constexpr int kWaves = 4, kR = 4;
+  constexpr int kChains = kR * kCols;
+  constexpr int kLanes = 64 / kChains;       // 8 lanes for 2 columns, 4 for 4, 2 for 8
+  constexpr int kTerms = kGvChunk / kLanes;  // blocks per fold lane
+  static_assert(kLanes == 8 || kLanes == 4 || kLanes == 2, "fold groups inside one DPP row");
+  const size_t nb = kOneChunk ? static_cast<size_t>(kGvChunk) : nb_arg;
+  __shared__ __align__(16) float tl[kWaves][kChains][kGvChunk + 4];
+  __shared__ __align__(16) float dyl[kWaves][kCols][kGvChunk];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+  const int l = tid & 63;
+  const size_t row0 = (static_cast<size_t>(blockIdx.x) * kWaves + w) * kR;
+  const int ch = l / kLanes;                  // chain: row ch / kCols, column ch % kCols
+  const int fr = ch / kCols, fc = ch % kCols;
+  const int fp = l & (kLanes - 1);            // position of this lane in its chain
+  float sumf = 0.0f;
+
+  for (size_t c0 = 0; c0 < nb; c0 += kGvChunk) {
+    const int nbc = static_cast<int>(min(static_cast<size_t>(kGvChunk), nb - c0));
+    const int b0 = 2 * l;
+    if (kOneChunk || b0 < nbc) {  // nbc is even: the pair is whole or absent
+      uint32_t wr[kR][9];
+#pragma unroll
+      for (int r = 0; r < kR; ++r)
+        load36(vx + min(row0 + r, nr - 1) * bx + (c0 + b0) * kQ4Bytes, wr[r]);
+      ActPair ap[kCols];
+#pragma unroll
+      for (int c = 0; c < kCols; ++c) {
+        load_act_pair(vy + static_cast<size_t>(min(c, ncols - 1)) * by + (c0 + b0) * kQ8Bytes,
+                      ap[c]);
+        dyl[w][c][b0] = ap[c].d0;
+        dyl[w][c][b0 + 1] = ap[c].d1;
+      }
+#pragma unroll
+      for (int r = 0; r < kR; ++r) {
+        // block 2l: d = bytes 0-1, quants bytes 2..17; block 2l+1: d = bytes
+        // 18-19, quants bytes 20..35 (dwords 5..8)
+        uint32_t qa[4], qb[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          qa[k] = funnel16(wr[r][k], wr[r][k + 1]);
+          qb[k] = wr[r][k + 5];
+        }
+        const float dx0 = fp16_bits_to_f32(wr[r][0] & 0xffffu);
+        const float dx1 = fp16_bits_to_f32(wr[r][4] >> 16);
+#pragma unroll
+        for (int c = 0; c < kCols; ++c) {
+          float2 t;
+          t.x = static_cast<float>(nibble_dot(qa, ap[c].q0, ap[c].c0)) * dx0;
+          t.y = static_cast<float>(nibble_dot(qb, ap[c].q1, ap[c].c1)) * dx1;
+          *reinterpret_cast<float2 *>(&tl[w][r * kCols + c][b0]) = t;
+        }
+      }
+    } else {
+      // blocks past the chunk: t = dy = 0, and fma(0, 0, sumf) == sumf (sumf is never -0)
+#pragma unroll
+      for (int c = 0; c < kCols; ++c) {
+        dyl[w][c][b0] = 0.0f;
+        dyl[w][c][b0 + 1] = 0.0f;
+      }
+#pragma unroll
+      for (int q = 0; q < kChains; ++q)
+        *reinterpret_cast<float2 *>(&tl[w][q][b0]) = make_float2(0.0f, 0.0f);
+    }
+    wave_lds_sync();  // the LDS rows are this wave's own
+    float t[kTerms], dy[kTerms];
+#pragma unroll
+    for (int k = 0; k < kTerms; k += 4) {
+      const float4 tv = *reinterpret_cast<const float4 *>(&tl[w][ch][fp * kTerms + k]);
+      const float4 dv = *reinterpret_cast<const float4 *>(&dyl[w][fc][fp * kTerms + k]);
+      t[k] = tv.x; t[k + 1] = tv.y; t[k + 2] = tv.z; t[k + 3] = tv.w;
+      dy[k] = dv.x; dy[k + 1] = dv.y; dy[k + 2] = dv.z; dy[k + 3] = dv.w;
+    }
+    if constexpr (kOneChunk) {
+      sumf = fold_chain<kLanes, kTerms>(t, dy, 0.0f);
+    } else {
+      // the previous chunk's sum sits in the last lane of the chain: seed lane 0
+      const float carry = __shfl(sumf, (l & ~(kLanes - 1)) + kLanes - 1);
+      sumf = fold_chain<kLanes, kTerms>(t, dy, fp == 0 ? carry : 0.0f);
+      wave_lds_sync();  // the LDS rows are this wave's own
+    }
+  }
+  if (fp == kLanes - 1 && row0 + fr < nr && fc < ncols)
+    s[(row0 + fr) * bs + fc] = sumf;
+}
+
 }  // namespace tcrv
 
 namespace tcrv_host {
@@ -321,6 +420,8 @@ constexpr int kGemvRows = 2;
 // (4096^2, us: 1x4 4.16, 2x4 4.46, 4x4 4.00, 8x2 4.13, 8x4 5.06, 2x8 4.80, 4x2 4.28).
 constexpr int kDirectWaves = 4;
 constexpr int kDirectRows = 4;
+// Token counts up to which the a7 GEMM runs as multi-column GEMVs.
+constexpr size_t kGemvColsMax = 64;
 
 // The register-direct GEMV with kR rows per wave (kDirectWaves waves per
 // work-group); every shape computes the same per-row fold, bit for bit.
@@ -370,6 +471,51 @@ int gemv_q4_0_q8_0(size_t n, float *s, size_t os, const uint8_t *vx, size_t bx,
       <<<dim3(static_cast<unsigned>(grid)), dim3(tcrv::kGvWaves * 64), 0, st>>>(
           nb, s, os, vx, bx, vy, nr);
   return launch_status();
+}
+
+template <int kCols>
+int launch_cols(size_t nb, float *s, size_t bs, const uint8_t *vx, size_t bx, const uint8_t *vy,
+                size_t by, size_t nr, int ncols, hipStream_t st) {
+  const size_t grid = (nr + 15) / 16;  // 4 waves x 4 rows
+  if (grid > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  if (nb == static_cast<size_t>(tcrv::kGvChunk))
+    tcrv::gemv_q4_0_q8_0_cols<kCols, true><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(
+        nb, s, bs, vx, bx, vy, by, nr, ncols);
+  else
+    tcrv::gemv_q4_0_q8_0_cols<kCols, false>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(nb, s, bs, vx, bx, vy, by, nr,
+                                                                  ncols);
+  return launch_status();
+}
+
+int gemv_cols_q4_0_q8_0(size_t nb, float *s, size_t bs, const uint8_t *vx, size_t bx,
+                        const uint8_t *vy, size_t by, size_t nr, size_t nc, void *stream) {
+  if (nb % 2 != 0 || !aligned4(vx) || !aligned4(vy) || (nr > 1 && bx % 4 != 0) || by % 4 != 0)
+    return TCRV_HIP_ERR_UNSUPPORTED;
+  hipStream_t st = as_stream(stream);
+  for (size_t c0 = 0; c0 < nc;) {
+    const size_t rem = nc - c0;
+    float *sc = s + c0;
+    const uint8_t *yc = vy + c0 * by;
+    int rc;
+    if (rem >= 5) {  // eight columns (five to seven present when fewer are left)
+      rc = launch_cols<8>(nb, sc, bs, vx, bx, yc, by, nr, static_cast<int>(rem < 8 ? rem : 8), st);
+      c0 += rem < 8 ? rem : 8;
+    } else if (rem >= 3) {  // four columns (three present when three are left)
+      rc = launch_cols<4>(nb, sc, bs, vx, bx, yc, by, nr, static_cast<int>(rem), st);
+      c0 += rem;
+    } else if (rem == 2) {
+      rc = launch_cols<2>(nb, sc, bs, vx, bx, yc, by, nr, 2, st);
+      c0 += 2;
+    } else {
+      rc = launch_direct<kDirectRows>(nb, sc, bs, vx, bx, yc, nr, st);
+      c0 += 1;
+    }
+    if (rc != TCRV_HIP_OK)
+      return rc;
+  }
+  return TCRV_HIP_OK;
 }
 
 int gemv_q4_0_soa_q8_0(size_t nb, float *s, const uint8_t *vx, const uint8_t *vy, size_t nr,
@@ -489,6 +635,12 @@ int tcrv_hip_q4_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t
     return TCRV_HIP_ERR_BAD_SIZE;
   if (nr == 1) {  // one weight row against nc columns: bandwidth-bound block dots
     const int st = tcrv_host::q4_0_rows_direct(nb, s, 1, vx, 0, vy, by, nc, stream);
+    if (st != TCRV_HIP_ERR_UNSUPPORTED)
+      return st;
+  } else if (nc <= tcrv_host::kGemvColsMax) {
+    // a few tokens: the weights are read once per group of up to four columns
+    // (the MFMA GEMM would run only nr / 256 work-groups)
+    const int st = tcrv_host::gemv_cols_q4_0_q8_0(nb, s, bs, vx, bx, vy, by, nr, nc, stream);
     if (st != TCRV_HIP_ERR_UNSUPPORTED)
       return st;
   }
