@@ -321,6 +321,33 @@ def test_q4_0_gemm_few_tokens(hip, oracle, dev, nr, nc, nb, ypad):
 
 # ------------------------------------------------------------------ a9 GEMM ---
 
+@pytest.mark.parametrize("nr,nc,nb,ypad", [
+    (4096, 2, 128, 0),   # one chunk, two columns
+    (4096, 5, 128, 0),   # an eight-column group with five present
+    (100, 7, 130, 16),   # partial work-group, two chunks, seven columns
+    (300, 11, 258, 4),   # three chunks, 8 + 3 columns
+    (64, 13, 64, 0),     # nb < 128, 8 + 4 + 1 (the last column through the block dots)
+    (48, 64, 8, 0),      # the largest token count of the multi-column path
+    (40, 3, 7, 0),       # odd nb: the MFMA GEMM instead
+])
+def test_q8_0_gemm_few_tokens(hip, oracle, dev, nr, nc, nb, ypad):
+    """The a9 GEMM with a few tokens runs as GEMVs over groups of up to eight
+    activation columns: every output equals the oracle's (the a5 fold with the
+    exact d_x*d_y), and the output row padding stays untouched."""
+    n = nb * 32
+    w = synth.q8_0_matrix(nr, n, 1015, 0.02)
+    a = np.pad(synth.q8_0_matrix(nc, n, 1014, 1.0), ((0, 0), (0, ypad)))
+    w[0, 2:34] = 0x80
+    a[0, 2:34] = 0x80  # -128 x -128 block sums
+    bs = nc + 5
+    s = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+    hip.q8_0_q8_0_gemm(n, s, to_dev(w, dev), to_dev(a, dev), a.shape[1], nr, nc, w.shape[1], bs)
+    want = oracle.gemm_q8_0(n, w, a, a.shape[1], nr, nc, w.shape[1], bs, 8).reshape(nr, bs)
+    got = from_dev(s).reshape(nr, bs)
+    assert_f32_parity(got[:, :nc], want[:, :nc], what=f"q8 gemm {nr}x{nc}x{n}")
+    assert np.all(got[:, nc:] == -7.0)
+
+
 @pytest.mark.parametrize("nr,nc,nb,xpad,ypad", [
     (128, 128, 8, 0, 0),      # one tile, one K chunk
     (256, 128, 128, 0, 0),    # full K, two tiles

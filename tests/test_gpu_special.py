@@ -63,6 +63,8 @@ def q4(rows, nb, seed, nonfinite_every=0):
     (33, 20, 5, 2),      # rows 2-byte aligned only: the raw-block kernel
     (64, 1, 8, 0),       # decode shape: register-direct block dots
     (1, 40, 8, 0),       # one weight row
+    (200, 6, 8, 0),      # a few tokens: the multi-column GEMV (8 columns, six present)
+    (64, 3, 10, 0),      # a few tokens: 4 columns, three present
 ])
 def test_q8_0_gemm_special_scales(hip, oracle, dev, nr, nc, nb, pad):
     n = nb * 32

@@ -410,6 +410,111 @@ __global__ __launch_bounds__(256) void gemv_q4_0_q8_0_cols(size_t nb_arg, float 
     s[(row0 + fr) * bs + fc] = sumf;
 }
 
+// Q8_0 block pair 2l, 2l+1 (68 bytes, dword aligned) -> quants of each block as
+// 8 aligned dwords and the fp32 scales.
+struct Q8Pair {
+  uint32_t q0[8], q1[8];
+  float d0, d1;
+};
+
+__device__ __forceinline__ void load_q8_pair(const uint8_t *p, Q8Pair &a) {
+  const uint32_t *q = reinterpret_cast<const uint32_t *>(p);
+  uint32_t r[17];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(q + 4 * k);
+    r[4 * k + 0] = v.x; r[4 * k + 1] = v.y; r[4 * k + 2] = v.z; r[4 * k + 3] = v.w;
+  }
+  r[16] = q[16];
+  a.d0 = fp16_bits_to_f32(r[0] & 0xffffu);
+  a.d1 = fp16_bits_to_f32(r[8] >> 16);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    a.q0[k] = funnel16(r[k], r[k + 1]);
+    a.q1[k] = r[k + 9];
+  }
+}
+
+// The a9 (Q8_0 x Q8_0) GEMM with a few tokens, as gemv_q4_0_q8_0_cols: each
+// wave loads its 4 weight rows' block pairs once and dots them with kCols
+// activation columns; the a5 fold of each (row, column) is fma((float)sumi,
+// d_x * d_y, acc) with the scale product exact in fp32, so (float)sumi and
+// d_x * d_y go through the wave's LDS and fold on 64 / (4 kCols) lanes in
+// ascending block order.
+template <int kCols, bool kOneChunk>
+__global__ __launch_bounds__(256) void gemv_q8_0_q8_0_cols(size_t nb_arg, float *s, size_t bs,
+                                                           const uint8_t *vx, size_t bx,
+                                                           const uint8_t *vy, size_t by,
+                                                           size_t nr, int ncols) {
+  constexpr int kWaves = 4, kR = 4;
+  constexpr int kChains = kR * kCols;
+  constexpr int kLanes = 64 / kChains;       // 8 lanes for 2 columns, 4 for 4, 2 for 8
+  constexpr int kTerms = kGvChunk / kLanes;  // blocks per fold lane
+  static_assert(kLanes == 8 || kLanes == 4 || kLanes == 2, "fold groups inside one DPP row");
+  const size_t nb = kOneChunk ? static_cast<size_t>(kGvChunk) : nb_arg;
+  __shared__ __align__(16) float2 tl[kWaves][kChains][kGvChunk + 2];  // ((float)sumi, d_x*d_y)
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+  const int l = tid & 63;
+  const size_t row0 = (static_cast<size_t>(blockIdx.x) * kWaves + w) * kR;
+  const int ch = l / kLanes;                  // chain: row ch / kCols, column ch % kCols
+  const int fr = ch / kCols, fc = ch % kCols;
+  const int fp = l & (kLanes - 1);            // position of this lane in its chain
+  float sumf = 0.0f;
+
+  for (size_t c0 = 0; c0 < nb; c0 += kGvChunk) {
+    const int nbc = static_cast<int>(min(static_cast<size_t>(kGvChunk), nb - c0));
+    const int b0 = 2 * l;
+    if (kOneChunk || b0 < nbc) {  // nbc is even: the pair is whole or absent
+      Q8Pair wp[kR], ap[kCols];
+#pragma unroll
+      for (int r = 0; r < kR; ++r)
+        load_q8_pair(vx + min(row0 + r, nr - 1) * bx + (c0 + b0) * kQ8Bytes, wp[r]);
+#pragma unroll
+      for (int c = 0; c < kCols; ++c)
+        load_q8_pair(vy + static_cast<size_t>(min(c, ncols - 1)) * by + (c0 + b0) * kQ8Bytes,
+                     ap[c]);
+#pragma unroll
+      for (int r = 0; r < kR; ++r)
+#pragma unroll
+        for (int c = 0; c < kCols; ++c) {
+          int s0 = 0, s1 = 0;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            s0 = sdot4(wp[r].q0[k], ap[c].q0[k], s0);
+            s1 = sdot4(wp[r].q1[k], ap[c].q1[k], s1);
+          }
+          *reinterpret_cast<float4 *>(&tl[w][r * kCols + c][b0]) =
+              make_float4(static_cast<float>(s0), wp[r].d0 * ap[c].d0, static_cast<float>(s1),
+                          wp[r].d1 * ap[c].d1);
+        }
+    } else {
+      // blocks past the chunk: fma(0, 0, sumf) == sumf (sumf is never -0)
+#pragma unroll
+      for (int q = 0; q < kChains; ++q)
+        *reinterpret_cast<float4 *>(&tl[w][q][b0]) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    wave_lds_sync();  // the LDS rows are this wave's own
+    float t[kTerms], dxy[kTerms];
+#pragma unroll
+    for (int k = 0; k < kTerms; k += 2) {
+      const float4 v = *reinterpret_cast<const float4 *>(&tl[w][ch][fp * kTerms + k]);
+      t[k] = v.x; dxy[k] = v.y; t[k + 1] = v.z; dxy[k + 1] = v.w;
+    }
+    if constexpr (kOneChunk) {
+      sumf = fold_chain<kLanes, kTerms>(t, dxy, 0.0f);
+    } else {
+      // the previous chunk's sum sits in the last lane of the chain: seed lane 0
+      const float carry = __shfl(sumf, (l & ~(kLanes - 1)) + kLanes - 1);
+      sumf = fold_chain<kLanes, kTerms>(t, dxy, fp == 0 ? carry : 0.0f);
+      wave_lds_sync();  // the LDS rows are this wave's own
+    }
+  }
+  if (fp == kLanes - 1 && row0 + fr < nr && fc < ncols)
+    s[(row0 + fr) * bs + fc] = sumf;
+}
+
 }  // namespace tcrv
 
 namespace tcrv_host {
@@ -420,8 +525,6 @@ constexpr int kGemvRows = 2;
 // (4096^2, us: 1x4 4.16, 2x4 4.46, 4x4 4.00, 8x2 4.13, 8x4 5.06, 2x8 4.80, 4x2 4.28).
 constexpr int kDirectWaves = 4;
 constexpr int kDirectRows = 4;
-// Token counts up to which the a7 GEMM runs as multi-column GEMVs.
-constexpr size_t kGemvColsMax = 64;
 
 // The register-direct GEMV with kR rows per wave (kDirectWaves waves per
 // work-group); every shape computes the same per-row fold, bit for bit.
@@ -473,24 +576,34 @@ int gemv_q4_0_q8_0(size_t n, float *s, size_t os, const uint8_t *vx, size_t bx,
   return launch_status();
 }
 
-template <int kCols>
+template <bool kQ4, int kCols>
 int launch_cols(size_t nb, float *s, size_t bs, const uint8_t *vx, size_t bx, const uint8_t *vy,
                 size_t by, size_t nr, int ncols, hipStream_t st) {
   const size_t grid = (nr + 15) / 16;  // 4 waves x 4 rows
   if (grid > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
-  if (nb == static_cast<size_t>(tcrv::kGvChunk))
-    tcrv::gemv_q4_0_q8_0_cols<kCols, true><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(
-        nb, s, bs, vx, bx, vy, by, nr, ncols);
-  else
-    tcrv::gemv_q4_0_q8_0_cols<kCols, false>
-        <<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(nb, s, bs, vx, bx, vy, by, nr,
-                                                                  ncols);
+  const dim3 g(static_cast<unsigned>(grid)), b(256);
+  const bool one = nb == static_cast<size_t>(tcrv::kGvChunk);
+  if constexpr (kQ4) {
+    if (one)
+      tcrv::gemv_q4_0_q8_0_cols<kCols, true><<<g, b, 0, st>>>(nb, s, bs, vx, bx, vy, by, nr, ncols);
+    else
+      tcrv::gemv_q4_0_q8_0_cols<kCols, false><<<g, b, 0, st>>>(nb, s, bs, vx, bx, vy, by, nr, ncols);
+  } else {
+    if (one)
+      tcrv::gemv_q8_0_q8_0_cols<kCols, true><<<g, b, 0, st>>>(nb, s, bs, vx, bx, vy, by, nr, ncols);
+    else
+      tcrv::gemv_q8_0_q8_0_cols<kCols, false><<<g, b, 0, st>>>(nb, s, bs, vx, bx, vy, by, nr, ncols);
+  }
   return launch_status();
 }
 
-int gemv_cols_q4_0_q8_0(size_t nb, float *s, size_t bs, const uint8_t *vx, size_t bx,
-                        const uint8_t *vy, size_t by, size_t nr, size_t nc, void *stream) {
+// Columns in groups: eight while five or more are left (five to seven present
+// in the last), then four (three or four present), two, and a single column
+// through the decode GEMV (Q4_0) or the block dots (Q8_0).
+template <bool kQ4>
+int gemv_cols(size_t nb, float *s, size_t bs, const uint8_t *vx, size_t bx, const uint8_t *vy,
+              size_t by, size_t nr, size_t nc, void *stream) {
   if (nb % 2 != 0 || !aligned4(vx) || !aligned4(vy) || (nr > 1 && bx % 4 != 0) || by % 4 != 0)
     return TCRV_HIP_ERR_UNSUPPORTED;
   hipStream_t st = as_stream(stream);
@@ -498,24 +611,33 @@ int gemv_cols_q4_0_q8_0(size_t nb, float *s, size_t bs, const uint8_t *vx, size_
     const size_t rem = nc - c0;
     float *sc = s + c0;
     const uint8_t *yc = vy + c0 * by;
+    const size_t take = rem >= 5 ? (rem < 8 ? rem : 8) : rem;  // rem <= 4: one last group
     int rc;
-    if (rem >= 5) {  // eight columns (five to seven present when fewer are left)
-      rc = launch_cols<8>(nb, sc, bs, vx, bx, yc, by, nr, static_cast<int>(rem < 8 ? rem : 8), st);
-      c0 += rem < 8 ? rem : 8;
-    } else if (rem >= 3) {  // four columns (three present when three are left)
-      rc = launch_cols<4>(nb, sc, bs, vx, bx, yc, by, nr, static_cast<int>(rem), st);
-      c0 += rem;
-    } else if (rem == 2) {
-      rc = launch_cols<2>(nb, sc, bs, vx, bx, yc, by, nr, 2, st);
-      c0 += 2;
-    } else {
+    if (rem >= 5)
+      rc = launch_cols<kQ4, 8>(nb, sc, bs, vx, bx, yc, by, nr, static_cast<int>(take), st);
+    else if (rem >= 3)
+      rc = launch_cols<kQ4, 4>(nb, sc, bs, vx, bx, yc, by, nr, static_cast<int>(take), st);
+    else if (rem == 2)
+      rc = launch_cols<kQ4, 2>(nb, sc, bs, vx, bx, yc, by, nr, 2, st);
+    else if constexpr (kQ4)
       rc = launch_direct<kDirectRows>(nb, sc, bs, vx, bx, yc, nr, st);
-      c0 += 1;
-    }
+    else
+      rc = q8_0_rows_direct(nb, sc, bs, vx, bx, yc, 0, nr, stream);
     if (rc != TCRV_HIP_OK)
       return rc;
+    c0 += take;
   }
   return TCRV_HIP_OK;
+}
+
+int gemv_cols_q4_0_q8_0(size_t nb, float *s, size_t bs, const uint8_t *vx, size_t bx,
+                        const uint8_t *vy, size_t by, size_t nr, size_t nc, void *stream) {
+  return gemv_cols<true>(nb, s, bs, vx, bx, vy, by, nr, nc, stream);
+}
+
+int gemv_cols_q8_0_q8_0(size_t nb, float *s, size_t bs, const uint8_t *vx, size_t bx,
+                        const uint8_t *vy, size_t by, size_t nr, size_t nc, void *stream) {
+  return gemv_cols<false>(nb, s, bs, vx, bx, vy, by, nr, nc, stream);
 }
 
 int gemv_q4_0_soa_q8_0(size_t nb, float *s, const uint8_t *vx, const uint8_t *vy, size_t nr,

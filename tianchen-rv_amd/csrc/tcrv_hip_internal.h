@@ -190,6 +190,17 @@ int q4_0_rows_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t b
 int q4_0_grid(size_t n, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by,
               size_t nr, size_t nc, size_t bs, void *stream);
 
+// The GEMMs with 2..kGemvColsMax tokens (batched decode) run as multi-column
+// GEMVs over groups of up to eight activation columns, the weights read once
+// per group (gemv.hip); an MFMA GEMM would run only nr / 256 work-groups.
+// TCRV_HIP_ERR_UNSUPPORTED for an odd block count or operands/strides that are
+// not 4-byte aligned.
+constexpr size_t kGemvColsMax = 64;
+int gemv_cols_q4_0_q8_0(size_t nb, float *s, size_t bs, const uint8_t *vx, size_t bx,
+                        const uint8_t *vy, size_t by, size_t nr, size_t nc, void *stream);
+int gemv_cols_q8_0_q8_0(size_t nb, float *s, size_t bs, const uint8_t *vx, size_t bx,
+                        const uint8_t *vy, size_t by, size_t nr, size_t nc, void *stream);
+
 // tcrv_hip_q8_0_q8_0_gemm_ws packs into its workspace and runs the tiled
 // kernel for this shape (otherwise it runs the plain GEMM and reads no
 // workspace); gemm_tiled.hip.
