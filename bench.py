@@ -58,6 +58,7 @@ DOT_BYTES = DOT_ROWS * (2 * (N // 32) * 34 + 4)                 # 142 671 872
 GEMM_OPS = 2.0 * N * N * N                                      # 137 438 953 472
 PACK_BYTES = 2 * N * (N // 32) * 18                             # 18 874 368
 REPACK8_BYTES = N * (N // 32) * 34 + (N // 32) * 34 + N * 4     # 17 846 528
+BATCH_TOKENS = 4  # the batched-decode GEMM entries of `configs`
 QUANT_BYTES = N * N * 4 + (N * N // 32) * 34                    # 84 934 656
 
 
@@ -488,6 +489,38 @@ def bench_configs(torch, lib, stream, args):
                                  "sets": sets}
     del S, Yv, soa, wd, reg
 
+    # batched decode: the a7 and a9 GEMMs with BATCH_TOKENS tokens (the
+    # multi-column GEMVs), every launch over its own copy of the weights; bytes
+    # are the weights, the tokens' rows and the outputs
+    act = inputs("gemm_a")[:BATCH_TOKENS].copy()
+    actd = torch.from_numpy(act).to(dev)
+    for name, wsrc, entry_fn, what in (
+            ("q4_0_q8_0_gemm_4_tokens", inputs("gemv_w"), lib.tcrv_hip_q4_0_q8_0_gemm,
+             "a7 Q4_0 x Q8_0 GEMM 4096 weight rows x 4 tokens x 4096 (batched decode)"),
+            ("q8_0_q8_0_gemm_4_tokens", inputs("gemm_b"), lib.tcrv_hip_q8_0_q8_0_gemm,
+             "a9 Q8_0 x Q8_0 GEMM 4096 weight rows x 4 tokens x 4096 (batched decode)")):
+        sets = copies_for(wsrc.size, 2)
+        Wc = torch.empty((sets, wsrc.size), dtype=torch.uint8, device=dev)
+        Wc[:] = torch.from_numpy(wsrc.reshape(-1)).to(dev)
+        Cb = torch.empty((sets, N * BATCH_TOKENS), device=dev)
+        fn = checked(entry_fn, name)
+        bx = wsrc.shape[1]
+        ptrs = [(Cb[i].data_ptr(), Wc[i].data_ptr()) for i in range(sets)]
+        reg = Region(torch, stream,
+                     lambda i, fn=fn, ptrs=ptrs, sets=sets, bx=bx: fn(
+                         N, ptrs[i % sets][0], ptrs[i % sets][1], actd.data_ptr(), act.shape[1],
+                         N, BATCH_TOKENS, bx, BATCH_TOKENS, sp), 400)
+        reg.run()
+        us = reg.run() * 1e3 / 400
+        same_as_eager(torch, stream, Cb[399 % sets],
+                      lambda o, fn=fn, bx=bx, k=399 % sets: fn(
+                          N, o, Wc[k].data_ptr(), actd.data_ptr(), act.shape[1], N,
+                          BATCH_TOKENS, bx, BATCH_TOKENS, sp), name)
+        nbytes = wsrc.size + act.size + N * BATCH_TOKENS * 4
+        out[name] = {"workload": what, "us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                     "sets": sets}
+        del Wc, Cb, reg
+
     # a10 quantize_row_q8_0: 4096 activation rows x 4096 f32 -> Q8_0 (the prefill
     # GEMM's activation operand; read 64 MiB, write 17.8 MB)
     xf = torch.from_numpy(inputs("gemm_a_f32")).to(dev)
@@ -831,6 +864,19 @@ def cpu_baseline_configs(seconds: float):
         "GEMM each), OpenMP over the 16 weight rows",
         lambda: ora.gemm_q4_0(N, w16, a8, a8.shape[1], 16, N, w16.shape[1], N, 1),
         lambda: ora.gemm_q4_0(N, w16, a8, a8.shape[1], 16, N, w16.shape[1], N, threads))
+    # batched decode: the whole 4096-row GEMMs with BATCH_TOKENS tokens, OpenMP
+    # over the weight rows (each output's fold serial)
+    act = a8[:BATCH_TOKENS].copy()
+    w8 = inputs("gemm_b")
+    for name, wsrc, gemm in (("q4_0_q8_0_gemm_4_tokens", w, ora.gemm_q4_0),
+                             ("q8_0_q8_0_gemm_4_tokens", w8, ora.gemm_q8_0)):
+        nbytes = wsrc.size + act.size + N * BATCH_TOKENS * 4
+        out[name] = entry(
+            nbytes, "GB/s", f"whole 4096 x {BATCH_TOKENS} x 4096 GEMMs, OpenMP over weight rows",
+            lambda wsrc=wsrc, gemm=gemm: gemm(N, wsrc, act, act.shape[1], N, BATCH_TOKENS,
+                                              wsrc.shape[1], BATCH_TOKENS, 1),
+            lambda wsrc=wsrc, gemm=gemm: gemm(N, wsrc, act, act.shape[1], N, BATCH_TOKENS,
+                                              wsrc.shape[1], BATCH_TOKENS, threads))
     wx16 = ora.pack_q4_0x16(src, nx16)
     ax4s = [ora.pack_q8_0x4(a8[16 * t:16 * t + 16].copy(), 16, nb, a8.shape[1])
             for t in range(threads)]
