@@ -202,7 +202,8 @@ TCRV_HIP_API int tcrv_hip_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx, 
  * block-dot ops carry bounded schedule attributes (integer_core_lmul,
  * multi_block_factor, strip_elision: RVVOps.td:3912-3972) that change how the
  * kernel runs and never what it computes.  rows_per_wave (2, 4 or 8; the plain
- * entry uses 4, tcrv_hip_route_schedule lists the candidates) sets how many
+ * entry uses 2 for nr <= 2048 and 4 above, tcrv_hip_route_schedule lists the
+ * candidates) sets how many
  * weight rows one wave of the register-direct kernel owns; the results are
  * bit-identical for every value.  Shapes served by the LDS-staged kernel (odd
  * n/32, rows not 4-byte aligned) ignore it.  Any other value returns

@@ -230,10 +230,13 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
   const int fp = l & (kLanes - 1);    // position of this lane in its row's chain
   float sumf = 0.0f;
 
-  for (size_t c0 = 0; c0 < nb; c0 += kGvChunk) {
-    const int nbc = static_cast<int>(min(static_cast<size_t>(kGvChunk), nb - c0));
-    const int b0 = 2 * l;
-    if (kOneChunk || b0 < nbc) {  // nbc is even: the pair is whole or absent
+  if constexpr (kOneChunk) {
+    // one chunk, and every lane owns a whole block pair.  Kept in the form of
+    // a loop of one pass: the compiler schedules the straight-line form's
+    // loads differently, and that measured slower (us, interleaved runs:
+    // 128256 x 4096 50.65 against 47.47, 14336 x 4096 8.09 against 7.94)
+    for (size_t c0 = 0; c0 < nb; c0 += kGvChunk) {
+      const int b0 = 2 * l;
       uint32_t wr[kR][9];
 #pragma unroll
       for (int r = 0; r < kR; ++r) {
@@ -281,30 +284,129 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
         t.y = static_cast<float>(nibble_dot(qb, ap.q1, ap.c1)) * dx1;
         *reinterpret_cast<float2 *>(&tl[w][r][b0]) = t;
       }
-    } else {
-      // blocks past the chunk: t = dy = 0, and fma(0, 0, sumf) == sumf (sumf is never -0)
+      wave_lds_sync();  // the LDS rows are this wave's own
+      float t[kTerms], dy[kTerms];
+#pragma unroll
+      for (int k = 0; k < kTerms; k += 4) {
+        const float4 tv = *reinterpret_cast<const float4 *>(&tl[w][fr][fp * kTerms + k]);
+        const float4 dv = *reinterpret_cast<const float4 *>(&dyl[w][fp * kTerms + k]);
+        t[k] = tv.x; t[k + 1] = tv.y; t[k + 2] = tv.z; t[k + 3] = tv.w;
+        dy[k] = dv.x; dy[k + 1] = dv.y; dy[k + 2] = dv.z; dy[k + 3] = dv.w;
+      }
+      sumf = fold_chain<kLanes, kTerms>(t, dy, 0.0f);
+    }
+  } else {
+    const int b0 = 2 * l;
+
+    // this lane's block pair of chunk c0 for the wave's rows (36 bytes each)
+    auto load_rows = [&](size_t c0, uint32_t (&wr)[kR][9]) {
+#pragma unroll
+      for (int r = 0; r < kR; ++r) {
+        const size_t row = min(row0 + r, nr - 1);  // rows past nr: computed, never stored
+        if constexpr (kSoA) {
+          const size_t blk = row * nb + c0 + b0;
+          const uint4 *q = reinterpret_cast<const uint4 *>(vx + blk * 16);
+          const uint4 qa4 = q[0], qb4 = q[1];
+          wr[r][0] = qa4.x; wr[r][1] = qa4.y; wr[r][2] = qa4.z; wr[r][3] = qa4.w;
+          wr[r][4] = qb4.x; wr[r][5] = qb4.y; wr[r][6] = qb4.z; wr[r][7] = qb4.w;
+          wr[r][8] = *reinterpret_cast<const uint32_t *>(vx + nr * nb * 16 + blk * 2);
+        } else {
+          load36(vx + row * bx + (c0 + b0) * kQ4Bytes, wr[r]);
+        }
+      }
+    };
+    // the terms fl(sumi * d_x) of the pair for every row, and d_y, to the wave's LDS
+    auto terms = [&](const uint32_t (&wr)[kR][9], const ActPair &ap) {
+      dyl[w][b0] = ap.d0;
+      dyl[w][b0 + 1] = ap.d1;
+#pragma unroll
+      for (int r = 0; r < kR; ++r) {
+        // block 2l: d = bytes 0-1, quants bytes 2..17 (shift by 2 bytes);
+        // block 2l+1: d = bytes 18-19, quants bytes 20..35 (dwords 5..8)
+        uint32_t qa[4], qb[4];
+        float dx0, dx1;
+        if constexpr (kSoA) {  // quants dwords 0-3 and 4-7, the two scales in dword 8
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            qa[k] = wr[r][k];
+            qb[k] = wr[r][k + 4];
+          }
+          dx0 = fp16_bits_to_f32(wr[r][8] & 0xffffu);
+          dx1 = fp16_bits_to_f32(wr[r][8] >> 16);
+        } else {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            qa[k] = funnel16(wr[r][k], wr[r][k + 1]);
+            qb[k] = wr[r][k + 5];
+          }
+          dx0 = fp16_bits_to_f32(wr[r][0] & 0xffffu);
+          dx1 = fp16_bits_to_f32(wr[r][4] >> 16);
+        }
+        float2 t;
+        t.x = static_cast<float>(nibble_dot(qa, ap.q0, ap.c0)) * dx0;
+        t.y = static_cast<float>(nibble_dot(qb, ap.q1, ap.c1)) * dx1;
+        *reinterpret_cast<float2 *>(&tl[w][r][b0]) = t;
+      }
+    };
+    // blocks past the chunk: t = dy = 0, and fma(0, 0, sumf) == sumf (sumf is never -0)
+    auto no_terms = [&] {
       dyl[w][b0] = 0.0f;
       dyl[w][b0 + 1] = 0.0f;
 #pragma unroll
       for (int r = 0; r < kR; ++r)
         *reinterpret_cast<float2 *>(&tl[w][r][b0]) = make_float2(0.0f, 0.0f);
-    }
-    wave_lds_sync();  // the LDS rows are this wave's own
-    float t[kTerms], dy[kTerms];
+    };
+    // each row's chain over the chunk's terms, seeded with `seed` in lane 0
+    auto fold = [&](float seed) {
+      wave_lds_sync();  // the LDS rows are this wave's own
+      float t[kTerms], dy[kTerms];
 #pragma unroll
-    for (int k = 0; k < kTerms; k += 4) {
-      const float4 tv = *reinterpret_cast<const float4 *>(&tl[w][fr][fp * kTerms + k]);
-      const float4 dv = *reinterpret_cast<const float4 *>(&dyl[w][fp * kTerms + k]);
-      t[k] = tv.x; t[k + 1] = tv.y; t[k + 2] = tv.z; t[k + 3] = tv.w;
-      dy[k] = dv.x; dy[k + 1] = dv.y; dy[k + 2] = dv.z; dy[k + 3] = dv.w;
+      for (int k = 0; k < kTerms; k += 4) {
+        const float4 tv = *reinterpret_cast<const float4 *>(&tl[w][fr][fp * kTerms + k]);
+        const float4 dv = *reinterpret_cast<const float4 *>(&dyl[w][fp * kTerms + k]);
+        t[k] = tv.x; t[k + 1] = tv.y; t[k + 2] = tv.z; t[k + 3] = tv.w;
+        dy[k] = dv.x; dy[k + 1] = dv.y; dy[k + 2] = dv.z; dy[k + 3] = dv.w;
+      }
+      return fold_chain<kLanes, kTerms>(t, dy, seed);
+    };
+
+    // the loads of chunk c0 + kGvChunk are issued before chunk c0's terms and
+    // fold, so a long row's chunks do not wait for each other's loads
+    uint32_t wr[kR][9];
+    ActPair ap;
+    bool have = b0 < static_cast<int>(min(static_cast<size_t>(kGvChunk), nb));
+    if (have) {
+      load_rows(0, wr);
+      load_act_pair(vy + b0 * kQ8Bytes, ap);
     }
-    if constexpr (kOneChunk) {
-      sumf = fold_chain<kLanes, kTerms>(t, dy, 0.0f);
-    } else {
+    for (size_t c0 = 0; c0 < nb; c0 += kGvChunk) {
+      const size_t c1 = c0 + kGvChunk;
+      // nbc is even: a lane's pair is whole or absent
+      const bool have1 =
+          c1 < nb && b0 < static_cast<int>(min(static_cast<size_t>(kGvChunk), nb - c1));
+      uint32_t wn[kR][9];
+      ActPair an;
+      if (have1) {
+        load_rows(c1, wn);
+        load_act_pair(vy + (c1 + b0) * kQ8Bytes, an);
+      }
+      if (have)
+        terms(wr, ap);
+      else
+        no_terms();
       // the previous chunk's sum sits in the last lane of the group: seed lane 0
       const float carry = __shfl(sumf, (l & ~(kLanes - 1)) + kLanes - 1);
-      sumf = fold_chain<kLanes, kTerms>(t, dy, fp == 0 ? carry : 0.0f);
+      sumf = fold(fp == 0 ? carry : 0.0f);
       wave_lds_sync();  // the LDS rows are this wave's own
+      if (have1) {
+#pragma unroll
+        for (int r = 0; r < kR; ++r)
+#pragma unroll
+          for (int k = 0; k < 9; ++k)
+            wr[r][k] = wn[r][k];
+        ap = an;
+      }
+      have = have1;
     }
   }
   if (fp == kLanes - 1 && l / kLanes < kR && row0 + fr < nr)
@@ -525,6 +627,12 @@ constexpr int kGemvRows = 2;
 // (4096^2, us: 1x4 4.16, 2x4 4.46, 4x4 4.00, 8x2 4.13, 8x4 5.06, 2x8 4.80, 4x2 4.28).
 constexpr int kDirectWaves = 4;
 constexpr int kDirectRows = 4;
+// Up to this many rows the shape-free entries run two rows per wave: four
+// leave too few work-groups to cover the chip (us, 2 against 4 rows per wave:
+// 256 x 4096 2.52/2.95, 1024 x 4096 2.70/3.07, 2048 x 4096 3.08/3.25,
+// 1024 x 14336 7.53/8.28; past it, 3072 x 4096 3.80/3.37, 4096^2 3.94/3.70).
+constexpr size_t kDirectSmallRows = 2048;
+inline int direct_rows(size_t nr) { return nr <= kDirectSmallRows ? 2 : kDirectRows; }
 
 // The register-direct GEMV with kR rows per wave (kDirectWaves waves per
 // work-group); every shape computes the same per-row fold, bit for bit.
@@ -620,7 +728,8 @@ int gemv_cols(size_t nb, float *s, size_t bs, const uint8_t *vx, size_t bx, cons
     else if (rem == 2)
       rc = launch_cols<kQ4, 2>(nb, sc, bs, vx, bx, yc, by, nr, 2, st);
     else if constexpr (kQ4)
-      rc = launch_direct<kDirectRows>(nb, sc, bs, vx, bx, yc, nr, st);
+      rc = nr <= kDirectSmallRows ? launch_direct<2>(nb, sc, bs, vx, bx, yc, nr, st)
+                                  : launch_direct<kDirectRows>(nb, sc, bs, vx, bx, yc, nr, st);
     else
       rc = q8_0_rows_direct(nb, sc, bs, vx, bx, yc, 0, nr, stream);
     if (rc != TCRV_HIP_OK)
@@ -722,7 +831,7 @@ int tcrv_hip_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx, size_t bx,
     return TCRV_HIP_OK;
   if (n / tcrv::kQK == 0)
     return tcrv_host::zero_outputs(s, nr, 1, 1, stream);
-  return tcrv_host::gemv_q4_0_q8_0(n, s, 1, vx, bx, vy, nr, stream, tcrv_host::kDirectRows);
+  return tcrv_host::gemv_q4_0_q8_0(n, s, 1, vx, bx, vy, nr, stream, tcrv_host::direct_rows(nr));
 }
 
 int tcrv_hip_gemv_q4_0_q8_0_shaped(size_t n, float *s, const uint8_t *vx, size_t bx,
@@ -747,7 +856,7 @@ int tcrv_hip_q4_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t
   if (n / tcrv::kQK == 0)
     return tcrv_host::zero_outputs(s, nr * nc, bs, nc, stream);
   if (nc == 1)
-    return tcrv_host::gemv_q4_0_q8_0(n, s, bs, vx, bx, vy, nr, stream, tcrv_host::kDirectRows);
+    return tcrv_host::gemv_q4_0_q8_0(n, s, bs, vx, bx, vy, nr, stream, tcrv_host::direct_rows(nr));
   if (!s || !vx || !vy)
     return TCRV_HIP_ERR_NULL_POINTER;
   if (!tcrv_host::aligned2(vx) || !tcrv_host::aligned2(vy) || (nr > 1 && (bx & 1u)) || (by & 1u))

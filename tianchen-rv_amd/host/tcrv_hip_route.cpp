@@ -207,7 +207,8 @@ const tcrv_hip_schedule kSchedules[] = {
     // 8 rows per wave, on 16 for 2
     {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_DECODE, "gemv_q4_0_q8_0_direct", "rows_per_wave", 2,
      0, "tcrv_hip_gemv_q4_0_q8_0_shaped", 3.836,
-     "2048 waves: two per SIMD share the read; the per-row fold chain is 15 lane hops"},
+     "2048 waves: two per SIMD share the read; the per-row fold chain is 15 lane hops "
+     "(the plain entry's choice up to 2048 rows, where 4 leave too few work-groups)"},
     {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_DECODE, "gemv_q4_0_q8_0_direct", "rows_per_wave", 4,
      1, "tcrv_hip_gemv_q4_0_q8_0_shaped", 3.565,
      "measured fastest: one wave per SIMD, every lane busy in the decode and 32 fold lanes"},
