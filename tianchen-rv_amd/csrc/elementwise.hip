@@ -17,6 +17,29 @@ __device__ __forceinline__ void store_stream(float4 v, float4 *p) {
   __builtin_nontemporal_store(x, reinterpret_cast<f32x4 *>(p));
 }
 
+// 128-bit streaming load (the input is read once).
+__device__ __forceinline__ float4 load_stream(const float *p) {
+  const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
+  return make_float4(x.x, x.y, x.z, x.w);
+}
+
+// copy_lds_to_span with streaming 128-bit stores when dst is 16-byte aligned.
+__device__ __forceinline__ void copy_lds_to_span_stream(uint8_t *dst, const uint8_t *src,
+                                                        int nbytes, int tid, int nthreads) {
+  if ((reinterpret_cast<uintptr_t>(dst) & 15u) != 0) {
+    copy_lds_to_span(dst, src, nbytes, tid, nthreads);
+    return;
+  }
+  const int nchunks = nbytes >> 4;
+  for (int c = tid; c < nchunks; c += nthreads)
+    __builtin_nontemporal_store(reinterpret_cast<const f32x4 *>(src)[c],
+                                reinterpret_cast<f32x4 *>(dst) + c);
+  const int tail_halves = (nbytes - (nchunks << 4)) >> 1;
+  if (tid < tail_halves)
+    reinterpret_cast<uint16_t *>(dst + (nchunks << 4))[tid] =
+        reinterpret_cast<const uint16_t *>(src + (nchunks << 4))[tid];
+}
+
 // ---------------------------------------------------------------------------
 // a1: out[i] = lhs[i] + rhs[i].  The reference emits a VL strip loop of
 // vle32/vfadd/vse32 (lib/Conversion/RVV/RVVToEmitC.cpp:605, :1873-1911); here
@@ -71,7 +94,8 @@ __global__ __launch_bounds__(kAddThreads) void add_f32_scalar(const float *lhs, 
 // int8 * fp16-valued float is exact in binary32, so the result is bit-exact.
 // One float4 per thread measured fastest: 64 blocks per 512 threads 12.8 us
 // for 4096^2, 32 per 256 13.0 us, 16 per 128 13.4 us; 128 blocks per 256
-// threads 13.9 us and 256-1024 blocks per 256 threads 14.0-15.5 us.
+// threads 13.9 us and 256-1024 blocks per 256 threads 14.0-15.5 us.  The
+// quantizer's nontemporal loads do not pay here: 19.2 against 12.5 us.
 // ---------------------------------------------------------------------------
 constexpr int kDqThreads = 512;
 constexpr int kDqBlocks = 64;
@@ -119,10 +143,13 @@ __global__ __launch_bounds__(kDqThreads) void dequantize_q8_0(const uint8_t *vx,
 // Division and reciprocal are the correctly rounded IEEE operations, as the
 // reference's scalar `amax / 127.0f` and `1.0f/d` are.  A work-group stages
 // its kQzBlocks output blocks (64*34 = 2176 bytes, a 16-byte multiple) in LDS
-// and writes them with 128-bit stores.
+// and writes them with 128-bit stores.  Loads and stores are nontemporal
+// (4096^2, interleaved runs: 14.89 against 16.19 us with ordinary ones).
 // ---------------------------------------------------------------------------
 constexpr int kQzThreads = 256;
-constexpr int kQzPer = 2;  // blocks per 8-lane group (1/2/4: 18.1/16.2/17.1 us at 4096^2)
+// blocks per 8-lane group (streaming, 4096^2: 1/2/4 15.81/14.89/15.59 us; 128
+// threads with 2 15.64, 512 slower also without streaming)
+constexpr int kQzPer = 2;
 constexpr int kQzBlocks = kQzPer * kQzThreads / 8;
 
 // Branch-free: the clamp to the i16 range (v_med3_f32) commutes with the
@@ -166,7 +193,7 @@ __global__ __launch_bounds__(kQzThreads) void quantize_q8_0(const float *x, uint
     const int lb = (threadIdx.x >> 3) + k * (kQzThreads / 8);  // block within the work-group
     const float *xp = x + (blk0 + min(lb, nblk - 1)) * kQK + 4 * part;
     if constexpr (kVec)
-      v[k] = *reinterpret_cast<const float4 *>(xp);
+      v[k] = load_stream(xp);
     else
       v[k] = make_float4(xp[0], xp[1], xp[2], xp[3]);
   }
@@ -191,7 +218,7 @@ __global__ __launch_bounds__(kQzThreads) void quantize_q8_0(const float *x, uint
     }
   }
   __syncthreads();
-  copy_lds_to_span(vy + blk0 * kQ8Bytes, lds, nblk * kQ8Bytes, threadIdx.x, kQzThreads);
+  copy_lds_to_span_stream(vy + blk0 * kQ8Bytes, lds, nblk * kQ8Bytes, threadIdx.x, kQzThreads);
 }
 
 }  // namespace
