@@ -59,8 +59,9 @@ constexpr int kPackSpan = 8;  // blocks per lane (4096 rows x 128 blocks: 7.3 us
 
 // Lane r's part of one record: its row's 32 quants (two 16-byte slots of the
 // record's 64-slot halves) and its fp16 scale.  kStream: nontemporal stores,
-// for a pack whose output is not read right away (4096 rows x 128 blocks,
-// interleaved runs: Q8_0 6.93 against 8.03 us, Q4_0 5.34 against 6.39 us).
+// for a pack whose output is not read right away (4096 rows x 128 blocks, 24
+// rotating operands past the Infinity Cache, interleaved runs: Q8_0 8.13
+// against 9.79 us, Q4_0 5.31 against 7.56 us).
 // The packs inside one GEMM call keep ordinary stores: the GEMM that follows
 // reads the records from the caches (Q4_0 4096^3 ws entry: 224.6 against
 // 210.5 us with streaming stores).

@@ -33,9 +33,10 @@ constexpr int kQ8x16Bytes = 544;
 // rows 4q..4q+3, i.e. output dword 8 + 4(4k+j) + q; for each k the group's 16
 // lanes store 16 consecutive dwords.  The scale d of source block r is the
 // output's fp16 d[r]: one 16-bit store per lane, 32 contiguous bytes per group.
-// The quant stores are nontemporal (Q4_0 4096^2, interleaved runs: 4.45
-// against 5.65 us); nontemporal loads give that back (5.65 us), since a
-// 16-lane group's loads share cache lines across its instructions.
+// Ordinary loads and stores: with 64 rotating weight sets (past the 256 MB
+// Infinity Cache), nontemporal stores measured 5.43 against 5.27 us; they gain
+// only where the source stays cached.  Nontemporal loads lose outright, since
+// a 16-lane group's loads share cache lines across its instructions.
 // ---------------------------------------------------------------------------
 template <bool kQ4>
 __global__ __launch_bounds__(256) void pack_x16_quad(size_t nblocks, const uint8_t *src,
@@ -78,7 +79,7 @@ __global__ __launch_bounds__(256) void pack_x16_quad(size_t nblocks, const uint8
     const uint32_t tq = __builtin_amdgcn_perm(p1, x, sel1);
     const uint32_t p2 = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
         0, static_cast<int>(tq), 0x4E /* quad_perm:[2,3,0,1] */, 0xf, 0xf, false));
-    __builtin_nontemporal_store(__builtin_amdgcn_perm(p2, tq, sel2), out + 8 + 4 * (4 * k + j) + q);
+    out[8 + 4 * (4 * k + j) + q] = __builtin_amdgcn_perm(p2, tq, sel2);
   }
   reinterpret_cast<uint16_t *>(out)[r] = static_cast<uint16_t>(d);
 }
