@@ -169,7 +169,10 @@ def same_as_eager(torch, stream, graph_out, eager_launch, what):
 
 
 def copies_for(nbytes: int, minimum: int = 2) -> int:
-    return max(minimum, -(-(MALL_BYTES + (MALL_BYTES >> 2)) // nbytes))
+    """Rotating input sets for a kernel that moves nbytes per launch: at least
+    2.5 x the Infinity Cache.  A rotation only 1.6 x it still hits: add_f32
+    over 2 sets (403 MB) ran 27.8 us, over 3-8 sets (604 MB-1.6 GB) 34.5-34.7 us."""
+    return max(minimum, -(-(MALL_BYTES * 5 // 2) // nbytes))
 
 
 def bench_gemv(torch, lib, stream, args):
