@@ -354,10 +354,12 @@ def test_q8_0_gemm_few_tokens(hip, oracle, dev, nr, nc, nb, ypad):
     (100, 70, 9, 16, 32),     # partial tiles, partial K chunk, padded strides
     (33, 1, 3, 0, 0),         # single column (decode-shaped), odd nb: the MFMA path
     (4096, 1, 128, 0, 0),     # decode: the register-direct GEMV
+    (1023, 1, 260, 0, 0),     # decode, one pair per wave: 2 chunks + 4 blocks, ragged rows
     (77, 1, 6, 4, 0),         # decode, padded rows, output stride bs = 6
     (1, 1, 2, 0, 0),          # one output
     (1, 45, 1, 0, 0),         # single weight row, one block
     (1, 300, 64, 0, 8),       # single weight row: register-direct block dots
+    (1, 33, 260, 0, 0),       # single weight row, 2 chunks + 4 blocks
     (512, 512, 128, 0, 0),
     # 256+ weight rows take the wide 256x128 tile with 4-block K chunks
     (300, 130, 7, 16, 32),    # partial wide tiles both ways, 4 + 3 blocks, padded strides

@@ -184,21 +184,22 @@ __global__ __launch_bounds__(64) void block_dot_pairs(size_t nb, float *s, int32
 
 // ---------------------------------------------------------------------------
 // Register-direct row pairs (rows 4-byte aligned, even block count): a wave
-// owns kDdPairs row pairs.  For each pair, lane l loads its block pair 2l,
+// owns kPairs row pairs.  For each pair, lane l loads its block pair 2l,
 // 2l+1 of both rows straight into registers (68 or 36 bytes, dword aligned --
 // across the wave the loads cover the row chunk contiguously), computes the
 // two blocks' fold operands and writes them to LDS; then DPP row r folds pair
-// r % kDdPairs with fold_chain, 8 consecutive blocks per lane, so the pairs'
+// r % kPairs with fold_chain, 8 consecutive blocks per lane, so the pairs'
 // serial folds run side by side in the same instructions and no LDS access
-// sits on the dependency chain (with two pairs per wave, DPP rows 2 and 3
-// fold copies of pairs 0 and 1, which are not stored).  Two pairs per wave
-// measured faster than four (25.6 vs 26.8 us for 16384 Q8_0 pairs of 4096):
-// a wave walks its pairs one after another, so fewer pairs per wave means
-// more, shorter waves.
+// sits on the dependency chain (with fewer than four pairs per wave, the
+// other DPP rows fold copies, which are not stored).  Pairs per wave:
+// two when both operands are distinct rows (16384 Q8_0 pairs of 4096: 24.5
+// against 25.5 us with one, 26.8 with four) -- a wave walks its pairs one
+// after another, so fewer pairs per wave means more, shorter waves -- and one
+// when a stride is 0, one row shared by every pair (the decode GEMV, over 640
+// MB of rotating weights: 4096^2 5.34 against 6.01 us, 14336 x 4096 12.2
+// against 14.3 us, 1024 x 4096 3.31 against 4.01 us).
 // ---------------------------------------------------------------------------
 constexpr int kDdWaves = 4;
-constexpr int kDdPairs = 2;                           // pairs per wave
-static_assert(4 % kDdPairs == 0, "each DPP row folds one pair");
 constexpr int kDdLanes = 16;                          // fold lanes per pair
 constexpr int kDdTerms = kChunkBlocks / kDdLanes;     // 8 blocks per fold lane
 constexpr int kDdStride = kChunkBlocks + 8;           // float2 per pair row (padded)
@@ -254,23 +255,24 @@ __device__ __forceinline__ float2 fold_terms(int sumi, uint32_t dx_bits, uint32_
 
 // Output of pair p: s[p * os].  by = 0 pairs every x row with one y row (the
 // GEMM's nc = 1 decode shape).
-template <DotFmt F>
+template <DotFmt F, int kPairs>
 __global__ __launch_bounds__(kDdWaves * 64) void block_dot_direct(size_t nb, float *s, size_t os,
                                                                    const uint8_t *vx, size_t bx,
                                                                    const uint8_t *vy, size_t by,
                                                                    size_t npairs) {
   constexpr int kXBytes = F == DotFmt::kQ8Q8 ? kQ8Bytes : kQ4Bytes;
-  __shared__ __align__(16) float2 tl[kDdWaves][kDdPairs][kDdStride];
+  static_assert(kPairs == 1 || kPairs == 2 || kPairs == 4, "each DPP row folds one pair");
+  __shared__ __align__(16) float2 tl[kDdWaves][kPairs][kDdStride];
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const size_t p0 = (static_cast<size_t>(blockIdx.x) * kDdWaves + w) * kDdPairs;
-  const int fr = (l >> 4) % kDdPairs, fp = l & (kDdLanes - 1);  // pair folded, lane in chain
+  const size_t p0 = (static_cast<size_t>(blockIdx.x) * kDdWaves + w) * kPairs;
+  const int fr = (l >> 4) % kPairs, fp = l & (kDdLanes - 1);  // pair folded, lane in chain
   float sumf = 0.0f;
 
   for (size_t c0 = 0; c0 < nb; c0 += kChunkBlocks) {
     const int nbc = static_cast<int>(min(static_cast<size_t>(kChunkBlocks), nb - c0));
     const int b0 = 2 * l;
 #pragma unroll
-    for (int r = 0; r < kDdPairs; ++r) {
+    for (int r = 0; r < kPairs; ++r) {
       const size_t p = min(p0 + r, npairs - 1);  // pairs past npairs: computed, never stored
       float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);  // absent blocks: fma(0, 0, sumf) == sumf
       if (b0 < nbc) {  // nbc is even: the pair is whole or absent
@@ -307,7 +309,7 @@ __global__ __launch_bounds__(kDdWaves * 64) void block_dot_direct(size_t nb, flo
     sumf = fold_chain<kDdLanes, kDdTerms>(ta, tb, fp == 0 ? carry : 0.0f);
     wave_lds_sync();  // the LDS rows are this wave's own
   }
-  if (fp == kDdLanes - 1 && (l >> 4) < kDdPairs && p0 + fr < npairs)
+  if (fp == kDdLanes - 1 && (l >> 4) < kPairs && p0 + fr < npairs)
     s[(p0 + fr) * os] = sumf;
 }
 
@@ -316,6 +318,24 @@ __global__ __launch_bounds__(kDdWaves * 64) void block_dot_direct(size_t nb, flo
 namespace tcrv_host {
 
 using tcrv::DotFmt;
+
+// The register-direct row pairs, one pair per wave when a stride is 0 (one row
+// shared by every pair), else two.
+template <DotFmt F>
+int launch_direct_pairs(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
+                        const uint8_t *vy, size_t by, size_t npairs, hipStream_t st) {
+  const bool shared = bx == 0 || by == 0;
+  const size_t per_group = static_cast<size_t>(tcrv::kDdWaves) * (shared ? 1 : 2);
+  const size_t groups = (npairs + per_group - 1) / per_group;
+  if (groups > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  const dim3 g(static_cast<unsigned>(groups)), b(tcrv::kDdWaves * 64);
+  if (shared)
+    tcrv::block_dot_direct<F, 1><<<g, b, 0, st>>>(nb, s, os, vx, bx, vy, by, npairs);
+  else
+    tcrv::block_dot_direct<F, 2><<<g, b, 0, st>>>(nb, s, os, vx, bx, vy, by, npairs);
+  return launch_status();
+}
 
 template <DotFmt F>
 int launch_pairs(size_t n, float *s, int32_t *sums, const uint8_t *vx, size_t bx,
@@ -338,13 +358,8 @@ int launch_pairs(size_t n, float *s, int32_t *sums, const uint8_t *vx, size_t bx
   hipStream_t st = as_stream(stream);
   const bool direct = !sums && ncols == 0 && nb % 2 == 0 && aligned4(vx) && aligned4(vy) &&
                       (xrows == 1 || bx % 4 == 0) && (yrows == 1 || by % 4 == 0);
-  if (direct) {
-    constexpr size_t per_group = tcrv::kDdWaves * tcrv::kDdPairs;
-    const size_t groups = (npairs + per_group - 1) / per_group;
-    tcrv::block_dot_direct<F><<<dim3(static_cast<unsigned>(groups)), dim3(tcrv::kDdWaves * 64),
-                                0, st>>>(nb, s, 1, vx, bx, vy, by, npairs);
-    return launch_status();
-  }
+  if (direct)
+    return launch_direct_pairs<F>(nb, s, 1, vx, bx, vy, by, npairs, st);
   if (sums)
     tcrv::block_dot_pairs<F, true><<<dim3(static_cast<unsigned>(npairs)), dim3(64), 0, st>>>(
         nb, s, sums, vx, bx, vy, by, ncols, bs);
@@ -390,13 +405,7 @@ int rows_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx, co
                 size_t by, size_t npairs, void *stream) {
   if (nb % 2 != 0 || !aligned4(vx) || !aligned4(vy) || bx % 4 != 0 || by % 4 != 0)
     return TCRV_HIP_ERR_UNSUPPORTED;
-  constexpr size_t per_group = tcrv::kDdWaves * tcrv::kDdPairs;
-  const size_t groups = (npairs + per_group - 1) / per_group;
-  if (groups > 0x7fffffffu)
-    return TCRV_HIP_ERR_TOO_LARGE;
-  tcrv::block_dot_direct<F><<<dim3(static_cast<unsigned>(groups)), dim3(tcrv::kDdWaves * 64), 0,
-                              as_stream(stream)>>>(nb, s, os, vx, bx, vy, by, npairs);
-  return launch_status();
+  return launch_direct_pairs<F>(nb, s, os, vx, bx, vy, by, npairs, as_stream(stream));
 }
 
 int q8_0_rows_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
