@@ -493,33 +493,38 @@ def bench_configs(torch, lib, stream, args):
     del S, Yv, soa, wd, reg
 
     # batched decode: the a7 and a9 GEMMs with BATCH_TOKENS tokens (the
-    # multi-column GEMVs), every launch over its own copy of the weights; bytes
-    # are the weights, the tokens' rows and the outputs
+    # multi-column GEMVs), and the a9 GEMM with one token (the Q8_0 decode
+    # GEMV), every launch over its own copy of the weights; bytes are the
+    # weights, the tokens' rows and the outputs
     act = inputs("gemm_a")[:BATCH_TOKENS].copy()
     actd = torch.from_numpy(act).to(dev)
-    for name, wsrc, entry_fn, what in (
+    for name, wsrc, entry_fn, nt, what in (
             ("q4_0_q8_0_gemm_4_tokens", inputs("gemv_w"), lib.tcrv_hip_q4_0_q8_0_gemm,
+             BATCH_TOKENS,
              "a7 Q4_0 x Q8_0 GEMM 4096 weight rows x 4 tokens x 4096 (batched decode)"),
             ("q8_0_q8_0_gemm_4_tokens", inputs("gemm_b"), lib.tcrv_hip_q8_0_q8_0_gemm,
-             "a9 Q8_0 x Q8_0 GEMM 4096 weight rows x 4 tokens x 4096 (batched decode)")):
+             BATCH_TOKENS,
+             "a9 Q8_0 x Q8_0 GEMM 4096 weight rows x 4 tokens x 4096 (batched decode)"),
+            ("q8_0_q8_0_gemv", inputs("gemm_b"), lib.tcrv_hip_q8_0_q8_0_gemm, 1,
+             "a9 Q8_0 x Q8_0 GEMM 4096 weight rows x 1 token x 4096 (the Q8_0 decode GEMV)")):
         sets = copies_for(wsrc.size, 2)
         Wc = torch.empty((sets, wsrc.size), dtype=torch.uint8, device=dev)
         Wc[:] = torch.from_numpy(wsrc.reshape(-1)).to(dev)
-        Cb = torch.empty((sets, N * BATCH_TOKENS), device=dev)
+        Cb = torch.empty((sets, N * nt), device=dev)
         fn = checked(entry_fn, name)
         bx = wsrc.shape[1]
         ptrs = [(Cb[i].data_ptr(), Wc[i].data_ptr()) for i in range(sets)]
         reg = Region(torch, stream,
-                     lambda i, fn=fn, ptrs=ptrs, sets=sets, bx=bx: fn(
+                     lambda i, fn=fn, ptrs=ptrs, sets=sets, bx=bx, nt=nt: fn(
                          N, ptrs[i % sets][0], ptrs[i % sets][1], actd.data_ptr(), act.shape[1],
-                         N, BATCH_TOKENS, bx, BATCH_TOKENS, sp), 400)
+                         N, nt, bx, nt, sp), 400)
         reg.run()
         us = reg.run() * 1e3 / 400
         same_as_eager(torch, stream, Cb[399 % sets],
-                      lambda o, fn=fn, bx=bx, k=399 % sets: fn(
+                      lambda o, fn=fn, bx=bx, k=399 % sets, nt=nt: fn(
                           N, o, Wc[k].data_ptr(), actd.data_ptr(), act.shape[1], N,
-                          BATCH_TOKENS, bx, BATCH_TOKENS, sp), name)
-        nbytes = wsrc.size + act.size + N * BATCH_TOKENS * 4
+                          nt, bx, nt, sp), name)
+        nbytes = wsrc.size + act.shape[1] * nt + N * nt * 4
         out[name] = {"workload": what, "us": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
                      "sets": sets}
         del Wc, Cb, reg
@@ -871,15 +876,17 @@ def cpu_baseline_configs(seconds: float):
     # over the weight rows (each output's fold serial)
     act = a8[:BATCH_TOKENS].copy()
     w8 = inputs("gemm_b")
-    for name, wsrc, gemm in (("q4_0_q8_0_gemm_4_tokens", w, ora.gemm_q4_0),
-                             ("q8_0_q8_0_gemm_4_tokens", w8, ora.gemm_q8_0)):
-        nbytes = wsrc.size + act.size + N * BATCH_TOKENS * 4
+    for name, wsrc, gemm, nt in (("q4_0_q8_0_gemm_4_tokens", w, ora.gemm_q4_0, BATCH_TOKENS),
+                                 ("q8_0_q8_0_gemm_4_tokens", w8, ora.gemm_q8_0, BATCH_TOKENS),
+                                 ("q8_0_q8_0_gemv", w8, ora.gemm_q8_0, 1)):
+        nbytes = wsrc.size + act.shape[1] * nt + N * nt * 4
         out[name] = entry(
-            nbytes, "GB/s", f"whole 4096 x {BATCH_TOKENS} x 4096 GEMMs, OpenMP over weight rows",
-            lambda wsrc=wsrc, gemm=gemm: gemm(N, wsrc, act, act.shape[1], N, BATCH_TOKENS,
-                                              wsrc.shape[1], BATCH_TOKENS, 1),
-            lambda wsrc=wsrc, gemm=gemm: gemm(N, wsrc, act, act.shape[1], N, BATCH_TOKENS,
-                                              wsrc.shape[1], BATCH_TOKENS, threads))
+            nbytes, "GB/s", f"whole 4096 x {nt} x 4096 GEMMs over one weight copy (the "
+            "host's caches hold it), OpenMP over weight rows",
+            lambda wsrc=wsrc, gemm=gemm, nt=nt: gemm(N, wsrc, act[:nt].copy(), act.shape[1], N,
+                                                     nt, wsrc.shape[1], nt, 1),
+            lambda wsrc=wsrc, gemm=gemm, nt=nt: gemm(N, wsrc, act[:nt].copy(), act.shape[1], N,
+                                                     nt, wsrc.shape[1], nt, threads))
     wx16 = ora.pack_q4_0x16(src, nx16)
     ax4s = [ora.pack_q8_0x4(a8[16 * t:16 * t + 16].copy(), 16, nb, a8.shape[1])
             for t in range(threads)]
