@@ -227,7 +227,7 @@ def test_gemv_q4_0_nonfinite_activation_scale(hip, oracle, dev):
         assert_f32_parity_nan(from_dev(s), want, what=f"gemv activation d={bits:#06x}")
 
 
-@pytest.mark.parametrize("rows,nb,pad", [(64, 128, 0), (19, 9, 2)])
+@pytest.mark.parametrize("rows,nb,pad", [(64, 128, 0), (19, 9, 2), (24, 260, 0)])
 def test_block_dots_special_scales(hip, oracle, dev, rows, nb, pad):
     n = nb * 32
     x8 = np.pad(q8(rows, nb, 21, 1.0, nonfinite_every=8), ((0, 0), (0, pad)))
