@@ -44,8 +44,8 @@ __device__ __forceinline__ void copy_lds_to_span_stream(uint8_t *dst, const uint
 // a1: out[i] = lhs[i] + rhs[i].  The reference emits a VL strip loop of
 // vle32/vfadd/vse32 (lib/Conversion/RVV/RVVToEmitC.cpp:605, :1873-1911); here
 // each thread moves kAddUnroll 128-bit vectors per operand, all loads issued
-// before the adds (2 measured fastest for n = 2^24: 27.8 us against 28.0, 28.7
-// and 29.1 us for 1, 4 and 8).  Loads and stores are nontemporal: over 3-6
+// before the adds (2 measured fastest for n = 2^24 over 2 rotating sets: 27.8
+// us against 28.0, 28.7 and 29.1 us for 1, 4 and 8).  Loads and stores are nontemporal: over 3-6
 // rotating sets (past the Infinity Cache) 31.7-32.4 against 34.6-35.0 us with
 // ordinary loads.  IEEE binary32 addition is correctly rounded, so the result
 // is bit-identical to the scalar loop.
@@ -97,7 +97,8 @@ __global__ __launch_bounds__(kAddThreads) void add_f32_scalar(const float *lhs, 
 // One float4 per thread measured fastest: 64 blocks per 512 threads 12.8 us
 // for 4096^2, 32 per 256 13.0 us, 16 per 128 13.4 us; 128 blocks per 256
 // threads 13.9 us and 256-1024 blocks per 256 threads 14.0-15.5 us.  The
-// quantizer's nontemporal loads do not pay here: 19.2 against 12.5 us.
+// quantizer's nontemporal loads do not pay here: over 8 rotating sets (past the
+// Infinity Cache) 19.4 against 12.5 us.
 // ---------------------------------------------------------------------------
 constexpr int kDqThreads = 512;
 constexpr int kDqBlocks = 64;
