@@ -220,7 +220,10 @@ def test_q4_0_block_dot_rows(hip, oracle, dev, rows, nb, pad):
 
 # ------------------------------------------------------------ a7 GEMV / GEMM ---
 
-@pytest.mark.parametrize("nr,nb", [(4096, 128), (1, 128), (13, 5), (1000, 131), (64, 256)])
+@pytest.mark.parametrize("nr,nb", [(4096, 128), (1, 128), (13, 5), (1000, 131), (64, 256),
+                                   (2048, 258),   # 2 rows per wave, chunk prefetch, a 2-block tail
+                                   (2049, 128),   # 4 rows per wave from 2049 rows, ragged last wave
+                                   (2500, 260)])  # 4 rows per wave with the chunk prefetch
 def test_gemv_q4_0_q8_0(hip, oracle, dev, nr, nb):
     n = nb * 32
     w = synth.q4_0_matrix(nr, n, 1006, 0.02)
