@@ -223,7 +223,9 @@ def test_q4_0_block_dot_rows(hip, oracle, dev, rows, nb, pad):
 @pytest.mark.parametrize("nr,nb", [(4096, 128), (1, 128), (13, 5), (1000, 131), (64, 256),
                                    (2048, 258),   # 2 rows per wave, chunk prefetch, a 2-block tail
                                    (2049, 128),   # 4 rows per wave from 2049 rows, ragged last wave
-                                   (2500, 260)])  # 4 rows per wave with the chunk prefetch
+                                   (2500, 260),   # 4 rows per wave with the chunk prefetch
+                                   (4096, 64),    # n = 2048 below 8192 rows: the chunked kernel
+                                   (8200, 64)])   # the half-wave kernel, a ragged last group
 def test_gemv_q4_0_q8_0(hip, oracle, dev, nr, nb):
     n = nb * 32
     w = synth.q4_0_matrix(nr, n, 1006, 0.02)
@@ -234,7 +236,7 @@ def test_gemv_q4_0_q8_0(hip, oracle, dev, nr, nb):
     assert_f32_parity(from_dev(s), want, what=f"gemv nr={nr} nb={nb}")
 
 
-@pytest.mark.parametrize("nr,nb", [(1000, 128), (333, 40), (129, 200), (70, 9)])
+@pytest.mark.parametrize("nr,nb", [(1000, 128), (333, 40), (129, 200), (70, 9), (8200, 64)])
 def test_gemv_shapes_are_bit_identical(hip, oracle, dev, nr, nb):
     """The decode GEMV's schedule knob (rows per wave 2, 4, 8) changes how it
     runs, never what it computes: every shape equals the oracle and the plain

@@ -413,6 +413,75 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
     s[(row0 + fr) * os] = sumf;
 }
 
+// Rows of exactly 64 blocks (n = 2048): the register-direct GEMV with each
+// half-wave on its own rows -- lanes 0-31 take rows 0..kR-1 of the wave and
+// lanes 32-63 rows kR..2kR-1, lane l owning blocks 2(l % 32), 2(l % 32) + 1 --
+// so no lane idles (the one-chunk kernel would leave lanes 32-63 without a
+// block).  The 2kR rows fold on 8 lanes each, 8 terms per lane: the same
+// 64-step chain per row as the chunked kernel, bit for bit.
+template <int kWaves, int kR>
+__global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_half(float *s, size_t os,
+                                                                  const uint8_t *vx, size_t bx,
+                                                                  const uint8_t *vy, size_t nr) {
+  constexpr int kNb = kGvChunk / 2;  // 64 blocks a row
+  constexpr int kRows = 2 * kR;      // rows a wave
+  constexpr int kLanes = 8;
+  constexpr int kTerms = kNb / kLanes;  // 8 blocks per fold lane
+  static_assert(kRows * kLanes == 64, "every lane folds");
+  __shared__ __align__(16) float tl[kWaves][kRows][kNb + 4];
+  __shared__ __align__(16) float dyl[kWaves][kNb];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+  const int l = tid & 63;
+  const int hw = l >> 5;         // half-wave: rows hw*kR .. hw*kR + kR - 1
+  const int b0 = 2 * (l & 31);   // this lane's block pair
+  const size_t rowb = (static_cast<size_t>(blockIdx.x) * kWaves + w) * kRows;
+  const int fr = l / kLanes;     // row of this lane in the fold
+  const int fp = l & (kLanes - 1);
+  uint32_t wr[kR][9];
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    const size_t row = min(rowb + hw * kR + r, nr - 1);  // rows past nr: computed, never stored
+    load36(vx + row * bx + b0 * kQ4Bytes, wr[r]);
+  }
+  ActPair ap;
+  load_act_pair(vy + b0 * kQ8Bytes, ap);
+  if (hw == 0) {
+    dyl[w][b0] = ap.d0;
+    dyl[w][b0 + 1] = ap.d1;
+  }
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    // block 2l: d = bytes 0-1, quants bytes 2..17; block 2l+1: d = bytes 18-19,
+    // quants bytes 20..35 (dwords 5..8)
+    uint32_t qa[4], qb[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      qa[k] = funnel16(wr[r][k], wr[r][k + 1]);
+      qb[k] = wr[r][k + 5];
+    }
+    const float dx0 = fp16_bits_to_f32(wr[r][0] & 0xffffu);
+    const float dx1 = fp16_bits_to_f32(wr[r][4] >> 16);
+    float2 t;
+    t.x = static_cast<float>(nibble_dot(qa, ap.q0, ap.c0)) * dx0;
+    t.y = static_cast<float>(nibble_dot(qb, ap.q1, ap.c1)) * dx1;
+    *reinterpret_cast<float2 *>(&tl[w][hw * kR + r][b0]) = t;
+  }
+  wave_lds_sync();  // the LDS rows are this wave's own
+  float t[kTerms], dy[kTerms];
+#pragma unroll
+  for (int k = 0; k < kTerms; k += 4) {
+    const float4 tv = *reinterpret_cast<const float4 *>(&tl[w][fr][fp * kTerms + k]);
+    const float4 dv = *reinterpret_cast<const float4 *>(&dyl[w][fp * kTerms + k]);
+    t[k] = tv.x; t[k + 1] = tv.y; t[k + 2] = tv.z; t[k + 3] = tv.w;
+    dy[k] = dv.x; dy[k + 1] = dv.y; dy[k + 2] = dv.z; dy[k + 3] = dv.w;
+  }
+  const float sumf = fold_chain<kLanes, kTerms>(t, dy, 0.0f);
+  if (fp == kLanes - 1 && rowb + fr < nr)
+    s[(rowb + fr) * os] = sumf;
+}
+
 // Multi-column form of the register-direct GEMV, for the a7 GEMM with a few
 // tokens (batched decode, nc = 2..kGemvColsMax): each wave loads its 4 weight
 // rows' block pairs once and dots them with kCols activation columns (ncols of
@@ -634,6 +703,12 @@ constexpr int kDirectRows = 4;
 constexpr size_t kDirectSmallRows = 2048;
 inline int direct_rows(size_t nr) { return nr <= kDirectSmallRows ? 2 : kDirectRows; }
 
+// Rows of 64 blocks run the half-wave kernel from this many rows: it has half
+// the work-groups of the chunked kernel, which pays once those fill the chip
+// (n = 2048, us, half-wave against chunked: 8192 rows 4.06/4.25, 11008 rows
+// 4.92/5.58; 4096 rows 3.62/3.32, 2560 rows 3.43/3.08).
+constexpr size_t kHalfMinRows = 8192;
+
 // The register-direct GEMV with kR rows per wave (kDirectWaves waves per
 // work-group); every shape computes the same per-row fold, bit for bit.
 template <int kR>
@@ -647,7 +722,11 @@ int launch_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
   if (nb == static_cast<size_t>(tcrv::kGvChunk))
     tcrv::gemv_q4_0_q8_0_direct<kW, kR, true>
         <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(nb, s, os, vx, bx, vy, nr);
-  else
+  else if (kR == 4 && nb == static_cast<size_t>(tcrv::kGvChunk / 2) && nr >= kHalfMinRows) {
+    const size_t grid_half = (nr + 2 * rows_per_wg - 1) / (2 * rows_per_wg);
+    tcrv::gemv_q4_0_q8_0_half<kW, 4>
+        <<<dim3(static_cast<unsigned>(grid_half)), dim3(kW * 64), 0, st>>>(s, os, vx, bx, vy, nr);
+  } else
     tcrv::gemv_q4_0_q8_0_direct<kW, kR, false>
         <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(nb, s, os, vx, bx, vy, nr);
   return launch_status();
