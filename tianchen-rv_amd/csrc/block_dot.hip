@@ -313,6 +313,57 @@ __global__ __launch_bounds__(kDdWaves * 64) void block_dot_direct(size_t nb, flo
     s[(p0 + fr) * os] = sumf;
 }
 
+// Rows of exactly 64 blocks (n = 2048): two pairs per wave side by side, lanes
+// 0-31 on pair 0 and lanes 32-63 on pair 1, lane l owning blocks 2(l % 32),
+// 2(l % 32) + 1, so no lane idles (block_dot_direct would leave lanes 32-63
+// without a block).  DPP rows 0 and 1 fold the two pairs, 4 blocks per lane:
+// the same 64-step chain per pair, bit for bit.
+template <DotFmt F>
+__global__ __launch_bounds__(kDdWaves * 64) void block_dot_half(float *s, size_t os,
+                                                                 const uint8_t *vx, size_t bx,
+                                                                 const uint8_t *vy, size_t by,
+                                                                 size_t npairs) {
+  constexpr int kXBytes = F == DotFmt::kQ8Q8 ? kQ8Bytes : kQ4Bytes;
+  constexpr int kNb = kChunkBlocks / 2;        // 64 blocks a row
+  constexpr int kTerms = kNb / kDdLanes;       // 4 blocks per fold lane
+  __shared__ __align__(16) float2 tl[kDdWaves][2][kNb + 8];
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int hw = l >> 5, b0 = 2 * (l & 31);
+  const size_t p0 = (static_cast<size_t>(blockIdx.x) * kDdWaves + w) * 2;
+  const int fr = (l >> 4) & 1, fp = l & (kDdLanes - 1);  // pair folded, lane in chain
+  {
+    const size_t p = min(p0 + hw, npairs - 1);  // pairs past npairs: computed, never stored
+    uint32_t y0[8], y1[8], dy0, dy1;
+    load_q8_pair(vy + p * by + b0 * kQ8Bytes, y0, y1, dy0, dy1);
+    int s0, s1;
+    uint32_t dx0, dx1;
+    if constexpr (F == DotFmt::kQ8Q8) {
+      uint32_t x0[8], x1[8];
+      load_q8_pair(vx + p * bx + b0 * kXBytes, x0, x1, dx0, dx1);
+      s0 = q8_q8_sumi(x0, y0);
+      s1 = q8_q8_sumi(x1, y1);
+    } else {
+      uint32_t x0[4], x1[4];
+      load_q4_pair(vx + p * bx + b0 * kXBytes, x0, x1, dx0, dx1);
+      s0 = q4_q8_sumi(x0, y0);
+      s1 = q4_q8_sumi(x1, y1);
+    }
+    const float2 t0 = fold_terms<F>(s0, dx0, dy0);
+    const float2 t1 = fold_terms<F>(s1, dx1, dy1);
+    *reinterpret_cast<float4 *>(&tl[w][hw][b0]) = make_float4(t0.x, t0.y, t1.x, t1.y);
+  }
+  wave_lds_sync();  // the LDS rows are this wave's own
+  float ta[kTerms], tb[kTerms];
+#pragma unroll
+  for (int k = 0; k < kTerms; k += 2) {
+    const float4 v = *reinterpret_cast<const float4 *>(&tl[w][fr][fp * kTerms + k]);
+    ta[k] = v.x; tb[k] = v.y; ta[k + 1] = v.z; tb[k + 1] = v.w;
+  }
+  const float sumf = fold_chain<kDdLanes, kTerms>(ta, tb, 0.0f);
+  if (fp == kDdLanes - 1 && (l >> 4) < 2 && p0 + fr < npairs)
+    s[(p0 + fr) * os] = sumf;
+}
+
 }  // namespace tcrv
 
 namespace tcrv_host {
@@ -320,7 +371,10 @@ namespace tcrv_host {
 using tcrv::DotFmt;
 
 // The register-direct row pairs, one pair per wave when a stride is 0 (one row
-// shared by every pair), else two.
+// shared by every pair), else two; rows of exactly 64 blocks two pairs per
+// wave, one per half-wave (the Q8_0 decode GEMV at n = 2048, us, against one
+// pair per wave: 4096 rows 3.72/4.83, 11008 rows 6.24/8.27, 2048 rows
+// 2.99/3.57; 16384 distinct row pairs 13.8/13.8).
 template <DotFmt F>
 int launch_direct_pairs(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
                         const uint8_t *vy, size_t by, size_t npairs, hipStream_t st) {
@@ -330,6 +384,12 @@ int launch_direct_pairs(size_t nb, float *s, size_t os, const uint8_t *vx, size_
   if (groups > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
   const dim3 g(static_cast<unsigned>(groups)), b(tcrv::kDdWaves * 64);
+  if (nb == static_cast<size_t>(tcrv::kChunkBlocks / 2)) {
+    const size_t per_half = static_cast<size_t>(tcrv::kDdWaves) * 2;
+    tcrv::block_dot_half<F><<<dim3(static_cast<unsigned>((npairs + per_half - 1) / per_half)), b, 0,
+                              st>>>(s, os, vx, bx, vy, by, npairs);
+    return launch_status();
+  }
   if (shared)
     tcrv::block_dot_direct<F, 1><<<g, b, 0, st>>>(nb, s, os, vx, bx, vy, by, npairs);
   else
