@@ -224,8 +224,8 @@ def test_q4_0_block_dot_rows(hip, oracle, dev, rows, nb, pad):
                                    (2048, 258),   # 2 rows per wave, chunk prefetch, a 2-block tail
                                    (2049, 128),   # 4 rows per wave from 2049 rows, ragged last wave
                                    (2500, 260),   # 4 rows per wave with the chunk prefetch
-                                   (4096, 64),    # n = 2048 below 8192 rows: the chunked kernel
-                                   (8200, 64)])   # the half-wave kernel, a ragged last group
+                                   (4096, 64),    # n = 2048: the half-wave kernel, 4 rows a wave
+                                   (8200, 64)])   # the half-wave kernel, 8 rows a wave, ragged
 def test_gemv_q4_0_q8_0(hip, oracle, dev, nr, nb):
     n = nb * 32
     w = synth.q4_0_matrix(nr, n, 1006, 0.02)

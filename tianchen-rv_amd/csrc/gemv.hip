@@ -417,16 +417,16 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
 // half-wave on its own rows -- lanes 0-31 take rows 0..kR-1 of the wave and
 // lanes 32-63 rows kR..2kR-1, lane l owning blocks 2(l % 32), 2(l % 32) + 1 --
 // so no lane idles (the one-chunk kernel would leave lanes 32-63 without a
-// block).  The 2kR rows fold on 8 lanes each, 8 terms per lane: the same
-// 64-step chain per row as the chunked kernel, bit for bit.
+// block).  The 2kR rows fold on 64 / 2kR lanes each: the same 64-step chain
+// per row as the chunked kernel, bit for bit.
 template <int kWaves, int kR>
 __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_half(float *s, size_t os,
                                                                   const uint8_t *vx, size_t bx,
                                                                   const uint8_t *vy, size_t nr) {
   constexpr int kNb = kGvChunk / 2;  // 64 blocks a row
   constexpr int kRows = 2 * kR;      // rows a wave
-  constexpr int kLanes = 8;
-  constexpr int kTerms = kNb / kLanes;  // 8 blocks per fold lane
+  constexpr int kLanes = 64 / kRows; // fold lanes per row: 8 for 8 rows, 16 for 4
+  constexpr int kTerms = kNb / kLanes;  // blocks per fold lane
   static_assert(kRows * kLanes == 64, "every lane folds");
   __shared__ __align__(16) float tl[kWaves][kRows][kNb + 4];
   __shared__ __align__(16) float dyl[kWaves][kNb];
@@ -703,10 +703,11 @@ constexpr int kDirectRows = 4;
 constexpr size_t kDirectSmallRows = 2048;
 inline int direct_rows(size_t nr) { return nr <= kDirectSmallRows ? 2 : kDirectRows; }
 
-// Rows of 64 blocks run the half-wave kernel from this many rows: it has half
-// the work-groups of the chunked kernel, which pays once those fill the chip
-// (n = 2048, us, half-wave against chunked: 8192 rows 4.06/4.25, 11008 rows
-// 4.92/5.58; 4096 rows 3.62/3.32, 2560 rows 3.43/3.08).
+// Rows of 64 blocks (n = 2048) run the half-wave kernel: with 8 rows per wave
+// from this many rows, where its work-groups fill the chip (us, against the
+// chunked kernel: 8192 rows 4.06/4.25, 11008 rows 4.92/5.58; at 4096 rows
+// 3.62/3.32), else with 4 rows per wave, as many work-groups as the chunked
+// kernel (2560 rows 2.95/3.11, 4096 rows 3.20/3.33, 5632 rows 3.77/4.10).
 constexpr size_t kHalfMinRows = 8192;
 
 // The register-direct GEMV with kR rows per wave (kDirectWaves waves per
@@ -726,6 +727,9 @@ int launch_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
     const size_t grid_half = (nr + 2 * rows_per_wg - 1) / (2 * rows_per_wg);
     tcrv::gemv_q4_0_q8_0_half<kW, 4>
         <<<dim3(static_cast<unsigned>(grid_half)), dim3(kW * 64), 0, st>>>(s, os, vx, bx, vy, nr);
+  } else if (kR == 4 && nb == static_cast<size_t>(tcrv::kGvChunk / 2)) {
+    tcrv::gemv_q4_0_q8_0_half<kW, 2>
+        <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(s, os, vx, bx, vy, nr);
   } else
     tcrv::gemv_q4_0_q8_0_direct<kW, kR, false>
         <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(nb, s, os, vx, bx, vy, nr);
