@@ -225,7 +225,8 @@ def test_q4_0_block_dot_rows(hip, oracle, dev, rows, nb, pad):
                                    (2049, 128),   # 4 rows per wave from 2049 rows, ragged last wave
                                    (2500, 260),   # 4 rows per wave with the chunk prefetch
                                    (4096, 64),    # n = 2048: the half-wave kernel, 4 rows a wave
-                                   (8200, 64)])   # the half-wave kernel, 8 rows a wave, ragged
+                                   (8200, 64),    # the half-wave kernel, 8 rows a wave, ragged
+                                   (4100, 32)])   # n = 1024: a quarter-wave group per 2 rows
 def test_gemv_q4_0_q8_0(hip, oracle, dev, nr, nb):
     n = nb * 32
     w = synth.q4_0_matrix(nr, n, 1006, 0.02)
@@ -236,7 +237,8 @@ def test_gemv_q4_0_q8_0(hip, oracle, dev, nr, nb):
     assert_f32_parity(from_dev(s), want, what=f"gemv nr={nr} nb={nb}")
 
 
-@pytest.mark.parametrize("nr,nb", [(1000, 128), (333, 40), (129, 200), (70, 9), (8200, 64)])
+@pytest.mark.parametrize("nr,nb", [(1000, 128), (333, 40), (129, 200), (70, 9), (8200, 64),
+                                   (1000, 32)])
 def test_gemv_shapes_are_bit_identical(hip, oracle, dev, nr, nb):
     """The decode GEMV's schedule knob (rows per wave 2, 4, 8) changes how it
     runs, never what it computes: every shape equals the oracle and the plain

@@ -413,29 +413,32 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_direct(
     s[(row0 + fr) * os] = sumf;
 }
 
-// Rows of exactly 64 blocks (n = 2048): the register-direct GEMV with each
-// half-wave on its own rows -- lanes 0-31 take rows 0..kR-1 of the wave and
-// lanes 32-63 rows kR..2kR-1, lane l owning blocks 2(l % 32), 2(l % 32) + 1 --
-// so no lane idles (the one-chunk kernel would leave lanes 32-63 without a
-// block).  The 2kR rows fold on 64 / 2kR lanes each: the same 64-step chain
-// per row as the chunked kernel, bit for bit.
-template <int kWaves, int kR>
+// Rows of exactly 128 / kSplit blocks (n = 2048 for kSplit = 2, 1024 for 4):
+// the register-direct GEMV with the wave cut into kSplit lane groups, group g
+// on rows g*kR .. g*kR + kR - 1 of the wave, lane l owning blocks 2(l % G),
+// 2(l % G) + 1 (G = 64 / kSplit lanes a group), so no lane idles (the chunked
+// kernel would leave all but the first group without a block).  The kSplit*kR
+// rows fold on 64 / (kSplit*kR) lanes each: the same chain per row as the
+// chunked kernel, bit for bit.
+template <int kWaves, int kR, int kSplit = 2>
 __global__ __launch_bounds__(kWaves * 64) void gemv_q4_0_q8_0_half(float *s, size_t os,
                                                                   const uint8_t *vx, size_t bx,
                                                                   const uint8_t *vy, size_t nr) {
-  constexpr int kNb = kGvChunk / 2;  // 64 blocks a row
-  constexpr int kRows = 2 * kR;      // rows a wave
-  constexpr int kLanes = 64 / kRows; // fold lanes per row: 8 for 8 rows, 16 for 4
-  constexpr int kTerms = kNb / kLanes;  // blocks per fold lane
-  static_assert(kRows * kLanes == 64, "every lane folds");
+  constexpr int kNb = kGvChunk / kSplit;  // blocks a row
+  constexpr int kGroup = 64 / kSplit;     // lanes a group
+  constexpr int kRows = kSplit * kR;      // rows a wave
+  constexpr int kLanes = 64 / kRows;      // fold lanes per row
+  constexpr int kTerms = kNb / kLanes;    // blocks per fold lane
+  static_assert(kRows * kLanes == 64 && kTerms % 4 == 0 && kLanes <= 16,
+                "every lane folds, whole float4 reads, groups inside one DPP row");
   __shared__ __align__(16) float tl[kWaves][kRows][kNb + 4];
   __shared__ __align__(16) float dyl[kWaves][kNb];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6;
   const int l = tid & 63;
-  const int hw = l >> 5;         // half-wave: rows hw*kR .. hw*kR + kR - 1
-  const int b0 = 2 * (l & 31);   // this lane's block pair
+  const int hw = l / kGroup;            // lane group: rows hw*kR .. hw*kR + kR - 1
+  const int b0 = 2 * (l % kGroup);      // this lane's block pair
   const size_t rowb = (static_cast<size_t>(blockIdx.x) * kWaves + w) * kRows;
   const int fr = l / kLanes;     // row of this lane in the fold
   const int fp = l & (kLanes - 1);
@@ -709,6 +712,9 @@ inline int direct_rows(size_t nr) { return nr <= kDirectSmallRows ? 2 : kDirectR
 // 3.62/3.32), else with 4 rows per wave, as many work-groups as the chunked
 // kernel (2560 rows 2.95/3.11, 4096 rows 3.20/3.33, 5632 rows 3.77/4.10).
 constexpr size_t kHalfMinRows = 8192;
+// Rows of 32 blocks (n = 1024) run it with four lane groups, 2 rows each (us,
+// against the chunked kernel: 2560 rows 2.65/2.96, 4096 rows 2.75/3.07, 8192
+// rows 3.10/3.93, 14336 rows 3.75/6.35).
 
 // The register-direct GEMV with kR rows per wave (kDirectWaves waves per
 // work-group); every shape computes the same per-row fold, bit for bit.
@@ -730,6 +736,10 @@ int launch_direct(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
   } else if (kR == 4 && nb == static_cast<size_t>(tcrv::kGvChunk / 2)) {
     tcrv::gemv_q4_0_q8_0_half<kW, 2>
         <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(s, os, vx, bx, vy, nr);
+  } else if (kR == 4 && nb == static_cast<size_t>(tcrv::kGvChunk / 4)) {
+    const size_t grid_q = (nr + 2 * rows_per_wg - 1) / (2 * rows_per_wg);  // 8 rows a wave
+    tcrv::gemv_q4_0_q8_0_half<kW, 2, 4>
+        <<<dim3(static_cast<unsigned>(grid_q)), dim3(kW * 64), 0, st>>>(s, os, vx, bx, vy, nr);
   } else
     tcrv::gemv_q4_0_q8_0_direct<kW, kR, false>
         <<<dim3(static_cast<unsigned>(grid)), dim3(kW * 64), 0, st>>>(nb, s, os, vx, bx, vy, nr);
