@@ -187,7 +187,8 @@ def test_q4_0_block_dot_single_ggml_abi(hip, oracle, dev):
 # chunks, two chunks with a carried sum, pair counts that are not a multiple of
 # the 16 pairs per work-group); odd nb or 2-byte aligned rows the LDS one
 @pytest.mark.parametrize("rows,nb,pad", [(16384, 128, 0), (33, 131, 16), (5, 1, 0), (9, 256, 32),
-                                         (21, 6, 0), (7, 130, 4), (3, 4, 2), (4101, 64, 4)])
+                                         (21, 6, 0), (7, 130, 4), (3, 4, 2), (4101, 64, 4),
+                                         (4103, 32, 8)])
 def test_q8_0_block_dot_rows(hip, oracle, dev, rows, nb, pad):
     n = nb * 32
     vx = synth.q8_0_matrix(rows, n, 1004, 1.0)
@@ -203,7 +204,8 @@ def test_q8_0_block_dot_rows(hip, oracle, dev, rows, nb, pad):
 
 
 @pytest.mark.parametrize("rows,nb,pad", [(16384, 128, 0), (33, 131, 16), (5, 1, 0), (9, 256, 32),
-                                         (21, 6, 0), (7, 130, 4), (7, 130, 2), (4101, 64, 4)])
+                                         (21, 6, 0), (7, 130, 4), (7, 130, 2), (4101, 64, 4),
+                                         (4103, 32, 8)])
 def test_q4_0_block_dot_rows(hip, oracle, dev, rows, nb, pad):
     n = nb * 32
     vx = synth.q4_0_matrix(rows, n, 1006, 0.02)
@@ -363,6 +365,7 @@ def test_q8_0_gemm_few_tokens(hip, oracle, dev, nr, nc, nb, ypad):
     (4096, 1, 128, 0, 0),     # decode: the register-direct GEMV
     (1023, 1, 260, 0, 0),     # decode, one pair per wave: 2 chunks + 4 blocks, ragged rows
     (1001, 1, 64, 0, 0),      # decode, n = 2048: two pairs per wave, one per half-wave
+    (1003, 1, 32, 0, 0),      # decode, n = 1024: four pairs per wave, one per lane group
     (77, 1, 6, 4, 0),         # decode, padded rows, output stride bs = 6
     (1, 1, 2, 0, 0),          # one output
     (1, 45, 1, 0, 0),         # single weight row, one block

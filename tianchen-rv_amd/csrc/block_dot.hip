@@ -313,24 +313,27 @@ __global__ __launch_bounds__(kDdWaves * 64) void block_dot_direct(size_t nb, flo
     s[(p0 + fr) * os] = sumf;
 }
 
-// Rows of exactly 64 blocks (n = 2048): two pairs per wave side by side, lanes
-// 0-31 on pair 0 and lanes 32-63 on pair 1, lane l owning blocks 2(l % 32),
-// 2(l % 32) + 1, so no lane idles (block_dot_direct would leave lanes 32-63
-// without a block).  DPP rows 0 and 1 fold the two pairs, 4 blocks per lane:
-// the same 64-step chain per pair, bit for bit.
-template <DotFmt F>
+// Rows of exactly 128 / kSplit blocks (n = 2048 for kSplit = 2, 1024 for 4):
+// kSplit pairs per wave side by side, lane group g = l / (64 / kSplit) on pair
+// g, lane l owning blocks 2(l % G), 2(l % G) + 1 (G lanes a group), so no lane
+// idles (block_dot_direct would leave all but the first group without a
+// block).  DPP row r folds pair r % kSplit (copies past kSplit are not
+// stored), 16 lanes: the same chain per pair, bit for bit.
+template <DotFmt F, int kSplit = 2>
 __global__ __launch_bounds__(kDdWaves * 64) void block_dot_half(float *s, size_t os,
                                                                  const uint8_t *vx, size_t bx,
                                                                  const uint8_t *vy, size_t by,
                                                                  size_t npairs) {
   constexpr int kXBytes = F == DotFmt::kQ8Q8 ? kQ8Bytes : kQ4Bytes;
-  constexpr int kNb = kChunkBlocks / 2;        // 64 blocks a row
-  constexpr int kTerms = kNb / kDdLanes;       // 4 blocks per fold lane
-  __shared__ __align__(16) float2 tl[kDdWaves][2][kNb + 8];
+  constexpr int kNb = kChunkBlocks / kSplit;   // blocks a row
+  constexpr int kGroup = 64 / kSplit;          // lanes a group
+  constexpr int kTerms = kNb / kDdLanes;       // blocks per fold lane
+  static_assert(kSplit == 2 || kSplit == 4, "one DPP row per pair");
+  __shared__ __align__(16) float2 tl[kDdWaves][kSplit][kNb + 8];
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int hw = l >> 5, b0 = 2 * (l & 31);
-  const size_t p0 = (static_cast<size_t>(blockIdx.x) * kDdWaves + w) * 2;
-  const int fr = (l >> 4) & 1, fp = l & (kDdLanes - 1);  // pair folded, lane in chain
+  const int hw = l / kGroup, b0 = 2 * (l % kGroup);
+  const size_t p0 = (static_cast<size_t>(blockIdx.x) * kDdWaves + w) * kSplit;
+  const int fr = (l >> 4) % kSplit, fp = l & (kDdLanes - 1);  // pair folded, lane in chain
   {
     const size_t p = min(p0 + hw, npairs - 1);  // pairs past npairs: computed, never stored
     uint32_t y0[8], y1[8], dy0, dy1;
@@ -360,7 +363,7 @@ __global__ __launch_bounds__(kDdWaves * 64) void block_dot_half(float *s, size_t
     ta[k] = v.x; tb[k] = v.y; ta[k + 1] = v.z; tb[k + 1] = v.w;
   }
   const float sumf = fold_chain<kDdLanes, kTerms>(ta, tb, 0.0f);
-  if (fp == kDdLanes - 1 && (l >> 4) < 2 && p0 + fr < npairs)
+  if (fp == kDdLanes - 1 && (l >> 4) < kSplit && p0 + fr < npairs)
     s[(p0 + fr) * os] = sumf;
 }
 
@@ -374,7 +377,9 @@ using tcrv::DotFmt;
 // shared by every pair), else two; rows of exactly 64 blocks two pairs per
 // wave, one per half-wave (the Q8_0 decode GEMV at n = 2048, us, against one
 // pair per wave: 4096 rows 3.72/4.83, 11008 rows 6.24/8.27, 2048 rows
-// 2.99/3.57; 16384 distinct row pairs 13.8/13.8).
+// 2.99/3.57; 16384 distinct row pairs 13.8/13.8), rows of 32 blocks four
+// (n = 1024: 4096 rows 2.74/4.35, 14336 rows 4.85/8.95; 16384 distinct row
+// pairs 7.86/10.05).
 template <DotFmt F>
 int launch_direct_pairs(size_t nb, float *s, size_t os, const uint8_t *vx, size_t bx,
                         const uint8_t *vy, size_t by, size_t npairs, hipStream_t st) {
@@ -388,6 +393,12 @@ int launch_direct_pairs(size_t nb, float *s, size_t os, const uint8_t *vx, size_
     const size_t per_half = static_cast<size_t>(tcrv::kDdWaves) * 2;
     tcrv::block_dot_half<F><<<dim3(static_cast<unsigned>((npairs + per_half - 1) / per_half)), b, 0,
                               st>>>(s, os, vx, bx, vy, by, npairs);
+    return launch_status();
+  }
+  if (nb == static_cast<size_t>(tcrv::kChunkBlocks / 4)) {
+    const size_t per_q = static_cast<size_t>(tcrv::kDdWaves) * 4;
+    tcrv::block_dot_half<F, 4><<<dim3(static_cast<unsigned>((npairs + per_q - 1) / per_q)), b, 0,
+                                 st>>>(s, os, vx, bx, vy, by, npairs);
     return launch_status();
   }
   if (shared)
