@@ -205,9 +205,10 @@ TCRV_HIP_API int tcrv_hip_gemv_q4_0_q8_0(size_t n, float *s, const uint8_t *vx, 
  * entry uses 2 for nr <= 2048 and 4 above, tcrv_hip_route_schedule lists the
  * candidates) sets how many
  * weight rows one wave of the register-direct kernel owns; the results are
- * bit-identical for every value.  Shapes served by the LDS-staged kernel (odd
- * n/32, rows not 4-byte aligned) ignore it.  Any other value returns
- * TCRV_HIP_ERR_BAD_SIZE. */
+ * bit-identical for every value.  For n = 2048 and 1024, 4 selects the
+ * lane-group kernels, whose waves own 4 or 8 rows by n and nr.  Shapes served
+ * by the LDS-staged kernel (odd n/32, rows not 4-byte aligned) ignore it.  Any
+ * other value returns TCRV_HIP_ERR_BAD_SIZE. */
 TCRV_HIP_API int tcrv_hip_gemv_q4_0_q8_0_shaped(size_t n, float *s, const uint8_t *vx, size_t bx,
                                                 const uint8_t *vy, size_t nr, int rows_per_wave,
                                                 void *stream);
