@@ -53,6 +53,7 @@ METRIC = "Q4_0 GEMV GB/s (% HBM peak); Q8_0 GEMM int8 TOPS (% MFMA peak)"
 GEMV_BYTES = N * (N // 32) * 18 + (N // 32) * 34 + N * 4        # 9 457 920
 ADD_BYTES = 12 * (1 << 24)                                      # 201 326 592
 DEQ_BYTES = (N * N // 32) * (34 + 128)                          # 84 934 656
+DEQ4_BYTES = (N * N // 32) * (18 + 128)                         # 76 546 048
 DOT_ROWS = 16384
 DOT_BYTES = DOT_ROWS * (2 * (N // 32) * 34 + 4)                 # 142 671 872
 GEMM_OPS = 2.0 * N * N * N                                      # 137 438 953 472
@@ -80,6 +81,8 @@ def inputs(name: str):
             "add_a": lambda: synth.uniform_f32(seeds["add_a"], 1 << 24),
             "add_b": lambda: synth.uniform_f32(seeds["add_b"], 1 << 24),
             "dequant_q": lambda: synth.quantize_q8_0(
+                synth.normal_f32(seeds["dequant_w"], N * N, 0.0, 0.02)),
+            "dequant_q4": lambda: synth.quantize_q4_0(
                 synth.normal_f32(seeds["dequant_w"], N * N, 0.0, 0.02)),
             "dot_x": lambda: synth.q8_0_matrix(DOT_ROWS, N, seeds["dot_x"], 1.0),
             "dot_y": lambda: synth.q8_0_matrix(DOT_ROWS, N, seeds["dot_y"], 1.0),
@@ -387,6 +390,26 @@ def bench_configs(torch, lib, stream, args):
                            "GB/s": round(DEQ_BYTES / us / 1e3, 1), "sets": sets}
     del Q, Y, reg
 
+    # the Q4_0 block dequant of the same N(0, 0.02) values quantized to Q4_0
+    # (d = max / -8): 18 B in and 128 B out per block
+    q4 = inputs("dequant_q4")
+    sets = copies_for(DEQ4_BYTES, 2)
+    Q = torch.empty((sets, q4.size), dtype=torch.uint8, device=dev)
+    Q[:] = torch.from_numpy(q4).to(dev)
+    Y = torch.empty((sets, nb * 32), device=dev)
+    fn = checked(lib.tcrv_hip_dequantize_row_q4_0, "dequant_q4")
+    ptrs = [(Q[i].data_ptr(), Y[i].data_ptr()) for i in range(sets)]
+    reg = Region(torch, stream, lambda i: fn(*ptrs[i % sets], N * N, sp), steps)
+    reg.run()
+    us = reg.run() * 1e3 / steps
+    same_as_eager(torch, stream, Y[(steps - 1) % sets],
+                  lambda o: fn(Q[(steps - 1) % sets].data_ptr(), o, N * N, sp), "dequant_q4")
+    out["dequant_q4_0"] = {"workload": "a3b Q4_0 dequant 4096x4096 (the configs[1] values "
+                                       "quantized to Q4_0)", "us": round(us, 3),
+                           "GB/s": round(DEQ4_BYTES / us / 1e3, 1), "sets": sets,
+                           "bytes_per_launch": DEQ4_BYTES}
+    del Q, Y, reg
+
     # block dot
     xq = inputs("dot_x")
     yq = inputs("dot_y")
@@ -633,9 +656,13 @@ def bench_configs(torch, lib, stream, args):
                                     "regions": 3}
     for k, v in out.items():
         if "GB/s" in v:
+            v["roofline"] = {"bound": "hbm", "achieved": v["GB/s"], "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(v["GB/s"] / HBM_PEAK_GBS, 4)}
             log(f"{k}: {v['us']:.1f} us, {v['GB/s']:.0f} GB/s "
                 f"({100 * v['GB/s'] / HBM_PEAK_GBS:.1f}% of HBM peak)")
         else:
+            v["roofline"] = {"bound": "mfma", "achieved": v["TOPS"], "peak": INT8_PEAK_TOPS,
+                             "unit": "TOPS", "frac": round(v["TOPS"] / INT8_PEAK_TOPS, 4)}
             log(f"{k}: {v['us']:.1f} us, {v['TOPS']:.0f} TOPS "
                 f"({100 * v['TOPS'] / INT8_PEAK_TOPS:.1f}% of dense int8 peak)")
     return out
@@ -801,6 +828,13 @@ def cpu_baseline_configs(seconds: float):
     out["dequant_q8_0"] = entry(
         DEQ_BYTES, "GB/s", "whole 4096x4096 dequants", lambda: ora.dequantize_row_q8_0(q, N * N),
         lambda: split_run(pool, [lambda i=i, j=j: ora.dequantize_row_q8_0(q[34 * i:34 * j],
+                                                                         32 * (j - i))
+                                 for i, j in slices(nbq, threads)]))
+    q4 = inputs("dequant_q4")
+    out["dequant_q4_0"] = entry(
+        DEQ4_BYTES, "GB/s", "whole 4096x4096 Q4_0 dequants",
+        lambda: ora.dequantize_row_q4_0(q4, N * N),
+        lambda: split_run(pool, [lambda i=i, j=j: ora.dequantize_row_q4_0(q4[18 * i:18 * j],
                                                                          32 * (j - i))
                                  for i, j in slices(nbq, threads)]))
     xq = inputs("dot_x")

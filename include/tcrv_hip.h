@@ -1,6 +1,6 @@
 /*
  * tcrv_hip.h -- C-ABI of libtcrv_hip.so, the MI355X (gfx950) runtime library
- * for the kernels TianChen-RV compiles: elementwise add, ggml Q8_0 dequant,
+ * for the kernels TianChen-RV compiles: elementwise add, ggml Q8_0/Q4_0 dequant,
  * the Q8_0.Q8_0 and Q4_0.Q8_0 block dots, and the quantized GEMV/GEMM.
  *
  * Every entry point keeps the parameter roles and order of the reference's
@@ -114,6 +114,16 @@ TCRV_HIP_API int tcrv_hip_add_i32(const int32_t *lhs, const int32_t *rhs, int32_
  * reference op; block layout RVVDialectWideningOps.cpp:3358-3372).
  * y[32b+j] = qs_b[j] * d_b for b < n/32.  y 4-byte aligned. */
 TCRV_HIP_API int tcrv_hip_dequantize_row_q8_0(const uint8_t *vx, float *y, size_t n, void *stream);
+
+/* ---- a3b: Q4_0 dequantize -------------------------------------------------
+ * ggml dequantize_row_q4_0(const block_q4_0 *x, float *y, int64_t k) (no
+ * reference op; block layout RVVOps.td:3893-3897, nibble decode the op's
+ * offset-binary (nibble - 8), RVVOps.td:3837-3842).  For b < n/32, j < 16:
+ *   y[32b+j]    = ((qs_b[j] & 15) - 8) * d_b
+ *   y[32b+16+j] = ((qs_b[j] >> 4) - 8) * d_b
+ * Bit-exact (a 4-bit integer times an fp16 value is exact in binary32).
+ * vx 2-byte aligned, y 4-byte aligned (16-byte aligned takes 128-bit stores). */
+TCRV_HIP_API int tcrv_hip_dequantize_row_q4_0(const uint8_t *vx, float *y, size_t n, void *stream);
 
 /* ---- a10: f32 -> Q8_0 activation quantizer --------------------------------
  * Replaces tcrv_emitc_..._quantize_row_q8_0(size_t n, const float *x,

@@ -159,6 +159,32 @@ void tcrv_oracle_dequantize_row_q8_0(size_t n, float *y, const uint8_t *vx) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* a3b: Q4_0 dequantize (ggml dequantize_row_q4_0).  Block layout: fp16 d @0, */
+/* 16 packed bytes @2, element j in the low nibble of qs[j] and element j+16 */
+/* in the high one (RVVOps.td:3893-3897).  The nibble decode is the op's     */
+/* offset-binary one (RVVOps.td:3837-3842; emitOffsetBinaryDecodeValue       */
+/* RVVToEmitC.cpp:2524-2561): v = w ^ 0x88, lo = (int8)(v << 4) >> 4,       */
+/* hi = (int8)v >> 4, i.e. nibble - 8.  A 4-bit integer times an fp16-valued */
+/* float is exact in binary32.                                               */
+/* ------------------------------------------------------------------------ */
+
+void tcrv_oracle_dequantize_row_q4_0(size_t n, float *y, const uint8_t *vx) {
+  size_t nb = n / TCRV_QK;
+  for (size_t b = 0; b < nb; ++b) {
+    const uint8_t *blk = vx + b * TCRV_Q4_0_BLOCK_BYTES;
+    float d = load_d(blk);
+    const uint8_t *qs = blk + 2;
+    for (size_t j = 0; j < TCRV_QK / 2; ++j) {
+      uint8_t v = (uint8_t)(qs[j] ^ 0x88u);
+      int8_t lo = (int8_t)((int8_t)(uint8_t)(v << 4) >> 4);
+      int8_t hi = (int8_t)((int8_t)v >> 4);
+      y[b * TCRV_QK + j] = (float)lo * d;
+      y[b * TCRV_QK + TCRV_QK / 2 + j] = (float)hi * d;
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------ */
 /* a4: packed-i4 offset-binary x i8 integer core (one Q4_0 block x one Q8_0  */
 /* block).  emitOffsetBinaryDecodeValue RVVToEmitC.cpp:2524-2561:            */
 /*   v = w ^ 0x88; lo = (int8)(v << 4) >> 4; hi = (int8)v >> 4;             */

@@ -55,6 +55,11 @@ int tcrv_oracle_binary(int kind, int elem, const void *lhs, const void *rhs, voi
 /* a3: y[32b+j] = qs_b[j] * fp16->f32(d_b) (ggml dequantize_row_q8_0). */
 void tcrv_oracle_dequantize_row_q8_0(size_t n, float *y, const uint8_t *vx);
 
+/* a3b: y[32b+j] = (lo nibble of qs_b[j] - 8) * d_b, y[32b+16+j] = (hi nibble
+ * of qs_b[j] - 8) * d_b for j < 16 (ggml dequantize_row_q4_0; the op's
+ * offset-binary decode, RVVOps.td:3837-3842). */
+void tcrv_oracle_dequantize_row_q4_0(size_t n, float *y, const uint8_t *vx);
+
 /* a4: the packed-i4 offset-binary x i8 integer core for one Q4_0 block against
  * one Q8_0 block (RVVToEmitC.cpp:2524-2589). */
 int32_t tcrv_oracle_q4_0_q8_0_block_sumi(const uint8_t *xb, const uint8_t *yb);

@@ -9,7 +9,8 @@ anchors: tests/test_golden.py checks that the oracle still reproduces them and
 re-derives their integer sums by brute force; the GPU tests check every kernel
 against them byte for byte.
 
-    python3 tests/golden/make_golden.py      (rewrites tests/golden/*.npz)
+    python3 tests/golden/make_golden.py            (rewrites tests/golden/*.npz)
+    python3 tests/golden/make_golden.py NAME ...   (rewrites only those fixtures)
 """
 import os
 import sys
@@ -43,6 +44,19 @@ def main():
     x[64:96] = 1e-30
     q = ora.quantize_q8_0(x)
     out["quant"] = dict(x=x, q=q, deq=ora.dequantize_row_q8_0(q, x.size))
+
+    # a3b: Q4_0 dequantize of 24 blocks: every weight byte value (blocks 0-15),
+    # special fp16 scales (+-0, subnormals, 65504, inf, NaN) on blocks 0-11, and
+    # 8 blocks quantized from seeded N(0, 0.02) values; n has a trailing partial
+    # block of 17 elements, which is dropped
+    w = synth.quantize_q4_0(synth.normal_f32(26, 24 * 32, 0.0, 0.02)).reshape(24, 18)
+    w[:16, 2:] = np.arange(256, dtype=np.uint8).reshape(16, 16)
+    special = np.array([0x0000, 0x8000, 0x0001, 0x83ff, 0x7bff, 0xfbff, 0x7c00, 0xfc00,
+                        0x7e00, 0x3c00, 0xbc00, 0x0400], dtype=np.uint16)
+    w[:12, 0:2] = special.view(np.uint8).reshape(12, 2)
+    w = w.reshape(-1)
+    n = 24 * 32 + 17
+    out["dequant_q4"] = dict(n=np.int64(n), q=w, deq=ora.dequantize_row_q4_0(w, n))
 
     # a5: 4 Q8_0 pairs at n = 128, with a -128 x -128 block
     n = 128
@@ -96,7 +110,10 @@ def main():
     out["repack_gemm"] = dict(n=np.int64(n), p4=p4, act=a8r, ax4=ax4,
                               s=ora.repack_gemm_q4_0(n, p4, ax4, 8, 32, 32))
 
+    only = set(sys.argv[1:])
     for name, arrays in out.items():
+        if only and name not in only:
+            continue
         path = os.path.join(HERE, f"{name}.npz")
         np.savez(path, **arrays)
         print(f"wrote {path} ({os.path.getsize(path)} bytes)")

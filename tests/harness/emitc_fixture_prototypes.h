@@ -49,4 +49,12 @@ extern "C" int tcrv_emitc_rvv_q4_0_q8_0_integer_core_kernel_rvv_q4_0_q8_0_intege
     const int8_t *w, const int8_t *qlo, const int8_t *qhi, const int32_t *acc, int32_t *out,
     size_t n, void *stream);
 
+// No fixture (the reference has no block-dequant op): ggml's
+// dequantize_row_q8_0 / dequantize_row_q4_0(const block *x, float *y, int64_t k)
+// in the boundary's (vx, y, n) form.
+extern "C" int tcrv_emitc_ggml_dequantize_row_q8_0_kernel_ggml_dequantize_row_q8_0(
+    const uint8_t *vx, float *y, size_t n, void *stream);
+extern "C" int tcrv_emitc_ggml_dequantize_row_q4_0_kernel_ggml_dequantize_row_q4_0(
+    const uint8_t *vx, float *y, size_t n, void *stream);
+
 #endif  // TCRV_EMITC_FIXTURE_PROTOTYPES_H_

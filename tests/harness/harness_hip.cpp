@@ -336,6 +336,35 @@ int exported_variants() {
     if (same("quantize", got, want, "97 blocks"))
       return 1;
   }
+  // both block dequants over 97 blocks of one row (finite scales)
+  {
+    const size_t nd = 97 * 32;
+    const std::vector<uint8_t> q8 = quantized_rows(1, nd, 2015, 0.7f, true);
+    const std::vector<uint8_t> q4 = quantized_rows(1, nd, 2016, 0.7f, false);
+    std::vector<float> got(nd), want(nd);
+    DeviceBuffer<uint8_t> d8(q8.size()), d4(q4.size());
+    DeviceBuffer<float> dy(nd);
+    if (!upload(d8, q8) || !upload(d4, q4) || !dy.p)
+      return fail("upload", -1);
+    EXPORTED_OK("q8_0 dequant",
+                tcrv_emitc_ggml_dequantize_row_q8_0_kernel_ggml_dequantize_row_q8_0(
+                    d8.p, dy.p, nd, nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    if (!download(got, dy))
+      return fail("download", -1);
+    tcrv_oracle_dequantize_row_q8_0(nd, want.data(), q8.data());
+    if (same("q8_0 dequant", got, want, "97 blocks"))
+      return 1;
+    EXPORTED_OK("q4_0 dequant",
+                tcrv_emitc_ggml_dequantize_row_q4_0_kernel_ggml_dequantize_row_q4_0(
+                    d4.p, dy.p, nd, nullptr));
+    HIP_OK(hipDeviceSynchronize());
+    if (!download(got, dy))
+      return fail("download", -1);
+    tcrv_oracle_dequantize_row_q4_0(nd, want.data(), q4.data());
+    if (same("q4_0 dequant", got, want, "97 blocks"))
+      return 1;
+  }
   // the integer core over 1003 bytes (the vector and the tail paths)
   {
     const size_t ni = 1003;

@@ -27,6 +27,7 @@ _SIGS = {
     "tcrv_oracle_add_i32": ([_p, _p, _p, _sz], None),
     "tcrv_oracle_binary": ([_int, _int, _p, _p, _p, _sz], _int),
     "tcrv_oracle_dequantize_row_q8_0": ([_sz, _p, _p], None),
+    "tcrv_oracle_dequantize_row_q4_0": ([_sz, _p, _p], None),
     "tcrv_oracle_q4_0_q8_0_block_sumi": ([_p, _p], _i32),
     "tcrv_oracle_q8_0_q8_0_block_sumi": ([_p, _p], _i32),
     "tcrv_oracle_packed_i4_offset_binary_x_i8_product_reduce": ([_p, _p, _p, _p, _p, _sz], None),
@@ -93,6 +94,11 @@ class Oracle:
     def dequantize_row_q8_0(self, vx: np.ndarray, n: int) -> np.ndarray:
         y = np.zeros((n // 32) * 32, dtype=np.float32)
         self.lib.tcrv_oracle_dequantize_row_q8_0(n, _a(y), _a(vx))
+        return y
+
+    def dequantize_row_q4_0(self, vx: np.ndarray, n: int) -> np.ndarray:
+        y = np.zeros((n // 32) * 32, dtype=np.float32)
+        self.lib.tcrv_oracle_dequantize_row_q4_0(n, _a(y), _a(vx))
         return y
 
     # -- a4/a5/a6 ----------------------------------------------------------

@@ -42,7 +42,7 @@ def generated(tmp_path_factory):
 def test_every_fixture_variant_is_exported_by_its_derived_name(generated):
     _, cpp, hdr = generated
     rows = manifest_variants()
-    assert len(rows) == 11
+    assert len(rows) == 13
     for op, kernel, variant, *_ in rows:
         name = f"tcrv_emitc_{kernel}_{variant}"
         assert re.search(r'extern "C" int ' + name + r"\(", cpp), name
@@ -62,7 +62,7 @@ def test_generated_unit_compiles_with_gxx(generated):
                     str(out / "x.o")], check=True)
     syms = subprocess.run(["nm", "--defined-only", str(out / "x.o")], capture_output=True,
                           text=True, check=True).stdout
-    assert sum(1 for ln in syms.splitlines() if " T tcrv_emitc_" in ln) == 11
+    assert sum(1 for ln in syms.splitlines() if " T tcrv_emitc_" in ln) == 13
 
 
 def test_generated_prototypes_match_the_fixtures(generated):

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-NAMES = ["add", "quant", "dot_q8", "dot_q4", "gemm_q8", "gemm_q4", "repack", "repack_gemm"]
+NAMES = ["add", "quant", "dequant_q4", "dot_q8", "dot_q4", "gemm_q8", "gemm_q4", "repack", "repack_gemm"]
 
 
 def load(name):
@@ -18,6 +18,14 @@ def load(name):
 
 def bits(a):
     return np.ascontiguousarray(a).view(np.uint8)
+
+
+def same_f32_nan_as_nan(got, want):
+    """Bit-equal, except that a NaN matches any NaN (a NaN's sign and payload
+    are the arithmetic unit's, e.g. 0 * inf gives x86's negative default NaN)."""
+    nan = np.isnan(want)
+    return (np.array_equal(np.isnan(got), nan)
+            and np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)))
 
 
 def test_fixtures_present():
@@ -32,6 +40,8 @@ def test_oracle_reproduces_fixtures(oracle):
     g = load("quant")
     assert np.array_equal(oracle.quantize_q8_0(g["x"]), g["q"])
     assert np.array_equal(bits(oracle.dequantize_row_q8_0(g["q"], g["x"].size)), bits(g["deq"]))
+    g = load("dequant_q4")
+    assert np.array_equal(bits(oracle.dequantize_row_q4_0(g["q"], int(g["n"]))), bits(g["deq"]))
     for name, f in (("dot_q8", oracle.vec_dot_q8_0_rows), ("dot_q4", oracle.vec_dot_q4_0_rows)):
         g = load(name)
         n, vx, vy = int(g["n"]), g["vx"], g["vy"]
@@ -58,6 +68,21 @@ def test_oracle_reproduces_fixtures(oracle):
     assert np.array_equal(oracle.pack_q8_0x4(a, 8, n // 32, a.shape[1]), g["ax4"])
     assert np.array_equal(bits(oracle.repack_gemm_q4_0(n, g["p4"], g["ax4"], 8, 32, 32)),
                           bits(g["s"]))
+
+
+def test_fixture_dequant_q4_closed_form():
+    # (nibble - 8) * d by numpy, element j the low nibble of byte j and
+    # element 16 + j its high nibble; the trailing partial block is dropped
+    g = load("dequant_q4")
+    b = g["q"].reshape(-1, 18)
+    assert g["deq"].size == (int(g["n"]) // 32) * 32 == b.shape[0] * 32
+    d = b[:, 0:2].copy().view(np.float16).reshape(-1).astype(np.float32)
+    qs = b[:, 2:].astype(np.int64)
+    vals = np.concatenate([(qs & 15) - 8, (qs >> 4) - 8], axis=1).astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        want = (vals * d[:, None]).reshape(-1)
+    assert same_f32_nan_as_nan(g["deq"], want)
+    assert np.isnan(g["deq"]).any() and np.isinf(g["deq"]).any()
 
 
 def test_fixture_block_sums_brute_force():
@@ -93,6 +118,11 @@ def test_kernels_reproduce_fixtures(hip, dev):
     y = empty_dev(g["x"].size, torch.float32, dev)
     hip.dequantize_row_q8_0(to_dev(g["q"], dev), y, g["x"].size)
     assert np.array_equal(bits(from_dev(y)), bits(g["deq"]))
+
+    g = load("dequant_q4")
+    y = empty_dev(g["deq"].size, torch.float32, dev)
+    hip.dequantize_row_q4_0(to_dev(g["q"], dev), y, int(g["n"]))
+    assert same_f32_nan_as_nan(from_dev(y), g["deq"])
 
     for name, f in (("dot_q8", hip.q8_0_q8_0_block_dot_rows),
                     ("dot_q4", hip.q4_0_q8_0_block_dot_rows)):

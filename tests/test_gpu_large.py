@@ -63,6 +63,29 @@ def test_dequantize_beyond_2_pow_32(hip, dev):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+def test_dequantize_q4_0_beyond_2_pow_32(hip, dev):
+    nb = BIG // 32 + 1  # 134217761 blocks: 2.42 GB in, 17.2 GB out
+    n = nb * 32
+    vx = torch.randint(0, 256, (nb, 18), dtype=torch.uint8, device=dev)
+    sc = torch.randint(0, 1 << 16, (nb,), dtype=torch.int32, device=dev)
+    exp = (torch.remainder(sc >> 10, 30) + 1) << 10
+    half = ((sc & 0x83FF) | exp).to(torch.int32)
+    vx[:, 0] = (half & 0xFF).to(torch.uint8)
+    vx[:, 1] = ((half >> 8) & 0xFF).to(torch.uint8)
+    y = torch.empty(n, dtype=torch.float32, device=dev)
+    hip.dequantize_row_q4_0(vx, y, n)
+    blocks = np.unique(np.concatenate([sample_indices(nb, 2048, 2), [nb - 1]]))
+    bi = torch.from_numpy(blocks).to(dev)
+    raw = vx[bi].cpu().numpy()
+    got = y.view(nb, 32)[bi].cpu().numpy()
+    del vx, y, sc, exp, half
+    free()
+    d = raw[:, :2].copy().view(np.float16).astype(np.float32)
+    qs = raw[:, 2:].astype(np.int64)
+    vals = np.concatenate([(qs & 15) - 8, (qs >> 4) - 8], axis=1).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), (vals * d).view(np.uint32))
+
+
 def test_q8_0_block_dot_rows_operands_over_2_gib(hip, oracle, dev):
     rows, nb = 520000, 128  # 2.26 GB per operand
     n = nb * 32

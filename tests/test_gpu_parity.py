@@ -6,7 +6,7 @@ import pytest
 import torch
 
 import synth
-from gpu_util import assert_f32_parity, empty_dev, from_dev, q4_tiles_gemm, to_dev
+from gpu_util import assert_f32_parity, assert_f32_parity_nan, empty_dev, from_dev, q4_tiles_gemm, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -63,6 +63,48 @@ def test_dequant_q8_0(hip, oracle, dev, nb):
     y = empty_dev(n, torch.float32, dev)
     hip.dequantize_row_q8_0(to_dev(vx, dev), y, n)
     assert_f32_parity(from_dev(y), oracle.dequantize_row_q8_0(vx, n), what=f"dequant nb={nb}")
+
+
+# -------------------------------------------------------------- a3b dequant ---
+
+@pytest.mark.parametrize("nb", [1, 7, 63, 64, 65, 129, 4096 * 4096 // 32])
+def test_dequant_q4_0(hip, oracle, dev, nb):
+    # 4096^2 is the config-2 shape with Q4_0 weights (N(0, 0.02), d = max / -8)
+    n = nb * 32
+    vx = synth.quantize_q4_0(synth.normal_f32(1003, n, 0.0, 0.02))
+    y = empty_dev(n, torch.float32, dev)
+    hip.dequantize_row_q4_0(to_dev(vx, dev), y, n)
+    assert_f32_parity(from_dev(y), oracle.dequantize_row_q4_0(vx, n), what=f"dequant q4 nb={nb}")
+
+
+def test_dequant_q4_0_edges(hip, oracle, dev):
+    # every weight byte value, special fp16 scales (+-0, subnormals, 65504,
+    # +-inf, quiet and signalling NaN), a trailing partial block (dropped, its
+    # outputs untouched), a source 2 bytes past a 16-byte boundary and an output
+    # only 4-byte aligned (scalar stores), across work-group edges
+    nb = 64 * 3 + 5
+    w = synth.quantize_q4_0(synth.normal_f32(41, nb * 32, 0.0, 0.02)).reshape(nb, 18)
+    w[:16, 2:] = np.arange(256, dtype=np.uint8).reshape(16, 16)
+    special = np.array([0x0000, 0x8000, 0x0001, 0x8001, 0x03ff, 0x7bff, 0xfbff, 0x7c00, 0xfc00,
+                        0x7e00, 0x7d01, 0xfe00], dtype=np.uint16)
+    w[:special.size, 0:2] = special.view(np.uint8).reshape(-1, 2)
+    w[70:70 + special.size, 0:2] = special.view(np.uint8).reshape(-1, 2)
+    w = w.reshape(-1)
+    n = nb * 32 + 31  # 31 trailing elements: no 198th block is read
+    want = oracle.dequantize_row_q4_0(w, n)
+    for src_off, dst_off in ((0, 0), (2, 0), (0, 1), (2, 1), (6, 3)):
+        buf = empty_dev(w.size + 16, torch.uint8, dev)
+        buf[src_off:src_off + w.size] = to_dev(w, dev)
+        y = torch.full((nb * 32 + 64,), 1234.5, dtype=torch.float32, device=dev)
+        hip.dequantize_row_q4_0(buf[src_off:src_off + w.size], y[dst_off:], n)
+        got = from_dev(y)
+        assert_f32_parity_nan(got[dst_off:dst_off + nb * 32], want,
+                              what=f"dequant q4 src+{src_off} dst+{4 * dst_off}")
+        assert np.all(got[:dst_off] == 1234.5) and np.all(got[dst_off + nb * 32:] == 1234.5)
+    # n < 32: nothing to do, nothing written
+    y = torch.full((32,), 7.0, dtype=torch.float32, device=dev)
+    hip.dequantize_row_q4_0(to_dev(w, dev), y, 31)
+    assert np.all(from_dev(y) == 7.0)
 
 
 # -------------------------------------------------------------- a10 quantize ---

@@ -27,7 +27,7 @@ def test_harness_runs_on_the_gpu():
     lines = r.stdout.splitlines()
     assert "add proof ok: 1031 elements checked (exported add)" in lines
     exported = [ln for ln in lines if ln.startswith("exported ")]
-    assert len(exported) == 10 and all("bit-identical to the oracle" in ln for ln in exported)
+    assert len(exported) == 12 and all("bit-identical to the oracle" in ln for ln in exported)
     assert sum(1 for ln in lines if ln.startswith("route ")) == 12
-    assert sum(1 for ln in lines if "bit-identical to the oracle" in ln) == 15
+    assert sum(1 for ln in lines if "bit-identical to the oracle" in ln) == 17
     assert lines[-1] == "harness ok"

@@ -55,6 +55,9 @@ def test_loads_and_reports_version_without_gpu():
     ("tcrv_hip_add_f32", (2, 16, 32, 8, 0), tcrv_hip.ERR_MISALIGNED),
     ("tcrv_hip_dequantize_row_q8_0", (257, 256, 64, 0), tcrv_hip.ERR_MISALIGNED),
     ("tcrv_hip_dequantize_row_q8_0", (256, 258, 64, 0), tcrv_hip.ERR_MISALIGNED),
+    ("tcrv_hip_dequantize_row_q4_0", (257, 256, 64, 0), tcrv_hip.ERR_MISALIGNED),
+    ("tcrv_hip_dequantize_row_q4_0", (256, 258, 64, 0), tcrv_hip.ERR_MISALIGNED),
+    ("tcrv_hip_dequantize_row_q4_0", (0, 256, 64, 0), tcrv_hip.ERR_NULL_POINTER),
     ("tcrv_hip_q8_0_q8_0_gemm", (64, 256, 257, 512, 80, 2, 2, 80, 2, 0), tcrv_hip.ERR_MISALIGNED),
     ("tcrv_hip_q8_0_q8_0_gemm", (64, 256, 256, 512, 81, 2, 2, 80, 2, 0), tcrv_hip.ERR_MISALIGNED),
     ("tcrv_hip_q8_0_q8_0_block_dot_rows", (64, 256, 256, 69, 512, 68, 2, 0),

@@ -125,6 +125,101 @@ def test_dequant_closed_form(oracle):
     assert not np.any(y[:32])
 
 
+# ------------------------------------------------------------------- a3b ---
+
+Q4_SPECIAL_D = np.array([0x0000, 0x8000, 0x0001, 0x8001, 0x03ff, 0x7bff, 0xfbff, 0x3c00,
+                         0xbc00, 0x7c00, 0xfc00, 0x7e00, 0x2e66], dtype=np.uint16)
+
+
+def q4_dequant_numpy(blocks):
+    """Independent statement of ggml's dequantize_row_q4_0: element j is the low
+    nibble of byte j minus 8, element j + 16 the high nibble minus 8, times d."""
+    d, vals = q4_fields(blocks)
+    with np.errstate(invalid="ignore"):  # 0 * inf
+        return (vals.astype(np.float32) * d[:, None]).reshape(-1)
+
+
+def same_bits_or_nan(got, want):
+    nan = np.isnan(want)
+    return (np.array_equal(np.isnan(got), nan)
+            and np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32)))
+
+
+def test_dequant_q4_0_every_byte_and_special_scales(oracle):
+    # all 256 weight bytes (16 blocks of 16) under each special fp16 scale:
+    # +-0, +-smallest subnormal, largest subnormal, +-65504, +-1, +-inf, NaN, 0.1
+    qs = np.arange(256, dtype=np.uint8).reshape(16, 16)
+    for h in Q4_SPECIAL_D:
+        blocks = np.zeros((16, 18), dtype=np.uint8)
+        blocks[:, 0:2] = np.array([h], dtype=np.uint16).view(np.uint8)
+        blocks[:, 2:] = qs
+        y = oracle.dequantize_row_q4_0(blocks.reshape(-1), 16 * 32)
+        d = np.float32(np.array([h], dtype=np.uint16).view(np.float16)[0])
+        # closed form per element: (nibble - 8) * d, nibble table from the byte
+        lo = (qs.astype(np.int64) & 15) - 8
+        hi = (qs.astype(np.int64) >> 4) - 8
+        with np.errstate(invalid="ignore"):
+            want = np.concatenate([lo, hi], axis=1).astype(np.float32) * d
+        assert same_bits_or_nan(y, want.reshape(-1)), hex(h)
+        assert same_bits_or_nan(y, q4_dequant_numpy(blocks.reshape(-1))), hex(h)
+    # the offset-binary table itself: 0 -> -8, 8 -> 0, 15 -> +7 (RVVOps.td:3837-3838)
+    one = np.zeros(18, dtype=np.uint8)
+    one[0:2] = np.array([0x3c00], dtype=np.uint16).view(np.uint8)
+    one[2:5] = [0x80, 0x08, 0xF0]
+    y = oracle.dequantize_row_q4_0(one, 32)
+    assert list(y[:3]) == [-8.0, 0.0, -8.0] and list(y[16:19]) == [0.0, -8.0, 7.0]
+
+
+def test_dequant_q4_0_planted_mistakes_fail(oracle):
+    # a plausible mistake in the element order or decode changes the output:
+    # interleaved order (lo, hi of byte 0, then byte 1, ...), halves swapped,
+    # nibbles without the -8 offset, the Q8_0 two's-complement reading
+    blocks = rand_q4_blocks(64)
+    y = oracle.dequantize_row_q4_0(blocks, 64 * 32)
+    d, vals = q4_fields(blocks)
+    interleaved = np.stack([vals[:, :16], vals[:, 16:]], axis=2).reshape(64, 32)
+    swapped = np.concatenate([vals[:, 16:], vals[:, :16]], axis=1)
+    unbiased = vals + 8
+    raw = vals + 8  # the nibbles 0..15
+    twos = np.where(raw < 8, raw, raw - 16)  # sign-extended without the 0x88 bias
+    for wrong in (interleaved, swapped, unbiased, twos):
+        assert not np.array_equal(y, (wrong.astype(np.float32) * d[:, None]).reshape(-1))
+    assert np.array_equal(y.view(np.uint32), q4_dequant_numpy(blocks).view(np.uint32))
+
+
+def test_dequant_q4_0_matches_block_dot_integer_core(oracle):
+    # The op pairs the low nibble of byte j with activation quant j and the high
+    # nibble with quant 16 + j (RVVOps.td:3841-3842).  With d = 1 the dequant's
+    # values are the decoded integers, so their dot with a Q8_0 block's quants
+    # must equal the integer core's block sum (pinned separately by brute force).
+    rng = np.random.default_rng(31)
+    xb = rand_q4_blocks(40, rng)
+    x = xb.reshape(-1, 18)
+    x[:, 0:2] = np.array([0x3c00], dtype=np.uint16).view(np.uint8)
+    yb = rand_q8_blocks(40, rng).reshape(-1, 34)
+    vals = oracle.dequantize_row_q4_0(xb, 40 * 32).reshape(40, 32).astype(np.int64)
+    for k in range(40):
+        want = int(np.dot(vals[k], yb[k, 2:].view(np.int8).astype(np.int64)))
+        assert oracle.q4_block_sumi(x[k].copy(), yb[k].copy()) == want
+
+
+def test_dequant_q4_0_round_trip_and_partial_block(oracle):
+    # dequant(quantize_q4_0(x)) stays within |d| (+ the fp16 rounding of d times
+    # 8) of x: an element at -8/+7.5..8 steps of d saturates to 15 (7 d) at most
+    # one step away, every other element rounds to the nearest step
+    x = synth.normal_f32(77, 64 * 32, 0.0, 0.02)
+    q = oracle.quantize_q4_0(x)
+    y = oracle.dequantize_row_q4_0(q, x.size + 17)  # the trailing 17 elements are dropped
+    assert y.size == x.size
+    xb = x.reshape(-1, 32)
+    amax_idx = np.argmax(np.abs(xb), axis=1)
+    d32 = xb[np.arange(xb.shape[0]), amax_idx] / -8.0
+    d16 = q.reshape(-1, 18)[:, 0:2].copy().view(np.float16).reshape(-1).astype(np.float32)
+    err = np.abs(y.reshape(-1, 32) - xb)
+    bound = np.abs(d32)[:, None] * (1 + 1e-6) + 8 * np.abs(d16 - d32)[:, None]
+    assert np.all(err <= bound)
+
+
 # -------------------------------------------------------------------- a4 ---
 
 def test_q4_integer_core_exhaustive_weight_bytes(oracle):

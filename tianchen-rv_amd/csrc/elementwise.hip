@@ -1,6 +1,7 @@
 // elementwise.hip -- the HBM-streaming kernels of libtcrv_hip:
 //   a1  add_f32                (tcrv_rvv.binary{kind="add"})
 //   a3  dequantize_row_q8_0    (ggml block dequant)
+//   a3b dequantize_row_q4_0    (ggml block dequant)
 //   a10 quantize_row_q8_0      (tcrv_rvv.quantize_row_q8_0)
 // plus the library's status/version/synchronize entry points.
 #include "tcrv_hip_internal.h"
@@ -134,6 +135,56 @@ __global__ __launch_bounds__(kDqThreads) void dequantize_q8_0(const uint8_t *vx,
       d1[1] = r.y;
       d1[2] = r.z;
       d1[3] = r.w;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// a3b: y[32b+j] = (lo(qs_b[j]) - 8) * d_b, y[32b+16+j] = (hi(qs_b[j]) - 8) * d_b
+// (ggml dequantize_row_q4_0; the offset-binary nibble decode of RVVOps.td:
+// 3837-3842, layout :3893-3897).  The same shape as the Q8_0 kernel: a
+// work-group stages kDq4Blocks contiguous 18-byte blocks (64*18 = 1152 bytes,
+// a 16-byte multiple) through LDS with 128-bit loads, and each thread writes one
+// float4 of the output: lanes 8b..8b+3 the low nibbles of block b's bytes
+// 0-15, lanes 8b+4..8b+7 the high ones.  (n - 8) is exact in binary32 and a
+// 4-bit integer times an fp16-valued float is exact, so the result is
+// bit-exact.
+// ---------------------------------------------------------------------------
+constexpr int kDq4Threads = 512;
+constexpr int kDq4Blocks = kDq4Threads / 8;
+
+template <bool kVecOut>
+__global__ __launch_bounds__(kDq4Threads) void dequantize_q4_0(const uint8_t *vx, float *y,
+                                                               size_t nb) {
+  __shared__ __align__(16) uint8_t lds[kDq4Blocks * kQ4Bytes];
+  const size_t blk0 = static_cast<size_t>(blockIdx.x) * kDq4Blocks;
+  const int nblk = static_cast<int>(min(static_cast<size_t>(kDq4Blocks), nb - blk0));
+  copy_span_to_lds(lds, vx + blk0 * kQ4Bytes, nblk * kQ4Bytes, threadIdx.x, kDq4Threads);
+  __syncthreads();
+  const int nf4 = nblk * (kQK / 4);
+  for (int f = threadIdx.x; f < nf4; f += kDq4Threads) {
+    const int b = f >> 3;
+    const int part = f & 7;
+    const uint16_t *l16 = reinterpret_cast<const uint16_t *>(lds) + b * (kQ4Bytes / 2);
+    const float d = fp16_bits_to_f32(l16[0]);
+    const int j = (part & 3) * 4;  // first of the four packed bytes this lane decodes
+    const uint32_t u = static_cast<uint32_t>(l16[1 + (j >> 1)]) |
+                       (static_cast<uint32_t>(l16[2 + (j >> 1)]) << 16);
+    const uint32_t nib = (part < 4 ? u : u >> 4) & 0x0F0F0F0Fu;
+    float4 r;
+    r.x = (static_cast<float>(nib & 0xffu) - 8.0f) * d;
+    r.y = (static_cast<float>((nib >> 8) & 0xffu) - 8.0f) * d;
+    r.z = (static_cast<float>((nib >> 16) & 0xffu) - 8.0f) * d;
+    r.w = (static_cast<float>(nib >> 24) - 8.0f) * d;
+    // output element of this lane's r.x: 32b + j (low) or 32b + 16 + j (high)
+    const size_t e = (blk0 + b) * kQK + (part < 4 ? 0 : kQK / 2) + j;
+    if constexpr (kVecOut) {
+      store_stream(r, reinterpret_cast<float4 *>(y + e));
+    } else {
+      y[e] = r.x;
+      y[e + 1] = r.y;
+      y[e + 2] = r.z;
+      y[e + 3] = r.w;
     }
   }
 }
@@ -310,6 +361,27 @@ int tcrv_hip_dequantize_row_q8_0(const uint8_t *vx, float *y, size_t n, void *st
                             as_stream(stream)>>>(vx, y, nb);
   else
     dequantize_q8_0<false><<<dim3(static_cast<unsigned>(grid)), dim3(kDqThreads), 0,
+                             as_stream(stream)>>>(vx, y, nb);
+  return launch_status();
+}
+
+int tcrv_hip_dequantize_row_q4_0(const uint8_t *vx, float *y, size_t n, void *stream) {
+  using namespace tcrv_host;
+  const size_t nb = n / kQK;
+  if (nb == 0)
+    return TCRV_HIP_OK;
+  if (!vx || !y)
+    return TCRV_HIP_ERR_NULL_POINTER;
+  if (!aligned2(vx) || !aligned4(y))
+    return TCRV_HIP_ERR_MISALIGNED;
+  const size_t grid = (nb + kDq4Blocks - 1) / kDq4Blocks;
+  if (grid > 0x7fffffffu)
+    return TCRV_HIP_ERR_TOO_LARGE;
+  if (aligned16(y))
+    dequantize_q4_0<true><<<dim3(static_cast<unsigned>(grid)), dim3(kDq4Threads), 0,
+                            as_stream(stream)>>>(vx, y, nb);
+  else
+    dequantize_q4_0<false><<<dim3(static_cast<unsigned>(grid)), dim3(kDq4Threads), 0,
                              as_stream(stream)>>>(vx, y, nb);
   return launch_status();
 }

@@ -121,7 +121,10 @@ struct HipKernelRoute {
 //   pack:           rvv-to-emitc-pack-q4-0-to-q4-0x16.mlir:19-21
 //   quantize:       rvv-to-emitc-ggml-quantize-row-q8-0.mlir
 // The Q8_0 GEMM has no reference op; it takes the q4_0 GEMM's ABI with Q8_0
-// weights.  A row is found by its exact op identity (the op name); nothing is
+// weights.  Nor do the block dequants (tcrv_rvv.dequantize, RVVOps.td:
+// 8601-8632, is i32 -> f32 with one scale): their rows are keyed by the ggml
+// function they restate (ggml.dequantize_row_q8_0 / _q4_0) and take its
+// parameters (x, y, k) as (vx, y, n).  A row is found by its exact op identity (the op name); nothing is
 // read from a name beyond that.
 constexpr const char *kN = "runtime-element-count";
 constexpr const char *kOut = "output-buffer";
@@ -192,6 +195,12 @@ const HipKernelRoute kHipKernelRoutes[] = {
      9},
     {"tcrv_rvv.quantize_row_q8_0", "tcrv_hip_quantize_row_q8_0",
      {{"n", "size_t", kN}, {"x", "const float *", kLhs}, {"vy", "uint8_t *", kOut}},
+     3},
+    {"ggml.dequantize_row_q8_0", "tcrv_hip_dequantize_row_q8_0",
+     {{"vx", "const uint8_t *", kLhs}, {"y", "float *", kOut}, {"n", "size_t", kN}},
+     3},
+    {"ggml.dequantize_row_q4_0", "tcrv_hip_dequantize_row_q4_0",
+     {{"vx", "const uint8_t *", kLhs}, {"y", "float *", kOut}, {"n", "size_t", kN}},
      3},
 };
 constexpr size_t kNumRoutes = std::size(kHipKernelRoutes);

@@ -56,6 +56,7 @@ SIGNATURES = {
     "tcrv_hip_add_i32": [_p, _p, _p, _sz, _p],
     "tcrv_hip_binary": [_int, _int, _p, _p, _p, _sz, _p],
     "tcrv_hip_dequantize_row_q8_0": [_p, _p, _sz, _p],
+    "tcrv_hip_dequantize_row_q4_0": [_p, _p, _sz, _p],
     "tcrv_hip_quantize_row_q8_0": [_sz, _p, _p, _p],
     "tcrv_hip_q8_0_q8_0_block_dot": [_sz, _p, _p, _p, _p],
     "tcrv_hip_q8_0_q8_0_block_dot_rows": [_sz, _p, _p, _sz, _p, _sz, _sz, _p],
@@ -197,6 +198,10 @@ def binary(kind: int, elem: str, lhs, rhs, out, n: Optional[int] = None, stream=
 
 def dequantize_row_q8_0(vx, y, n: int, stream=None):
     return call("tcrv_hip_dequantize_row_q8_0", vx, y, n, _stream(stream))
+
+
+def dequantize_row_q4_0(vx, y, n: int, stream=None):
+    return call("tcrv_hip_dequantize_row_q4_0", vx, y, n, _stream(stream))
 
 
 def quantize_row_q8_0(n: int, x, vy, stream=None):
