@@ -42,7 +42,9 @@ constexpr int kDStages = 2;  // chunks c+1 .. c+kDStages-1 in flight while chunk
                              // folded (2 or 3)
 constexpr int kDSlots = (kDDma + 15) / 16;   // DMA instructions per wave and chunk
 static_assert(kDStages == 2 || kDStages == 3, "prefetch distance 1 or 2");
-static_assert(kDStages * (kDKB * 12288 + kDKB * (kDBM + kDBN + 32) * 2) <= 160 * 1024,
+// the Q4_0 kernel also keeps its token scales widened to fp32: kDBN per block
+static_assert(kDStages * (kDKB * 12288 + kDKB * (kDBM + kDBN + 32) * 2 + kDKB * kDBN * 4) <=
+                  160 * 1024,
               "the stages fit the 160 KB of LDS");
 
 // ---------------------------------------------------------------- pack ---
@@ -402,8 +404,10 @@ __device__ __forceinline__ int dma_chunk(const DmaSlots &d, size_t c, int nbc, i
 // every wave's DMA of the older chunks is visible and no wave still reads the
 // stage the next DMA overwrites.  s_waitcnt takes an immediate, hence the
 // switch (gfx9 encoding: vmcnt in bits 3:0, expcnt 6:4 = 7 (no wait), lgkmcnt
-// 11:8 = 0).
-__device__ __forceinline__ void wait_dma_barrier(int pending) {
+// 11:8 = 0).  `before_barrier` runs between the wait and the barrier (what it
+// writes to LDS is complete before the barrier: its lgkmcnt is waited too).
+template <typename BeforeBarrier>
+__device__ __forceinline__ void wait_dma_barrier(int pending, BeforeBarrier &&before_barrier) {
   switch (__builtin_amdgcn_readfirstlane(pending)) {  // the same in every lane
   case 0: __builtin_amdgcn_s_waitcnt(0x070); break;
   case 1: __builtin_amdgcn_s_waitcnt(0x071); break;
@@ -414,7 +418,34 @@ __device__ __forceinline__ void wait_dma_barrier(int pending) {
   case 6: __builtin_amdgcn_s_waitcnt(0x076); break;
   default: __builtin_amdgcn_s_waitcnt(0x077); break;
   }
+  before_barrier();
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): its LDS writes are done
   __builtin_amdgcn_s_barrier();
+}
+
+__device__ __forceinline__ void wait_dma_barrier(int pending) {
+  wait_dma_barrier(pending, [] {});
+}
+
+// The Q4_0 fold reads d_y as fp32 (mfma_fold.h, q4_fold).  The wave whose DMA
+// slot brings block b's scales (slot kDQuantDma + b of the chunk, wave
+// (kDQuantDma + b) % 16) widens that block's kDBN token scales once its own
+// loads have landed -- the vmcnt wait alone orders them for the wave itself --
+// into the fp32 row `fy` of the chunk's stage, before the barrier that
+// publishes the chunk; two scales per lane.  dsh_st: the stage's fp16 scales.
+__device__ __forceinline__ void widen_token_scales(const uint16_t *dsh_st, float *fy_st,
+                                                   int nbc, int wave, int lane) {
+#pragma unroll
+  for (int b = 0; b < kDKB; ++b) {
+    if ((kDQuantDma + b) % 16 == wave && b < nbc) {
+#pragma unroll
+      for (int k = 0; k < kDBN / 64; ++k) {
+        const int t = lane + 64 * k;
+        fy_st[b * kDBN + t] =
+            static_cast<float>(__builtin_bit_cast(_Float16, dsh_st[b * kDHRow + kDBM + t]));
+      }
+    }
+  }
 }
 
 // Work-group: 256 weight rows x 128 tokens, 16 waves, each wave two 32x32
@@ -428,7 +459,7 @@ __device__ __forceinline__ void wait_dma_barrier(int pending) {
 template <bool kPipe, bool kQ4>
 __device__ __forceinline__ void gemm_tiles_body(size_t nb, float *s, const uint8_t *tx,
                                                 const uint8_t *ty, size_t nr, size_t nc,
-                                                size_t bs, int8_t *qs, uint16_t *dsh) {
+                                                size_t bs, int8_t *qs, uint16_t *dsh, float *fyd) {
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -460,9 +491,20 @@ __device__ __forceinline__ void gemm_tiles_body(size_t nb, float *s, const uint8
   DmaSlots slots;
   dma_slots(slots, qs, dsh, tx, ty, gx0, ngx, gy0, ngy, nb, wave, lane);
   constexpr int kAhead = kDStages - 1;  // chunks in flight beyond the one folded
+  constexpr int kHStage = kDKB * kDHRow;
+  constexpr int kFyStage = kDKB * kDBN;
+  // what runs between a chunk's DMA wait and the barrier that publishes it:
+  // the Q4_0 fold's fp32 token scales of chunk cc (in stage sc)
+  auto publish = [&](size_t cc, int sc) {
+    if constexpr (kQ4) {
+      if (cc < nchunks)
+        widen_token_scales(dsh + sc * kHStage, fyd + sc * kFyStage, blocks_of(cc), wave, lane);
+    }
+  };
   dma_chunk(slots, 0, blocks_of(0), 0, wave, lane);
   int pending = kAhead > 1 && nchunks > 1 ? dma_chunk(slots, 1, blocks_of(1), 1, wave, lane) : 0;
-  wait_dma_barrier(pending);  // chunk 0 is in LDS, the zero rows written
+  // chunk 0 is in LDS, the zero rows written
+  wait_dma_barrier(pending, [&] { publish(0, 0); });
 
   // this lane's operands in stage 0, block 0, for the wave's first tile
   const int8_t *qa0 = qs + (h * kDRows + wm * 64 + li) * 16;
@@ -470,12 +512,11 @@ __device__ __forceinline__ void gemm_tiles_body(size_t nb, float *s, const uint8
   const uint16_t *hx0 = dsh + (h ? kDRows + li : wm * 64 + li);
   const uint16_t *hx1 = dsh + (h ? kDRows + li : wm * 64 + 32 + li);
   const uint16_t *hy = dsh + (h ? kDRows + li : kDBM + wn * 32 + li);
-  constexpr int kHStage = kDKB * kDHRow;
 
   // the Q4_0 fold (transposed tiles): d_x of the lane's weight row of tile 0,
-  // d_y of its tokens 4h.. (4 of every 8)
+  // the fp32 d_y of its tokens 4h.. (4 of every 8)
   const uint16_t *qx = dsh + wm * 64 + li;
-  const uint16_t *qy = dsh + kDBM + wn * 32 + 4 * h;
+  const float *qy = fyd + wn * 32 + 4 * h;
 
   int st = 0;  // stage of chunk c
   size_t c = 0;
@@ -488,8 +529,9 @@ __device__ __forceinline__ void gemm_tiles_body(size_t nb, float *s, const uint8
                   ? dma_chunk(slots, c + kAhead, blocks_of(c + kAhead), sta, wave, lane)
                   : 0;
     fold();
-    wait_dma_barrier(kAhead > 1 ? pending : 0);
-    st = st + 1 == kDStages ? 0 : st + 1;
+    const int stn = st + 1 == kDStages ? 0 : st + 1;
+    wait_dma_barrier(kAhead > 1 ? pending : 0, [&] { publish(c + 1, stn); });
+    st = stn;
   };
   const int nbc = static_cast<int>(nb - nfull * kDKB);
   if constexpr (kQ4) {
@@ -499,20 +541,21 @@ __device__ __forceinline__ void gemm_tiles_body(size_t nb, float *s, const uint8
       if (q4_chunk_nonfinite<kDHRow>(dsh + st * kHStage + wm * 64, kDKB, lane))
         break;
       chunk([&] {
-        fold_chunk_q4<false, kDKB, kDBlock, 32 * 16, kDHRow>(
-            acc, qa0 + st * kDStage, qb0 + st * kDStage, qx + st * kHStage, qy + st * kHStage,
+        fold_chunk_q4<false, kDKB, kDBlock, 32 * 16, kDHRow, kDBN>(
+            acc, qa0 + st * kDStage, qb0 + st * kDStage, qx + st * kHStage, qy + st * kFyStage,
             [](int) {});
       });
     }
     for (; c < nfull; ++c)
       chunk([&] {
-        fold_chunk_q4<true, kDKB, kDBlock, 32 * 16, kDHRow>(
-            acc, qa0 + st * kDStage, qb0 + st * kDStage, qx + st * kHStage, qy + st * kHStage,
+        fold_chunk_q4<true, kDKB, kDBlock, 32 * 16, kDHRow, kDBN>(
+            acc, qa0 + st * kDStage, qb0 + st * kDStage, qx + st * kHStage, qy + st * kFyStage,
             [](int) {});
       });
     if (nbc > 0)
-      fold_tail_q4<true, kDBlock, 32 * 16, kDHRow>(acc, qa0 + st * kDStage, qb0 + st * kDStage,
-                                                   qx + st * kHStage, qy + st * kHStage, nbc);
+      fold_tail_q4<true, kDBlock, 32 * 16, kDHRow, kDBN>(acc, qa0 + st * kDStage,
+                                                         qb0 + st * kDStage, qx + st * kHStage,
+                                                         qy + st * kFyStage, nbc);
   } else {
     for (; c < nfull; ++c)
       chunk([&] {
@@ -573,7 +616,7 @@ __global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q8(size_t nb, float *
                                                               size_t nc, size_t bs) {
   __shared__ __align__(16) int8_t qs[kDStages * kDStage];
   __shared__ __align__(16) uint16_t dsh[kDStages * kDKB * kDHRow];
-  gemm_tiles_body<kPipe, false>(nb, s, tx, ty, nr, nc, bs, qs, dsh);
+  gemm_tiles_body<kPipe, false>(nb, s, tx, ty, nr, nc, bs, qs, dsh, nullptr);
 }
 
 __global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q4(size_t nb, float *s,
@@ -582,7 +625,8 @@ __global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q4(size_t nb, float *
                                                               size_t nc, size_t bs) {
   __shared__ __align__(16) int8_t qs[kDStages * kDStage];
   __shared__ __align__(16) uint16_t dsh[kDStages * kDKB * kDHRow];
-  gemm_tiles_body<true, true>(nb, s, tx, ty, nr, nc, bs, qs, dsh);
+  __shared__ __align__(16) float fyd[kDStages * kDKB * kDBN];
+  gemm_tiles_body<true, true>(nb, s, tx, ty, nr, nc, bs, qs, dsh, fyd);
 }
 
 }  // namespace tcrv

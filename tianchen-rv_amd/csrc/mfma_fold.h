@@ -186,8 +186,9 @@ __device__ __forceinline__ void fold_tail_q8(float (&acc)[2][16], const int8_t *
 // The tile is computed transposed: the block-sum MFMA takes the tokens as its
 // A operand and the weights as B, so lane (c = lane % 32, h = lane / 32) holds
 // weight row c and tokens 8g + 4h + j (g, j < 4) of the tile.  d_x is then one
-// value per lane and tile-block (a 16-bit LDS read) and d_y one per element
-// (a 64-bit LDS read gives four).
+// value per lane and tile-block (a 16-bit LDS read) and d_y one per element,
+// read as fp32 (a 128-bit LDS read gives four) from a row the staging widened
+// once per chunk.
 //
 // The MFMA's accumulator input is the integer bit pattern of M = 1.5 * 2^23
 // (0x4B400000) in every element, so its results read as floats are
@@ -195,9 +196,10 @@ __device__ __forceinline__ void fold_tail_q8(float (&acc)[2][16], const int8_t *
 // whose spacing is 1.  Then fma(F, d_x, -M * d_x) = fl(sumi * d_x): the exact
 // F * d_x - M * d_x = sumi * d_x is rounded once, and -M * d_x is itself exact
 // (an fp16 significand times 1.5).  That fma (v_fma_f32) and fma(t, d_y, acc)
-// (v_fma_mix_f32, the fp16 d_y read in place) are the fold's two VALU
-// instructions per element; d_x and -M * d_x are one each per lane and
-// tile-block.
+// (v_fmac_f32 on d_y widened to fp32) are the fold's two VALU instructions per
+// element; d_x and -M * d_x are one each per lane and tile-block.  (With the
+// fp16 d_y read in place by v_fma_mix_f32 instead, a register-only copy of the
+// step ran 309 against 243 cycles per two tile-blocks at four waves per SIMD.)
 // An infinite d_x makes -M * d_x infinite, and the fast form NaN where the
 // reference has +-inf: a chunk with a non-finite d_x among the wave's weight
 // rows (q4_chunk_nonfinite, one test per chunk) is folded in the exact
@@ -241,22 +243,21 @@ __device__ __forceinline__ bool q4_chunk_nonfinite(const uint16_t *hx, int nbc, 
 }
 
 // The fold of one tile and block: F the seeded sums, ux the lane's d_x bits,
-// hy d_y of its tokens 4h.. of the block (rows 8g + 4h + 0..3 as fp16 pairs,
-// read per g); kExact: the three-instruction form.
+// fy d_y of its tokens 4h.. of the block as fp32 (tokens 8g + 4h + 0..3 at
+// fy + 8g, 16-byte aligned); kExact: the three-instruction form.
 template <bool kExact>
 __device__ __forceinline__ void q4_fold(float (&acc)[16], const v16f &F, uint32_t ux,
-                                        const uint16_t *hy) {
-  // Plain fp32 arithmetic on widened fp16 values (the compiler inserts the
-  // wait states a VALU read of a matrix-core result needs).  d_x is widened
-  // once and hidden from instruction selection, which would otherwise re-read
-  // it as fp16 in every product (v_fma_mix_f32 issues slower than v_fma_f32);
-  // d_y, one per element, is read in place by v_fma_mix_f32.
+                                        const float *fy) {
+  // Plain fp32 arithmetic (the compiler inserts the wait states a VALU read of
+  // a matrix-core result needs).  d_x is widened once and hidden from
+  // instruction selection, which would otherwise re-read it as fp16 in every
+  // product (v_fma_mix_f32 issues slower than v_fma_f32).
   float dx = f16_bits(ux);
   asm volatile("" : "+v"(dx));
   const float c = -kSeed * dx;  // -M * d_x, exact (unused by the exact form)
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    const uint2 dy = *reinterpret_cast<const uint2 *>(hy + 8 * g);
+    const float4 dy = *reinterpret_cast<const float4 *>(fy + 8 * g);
     // fl(sumi * d_x) of four rows, from F directly or from sumi = F - M
     // (exact), all four before the fmas that take them (each product a few
     // instructions ahead of its use).
@@ -265,11 +266,10 @@ __device__ __forceinline__ void q4_fold(float (&acc)[16], const v16f &F, uint32_
     for (int j = 0; j < 4; ++j)
       t[j] = kExact ? (F[4 * g + j] - kSeed) * dx : fmaf(F[4 * g + j], dx, c);
     asm volatile("" : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]));
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t w = j < 2 ? dy.x : dy.y;
-      acc[4 * g + j] = fmaf(t[j], f16_bits((j & 1) ? w >> 16 : w), acc[4 * g + j]);
-    }
+    acc[4 * g + 0] = fmaf(t[0], dy.x, acc[4 * g + 0]);
+    acc[4 * g + 1] = fmaf(t[1], dy.y, acc[4 * g + 1]);
+    acc[4 * g + 2] = fmaf(t[2], dy.z, acc[4 * g + 2]);
+    acc[4 * g + 3] = fmaf(t[3], dy.w, acc[4 * g + 3]);
   }
 #pragma unroll
   for (int e = 0; e < 16; ++e)
@@ -280,13 +280,13 @@ __device__ __forceinline__ void q4_fold(float (&acc)[16], const v16f &F, uint32_
 // s = 2b + i in ascending block order, the seeded MFMA of step s+1 issued in
 // step s (as fold_chunk_q8 with kPipe).  qw: this lane's weight quants of tile
 // 0, block 0 (tile 1 kTileStride bytes on); qt: its token quants; hx: its
-// weight row's d_x slot of tile 0, block 0 (tile 1 is 32 rows on); hy: d_y of
-// its tokens 4h.. of block 0 (q4_fold).
+// weight row's d_x slot of tile 0, block 0 (tile 1 is 32 rows on); fy: the
+// fp32 d_y of its tokens 4h.. of block 0, block b kFyRow floats on (q4_fold).
 template <bool kExact, int kBlocks, int kBlockStride, int kTileStride, int kScaleRow,
-          typename AfterStep>
+          int kFyRow, typename AfterStep>
 __device__ __forceinline__ void fold_chunk_q4(float (&acc)[2][16], const int8_t *qw,
                                               const int8_t *qt, const uint16_t *hx,
-                                              const uint16_t *hy, AfterStep &&after_step) {
+                                              const float *fy, AfterStep &&after_step) {
   v4i tq = q8_frag<kBlockStride>(qt, 0);
   v16f cur = q4_seeded_sums(tq, q8_frag<kBlockStride>(qw, 0));
 #pragma unroll
@@ -299,7 +299,7 @@ __device__ __forceinline__ void fold_chunk_q4(float (&acc)[2][16], const int8_t 
         tq = q8_frag<kBlockStride>(qt, b1);
       nxt = q4_seeded_sums(tq, q8_frag<kBlockStride>(qw + i1 * kTileStride, b1));
     }
-    q4_fold<kExact>(acc[i], cur, q8_scale<kScaleRow>(hx + 32 * i, b), hy + b * kScaleRow);
+    q4_fold<kExact>(acc[i], cur, q8_scale<kScaleRow>(hx + 32 * i, b), fy + b * kFyRow);
     if (s + 1 < 2 * kBlocks) {
       asm volatile("" : "+v"(nxt));
       cur = nxt;
@@ -310,16 +310,16 @@ __device__ __forceinline__ void fold_chunk_q4(float (&acc)[2][16], const int8_t 
 }
 
 // A trailing partial chunk of nbc blocks with the Q4_0 fold.
-template <bool kExact, int kBlockStride, int kTileStride, int kScaleRow>
+template <bool kExact, int kBlockStride, int kTileStride, int kScaleRow, int kFyRow>
 __device__ __forceinline__ void fold_tail_q4(float (&acc)[2][16], const int8_t *qw,
                                              const int8_t *qt, const uint16_t *hx,
-                                             const uint16_t *hy, int nbc) {
+                                             const float *fy, int nbc) {
   for (int b = 0; b < nbc; ++b) {
     const v4i tq = q8_frag<kBlockStride>(qt, b);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       q4_fold<kExact>(acc[i], q4_seeded_sums(tq, q8_frag<kBlockStride>(qw + i * kTileStride, b)),
-                      q8_scale<kScaleRow>(hx + 32 * i, b), hy + b * kScaleRow);
+                      q8_scale<kScaleRow>(hx + 32 * i, b), fy + b * kFyRow);
   }
 }
 
