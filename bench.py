@@ -108,7 +108,8 @@ def parse():
                     help="timed launches for each of add / dequant / block dot")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall time of the CPU-baseline sample (0 disables it)")
-    ap.add_argument("--only", choices=["all", "gemv", "gemv_rows", "gemm", "configs", "calib"],
+    ap.add_argument("--only", choices=["all", "gemv", "gemv_rows", "gemm", "configs", "schedules",
+                                       "calib"],
                     default="all",
                     help="calib: 10 launches of add_f32 over n = 2^24 (reads 128 MiB, writes "
                          "64 MiB each), the known-size kernel the HBM byte counters are "
@@ -280,6 +281,58 @@ def bench_gemv_rows(torch, lib, stream, args):
             f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak), {copies} copies")
         out[str(nr)] = {"us": round(us, 3), "GB/s": round(gbs, 1),
                         "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes, "copies": copies}
+        del wd, yd
+        torch.cuda.empty_cache()
+    return out
+
+
+SCHEDULE_SHAPES = ((4096, N), (2048, N))  # (weight rows, K) for the decode GEMV's knob
+
+
+def bench_schedules(torch, lib, stream, args):
+    """Every candidate of the schedule registry that an entry takes at run time
+    (tcrv_hip_route_schedule rows with an entry: the decode GEMV's
+    rows_per_wave through tcrv_hip_gemv_q4_0_q8_0_shaped), timed at the
+    registry's reference shapes over rotating weight copies past the Infinity
+    Cache, each candidate's output checked bit for bit against the plain
+    entry's.  The route tests compare the registry's defaults with a recorded
+    run of this (profiles/schedules.json)."""
+    import tcrv_hip
+    dev = torch.device("cuda:0")
+    w = inputs("gemv_w")
+    x = inputs("gemv_x")
+    wt = torch.from_numpy(w).to(dev)
+    xd = torch.from_numpy(x).to(dev)
+    bx, sp = w.shape[1], stream.cuda_stream
+    shaped = checked(lib.tcrv_hip_gemv_q4_0_q8_0_shaped, "gemv_shaped")
+    plain = checked(lib.tcrv_hip_gemv_q4_0_q8_0, "gemv")
+    out = []
+    sched = [r for r in tcrv_hip.route_schedules() if r["entry"]]
+    for nr, k in SCHEDULE_SHAPES:
+        copies = copies_for(nr * bx, 2)
+        wd = wt[:nr].reshape(1, -1).repeat(copies, 1)
+        yd = torch.empty((copies, nr), dtype=torch.float32, device=dev)
+        ref = torch.empty(nr, dtype=torch.float32, device=dev)
+        with torch.cuda.stream(stream):
+            plain(k, ref.data_ptr(), wd[0].data_ptr(), bx, xd.data_ptr(), nr, sp)
+        torch.cuda.synchronize()
+        for r in sched:
+            v = int(r["value"])
+
+            def launch(i, v=v):
+                j = i % copies
+                shaped(k, yd[j].data_ptr(), wd[j].data_ptr(), bx, xd.data_ptr(), nr, v, sp)
+
+            steps = max(256, copies)
+            Region(torch, stream, launch, steps).run()
+            reg = Region(torch, stream, launch, steps)
+            per = sorted(reg.run() * 1e3 / steps for _ in range(5))
+            if not torch.equal(yd[0].view(torch.int32), ref.view(torch.int32)):
+                raise RuntimeError(f"{r['knob']}={v}: output differs from the plain entry")
+            out.append({"op": r["op"], "m_regime": r["m_regime"], "knob": r["knob"], "value": v,
+                        "entry": r["entry"], "rows": nr, "k": k, "us": round(per[2], 4),
+                        "us_min": round(per[0], 4), "us_max": round(per[-1], 4)})
+            log(f"schedule {r['knob']}={v} at {nr}x{k}: {per[2]:.3f} us (min {per[0]:.3f})")
         del wd, yd
         torch.cuda.empty_cache()
     return out
@@ -1015,6 +1068,8 @@ def main():
         res["gemm"] = bench_gemm(torch, lib, stream, args)
     if args.only in ("all", "configs"):
         res["configs"] = bench_configs(torch, lib, stream, args)
+    if args.only in ("all", "schedules"):
+        res["schedules"] = bench_schedules(torch, lib, stream, args)
     cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
     cpu_gemm = (cpu_baseline_gemm(args.cpu_seconds / 2)
                 if args.cpu_seconds > 0 and "gemm" in res else None)
@@ -1103,6 +1158,12 @@ def main():
         if "value" not in line:
             first = next(iter(res["configs"].values()))
             line.update({"value": first["GB/s"], "unit": "GB/s", "ms_per_step": first["us"] / 1e3})
+    if "schedules" in res:
+        line["schedules"] = res["schedules"]
+        if "value" not in line:
+            first = res["schedules"][0]
+            line.update({"value": first["us"], "unit": "us", "higher_is_better": False,
+                         "ms_per_step": first["us"] / 1e3})
     line["cpu_baseline"] = cpu
     if args.only == "all":
         line["device"] = device_peaks(torch)

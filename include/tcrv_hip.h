@@ -273,7 +273,9 @@ TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm_ws(size_t n, float *s, const uint8_t *v
  * launching anything (4096 x 4096 x K 4096 needs 35.7 MB).  Every call on one
  * GPU shares that GPU's array: calls that overlap in time on one GPU race and
  * must be ordered by the caller (one stream).  The first call on a device
- * looks up the array's address (not capturable; make it outside a capture). */
+ * with a shape that uses the workspace looks up the array's address (not
+ * capturable; make it outside a capture); shapes that run the plain GEMM
+ * never touch the array. */
 TCRV_HIP_API size_t tcrv_hip_q8_0_q8_0_gemm_noalloc_max_bytes(void);
 TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm_noalloc(size_t n, float *s, const uint8_t *vx,
                                                  const uint8_t *vy, size_t by, size_t nr,

@@ -111,7 +111,9 @@ TCRV_HIP_API long tcrv_hip_route_find(const char *op);
  * registry for the gfx950 kernels: one row per (op, regime, knob, candidate
  * value).  A row with a non-NULL `entry` names the libtcrv_hip entry that takes
  * the knob as an argument (every value bit-identical); the others are
- * build-time shapes, listed with the measurement that chose among them. */
+ * build-time shapes.  The registry carries no timings: bench.py --only
+ * schedules times every selectable candidate at the op's reference shapes, and
+ * the tests check the defaults against a recorded run of it. */
 typedef struct {
   const char *op;      /* op identity of the route table */
   int m_regime;        /* TCRV_HIP_M_DECODE or TCRV_HIP_M_PREFILL; -1: not regime-specific */
@@ -120,7 +122,7 @@ typedef struct {
   int64_t value;       /* the candidate's value */
   int is_default;      /* 1: the value the op's own entry runs */
   const char *entry;   /* entry taking the knob, or NULL (fixed at build time) */
-  double measured_us;  /* per launch at the op's reference shape (4096 rows), or -1 */
+  double measured_us;  /* -1: timings are measured by bench.py, not stored here */
   const char *reason;  /* why the default is the default, or how the candidate compares */
 } tcrv_hip_schedule;
 /* Number of rows, and row `index` (TCRV_HIP_ERR_BAD_SIZE past the end). */

@@ -281,6 +281,24 @@ def test_gemv_q4_0_q8_0(hip, oracle, dev, nr, nb):
     assert_f32_parity(from_dev(s), want, what=f"gemv nr={nr} nb={nb}")
 
 
+# the lane-group kernels for rows of 2048 and 1024 quants with padded rows (bx
+# past the row bytes)
+@pytest.mark.parametrize("nr,nb,pad", [(4096, 64, 4), (8200, 64, 16), (4100, 32, 4),
+                                       (14336, 32, 16), (2048, 64, 4), (1024, 32, 16)])
+def test_gemv_q4_0_q8_0_padded_short_rows(hip, oracle, dev, nr, nb, pad):
+    n = nb * 32
+    w = np.pad(synth.q4_0_matrix(nr, n, 1016, 0.02), ((0, 0), (0, pad)))
+    x = synth.q8_0_matrix(1, n, 1017, 1.0).reshape(-1)
+    s = empty_dev(nr, torch.float32, dev)
+    dw = to_dev(w, dev)
+    hip.gemv_q4_0_q8_0(n, s, dw, w.shape[1], to_dev(x, dev), nr)
+    want = oracle.gemm_q4_0(n, w, x, 0, nr, 1, w.shape[1], 1, 8)[:nr]
+    assert_f32_parity(from_dev(s), want, what=f"gemv nr={nr} nb={nb} pad={pad}")
+    for rpw in (2, 4, 8):
+        hip.gemv_q4_0_q8_0_shaped(n, s, dw, w.shape[1], to_dev(x, dev), nr, rpw)
+        assert_f32_parity(from_dev(s), want, what=f"gemv rows_per_wave={rpw} pad={pad}")
+
+
 @pytest.mark.parametrize("nr,nb", [(1000, 128), (333, 40), (129, 200), (70, 9), (8200, 64),
                                    (1000, 32)])
 def test_gemv_shapes_are_bit_identical(hip, oracle, dev, nr, nb):

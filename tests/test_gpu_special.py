@@ -197,7 +197,10 @@ def test_repack_gemm_special_scales(hip, oracle, dev):
 
 # -------------------------------------------------------- GEMVs, block dots ---
 
-@pytest.mark.parametrize("nr,nb,pad", [(512, 128, 0), (33, 7, 2)])
+# (nr, nb = 64 / 32): the lane-group kernels for rows of 2048 and 1024 quants,
+# also with padded rows
+@pytest.mark.parametrize("nr,nb,pad", [(512, 128, 0), (33, 7, 2), (520, 64, 0), (8200, 64, 16),
+                                       (520, 32, 0), (4100, 32, 4)])
 def test_gemv_q4_0_special_scales(hip, oracle, dev, nr, nb, pad):
     n = nb * 32
     w = np.pad(q4(nr, nb, 17, nonfinite_every=16), ((0, 0), (0, pad)))
@@ -227,7 +230,9 @@ def test_gemv_q4_0_nonfinite_activation_scale(hip, oracle, dev):
         assert_f32_parity_nan(from_dev(s), want, what=f"gemv activation d={bits:#06x}")
 
 
-@pytest.mark.parametrize("rows,nb,pad", [(64, 128, 0), (19, 9, 2), (24, 260, 0)])
+# nb = 64 / 32: the block dots that run two or four row pairs per wave
+@pytest.mark.parametrize("rows,nb,pad", [(64, 128, 0), (19, 9, 2), (24, 260, 0), (70, 64, 0),
+                                         (70, 64, 4), (132, 32, 0), (132, 32, 16)])
 def test_block_dots_special_scales(hip, oracle, dev, rows, nb, pad):
     n = nb * 32
     x8 = np.pad(q8(rows, nb, 21, 1.0, nonfinite_every=8), ((0, 0), (0, pad)))
@@ -242,6 +247,11 @@ def test_block_dots_special_scales(hip, oracle, dev, rows, nb, pad):
                                  y8.shape[1], rows)
     want = oracle.vec_dot_q4_0_rows(n, x4, x4.shape[1], y8, y8.shape[1], rows, 8)
     assert_f32_parity_nan(from_dev(s), want, what="q4 block dot")
+    # one activation row shared by every weight row (the Q8_0 decode GEMV)
+    hip.q8_0_q8_0_gemm(n, s, to_dev(x8, dev), to_dev(y8[0].copy(), dev), 0, rows, 1,
+                       x8.shape[1], 1)
+    want = oracle.gemm_q8_0(n, x8, y8[0].copy(), 0, rows, 1, x8.shape[1], 1, 8)
+    assert_f32_parity_nan(from_dev(s), want, what="q8 decode gemv")
 
 
 @pytest.mark.parametrize("quant", ["q4_0", "q8_0"])

@@ -59,9 +59,9 @@ def test_route_library_exports_its_header():
 
 def test_schedule_registry_is_consistent():
     """Every registry row names an op of the route table; each (op, regime,
-    knob) has distinct candidate values and exactly one default, which is
-    within 1 % of the fastest measured candidate; a selectable row names an
-    entry the C-ABI header declares and libtcrv_hip exports."""
+    knob) has distinct candidate values and exactly one default; a selectable
+    row names an entry the C-ABI header declares and libtcrv_hip exports; the
+    registry stores no timings (bench.py measures them)."""
     ops = {r["op"] for r in tcrv_hip.route_table()}
     rows = tcrv_hip.route_schedules()
     assert rows
@@ -72,7 +72,7 @@ def test_schedule_registry_is_consistent():
     for r in rows:
         assert r["op"] in ops, r
         assert r["m_regime"] in (-1, tcrv_hip.M_DECODE, tcrv_hip.M_PREFILL), r
-        assert r["measured_us"] > 0 and r["reason"], r
+        assert r["measured_us"] == -1 and r["reason"], r
         if r["entry"]:
             assert re.search(r"TCRV_HIP_API\s+int\s+" + r["entry"] + r"\s*\(", hip_text), r
             assert re.search(r"\b" + r["entry"] + r"\b", exported), r
@@ -80,10 +80,32 @@ def test_schedule_registry_is_consistent():
     for key, cands in groups.items():
         values = [c["value"] for c in cands]
         assert len(set(values)) == len(values), key
-        defaults = [c for c in cands if c["is_default"]]
-        assert len(defaults) == 1, key
-        assert defaults[0]["measured_us"] <= 1.01 * min(c["measured_us"] for c in cands), key
+        assert sum(1 for c in cands if c["is_default"]) == 1, key
         assert len({c["entry"] for c in cands}) == 1, key  # a knob is selectable or not
+
+
+SCHEDULES = os.path.join(ROOT, "profiles", "schedules.json")
+
+
+def test_schedule_defaults_match_the_recorded_measurement():
+    """profiles/schedules.json is bench.py --only schedules' record (one MI355X):
+    every selectable candidate timed at the reference shapes.  At the
+    4096-row reference shape the registry's default is the fastest candidate
+    (within 1 %); up to 2048 rows the plain entry's rule (2 rows per wave) is."""
+    import json
+    with open(SCHEDULES) as f:
+        rec = json.load(f)
+    meas = rec["schedules"]
+    sel = [r for r in tcrv_hip.route_schedules() if r["entry"]]
+    assert sel
+    for (op, regime, knob) in {(r["op"], r["m_regime"], r["knob"]) for r in sel}:
+        cands = [r for r in sel if (r["op"], r["m_regime"], r["knob"]) == (op, regime, knob)]
+        default = next(r["value"] for r in cands if r["is_default"])
+        for rows, want in ((4096, default), (2048, 2)):
+            got = {m["value"]: m["us"] for m in meas
+                   if (m["op"], m["m_regime"], m["knob"], m["rows"]) == (op, regime, knob, rows)}
+            assert set(got) == {r["value"] for r in cands}, (knob, rows)
+            assert got[want] <= 1.01 * min(got.values()), (knob, rows, got)
 
 
 def test_schedule_default_lookup():

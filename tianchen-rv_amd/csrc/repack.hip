@@ -263,8 +263,9 @@ __global__ __launch_bounds__(64 * kRwWaves) void repack_gemv_waves(size_t nb, fl
 // 5.4 against 4.8 us at 4096 x 4096, the wave-staged kernel 4.9-5.0 us).  Lane
 // (block b = 16(w*passes + pass) + l/4, quarter k = l%4) loads the 64
 // contiguous bytes that hold positions 4k..4k+3 of block b for all 16 rows
-// (four 128-bit loads straight into registers, no LDS staging) and its eight
-// activation quants 4k.. and 16+4k.. (dword loads, realigned), turns each row
+// (four 128-bit loads straight into registers, no LDS staging) and reads its
+// eight activation quants 4k.. and 16+4k.. from the chunk the work-group
+// copied into LDS, turns each row
 // quad row-major with v_perm (transpose4x4), dots the masked nibbles (16 times
 // the signed quant, as in repack_gemv_waves) with the activation, and a quad
 // reduce-scatter (two DPP stages) leaves lane k the sums of rows 4k..4k+3 over
@@ -280,19 +281,6 @@ __device__ __forceinline__ int quad_add(int keep, int send) {
   return keep + __builtin_amdgcn_update_dpp(0, send, kCtrl, 0xf, 0xf, false);
 }
 
-// The four bytes at p (2-byte aligned): the dword at p when p is dword
-// aligned, else bytes 2-3 of the dword at p - 2 and the 16-bit word at p + 2,
-// so no byte past p + 3 is read (p + 3 may be a block's, or the activation's,
-// last byte).
-__device__ __forceinline__ uint32_t load_u32_a2(const uint8_t *p) {
-  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  if ((a & 2u) == 0)
-    return *reinterpret_cast<const uint32_t *>(p);
-  const uint32_t lo = *reinterpret_cast<const uint32_t *>(p - 2);
-  const uint32_t hi = *reinterpret_cast<const uint16_t *>(p + 2);
-  return funnel16(lo, hi);
-}
-
 __global__ __launch_bounds__(64 * kRdWaves) void repack_gemv_q4_direct(size_t nb, float *s,
                                                                        const uint8_t *vx,
                                                                        const uint8_t *vy) {
@@ -305,6 +293,7 @@ __global__ __launch_bounds__(64 * kRdWaves) void repack_gemv_q4_direct(size_t nb
   static_assert(kFoldTerms == 16 && kRdWaves >= 4, "waves 0-3 fold 16 rows, one run per lane");
   static_assert(kPasses * kRdWaves * 16 == kRdChunk, "whole passes");
   __shared__ __align__(16) float2 terms[16][kTermRow];
+  __shared__ __align__(16) uint8_t yl[kRdChunk * kQ8Bytes];  // the activation chunk
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63;
@@ -329,10 +318,20 @@ __global__ __launch_bounds__(64 * kRdWaves) void repack_gemv_q4_direct(size_t nb
       for (int i = 0; i < 4; ++i)
         qv[ps][i] = reinterpret_cast<const uint4 *>(blk + 32 + 64 * k)[i];
       dq[ps] = *reinterpret_cast<const uint2 *>(blk + 8 * k);  // d of rows 4k..4k+3
-      const uint8_t *ab = vy + (c0 + bc) * kQ8Bytes;
-      ylo[ps] = load_u32_a2(ab + 2 + 4 * k);
-      yhi[ps] = load_u32_a2(ab + 18 + 4 * k);
-      dah[ps] = *reinterpret_cast<const uint16_t *>(ab);
+    }
+    // The activation chunk is copied into LDS once per work-group with
+    // coalesced loads, after the weight loads are in flight; read per lane from
+    // global memory its quants are 2-byte misaligned pieces of 16 different
+    // blocks (up to five small loads a lane): 4.79 -> 4.70 us at 4096^2.
+    copy_span_to_lds(yl, vy + c0 * kQ8Bytes, nbc * kQ8Bytes, tid, 64 * kRdWaves);
+    __syncthreads();
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps) {
+      const int bc = min((w * kPasses + ps) * 16 + (l >> 2), nbc - 1);
+      const uint16_t *a16 = reinterpret_cast<const uint16_t *>(yl + bc * kQ8Bytes);
+      ylo[ps] = a16[1 + 2 * k] | (static_cast<uint32_t>(a16[2 + 2 * k]) << 16);
+      yhi[ps] = a16[9 + 2 * k] | (static_cast<uint32_t>(a16[10 + 2 * k]) << 16);
+      dah[ps] = a16[0];
     }
 #pragma unroll
     for (int ps = 0; ps < kPasses; ++ps) {

@@ -206,51 +206,59 @@ const HipKernelRoute kHipKernelRoutes[] = {
 constexpr size_t kNumRoutes = std::size(kHipKernelRoutes);
 
 // The schedule registry (tcrv_hip_route_schedule): for each knob of a kernel
-// the legal candidates, the default and the measurement that chose it -- per
-// launch at the op's reference shape (the 4096-row configs), on one MI355X, in
-// the same bench as the shipped figure.  Rows with an entry can be chosen per
-// call; the rest are template constants of the library build.
+// the legal candidates, the default and why.  Rows with an entry can be chosen
+// per call, and bench.py (--only schedules) times every such candidate at the
+// op's reference shapes; the rest are template constants of the library build,
+// chosen by a sweep of rebuilt libraries.  The registry itself carries no
+// timings (measured_us is -1).
 const tcrv_hip_schedule kSchedules[] = {
     // the decode GEMV (q4_0 GEMM, nc = 1): rows per wave of the register-direct
-    // kernel, 4 waves per work-group; the fold runs on 8 lanes per row for 4 or
-    // 8 rows per wave, on 16 for 2
+    // kernel, 4 waves per work-group.  The fold runs on 8 lanes per row for 4
+    // or 8 rows per wave, on 16 for 2.  The plain entry's own choice depends on
+    // the shape: 2 up to 2048 weight rows (4 would leave too few work-groups to
+    // cover the chip), 4 above; for rows of exactly 2048 or 1024 quants (n =
+    // 2048, 1024) a knob of 4 selects the lane-group kernels, whose waves own 4
+    // or 8 rows (2 or 4 lane groups of 32 or 16 lanes) by n and nr.
     {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_DECODE, "gemv_q4_0_q8_0_direct", "rows_per_wave", 2,
-     0, "tcrv_hip_gemv_q4_0_q8_0_shaped", 3.836,
-     "2048 waves: two per SIMD share the read; the per-row fold chain is 15 lane hops "
-     "(the plain entry's choice up to 2048 rows, where 4 leave too few work-groups)"},
+     0, "tcrv_hip_gemv_q4_0_q8_0_shaped", -1.0,
+     "2048 waves for 4096 rows: two per SIMD share the read, and the per-row fold chain has 15 "
+     "lane hops; the plain entry's choice up to 2048 weight rows"},
     {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_DECODE, "gemv_q4_0_q8_0_direct", "rows_per_wave", 4,
-     1, "tcrv_hip_gemv_q4_0_q8_0_shaped", 3.565,
-     "measured fastest: one wave per SIMD, every lane busy in the decode and 32 fold lanes"},
+     1, "tcrv_hip_gemv_q4_0_q8_0_shaped", -1.0,
+     "the default from 2049 weight rows (the 4096-row reference shape): one wave per SIMD, "
+     "every lane busy in the decode and 32 fold lanes; at n = 2048 and 1024 the lane-group "
+     "kernels"},
     {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_DECODE, "gemv_q4_0_q8_0_direct", "rows_per_wave", 8,
-     0, "tcrv_hip_gemv_q4_0_q8_0_shaped", 4.695,
-     "512 waves leave half the SIMDs idle during the read"},
-    // the tiled Q8_0 GEMM: blocks per K chunk (measured with two LDS stages for
-    // 5-6 blocks, three for 3-4)
+     0, "tcrv_hip_gemv_q4_0_q8_0_shaped", -1.0,
+     "512 waves for 4096 rows leave half the SIMDs idle during the read"},
+    // the tiled Q8_0 GEMM: blocks per K chunk (two LDS stages for 5-6 blocks,
+    // three for 3-4); a build-time constant
     {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles_q8", "k_chunk_blocks", 3, 0,
-     nullptr, 174.9, "three stages; more barriers per K"},
+     nullptr, -1.0, "three stages; the most barriers per K"},
     {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles_q8", "k_chunk_blocks", 4, 0,
-     nullptr, 170.1, "three stages"},
+     nullptr, -1.0, "three stages"},
     {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles_q8", "k_chunk_blocks", 5, 0,
-     nullptr, 163.5, "two stages; within the run-to-run spread of 6"},
+     nullptr, -1.0, "two stages; even with 6 in the sweep"},
     {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles_q8", "k_chunk_blocks", 6, 1,
-     nullptr, 164.0,
-     "measured fastest with 5 (two stages, 154 KB of LDS: one chunk in flight covers the DMA "
+     nullptr, -1.0,
+     "fastest in the sweep with 5 (two stages, 154 KB of LDS: one chunk in flight covers the DMA "
      "latency); 6 divides the 128 blocks of K = 4096 more evenly"},
-    // quantize_row_q8_0: 32-float blocks per 8-lane group
+    // quantize_row_q8_0: 32-float blocks per 8-lane group; a build-time constant
     {"tcrv_rvv.quantize_row_q8_0", -1, "quantize_q8_0", "blocks_per_lane_group", 1, 0, nullptr,
-     18.1, "fewer loads in flight per thread"},
+     -1.0, "fewer loads in flight per thread"},
     {"tcrv_rvv.quantize_row_q8_0", -1, "quantize_q8_0", "blocks_per_lane_group", 2, 1, nullptr,
-     16.2, "measured fastest"},
+     -1.0, "fastest in the sweep"},
     {"tcrv_rvv.quantize_row_q8_0", -1, "quantize_q8_0", "blocks_per_lane_group", 4, 0, nullptr,
-     17.1, "more registers, fewer waves"},
-    // tcrv_rvv.binary (add f32, n = 2^24): 16-byte vectors per operand and thread
-    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 1, 0, nullptr, 28.0,
+     -1.0, "more registers, fewer waves"},
+    // tcrv_rvv.binary (add f32, n = 2^24): 16-byte vectors per operand and
+    // thread; a build-time constant
+    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 1, 0, nullptr, -1.0,
      "loads of one vector in flight"},
-    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 2, 1, nullptr, 27.8,
-     "measured fastest"},
-    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 4, 0, nullptr, 28.7,
+    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 2, 1, nullptr, -1.0,
+     "fastest in the sweep"},
+    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 4, 0, nullptr, -1.0,
      "fewer work-groups in flight"},
-    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 8, 0, nullptr, 29.1,
+    {"tcrv_rvv.binary", -1, "add_f32_vec4", "vectors_per_thread", 8, 0, nullptr, -1.0,
      "fewer work-groups in flight"},
 };
 constexpr size_t kNumSchedules = std::size(kSchedules);
