@@ -518,8 +518,9 @@ constexpr int kWTasks = kWRows * (kWKB / 2);      // 768 block-pair tasks per ch
 //   v_mfma_f32_32x32x8_f16  -> d_x(row) * d_y(col): k-slot 0 carries the two
 //                              fp16 scales, every other k-slot is zero, so each
 //                              output is one product of two fp16 values, exact
-//                              in fp32 (16 matrix cycles, half the 2-block f32
-//                              outer product's per-block cost)
+//                              in fp32 (32 matrix cycles, measured: per block
+//                              what the 2-block f32 outer product costs, with
+//                              no VALU to build its operands)
 //   VALU: acc = fma((float)sumi, dxy, acc) -- the reference fold, in order.
 // The MFMAs of step s+1 (tile, block) are issued before the fold of step s, so
 // the matrix core works while the VALU folds (on this part one wave issues a

@@ -377,26 +377,46 @@ __device__ __forceinline__ void dma_slots(DmaSlots &d, int8_t *qs, uint16_t *dsh
   }
 }
 
-// Issues this wave's DMA of K chunk c (nbc blocks) into stage st; returns
-// how many DMA instructions it issued.
+// Issues slot k of this wave's DMA of K chunk c (nbc blocks) into stage st;
+// returns 1 if the slot moves a block of the chunk, else 0.
+__device__ __forceinline__ int dma_slot(const DmaSlots &d, int k, size_t c, int nbc, int st,
+                                        int wave, int lane) {
+  if (wave + 16 * k >= kDDma || d.blk[k] >= nbc)
+    return 0;
+  const size_t coff = c * kDKB * kTRec;
+  lds_void *to =
+      (lds_void *)((char __attribute__((address_space(3))) *)d.dst[k] + st * d.stage_bytes[k]);
+  if (k + 1 < kDSlots)
+    __builtin_amdgcn_global_load_lds(d.base[k] + coff + lane * 16, to, 16, 0, 0);
+  else if (d.on_last)
+    __builtin_amdgcn_global_load_lds(d.last + coff, to, 16, 0, 0);
+  return 1;
+}
+
+// Issues this wave's whole DMA of K chunk c into stage st (the prologue);
+// returns how many DMA instructions it issued.
 __device__ __forceinline__ int dma_chunk(const DmaSlots &d, size_t c, int nbc, int st,
                                          int wave, int lane) {
-  const size_t coff = c * kDKB * kTRec;
   int issued = 0;
 #pragma unroll
-  for (int k = 0; k < kDSlots; ++k) {
-    if (wave + 16 * k < kDDma && d.blk[k] < nbc) {
-      lds_void *to = (lds_void *)((char __attribute__((address_space(3))) *)d.dst[k] +
-                                  st * d.stage_bytes[k]);
-      if (k + 1 < kDSlots)
-        __builtin_amdgcn_global_load_lds(d.base[k] + coff + lane * 16, to, 16, 0, 0);
-      else if (d.on_last)
-        __builtin_amdgcn_global_load_lds(d.last + coff, to, 16, 0, 0);
-      ++issued;
-    }
-  }
+  for (int k = 0; k < kDSlots; ++k)
+    issued += dma_slot(d, k, c, nbc, st, wave, lane);
   return issued;
 }
+
+// Where a wave issues its DMA of the next chunk.  A global_load_lds leaves
+// the wave only once the CU takes it -- about one instruction per 14 cycles
+// per CU, one per ~68 cycles from a lone wave -- and costs its SIMD ~24-36
+// MFMA-pipe cycles even then (probe kernels mixing MFMA chains with LDS DMA).
+// All 16 waves issuing their ~5 slots right after the barrier queue together
+// and the four waves of a SIMD stall at once: ~700 cycles of a ~7700-cycle
+// chunk (per-wave cycle counters, Q8_0 4096^3).  kDmaSpread: slot k is issued
+// after fold step k instead, between the wave's MFMAs (Q8_0 4096^3 tiles
+// 164.7 -> 161.4 us, interleaved A/B).  The Q4_0 kernel keeps the DMA at the
+// chunk's start: it is at 128 VGPRs, and every spread placement spills.
+template <bool kQ4>
+constexpr bool kDmaSpread = !kQ4;
+static_assert(kDSlots <= 2 * kDKB, "a spread chunk issues one slot per fold step");
 
 // Waits until at most `pending` of this wave's memory loads are outstanding
 // (the DMA of the newest chunk; every older chunk has landed in LDS) and all
@@ -520,15 +540,23 @@ __device__ __forceinline__ void gemm_tiles_body(size_t nb, float *s, const uint8
 
   int st = 0;  // stage of chunk c
   size_t c = 0;
-  // One full chunk: the DMA of chunk c + kAhead is issued, chunk c folded, and
-  // the barrier passed once chunk c + 1 is in LDS (with one chunk ahead it is
-  // the newest DMA).
+  // One full chunk: the DMA of chunk c + kAhead is issued (before the fold or
+  // between its steps), chunk c folded, and the barrier passed once chunk c + 1
+  // is in LDS (with one chunk ahead it is the newest DMA).
   auto chunk = [&](auto fold) {
     const int sta = st + kAhead >= kDStages ? st + kAhead - kDStages : st + kAhead;
-    pending = c + kAhead < nchunks
-                  ? dma_chunk(slots, c + kAhead, blocks_of(c + kAhead), sta, wave, lane)
-                  : 0;
-    fold();
+    const bool ahead = c + kAhead < nchunks;
+    const int nba = ahead ? blocks_of(c + kAhead) : 0;
+    if constexpr (kDmaSpread<kQ4>) {
+      pending = 0;
+      fold([&](int s) {
+        if (s < kDSlots && ahead)
+          pending += dma_slot(slots, s, c + kAhead, nba, sta, wave, lane);
+      });
+    } else {
+      pending = ahead ? dma_chunk(slots, c + kAhead, nba, sta, wave, lane) : 0;
+      fold([](int) {});
+    }
     const int stn = st + 1 == kDStages ? 0 : st + 1;
     wait_dma_barrier(kAhead > 1 ? pending : 0, [&] { publish(c + 1, stn); });
     st = stn;
@@ -540,17 +568,17 @@ __device__ __forceinline__ void gemm_tiles_body(size_t nb, float *s, const uint8
     for (; c < nfull; ++c) {
       if (q4_chunk_nonfinite<kDHRow>(dsh + st * kHStage + wm * 64, kDKB, lane))
         break;
-      chunk([&] {
+      chunk([&](auto after_step) {
         fold_chunk_q4<false, kDKB, kDBlock, 32 * 16, kDHRow, kDBN>(
             acc, qa0 + st * kDStage, qb0 + st * kDStage, qx + st * kHStage, qy + st * kFyStage,
-            [](int) {});
+            after_step);
       });
     }
     for (; c < nfull; ++c)
-      chunk([&] {
+      chunk([&](auto after_step) {
         fold_chunk_q4<true, kDKB, kDBlock, 32 * 16, kDHRow, kDBN>(
             acc, qa0 + st * kDStage, qb0 + st * kDStage, qx + st * kHStage, qy + st * kFyStage,
-            [](int) {});
+            after_step);
       });
     if (nbc > 0)
       fold_tail_q4<true, kDBlock, 32 * 16, kDHRow, kDBN>(acc, qa0 + st * kDStage,
@@ -558,10 +586,10 @@ __device__ __forceinline__ void gemm_tiles_body(size_t nb, float *s, const uint8
                                                          qy + st * kFyStage, nbc);
   } else {
     for (; c < nfull; ++c)
-      chunk([&] {
+      chunk([&](auto after_step) {
         fold_chunk_q8<kPipe, kDKB, kDBlock, 32 * 16, kDHRow>(
             acc, qa0 + st * kDStage, qb0 + st * kDStage, hx0 + st * kHStage,
-            hx1 + st * kHStage, hy + st * kHStage, [](int) {});
+            hx1 + st * kHStage, hy + st * kHStage, after_step);
       });
     if (nbc > 0)
       fold_tail_q8<kDBlock, 32 * 16, kDHRow>(acc, qa0 + st * kDStage, qb0 + st * kDStage,
