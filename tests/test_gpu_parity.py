@@ -961,12 +961,15 @@ def test_pack_q8_0_to_gemm_tiles(hip, dev, nrows, nb, pad, off):
 
 
 @pytest.mark.parametrize("nr,nc,nb,xpad,ypad", [
-    (256, 128, 4, 0, 0),      # one tile, one chunk
-    (256, 128, 8, 0, 0),      # two chunks
-    (300, 130, 9, 16, 32),    # partial tiles both ways, 2 chunks + 1 block, padded strides
-    (520, 257, 13, 0, 4),     # three tile rows, 3 chunks + 1 block
+    (256, 128, 4, 0, 0),      # one tile, only a partial chunk (6-block chunks)
+    (256, 128, 6, 0, 0),      # exactly one full chunk: no DMA issued inside the fold
+    (256, 128, 8, 0, 0),      # one chunk + 2 blocks
+    (256, 64, 11, 0, 0),      # one chunk + 5: the tail's DMA, issued slot by slot in chunk
+                              # 0's fold, skips the slots of the block it does not have
+    (300, 130, 9, 16, 32),    # partial tiles both ways, 1 chunk + 3 blocks, padded strides
+    (520, 257, 13, 0, 4),     # three tile rows, 2 chunks + 1 block
     (256, 2, 1, 0, 0),        # one block: only the partial chunk
-    (640, 384, 130, 0, 0),    # 32 chunks + 2 blocks, groups past the last one re-read
+    (640, 384, 130, 0, 0),    # 21 chunks + 4 blocks, groups past the last one re-read
     (512, 200, 128, 0, 0),    # 16-byte aligned rows: both operands packed by 8-block spans
 ])
 def test_q8_0_gemm_tiles_and_ws(hip, oracle, dev, nr, nc, nb, xpad, ypad):
