@@ -125,3 +125,43 @@ def test_gemv_weights_over_2_gib(hip, oracle, dev):
     pick = np.unique(np.concatenate([sample_indices(nr, 256, 3), [nr - 1]]))
     want = oracle.gemm_q4_0(n, base[pick % 96], x, 0, len(pick), 1, rb, 1, 8)
     assert_f32_parity(got[pick], want, what="gemv over 2 GiB")
+
+
+def test_gemm_output_beyond_2_pow_32(hip, oracle, dev):
+    """The GEMM entries with an output of more than 2^32 elements (65600 x 65600 at a padded
+    stride, 17.2 GB of fp32): the tiled kernels (through the workspace entries, Q8_0 and
+    Q4_0 weights) and the plain Q8_0 entry, every output index formed in 64 bits.  K = 64
+    keeps the work small; sampled rows, the last included, against the CPU oracle."""
+    nr = nc = 65600
+    nb = 2
+    n = nb * 32
+    bs = nc + 8
+    assert (nr - 1) * bs + nc > 1 << 32
+    w8 = synth.q8_0_matrix(nr, n, 1011, 0.02)
+    w4 = synth.q4_0_matrix(nr, n, 1012, 0.02)
+    a = synth.q8_0_matrix(nc, n, 1013, 1.0)
+    rng = np.random.default_rng(9)
+    pick = np.unique(np.concatenate([[0, 1, nr // 2, nr - 2, nr - 1], rng.integers(0, nr, 59)]))
+    s = torch.empty(nr * bs, dtype=torch.float32, device=dev)
+    da = torch.from_numpy(a).to(dev)
+    rows = torch.from_numpy(pick).to(dev)
+    for name, w, entry, ref in (
+            ("q8_0 ws", w8, "q8_0_q8_0_gemm_ws", oracle.gemm_q8_0),
+            ("q4_0 ws", w4, "q4_0_q8_0_gemm_ws", oracle.gemm_q4_0),
+            ("q8_0 plain", w8, "q8_0_q8_0_gemm", oracle.gemm_q8_0)):
+        dw = torch.from_numpy(w).to(dev)
+        s.fill_(float("nan"))
+        if entry.endswith("_ws"):
+            wsb = getattr(hip, entry.replace("_ws", "_workspace_bytes"))(n, nr, nc)
+            ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+            getattr(hip, entry)(n, s, dw, da, a.shape[1], nr, nc, w.shape[1], bs, ws, wsb)
+            del ws
+        else:
+            getattr(hip, entry)(n, s, dw, da, a.shape[1], nr, nc, w.shape[1], bs)
+        got = s.view(nr, bs).index_select(0, rows).cpu().numpy()
+        del dw
+        want = ref(n, w[pick], a, a.shape[1], len(pick), nc, w.shape[1], bs, 8).reshape(len(pick), bs)
+        assert_f32_parity(got[:, :nc], want[:, :nc], what=f"{name} gemm, output past 2^32")
+        assert np.all(np.isnan(got[:, nc:])), f"{name}: a store past column nc"
+    del s, da, rows
+    free()
