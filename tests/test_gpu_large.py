@@ -165,3 +165,36 @@ def test_gemm_output_beyond_2_pow_32(hip, oracle, dev):
         assert np.all(np.isnan(got[:, nc:])), f"{name}: a store past column nc"
     del s, da, rows
     free()
+
+
+def test_gemm_tiled_operands_over_2_gib(hip, oracle, dev):
+    """The workspace entries (both operands packed into the GEMM-tile layout, then the DMA-
+    staged tiled kernel) with a packed weight operand past 2 GiB: 8192 weight rows x K 262144
+    (2.28 GB of records), so the DMA sources, record offsets and chunk offsets all need 64
+    bits.  Weight rows repeat a 96-row pattern (built on the device), so each sampled row's
+    bytes are known on the host."""
+    nr, nc, nb = 8192, 128, 8192
+    n = nb * 32
+    a = synth.q8_0_matrix(nc, n, 1015, 1.0)
+    da = torch.from_numpy(a).to(dev)
+    rng = np.random.default_rng(11)
+    pick = np.unique(np.concatenate([[0, 95, 96, nr // 2, nr - 1], rng.integers(0, nr, 27)]))
+    rows = torch.from_numpy(pick).to(dev)
+    bs = nc + 4
+    for name, base, entry, ref in (
+            ("q8_0", synth.q8_0_matrix(96, n, 1016, 0.02), "q8_0_q8_0_gemm_ws", oracle.gemm_q8_0),
+            ("q4_0", synth.q4_0_matrix(96, n, 1017, 0.02), "q4_0_q8_0_gemm_ws", oracle.gemm_q4_0)):
+        dw = torch.from_numpy(base).to(dev).repeat(nr // 96 + 1, 1)[:nr].contiguous()
+        wsb = getattr(hip, entry.replace("_ws", "_workspace_bytes"))(n, nr, nc)
+        assert wsb > 1 << 31
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        s = torch.full((nr * bs,), float("nan"), dtype=torch.float32, device=dev)
+        getattr(hip, entry)(n, s, dw, da, a.shape[1], nr, nc, base.shape[1], bs, ws, wsb)
+        got = s.view(nr, bs).index_select(0, rows).cpu().numpy()
+        del dw, ws, s
+        free()
+        want = ref(n, base[pick % 96], a, a.shape[1], len(pick), nc, base.shape[1], bs,
+                   8).reshape(len(pick), bs)
+        assert_f32_parity(got[:, :nc], want[:, :nc], what=f"{name} gemm_ws, operand past 2 GiB")
+    del da, rows
+    free()
