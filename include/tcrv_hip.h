@@ -249,16 +249,17 @@ TCRV_HIP_API int tcrv_hip_pack_q8_0_to_gemm_tiles(size_t nrows, size_t nb, const
 /* The Q8_0 x Q8_0 GEMM over operands in that layout (tx: nr weight rows, ty: nc
  * token rows, both 16-byte aligned): s[ir*bs + col] exactly as
  * tcrv_hip_q8_0_q8_0_gemm computes it from the plain rows.  Weights that are
- * packed once serve every later call. */
+ * packed once serve every later call.  n/32 at most 1 973 789 (a 64-row
+ * group's records under 4 GiB), else TCRV_HIP_ERR_TOO_LARGE. */
 TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm_tiles(size_t n, float *s, const uint8_t *tx,
                                                const uint8_t *ty, size_t nr, size_t nc,
                                                size_t bs, void *stream);
 /* tcrv_hip_q8_0_q8_0_gemm (same ABI and results) with a caller-owned device
  * workspace: both operands are packed into it (tx then ty) and the tiled GEMM
  * runs.  Needs tcrv_hip_q8_0_q8_0_gemm_workspace_bytes(n, nr, nc) bytes, 16-byte
- * aligned; shapes the tiled kernel does not serve (nr < 256, nc < 2) run
- * tcrv_hip_q8_0_q8_0_gemm and leave the workspace untouched.  Calls that share
- * a workspace must be ordered (one stream). */
+ * aligned; shapes the tiled kernel does not serve (nr < 256, nc < 2, n/32 over
+ * 1 973 789) run tcrv_hip_q8_0_q8_0_gemm and leave the workspace untouched.
+ * Calls that share a workspace must be ordered (one stream). */
 TCRV_HIP_API size_t tcrv_hip_q8_0_q8_0_gemm_workspace_bytes(size_t n, size_t nr, size_t nc);
 TCRV_HIP_API int tcrv_hip_q8_0_q8_0_gemm_ws(size_t n, float *s, const uint8_t *vx,
                                             const uint8_t *vy, size_t by, size_t nr, size_t nc,
@@ -300,9 +301,9 @@ TCRV_HIP_API int tcrv_hip_q4_0_q8_0_gemm_tiles(size_t n, float *s, const uint8_t
  * workspace: the Q4_0 weights and the Q8_0 tokens are packed into it (tx then
  * ty, one launch) and the tiled GEMM runs.  Needs
  * tcrv_hip_q4_0_q8_0_gemm_workspace_bytes(n, nr, nc) bytes, 16-byte aligned;
- * shapes the tiled kernel does not serve (nr < 256, nc < 2) run
- * tcrv_hip_q4_0_q8_0_gemm and leave the workspace untouched.  Calls that share
- * a workspace must be ordered (one stream). */
+ * shapes the tiled kernel does not serve (nr < 256, nc < 2, n/32 over
+ * 1 973 789) run tcrv_hip_q4_0_q8_0_gemm and leave the workspace untouched.
+ * Calls that share a workspace must be ordered (one stream). */
 TCRV_HIP_API size_t tcrv_hip_q4_0_q8_0_gemm_workspace_bytes(size_t n, size_t nr, size_t nc);
 TCRV_HIP_API int tcrv_hip_q4_0_q8_0_gemm_ws(size_t n, float *s, const uint8_t *vx,
                                             const uint8_t *vy, size_t by, size_t nr, size_t nc,

@@ -68,6 +68,9 @@ def test_loads_and_reports_version_without_gpu():
     ("tcrv_hip_q4_0_q8_0_block_dot_rows", (64, 256, 256, 24, 512, 80, 3, 0),
      tcrv_hip.ERR_BAD_SIZE),
     ("tcrv_hip_gemv_q4_0_q8_0", (64, 256, 512, 34, 1024, 3, 0), tcrv_hip.ERR_BAD_SIZE),
+    # the tiled Q8_0 GEMM's 32-bit chunk offsets: at most 1 973 789 blocks (n/32)
+    ("tcrv_hip_q8_0_q8_0_gemm_tiles", (1973790 * 32, 256, 512, 1024, 256, 2, 2, 0),
+     tcrv_hip.ERR_TOO_LARGE),
 ])
 def test_argument_errors_before_launch(name, args, want):
     assert tcrv_hip.call(name, *args, check=False) == want

@@ -378,7 +378,16 @@ __device__ __forceinline__ void dma_slots(DmaSlots &d, int8_t *qs, uint16_t *dsh
 }
 
 // Issues slot k of this wave's DMA of K chunk c (nbc blocks) into stage st;
-// returns 1 if the slot moves a block of the chunk, else 0.
+// returns 1 if the slot moves a block of the chunk, else 0.  kBuf: the quant
+// slots as buffer loads (buffer_load_dwordx4 ... offen lds: the slot's chunk-0
+// record half as the resource base in scalar registers, the chunk offset as
+// soffset, one 32-bit lane offset shared by every slot) instead of
+// global_load_lds with a 64-bit vector address per slot; the chunk offset is
+// then 32-bit (nb * kTRec < 2^32, which the entries check).  The Q8_0 kernel
+// takes it (4096^3 tiles 162.0 against 164.8 us, and 165.7 against 167.7 with
+// another issue placement, interleaved A/B); the Q4_0 kernel, at its register
+// limit, would spill 18-20 SGPRs.
+template <bool kBuf>
 __device__ __forceinline__ int dma_slot(const DmaSlots &d, int k, size_t c, int nbc, int st,
                                         int wave, int lane) {
   if (wave + 16 * k >= kDDma || d.blk[k] >= nbc)
@@ -386,21 +395,31 @@ __device__ __forceinline__ int dma_slot(const DmaSlots &d, int k, size_t c, int 
   const size_t coff = c * kDKB * kTRec;
   lds_void *to =
       (lds_void *)((char __attribute__((address_space(3))) *)d.dst[k] + st * d.stage_bytes[k]);
-  if (k + 1 < kDSlots)
-    __builtin_amdgcn_global_load_lds(d.base[k] + coff + lane * 16, to, 16, 0, 0);
-  else if (d.on_last)
+  if (k + 1 < kDSlots) {
+    if constexpr (kBuf) {
+      // dword 3: 32-bit data format (the form buffer_load_dword* takes on gfx9)
+      const __amdgpu_buffer_rsrc_t r =
+          __builtin_amdgcn_make_buffer_rsrc((void *)d.base[k], (short)0, -1, 0x00020000);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, to, 16, static_cast<unsigned>(lane * 16),
+                                               static_cast<unsigned>(coff), 0, 0);
+    } else {
+      __builtin_amdgcn_global_load_lds(d.base[k] + coff + lane * 16, to, 16, 0, 0);
+    }
+  } else if (d.on_last) {
     __builtin_amdgcn_global_load_lds(d.last + coff, to, 16, 0, 0);
+  }
   return 1;
 }
 
 // Issues this wave's whole DMA of K chunk c into stage st (the prologue);
 // returns how many DMA instructions it issued.
+template <bool kBuf>
 __device__ __forceinline__ int dma_chunk(const DmaSlots &d, size_t c, int nbc, int st,
                                          int wave, int lane) {
   int issued = 0;
 #pragma unroll
   for (int k = 0; k < kDSlots; ++k)
-    issued += dma_slot(d, k, c, nbc, st, wave, lane);
+    issued += dma_slot<kBuf>(d, k, c, nbc, st, wave, lane);
   return issued;
 }
 
@@ -521,8 +540,9 @@ __device__ __forceinline__ void gemm_tiles_body(size_t nb, float *s, const uint8
         widen_token_scales(dsh + sc * kHStage, fyd + sc * kFyStage, blocks_of(cc), wave, lane);
     }
   };
-  dma_chunk(slots, 0, blocks_of(0), 0, wave, lane);
-  int pending = kAhead > 1 && nchunks > 1 ? dma_chunk(slots, 1, blocks_of(1), 1, wave, lane) : 0;
+  dma_chunk<!kQ4>(slots, 0, blocks_of(0), 0, wave, lane);
+  int pending =
+      kAhead > 1 && nchunks > 1 ? dma_chunk<!kQ4>(slots, 1, blocks_of(1), 1, wave, lane) : 0;
   // chunk 0 is in LDS, the zero rows written
   wait_dma_barrier(pending, [&] { publish(0, 0); });
 
@@ -551,10 +571,10 @@ __device__ __forceinline__ void gemm_tiles_body(size_t nb, float *s, const uint8
       pending = 0;
       fold([&](int s) {
         if (s < kDSlots && ahead)
-          pending += dma_slot(slots, s, c + kAhead, nba, sta, wave, lane);
+          pending += dma_slot<!kQ4>(slots, s, c + kAhead, nba, sta, wave, lane);
       });
     } else {
-      pending = ahead ? dma_chunk(slots, c + kAhead, nba, sta, wave, lane) : 0;
+      pending = ahead ? dma_chunk<!kQ4>(slots, c + kAhead, nba, sta, wave, lane) : 0;
       fold([](int) {});
     }
     const int stn = st + 1 == kDStages ? 0 : st + 1;
@@ -662,6 +682,10 @@ __global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q4(size_t nb, float *
 namespace {
 
 constexpr bool kTiledPipe = true;
+// The Q8_0 tiled kernel's buffer-form DMA takes a K chunk's offset within a
+// 64-row group's records as a 32-bit soffset: nb * kTRec must stay below 2^32
+// (the last 1 KB kept for the lane offsets), K below 63 million.
+constexpr size_t kMaxTiledNb = ((static_cast<size_t>(1) << 32) - 1024) / tcrv::kTRec;
 
 size_t tile_bytes(size_t nrows, size_t nb) {
   return (nrows + tcrv::kTG - 1) / tcrv::kTG * nb * tcrv::kTRec;
@@ -795,6 +819,8 @@ int tcrv_hip_q8_0_q8_0_gemm_tiles(size_t n, float *s, const uint8_t *tx, const u
     return TCRV_HIP_ERR_BAD_SIZE;
   if (nb == 0)
     return zero_outputs(s, nr * nc, bs, nc, stream);
+  if (nb > kMaxTiledNb)
+    return TCRV_HIP_ERR_TOO_LARGE;
   if (!s || !tx || !ty)
     return TCRV_HIP_ERR_NULL_POINTER;
   if (!aligned16(tx) || !aligned16(ty))
@@ -808,9 +834,10 @@ namespace tcrv_host {
 
 // Shapes the tiled kernel does not serve run as tcrv_hip_q8_0_q8_0_gemm,
 // without the workspace: fewer weight rows than one 256-row tile, a single
-// token (decode), or no blocks.
+// token (decode), no blocks, or more than kMaxTiledNb blocks.
 bool gemm_ws_uses_workspace(size_t n, size_t nr, size_t nc) {
-  return nr >= static_cast<size_t>(tcrv::kDBM) && nc >= 2 && n / tcrv::kQK > 0;
+  const size_t nb = n / tcrv::kQK;
+  return nr >= static_cast<size_t>(tcrv::kDBM) && nc >= 2 && nb > 0 && nb <= kMaxTiledNb;
 }
 
 }  // namespace tcrv_host
