@@ -384,9 +384,9 @@ __device__ __forceinline__ void dma_slots(DmaSlots &d, int8_t *qs, uint16_t *dsh
 // soffset, one 32-bit lane offset shared by every slot) instead of
 // global_load_lds with a 64-bit vector address per slot; the chunk offset is
 // then 32-bit (nb * kTRec < 2^32, which the entries check).  The Q8_0 kernel
-// takes it (4096^3 tiles 162.0 against 164.8 us, and 165.7 against 167.7 with
-// another issue placement, interleaved A/B); the Q4_0 kernel, at its register
-// limit, would spill 18-20 SGPRs.
+// takes it (4096^3 tiles 171.1 -> 169.1 us, 110 instead of 118 VGPRs,
+// interleaved A/B); the Q4_0 kernel, at its register limit, would spill 18-20
+// SGPRs.
 template <bool kBuf>
 __device__ __forceinline__ int dma_slot(const DmaSlots &d, int k, size_t c, int nbc, int st,
                                         int wave, int lane) {
@@ -397,7 +397,9 @@ __device__ __forceinline__ int dma_slot(const DmaSlots &d, int k, size_t c, int 
       (lds_void *)((char __attribute__((address_space(3))) *)d.dst[k] + st * d.stage_bytes[k]);
   if (k + 1 < kDSlots) {
     if constexpr (kBuf) {
-      // dword 3: 32-bit data format (the form buffer_load_dword* takes on gfx9)
+      // no stride; every 32-bit offset in range (the addresses are the ones the
+      // global form would use); dword 3: 32-bit data format, as buffer_load_dword*
+      // takes it on gfx9
       const __amdgpu_buffer_rsrc_t r =
           __builtin_amdgcn_make_buffer_rsrc((void *)d.base[k], (short)0, -1, 0x00020000);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(r, to, 16, static_cast<unsigned>(lane * 16),
@@ -431,8 +433,9 @@ __device__ __forceinline__ int dma_chunk(const DmaSlots &d, size_t c, int nbc, i
 // and the four waves of a SIMD stall at once: ~700 cycles of a ~7700-cycle
 // chunk (per-wave cycle counters, Q8_0 4096^3).  kDmaSpread: slot k is issued
 // after fold step k instead, between the wave's MFMAs (Q8_0 4096^3 tiles
-// 164.7 -> 161.4 us, interleaved A/B).  The Q4_0 kernel keeps the DMA at the
-// chunk's start: it is at 128 VGPRs, and every spread placement spills.
+// 0.2-2 % faster on four boxes, interleaved A/B).  The Q4_0 kernel keeps the
+// DMA at the chunk's start: it is at its register limit, and every spread
+// placement spills.
 template <bool kQ4>
 constexpr bool kDmaSpread = !kQ4;
 static_assert(kDSlots <= 2 * kDKB, "a spread chunk issues one slot per fold step");
