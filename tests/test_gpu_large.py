@@ -198,3 +198,32 @@ def test_gemm_tiled_operands_over_2_gib(hip, oracle, dev):
         assert_f32_parity(got[:, :nc], want[:, :nc], what=f"{name} gemm_ws, operand past 2 GiB")
     del da, rows
     free()
+
+
+@pytest.mark.parametrize("nb", [1973789, 1973790])
+def test_q8_0_gemm_ws_at_the_tiled_block_bound(hip, oracle, dev, nb):
+    """K at the tiled Q8_0 GEMM's bound: n/32 = 1 973 789 blocks takes the tiled kernel, whose
+    last K chunk then sits 13 KB below 2^32 bytes into a group's records (the DMA's 32-bit
+    chunk offset); one block more runs the plain GEMM.  256 weight rows x 2 tokens; every row
+    repeats a 2048-block pattern along K (built on the device), so the sampled rows' bytes are
+    known on the host."""
+    nr, nc, pat = 256, 2, 2048
+    n = nb * 32
+    rb = nb * 34
+    reps = -(-nb // pat)
+    base_w = synth.q8_0_matrix(nr, pat * 32, 1031, 0.02)
+    base_a = synth.q8_0_matrix(nc, pat * 32, 1032, 1.0)
+    dw = torch.from_numpy(base_w).to(dev).repeat(1, reps)[:, :rb].contiguous()
+    da = torch.from_numpy(base_a).to(dev).repeat(1, reps)[:, :rb].contiguous()
+    wsb = hip.q8_0_q8_0_gemm_workspace_bytes(n, nr, nc)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    s = torch.full((nr * nc,), float("nan"), dtype=torch.float32, device=dev)
+    hip.q8_0_q8_0_gemm_ws(n, s, dw, da, rb, nr, nc, rb, nc, ws, wsb)
+    got = s.view(nr, nc).cpu().numpy()
+    del dw, da, ws, s
+    free()
+    pick = np.array([0, 1, 137, 255])
+    w_rows = np.ascontiguousarray(np.tile(base_w[pick], (1, reps))[:, :rb])
+    a_rows = np.ascontiguousarray(np.tile(base_a, (1, reps))[:, :rb])
+    want = oracle.gemm_q8_0(n, w_rows, a_rows, rb, len(pick), nc, rb, nc, 8).reshape(len(pick), nc)
+    assert_f32_parity(got[pick], want, what=f"q8_0 gemm_ws at nb = {nb}")
