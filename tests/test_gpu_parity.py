@@ -1026,6 +1026,61 @@ def test_q8_0_gemm_tiles_more_tiles_than_cus(hip, oracle, dev, nb):
         assert_f32_parity(got[r, :nc], row, what=f"row {r}")
 
 
+def _rounds(nr, nc, bm, bn, cus=256):
+    return -(-(-(-nr // bm) * -(-nc // bn)) // cus)
+
+
+@pytest.mark.parametrize("nr,nc,nb,xpad,ypad", [
+    (4096, 4096, 4, 0, 0),     # exactly one 4-block chunk: no DMA issued inside the fold
+    (4096, 4096, 5, 0, 0),     # one chunk + 1: chunk 0's fold issues only block 0's slots
+    (4096, 4096, 3, 0, 0),     # no full chunk: the tail alone
+    (4000, 4050, 13, 16, 4),   # partial tiles both ways, 3 chunks + 1, 2-byte aligned tokens
+    (65536, 256, 9, 0, 0),     # one token tile, 256 weight tiles
+    (256, 65536, 6, 2, 0),     # one weight tile, 256 token tiles, 2-byte aligned weights
+    (8192, 4096, 7, 0, 0),     # two rounds of work-groups
+])
+def test_q8_0_gemm_tiles_256x256(hip, oracle, dev, nr, nc, nb, xpad, ypad):
+    """Shapes that run the 256 x 256 work-group tile of the tiled Q8_0 GEMM (8 waves of
+    2 x 4 32 x 32 tiles, 4-block K chunks): the pre-packed entry and the workspace entry
+    equal the plain entry (another kernel, the same fold order) bit for bit over the whole
+    output, the padding columns stay untouched, and sampled rows, the last included, match
+    the oracle."""
+    assert _rounds(nr, nc, 256, 256) * 15 <= _rounds(nr, nc, 256, 128) * 8
+    n = nb * 32
+    w = np.pad(synth.q8_0_matrix(nr, n, 1041, 0.02), ((0, 0), (0, xpad)))
+    a = np.pad(synth.q8_0_matrix(nc, n, 1042, 1.0), ((0, 0), (0, ypad)))
+    w[0, 2:34] = 0x80
+    a[0, 2:34] = 0x80  # -128 x -128 block sums
+    dw, da = to_dev(w, dev), to_dev(a, dev)
+    bs = nc + 5
+    ref = empty_dev(nr * bs, torch.float32, dev)
+    hip.q8_0_q8_0_gemm(n, ref, dw, da, a.shape[1], nr, nc, w.shape[1], bs)
+    want = from_dev(ref).reshape(nr, bs)[:, :nc]
+    del ref
+    tx = empty_dev(hip.gemm_tiles_bytes(nr, nb), torch.uint8, dev)
+    ty = empty_dev(hip.gemm_tiles_bytes(nc, nb), torch.uint8, dev)
+    hip.pack_q8_0_to_gemm_tiles(nr, nb, dw, w.shape[1], tx)
+    hip.pack_q8_0_to_gemm_tiles(nc, nb, da, a.shape[1], ty)
+    s = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+    hip.q8_0_q8_0_gemm_tiles(n, s, tx, ty, nr, nc, bs)
+    got = from_dev(s).reshape(nr, bs)
+    assert np.array_equal(got[:, :nc].view(np.uint32), want.view(np.uint32)), "tiles != plain"
+    assert np.all(got[:, nc:] == -7.0)
+    del tx, ty
+    wsb = hip.q8_0_q8_0_gemm_workspace_bytes(n, nr, nc)
+    ws = empty_dev(wsb, torch.uint8, dev)
+    s.fill_(-7.0)
+    hip.q8_0_q8_0_gemm_ws(n, s, dw, da, a.shape[1], nr, nc, w.shape[1], bs, ws, wsb)
+    got = from_dev(s).reshape(nr, bs)
+    assert np.array_equal(got[:, :nc].view(np.uint32), want.view(np.uint32)), "ws != plain"
+    assert np.all(got[:, nc:] == -7.0)
+    rng = np.random.default_rng(nr ^ nc)
+    rows = np.unique(np.concatenate([[0, nr - 1], rng.choice(nr, 14, replace=False)]))
+    sub = np.ascontiguousarray(w[rows])
+    ora = oracle.gemm_q8_0(n, sub, a, a.shape[1], len(rows), nc, w.shape[1], nc, 8)
+    assert_f32_parity(got[rows, :nc], ora.reshape(len(rows), nc), what=f"{nr}x{nc}x{n} rows")
+
+
 def test_q8_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
     """Shapes the tiled kernel does not serve run the plain entry and leave the
     workspace alone; a workspace that is too small or misaligned is refused."""

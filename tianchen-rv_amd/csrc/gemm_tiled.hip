@@ -680,6 +680,151 @@ __global__ __launch_bounds__(kDThreads, 1) void gemm_tiles_q4(size_t nb, float *
   gemm_tiles_body<true, true>(nb, s, tx, ty, nr, nc, bs, qs, dsh, fyd);
 }
 
+// ---- the Q8_0 GEMM on 256 x 256 work-group tiles ----------------------------
+// 8 waves, two per SIMD, each folding 64 weight rows x 128 tokens (2 x 4 tiles,
+// 128 accumulator registers of the 256 a wave may hold at two waves per SIMD).
+// Against the 256 x 128 tile a K block's 512 staged rows feed twice the tiles:
+// a third fewer DMA instructions and half the LDS operand reads per tile and
+// block, and a 4096 x 4096 output is 256 work-groups, one per CU.  K chunks of
+// kEKB blocks in two LDS stages.  Wave w's DMA is its own row group's records
+// (groups 0-3 the weight tile's, 4-7 the token tile's): both halves of each of
+// the chunk's blocks, 1 KB per instruction from one scalar base; waves 0-3
+// also move the scales of block w (64 lanes: group l / 8, 16 bytes l % 8).
+constexpr int kEBM = 256, kEBN = 256, kEKB = 4;
+constexpr int kERows = kEBM + kEBN;   // 512 staged rows
+constexpr int kEHalf = kERows * 16;   // 8192: one half of one block, all rows
+constexpr int kEBlock = 2 * kEHalf;   // 16384
+constexpr int kEStage = kEKB * kEBlock;
+// fp16 scales per block row: 512 rows, then 128 zero rows (lanes 32-63 of
+// every tile, at its tile offset of up to 96 rows, read zeros: k-slots 4-7 of
+// the scale MFMA)
+constexpr int kEHRow = kERows + 128;
+constexpr int kEThreads = 512;
+constexpr int kEStages = 2;
+constexpr int kEQuantSlots = 2 * kEKB;  // quant DMA instructions per wave and chunk
+static_assert(kEStages * (kEStage + kEKB * kEHRow * 2) <= 160 * 1024,
+              "the stages fit the 160 KB of LDS");
+static_assert(kEKB <= 4, "the scale moves of a chunk are waves 0-3's");
+
+__device__ __forceinline__ void gemm_tiles256_body(size_t nb, float *s, const uint8_t *tx,
+                                                   const uint8_t *ty, size_t nr, size_t nc,
+                                                   size_t bs, int8_t *qs, uint16_t *dsh) {
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wm = wave & 3, wn = wave >> 2;  // 64 weight rows x 128 tokens per wave
+  const int li = lane & 31, h = lane >> 5;
+  const unsigned tiles_m = static_cast<unsigned>((nr + kEBM - 1) / kEBM);
+  const unsigned tiles_n = static_cast<unsigned>((nc + kEBN - 1) / kEBN);
+  unsigned tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const size_t m0 = static_cast<size_t>(tm) * kEBM;
+  const size_t n0 = static_cast<size_t>(tn) * kEBN;
+  const size_t ngx = (nr + kTG - 1) / kTG, ngy = (nc + kTG - 1) / kTG;
+  const size_t gx0 = m0 / kTG, gy0 = n0 / kTG;
+
+  float acc[2][4][16];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc[i][j][e] = 0.0f;
+
+  for (int k = tid; k < kEStages * kEKB * 128; k += kEThreads)  // the zero rows
+    dsh[(k >> 7) * kEHRow + kERows + (k & 127)] = 0;
+
+  // Row group g's records (groups past an operand's last re-read the last; their
+  // outputs are not stored).
+  auto group = [&](int g) {
+    return g < 4 ? tx + min(gx0 + g, ngx - 1) * nb * kTRec
+                 : ty + min(gy0 + (g - 4), ngy - 1) * nb * kTRec;
+  };
+  const uint8_t *own = group(wave);  // wave-uniform
+  const uint8_t *scl = group(lane >> 3) + static_cast<size_t>(wave) * kTRec + 2048 + (lane & 7) * 16;
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void *)own, (short)0, -1, 0x00020000);
+  constexpr int kHStage = kEKB * kEHRow;
+  // slot k < kEQuantSlots of chunk c into stage st: half k & 1 of block k >> 1
+  // (buffer form: the chunk's offset in the group's records as soffset, 32-bit as
+  // the entries check); slot kEQuantSlots: the scales of block `wave`
+  auto slot = [&](int k, size_t c, int nbc, int st) -> int {
+    if (k < kEQuantSlots) {
+      if ((k >> 1) >= nbc)
+        return 0;
+      lds_void *to = (lds_void *)(qs + st * kEStage + (k >> 1) * kEBlock + (k & 1) * kEHalf +
+                                  wave * kTG * 16);
+      const unsigned off = static_cast<unsigned>((c * kEKB + (k >> 1)) * kTRec + (k & 1) * 1024);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, to, 16, static_cast<unsigned>(lane * 16), off,
+                                               0, 0);
+      return 1;
+    }
+    if (wave >= nbc)
+      return 0;
+    __builtin_amdgcn_global_load_lds(scl + c * kEKB * kTRec,
+                                     (lds_void *)(dsh + st * kHStage + wave * kEHRow), 16, 0, 0);
+    return 1;
+  };
+  const size_t nchunks = (nb + kEKB - 1) / kEKB;
+  const size_t nfull = nb / kEKB;
+  auto blocks_of = [&](size_t c) {
+    return static_cast<int>(min(static_cast<size_t>(kEKB), nb - c * kEKB));
+  };
+#pragma unroll
+  for (int k = 0; k <= kEQuantSlots; ++k)
+    slot(k, 0, blocks_of(0), 0);
+  wait_dma_barrier(0);  // chunk 0 is in LDS, the zero rows written
+
+  // this lane's operands in stage 0, block 0, tile 0 (lanes 32-63: half 1 of the
+  // quants, the zero scale rows)
+  const int8_t *qa = qs + (h * kERows + wm * 64 + li) * 16;
+  const int8_t *qb = qs + (h * kERows + kEBM + wn * 128 + li) * 16;
+  const uint16_t *hx = dsh + (h ? kERows + li : wm * 64 + li);
+  const uint16_t *hy = dsh + (h ? kERows + li : kEBM + wn * 128 + li);
+
+  int st = 0;
+  for (size_t c = 0; c < nfull; ++c) {
+    const bool ahead = c + 1 < nchunks;
+    const int nba = ahead ? blocks_of(c + 1) : 0;
+    const int sta = st ^ 1;
+    // slot k of chunk c + 1 after fold step 3k, between the wave's MFMAs
+    fold_chunk_q8_2x4<kEKB, kEBlock, 32 * 16, kEHRow>(
+        acc, qa + st * kEStage, qb + st * kEStage, hx + st * kHStage, hy + st * kHStage,
+        [&](int s) {
+          if (s % 3 == 0 && s / 3 <= kEQuantSlots && ahead)
+            slot(s / 3, c + 1, nba, sta);
+        });
+    wait_dma_barrier(0);  // chunk c + 1 is in LDS; no wave reads stage st any more
+    st = sta;
+  }
+  const int nbc = static_cast<int>(nb - nfull * kEKB);
+  if (nbc > 0)
+    fold_tail_q8_2x4<kEBlock, 32 * 16, kEHRow>(acc, qa + st * kEStage, qb + st * kEStage,
+                                               hx + st * kHStage, hy + st * kHStage, nbc);
+
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const size_t col = n0 + wn * 128 + j * 32 + li;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const size_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (row < nr && col < nc)
+          s[row * bs + col] = acc[i][j][e];
+      }
+  }
+}
+
+__global__ __launch_bounds__(kEThreads, 1) void gemm_tiles256_q8(size_t nb, float *s,
+                                                                 const uint8_t *tx,
+                                                                 const uint8_t *ty, size_t nr,
+                                                                 size_t nc, size_t bs) {
+  __shared__ __align__(16) int8_t qs[kEStages * kEStage];
+  __shared__ __align__(16) uint16_t dsh[kEStages * kEKB * kEHRow];
+  gemm_tiles256_body(nb, s, tx, ty, nr, nc, bs, qs, dsh);
+}
+
 }  // namespace tcrv
 
 namespace {
@@ -777,15 +922,33 @@ int pack_tiles_both(size_t nb, const uint8_t *vx, size_t bx, size_t nr, uint8_t 
   return launch_status();
 }
 
+// Which Q8_0 kernel serves a shape: both fold every output in the same order, so
+// the choice is speed only.  One MI355X runs 256 work-groups of either kernel at
+// once (one per CU); a round of 256 x 256 tiles takes ~1.87 times a round of
+// 256 x 128 ones at equal K (4096^3: one round 150-152 us against two rounds in
+// 161 us), and a lone round of the smaller tile 93 us.  So the larger tile runs
+// when its rounds x 15 are at most the smaller tile's rounds x 8: at 4096 x 4096
+// outputs (one round against two) and at 8192 x 4096 (two against four), not at
+// 4096 x 2048 (half the CUs idle) or 4196 x 4166 (two against three).
+bool tiles256_first(size_t tiles, size_t tiles256) {
+  constexpr size_t kCUs = 256;
+  return (tiles256 + kCUs - 1) / kCUs * 15 <= (tiles + kCUs - 1) / kCUs * 8;
+}
+
 int gemm_tiles(size_t nb, float *s, const uint8_t *tx, const uint8_t *ty, size_t nr, size_t nc,
                size_t bs, hipStream_t st, bool q4 = false) {
   using namespace tcrv_host;
   const size_t tiles = ((nr + tcrv::kDBM - 1) / tcrv::kDBM) * ((nc + tcrv::kDBN - 1) / tcrv::kDBN);
   if (tiles > 0x7fffffffu)
     return TCRV_HIP_ERR_TOO_LARGE;
+  const size_t tiles256 =
+      ((nr + tcrv::kEBM - 1) / tcrv::kEBM) * ((nc + tcrv::kEBN - 1) / tcrv::kEBN);
   if (q4)
     tcrv::gemm_tiles_q4<<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kDThreads), 0, st>>>(
         nb, s, tx, ty, nr, nc, bs);
+  else if (tiles256_first(tiles, tiles256))
+    tcrv::gemm_tiles256_q8<<<dim3(static_cast<unsigned>(tiles256)), dim3(tcrv::kEThreads), 0,
+                             st>>>(nb, s, tx, ty, nr, nc, bs);
   else
     tcrv::gemm_tiles_q8<kTiledPipe><<<dim3(static_cast<unsigned>(tiles)),
                                       dim3(tcrv::kDThreads), 0, st>>>(nb, s, tx, ty, nr, nc, bs);

@@ -179,6 +179,84 @@ __device__ __forceinline__ void fold_tail_q8(float (&acc)[2][16], const int8_t *
   }
 }
 
+// ---- the Q8_0 fold over 2 x 4 tiles per wave ------------------------------
+// One chunk of kBlocks blocks for a wave's two weight tiles (A operand at
+// qa + i * kTile bytes, d_x at hx + 32 i) and four token tiles (B operand at
+// qb + j * kTile, d_y at hy + 32 j); block b is kBlockStride bytes and
+// kScaleRow scales further.  Steps s = 8b + 2j + i, so every tile's blocks are
+// folded in ascending order.  As in fold_chunk_q8 the block-sum MFMA of step
+// s+1 is issued in step s; here every LDS read also lands a whole step before
+// the MFMA that takes it (two waves per SIMD hide less latency than four): the
+// token operand and d_y of tile j+1 are read in step (b, j, 0), the next
+// block's weight operands and d_x in steps (b, 3, 0), (b, 3, 1) and
+// (b+1, 0, 0), each into the registers of an operand whose last MFMA has been
+// issued (two weight and two token fragments, two d_x and two d_y words).
+template <int kBlocks, int kBlockStride, int kTile, int kScaleRow, typename AfterStep>
+__device__ __forceinline__ void fold_chunk_q8_2x4(float (&acc)[2][4][16], const int8_t *qa,
+                                                  const int8_t *qb, const uint16_t *hx,
+                                                  const uint16_t *hy, AfterStep &&after_step) {
+  v4i w[2], t[2];
+  uint32_t ux[2], uy[2];
+  w[0] = q8_frag<kBlockStride>(qa, 0);
+  w[1] = q8_frag<kBlockStride>(qa + kTile, 0);
+  t[0] = q8_frag<kBlockStride>(qb, 0);
+  ux[0] = q8_scale<kScaleRow>(hx, 0);
+  ux[1] = q8_scale<kScaleRow>(hx + 32, 0);
+  uy[0] = q8_scale<kScaleRow>(hy, 0);
+  v16i cur = q8_sumi(w[0], t[0]);
+#pragma unroll
+  for (int s = 0; s < 8 * kBlocks; ++s) {
+    const int b = s >> 3, j = (s >> 1) & 3, i = s & 1;
+    if (i == 0) {
+      if (j < 3) {
+        t[(j + 1) & 1] = q8_frag<kBlockStride>(qb + (j + 1) * kTile, b);
+        uy[(j + 1) & 1] = q8_scale<kScaleRow>(hy + 32 * (j + 1), b);
+      } else if (b + 1 < kBlocks) {
+        t[0] = q8_frag<kBlockStride>(qb, b + 1);
+        uy[0] = q8_scale<kScaleRow>(hy, b + 1);
+        w[0] = q8_frag<kBlockStride>(qa, b + 1);
+      }
+      if (j == 0 && b > 0)
+        ux[1] = q8_scale<kScaleRow>(hx + 32, b);
+    } else if (j == 3 && b + 1 < kBlocks) {
+      w[1] = q8_frag<kBlockStride>(qa + kTile, b + 1);
+      ux[0] = q8_scale<kScaleRow>(hx, b + 1);
+    }
+    v16i nxt;
+    if (s + 1 < 8 * kBlocks)
+      nxt = q8_sumi(w[(s + 1) & 1], t[((s + 1) >> 1) & 1]);
+    const v16f dxy = q8_dxy(ux[i], uy[j & 1]);
+    q8_fold(acc[i][j], cur, dxy);
+    if (s + 1 < 8 * kBlocks) {
+      asm volatile("" : "+v"(nxt));
+      cur = nxt;
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // LDS reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x002, 40, 0); // VALU
+    __builtin_amdgcn_sched_barrier(0);
+    after_step(s);
+  }
+}
+
+// A trailing partial chunk of nbc blocks over the 2 x 4 tiles, one step at a time.
+template <int kBlockStride, int kTile, int kScaleRow>
+__device__ __forceinline__ void fold_tail_q8_2x4(float (&acc)[2][4][16], const int8_t *qa,
+                                                 const int8_t *qb, const uint16_t *hx,
+                                                 const uint16_t *hy, int nbc) {
+  for (int b = 0; b < nbc; ++b) {
+    const v4i w0 = q8_frag<kBlockStride>(qa, b), w1 = q8_frag<kBlockStride>(qa + kTile, b);
+    const uint32_t ux0 = q8_scale<kScaleRow>(hx, b), ux1 = q8_scale<kScaleRow>(hx + 32, b);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const v4i t = q8_frag<kBlockStride>(qb + j * kTile, b);
+      const uint32_t uy = q8_scale<kScaleRow>(hy + 32 * j, b);
+      q8_fold(acc[0][j], q8_sumi(w0, t), q8_dxy(ux0, uy));
+      q8_fold(acc[1][j], q8_sumi(w1, t), q8_dxy(ux1, uy));
+    }
+  }
+}
+
 // ---- the Q4_0 x Q8_0 fold ----------------------------------------------
 // Per tile and block the reference folds acc = fma(fl((float)sumi * d_x), d_y,
 // acc) (RVVToEmitCBlockQuantLinear.cpp:322-356): the product with d_x is
