@@ -88,11 +88,30 @@ __device__ __forceinline__ v16f q8_dxy(uint32_t ux, uint32_t uy) {
 // The fold of one step.  The empty asm pins the folded accumulators at this
 // point of the instruction stream: instruction selection otherwise sinks the
 // pure VALU work past every scheduling fence to the end of the chunk, where
-// all the steps' MFMA results are then live at once.
+// all the steps' MFMA results are then live at once.  kConvertFirst: all 16
+// conversions (in place) before the first fma, which then reads a scale
+// product whose MFMA was issued ~16 conversions earlier instead of ~4 (with
+// two waves per SIMD the other wave hides less of that wait: the 256 x 256
+// tiled kernel 154.3 -> 151.3 us at 4096^3; the four-wave kernels gain
+// nothing).  The same operations in the same order per element either way.
+template <bool kConvertFirst = false>
 __device__ __forceinline__ void q8_fold(float (&acc)[16], const v16i &sumi, const v16f &dxy) {
+  if constexpr (kConvertFirst) {
+    float f[16];
 #pragma unroll
-  for (int e = 0; e < 16; ++e)
-    acc[e] = fmaf(static_cast<float>(sumi[e]), dxy[e], acc[e]);
+    for (int e = 0; e < 16; ++e)
+      f[e] = static_cast<float>(sumi[e]);
+    asm volatile("" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]),
+                 "+v"(f[6]), "+v"(f[7]), "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]),
+                 "+v"(f[12]), "+v"(f[13]), "+v"(f[14]), "+v"(f[15]));
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      acc[e] = fmaf(f[e], dxy[e], acc[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      acc[e] = fmaf(static_cast<float>(sumi[e]), dxy[e], acc[e]);
+  }
 #pragma unroll
   for (int e = 0; e < 16; ++e)
     asm volatile("" : "+v"(acc[e]));
@@ -226,7 +245,7 @@ __device__ __forceinline__ void fold_chunk_q8_2x4(float (&acc)[2][4][16], const 
     if (s + 1 < 8 * kBlocks)
       nxt = q8_sumi(w[(s + 1) & 1], t[((s + 1) >> 1) & 1]);
     const v16f dxy = q8_dxy(ux[i], uy[j & 1]);
-    q8_fold(acc[i][j], cur, dxy);
+    q8_fold<true>(acc[i][j], cur, dxy);
     if (s + 1 < 8 * kBlocks) {
       asm volatile("" : "+v"(nxt));
       cur = nxt;
