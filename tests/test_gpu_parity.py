@@ -1081,6 +1081,51 @@ def test_q8_0_gemm_tiles_256x256(hip, oracle, dev, nr, nc, nb, xpad, ypad):
     assert_f32_parity(got[rows, :nc], ora.reshape(len(rows), nc), what=f"{nr}x{nc}x{n} rows")
 
 
+@pytest.mark.parametrize("nr,nc,nb,xpad,ypad", [
+    (4096, 4096, 4, 0, 0),     # exactly one 4-block chunk
+    (4096, 4096, 5, 0, 0),     # one chunk + 1
+    (4096, 4096, 3, 0, 0),     # the tail alone
+    (4000, 4050, 13, 16, 4),   # partial tiles both ways, 3 chunks + 1, 2-byte aligned tokens
+    (65536, 256, 9, 0, 0),     # one token tile
+    (256, 65536, 6, 2, 0),     # one weight tile
+    (8192, 4096, 7, 0, 0),     # two rounds of work-groups
+])
+def test_q4_0_gemm_tiles_256x256(hip, oracle, dev, nr, nc, nb, xpad, ypad):
+    """The tiled Q4_0 GEMM at the shapes that run its 256 x 256 work-group tile (8 waves of
+    2 x 4 transposed 32 x 32 tiles, fp32 token scales widened per chunk, stores through
+    LDS): the pre-packed entry and the workspace entry equal the plain Q4_0 entry (another
+    kernel, the same fold) bit for bit over the whole output, padding columns untouched,
+    sampled rows, the last included, against the oracle."""
+    assert _rounds(nr, nc, 256, 256) * 15 <= _rounds(nr, nc, 256, 128) * 8
+    n = nb * 32
+    w = np.pad(synth.q4_0_matrix(nr, n, 1043, 0.02), ((0, 0), (0, xpad)))
+    a = np.pad(synth.q8_0_matrix(nc, n, 1044, 1.0), ((0, 0), (0, ypad)))
+    a[0, 2:34] = 0x80
+    dw, da = to_dev(w, dev), to_dev(a, dev)
+    bs = nc + 5
+    ref = empty_dev(nr * bs, torch.float32, dev)
+    hip.q4_0_q8_0_gemm(n, ref, dw, da, a.shape[1], nr, nc, w.shape[1], bs)
+    want = from_dev(ref).reshape(nr, bs)[:, :nc]
+    del ref
+    s = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+    q4_tiles_gemm(hip, dev, n, w, a, nr, nc, bs, s)
+    got = from_dev(s).reshape(nr, bs)
+    assert np.array_equal(got[:, :nc].view(np.uint32), want.view(np.uint32)), "tiles != plain"
+    assert np.all(got[:, nc:] == -7.0)
+    wsb = hip.q4_0_q8_0_gemm_workspace_bytes(n, nr, nc)
+    ws = empty_dev(wsb, torch.uint8, dev)
+    s.fill_(-7.0)
+    hip.q4_0_q8_0_gemm_ws(n, s, dw, da, a.shape[1], nr, nc, w.shape[1], bs, ws, wsb)
+    got = from_dev(s).reshape(nr, bs)
+    assert np.array_equal(got[:, :nc].view(np.uint32), want.view(np.uint32)), "ws != plain"
+    assert np.all(got[:, nc:] == -7.0)
+    rng = np.random.default_rng(nr ^ nc ^ 1)
+    rows = np.unique(np.concatenate([[0, nr - 1], rng.choice(nr, 14, replace=False)]))
+    sub = np.ascontiguousarray(w[rows])
+    ora = oracle.gemm_q4_0(n, sub, a, a.shape[1], len(rows), nc, w.shape[1], nc, 8)
+    assert_f32_parity(got[rows, :nc], ora.reshape(len(rows), nc), what=f"{nr}x{nc}x{n} rows")
+
+
 def test_q8_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
     """Shapes the tiled kernel does not serve run the plain entry and leave the
     workspace alone; a workspace that is too small or misaligned is refused."""

@@ -175,6 +175,46 @@ def test_q4_0_gemm_nonfinite_dx_mid_k(hip, oracle, dev, nb):
     assert np.isinf(g[70]).any() and np.isnan(g[400]).all()  # the planted cases took effect
 
 
+@pytest.mark.parametrize("quant,nonfinite_every", [("q8_0", 16), ("q4_0", 16), ("q4_0", 0)])
+def test_gemm_ws_256x256_special_scales(hip, oracle, dev, quant, nonfinite_every):
+    """The 256 x 256 work-group tiles of the tiled GEMMs (4096 x 4096 outputs, through the
+    workspace entries): special scales in both operands, non-finite d_x in every 16th weight
+    row (every Q4_0 wave folds exactly from chunk 0) or, with none there, +-Inf and NaN
+    planted at chunk 0, in the middle of K, in the last full chunk and in the 1-block tail,
+    and an infinite d_x over a zero block sum.  Sampled rows, the planted ones included,
+    against the oracle."""
+    nr = nc = 4096
+    nb = 13  # 3 chunks of 4 blocks + 1
+    n = nb * 32
+    if quant == "q8_0":
+        w, blk = q8(nr, nb, 51, 0.02, nonfinite_every=nonfinite_every), 34
+    else:
+        w, blk = q4(nr, nb, 52, nonfinite_every=nonfinite_every), 18
+    a = q8(nc, nb, 53, 1.0, nonfinite_every=37)
+    planted = ((70, 2, 0x7C00), (130, 0, 0xFC00), (200, 12, 0x7E00), (330, 11, 0x7C00),
+               (400, 5, 0xFC00), (450, 9, 0x7C00))
+    if not nonfinite_every:
+        for r, b, bits in planted:
+            _set_scale(w, r, b, blk, bits)
+        q0 = 0x88 if quant == "q4_0" else 0x00  # every quant 0: block sums 0
+        w[400, 5 * blk + 2:6 * blk] = q0
+    wsb = getattr(hip, f"{quant}_q8_0_gemm_workspace_bytes")(n, nr, nc)
+    ws = empty_dev(wsb, torch.uint8, dev)
+    s = empty_dev(nr * nc, torch.float32, dev)
+    getattr(hip, f"{quant}_q8_0_gemm_ws")(n, s, to_dev(w, dev), to_dev(a, dev), a.shape[1], nr,
+                                          nc, w.shape[1], nc, ws, wsb)
+    got = from_dev(s).reshape(nr, nc)
+    rng = np.random.default_rng(5)
+    rows = np.unique(np.concatenate([[0, 1, 15, nr - 1], [r for r, _, _ in planted],
+                                     rng.choice(nr, 20, replace=False)]))
+    sub = np.ascontiguousarray(w[rows])
+    ref = oracle.gemm_q8_0 if quant == "q8_0" else oracle.gemm_q4_0
+    want = ref(n, sub, a, a.shape[1], len(rows), nc, w.shape[1], nc, 8)
+    assert_f32_parity_nan(got[rows].reshape(-1), want, what=f"{quant} 256x256 tiles")
+    if not nonfinite_every:
+        assert np.isinf(got[70]).any() and np.isnan(got[400]).all()  # the planted cases
+
+
 def _x16_source(w, nb, k):
     nc = w.shape[0]
     return np.ascontiguousarray(np.concatenate(

@@ -706,21 +706,195 @@ static_assert(kEStages * (kEStage + kEKB * kEHRow * 2) <= 160 * 1024,
               "the stages fit the 160 KB of LDS");
 static_assert(kEKB <= 4, "the scale moves of a chunk are waves 0-3's");
 
+// kQ4: the weight groups hold Q4_0 rows decoded to int8 (as gemm_tiles_q4's)
+// and the fold is the Q4_0 one on transposed tiles (fold_chunk_q4_2x4): the
+// waves that move a block's scales (waves 0-3, block w) also widen its 256
+// token scales to the fp32 row fyd before the barrier that publishes the
+// chunk, the fast fold runs until a chunk holds a non-finite d_x among the
+// wave's weight rows, and each tile is stored through a wave-private LDS
+// buffer (as gemm_tiles_body's Q4_0 stores).
+constexpr int kEFyStage = kEKB * kEBN;  // fp32 token scales per stage
+static_assert(kEStages * (kEStage + kEKB * kEHRow * 2 + kEFyStage * 4) <= 160 * 1024,
+              "the Q4_0 stages fit the 160 KB of LDS");
+
+// LDS DMA written as inline assembly, for code whose DMA the compiler must not
+// track (the exact-form loop of the 256 x 256 Q4_0 kernel).  The compiler then
+// inserts no wait for these loads: the kernels wait for them explicitly (the
+// vmcnt wait before each chunk's barrier), as they do for the intrinsic form.
+// M0 (the LDS destination) is saved and restored around the instruction, and
+// "memory" keeps every other memory access on its side of it.
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// buffer_load_dwordx4 ... offen lds: 16 bytes per lane from base + soff + voff
+// (resource: no stride, every 32-bit offset in range, dword 3 as
+// __builtin_amdgcn_make_buffer_rsrc takes it) into LDS at `to` + 16 * lane.
+__device__ __forceinline__ void buffer_load_lds_asm(const uint8_t *base, unsigned voff,
+                                                    unsigned soff, lds_void *to) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const v4u rsrc = {
+      static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<unsigned>(a))),
+      static_cast<unsigned>(
+          __builtin_amdgcn_readfirstlane(static_cast<unsigned>(a >> 32) & 0xFFFFu)),
+      0xFFFFFFFFu, 0x00020000u};
+  const unsigned m0 = static_cast<unsigned>(
+      __builtin_amdgcn_readfirstlane(static_cast<unsigned>(reinterpret_cast<uintptr_t>(to))));
+  const unsigned so = static_cast<unsigned>(__builtin_amdgcn_readfirstlane(soff));
+  unsigned saved;
+  asm volatile("s_mov_b32 %0, m0\n\t"
+               "s_mov_b32 m0, %1\n\t"
+               "s_nop 0\n\t"
+               "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+               "s_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "s"(m0), "v"(voff), "s"(rsrc), "s"(so)
+               : "memory");
+}
+
+// global_load_lds_dwordx4: 16 bytes per lane from `from` into LDS at `to` +
+// 16 * lane.
+__device__ __forceinline__ void global_load_lds_asm(const uint8_t *from, lds_void *to) {
+  const unsigned m0 = static_cast<unsigned>(
+      __builtin_amdgcn_readfirstlane(static_cast<unsigned>(reinterpret_cast<uintptr_t>(to))));
+  unsigned saved;
+  asm volatile("s_mov_b32 %0, m0\n\t"
+               "s_mov_b32 m0, %1\n\t"
+               "s_nop 0\n\t"
+               "global_load_lds_dwordx4 %2, off\n\t"
+               "s_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "s"(m0), "v"(from)
+               : "memory");
+}
+
+// One wave's view of a 256 x 256 work-group: its tile, its DMA slots and the
+// LDS operands of its lanes.
+struct Tiles256 {
+  int wave, lane, wm, wn, li, h;  // wm, wn: 64 weight rows x 128 tokens per wave
+  size_t m0, n0, nb, nchunks;
+  const uint8_t *own;  // the wave's row group's records (wave-uniform)
+  const uint8_t *scl;  // this lane's 16 scale bytes of block `wave` of chunk 0
+  int8_t *qs;
+  uint16_t *dsh;
+  float *fyd;
+
+  __device__ Tiles256(size_t nb_, const uint8_t *tx, const uint8_t *ty, size_t nr, size_t nc,
+                      int8_t *qs_, uint16_t *dsh_, float *fyd_)
+      : nb(nb_), qs(qs_), dsh(dsh_), fyd(fyd_) {
+    const int tid = threadIdx.x;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    lane = tid & 63;
+    wm = wave & 3;
+    wn = wave >> 2;
+    li = lane & 31;
+    h = lane >> 5;
+    const unsigned tiles_m = static_cast<unsigned>((nr + kEBM - 1) / kEBM);
+    const unsigned tiles_n = static_cast<unsigned>((nc + kEBN - 1) / kEBN);
+    unsigned tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    m0 = static_cast<size_t>(tm) * kEBM;
+    n0 = static_cast<size_t>(tn) * kEBN;
+    const size_t ngx = (nr + kTG - 1) / kTG, ngy = (nc + kTG - 1) / kTG;
+    const size_t gx0 = m0 / kTG, gy0 = n0 / kTG;
+    // row group g's records (groups past an operand's last re-read the last;
+    // their outputs are not stored)
+    auto group = [&](int g) {
+      return g < 4 ? tx + min(gx0 + g, ngx - 1) * nb * kTRec
+                   : ty + min(gy0 + (g - 4), ngy - 1) * nb * kTRec;
+    };
+    own = group(wave);
+    scl = group(lane >> 3) + static_cast<size_t>(wave) * kTRec + 2048 + (lane & 7) * 16;
+    nchunks = (nb + kEKB - 1) / kEKB;
+  }
+
+  __device__ int blocks_of(size_t c) const {
+    return static_cast<int>(min(static_cast<size_t>(kEKB), nb - c * kEKB));
+  }
+
+  // Slot k < kEQuantSlots of chunk c into stage st: half k & 1 of block k >> 1
+  // (buffer form: the wave's records as the resource base in scalar registers,
+  // the chunk's offset in them as soffset, 32-bit as the entries check); slot
+  // kEQuantSlots: the scales of block `wave`.  Returns 1 if it moved anything.
+  // kAsm: the same two instructions as inline assembly (buffer_load_lds_asm,
+  // global_load_lds_asm), which the compiler does not see as LDS writes.
+  template <bool kAsm = false>
+  __device__ int slot(int k, size_t c, int nbc, int st) const {
+    if (k < kEQuantSlots) {
+      if ((k >> 1) >= nbc)
+        return 0;
+      lds_void *to = (lds_void *)(qs + st * kEStage + (k >> 1) * kEBlock + (k & 1) * kEHalf +
+                                  wave * kTG * 16);
+      const unsigned off = static_cast<unsigned>((c * kEKB + (k >> 1)) * kTRec + (k & 1) * 1024);
+      if constexpr (kAsm) {
+        buffer_load_lds_asm(own, static_cast<unsigned>(lane * 16), off, to);
+      } else {
+        const __amdgpu_buffer_rsrc_t rsrc =
+            __builtin_amdgcn_make_buffer_rsrc((void *)own, (short)0, -1, 0x00020000);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, to, 16, static_cast<unsigned>(lane * 16),
+                                                 off, 0, 0);
+      }
+      return 1;
+    }
+    if (wave >= nbc)
+      return 0;
+    const uint8_t *from = scl + c * kEKB * kTRec;
+    lds_void *to = (lds_void *)(dsh + st * kEKB * kEHRow + wave * kEHRow);
+    if constexpr (kAsm)
+      global_load_lds_asm(from, to);
+    else
+      __builtin_amdgcn_global_load_lds(from, to, 16, 0, 0);
+    return 1;
+  }
+
+  // Between a chunk's DMA wait and its barrier: the Q4_0 fold's fp32 token
+  // scales of chunk cc in stage sc, widened by the wave that moved them (its
+  // own loads have landed after its wait), four per lane.
+  __device__ void publish_q4(size_t cc, int sc) const {
+    if (cc < nchunks && wave < blocks_of(cc)) {
+#pragma unroll
+      for (int k = 0; k < kEBN / 64; ++k) {
+        const int t = lane + 64 * k;
+        fyd[sc * kEFyStage + wave * kEBN + t] = static_cast<float>(__builtin_bit_cast(
+            _Float16, dsh[sc * kEKB * kEHRow + wave * kEHRow + kEBM + t]));
+      }
+    }
+  }
+
+  // this lane's operands in stage 0, block 0, tile 0 (lanes 32-63: half 1 of the
+  // quants; for the Q8_0 fold the zero scale rows)
+  __device__ const int8_t *qa() const { return qs + (h * kERows + wm * 64 + li) * 16; }
+  __device__ const int8_t *qb() const { return qs + (h * kERows + kEBM + wn * 128 + li) * 16; }
+  __device__ const uint16_t *hx() const { return dsh + (h ? kERows + li : wm * 64 + li); }
+  __device__ const uint16_t *hy() const { return dsh + (h ? kERows + li : kEBM + wn * 128 + li); }
+  // the Q4_0 fold: d_x of the lane's weight row li, fp32 d_y of its tokens 4h..
+  __device__ const uint16_t *q4x() const { return dsh + wm * 64 + li; }
+  __device__ const float *q4y() const { return fyd + wn * 128 + 4 * h; }
+};
+
+// Full chunk c of the 256 x 256 kernel in stage st: the fold (`fold(after_step)`,
+// slot k of chunk c + 1 issued after its step 3k), then the wait for chunk c + 1,
+// `publish(c + 1, stage)` and the barrier.  Returns the stage of chunk c + 1.
+template <bool kAsm = false, typename Fold, typename Publish>
+__device__ __forceinline__ int chunk256(const Tiles256 &t, size_t c, int st, Fold &&fold,
+                                        Publish &&publish) {
+  const bool ahead = c + 1 < t.nchunks;
+  const int nba = ahead ? t.blocks_of(c + 1) : 0;
+  const int sta = st ^ 1;
+  fold([&](int s) {
+    if (s % 3 == 0 && s / 3 <= kEQuantSlots && ahead)
+      t.template slot<kAsm>(s / 3, c + 1, nba, sta);
+  });
+  wait_dma_barrier(0, [&] { publish(c + 1, sta); });  // no wave reads stage st any more
+  return sta;
+}
+
+template <bool kQ4>
 __device__ __forceinline__ void gemm_tiles256_body(size_t nb, float *s, const uint8_t *tx,
                                                    const uint8_t *ty, size_t nr, size_t nc,
-                                                   size_t bs, int8_t *qs, uint16_t *dsh) {
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int wm = wave & 3, wn = wave >> 2;  // 64 weight rows x 128 tokens per wave
-  const int li = lane & 31, h = lane >> 5;
-  const unsigned tiles_m = static_cast<unsigned>((nr + kEBM - 1) / kEBM);
-  const unsigned tiles_n = static_cast<unsigned>((nc + kEBN - 1) / kEBN);
-  unsigned tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const size_t m0 = static_cast<size_t>(tm) * kEBM;
-  const size_t n0 = static_cast<size_t>(tn) * kEBN;
-  const size_t ngx = (nr + kTG - 1) / kTG, ngy = (nc + kTG - 1) / kTG;
-  const size_t gx0 = m0 / kTG, gy0 = n0 / kTG;
+                                                   size_t bs, int8_t *qs, uint16_t *dsh,
+                                                   float *fyd) {
+  const Tiles256 t(nb, tx, ty, nr, nc, qs, dsh, fyd);
+  const int tid = threadIdx.x, li = t.li, h = t.h, wm = t.wm, wn = t.wn;
+  constexpr int kHStage = kEKB * kEHRow;
 
   float acc[2][4][16];
 #pragma unroll
@@ -731,88 +905,109 @@ __device__ __forceinline__ void gemm_tiles256_body(size_t nb, float *s, const ui
       for (int e = 0; e < 16; ++e)
         acc[i][j][e] = 0.0f;
 
-  for (int k = tid; k < kEStages * kEKB * 128; k += kEThreads)  // the zero rows
-    dsh[(k >> 7) * kEHRow + kERows + (k & 127)] = 0;
+  if constexpr (!kQ4)
+    for (int k = tid; k < kEStages * kEKB * 128; k += kEThreads)  // the zero rows
+      dsh[(k >> 7) * kEHRow + kERows + (k & 127)] = 0;
 
-  // Row group g's records (groups past an operand's last re-read the last; their
-  // outputs are not stored).
-  auto group = [&](int g) {
-    return g < 4 ? tx + min(gx0 + g, ngx - 1) * nb * kTRec
-                 : ty + min(gy0 + (g - 4), ngy - 1) * nb * kTRec;
-  };
-  const uint8_t *own = group(wave);  // wave-uniform
-  const uint8_t *scl = group(lane >> 3) + static_cast<size_t>(wave) * kTRec + 2048 + (lane & 7) * 16;
-  const __amdgpu_buffer_rsrc_t rsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void *)own, (short)0, -1, 0x00020000);
-  constexpr int kHStage = kEKB * kEHRow;
-  // slot k < kEQuantSlots of chunk c into stage st: half k & 1 of block k >> 1
-  // (buffer form: the chunk's offset in the group's records as soffset, 32-bit as
-  // the entries check); slot kEQuantSlots: the scales of block `wave`
-  auto slot = [&](int k, size_t c, int nbc, int st) -> int {
-    if (k < kEQuantSlots) {
-      if ((k >> 1) >= nbc)
-        return 0;
-      lds_void *to = (lds_void *)(qs + st * kEStage + (k >> 1) * kEBlock + (k & 1) * kEHalf +
-                                  wave * kTG * 16);
-      const unsigned off = static_cast<unsigned>((c * kEKB + (k >> 1)) * kTRec + (k & 1) * 1024);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, to, 16, static_cast<unsigned>(lane * 16), off,
-                                               0, 0);
-      return 1;
-    }
-    if (wave >= nbc)
-      return 0;
-    __builtin_amdgcn_global_load_lds(scl + c * kEKB * kTRec,
-                                     (lds_void *)(dsh + st * kHStage + wave * kEHRow), 16, 0, 0);
-    return 1;
-  };
-  const size_t nchunks = (nb + kEKB - 1) / kEKB;
-  const size_t nfull = nb / kEKB;
-  auto blocks_of = [&](size_t c) {
-    return static_cast<int>(min(static_cast<size_t>(kEKB), nb - c * kEKB));
+  auto publish = [&](size_t cc, int sc) {
+    if constexpr (kQ4)
+      t.publish_q4(cc, sc);
   };
 #pragma unroll
   for (int k = 0; k <= kEQuantSlots; ++k)
-    slot(k, 0, blocks_of(0), 0);
-  wait_dma_barrier(0);  // chunk 0 is in LDS, the zero rows written
+    t.slot(k, 0, t.blocks_of(0), 0);
+  wait_dma_barrier(0, [&] { publish(0, 0); });  // chunk 0 is in LDS, the zero rows written
 
-  // this lane's operands in stage 0, block 0, tile 0 (lanes 32-63: half 1 of the
-  // quants, the zero scale rows)
-  const int8_t *qa = qs + (h * kERows + wm * 64 + li) * 16;
-  const int8_t *qb = qs + (h * kERows + kEBM + wn * 128 + li) * 16;
-  const uint16_t *hx = dsh + (h ? kERows + li : wm * 64 + li);
-  const uint16_t *hy = dsh + (h ? kERows + li : kEBM + wn * 128 + li);
-
+  const int8_t *qa = t.qa(), *qb = t.qb();
   int st = 0;
-  for (size_t c = 0; c < nfull; ++c) {
-    const bool ahead = c + 1 < nchunks;
-    const int nba = ahead ? blocks_of(c + 1) : 0;
-    const int sta = st ^ 1;
-    // slot k of chunk c + 1 after fold step 3k, between the wave's MFMAs
-    fold_chunk_q8_2x4<kEKB, kEBlock, 32 * 16, kEHRow>(
-        acc, qa + st * kEStage, qb + st * kEStage, hx + st * kHStage, hy + st * kHStage,
-        [&](int s) {
-          if (s % 3 == 0 && s / 3 <= kEQuantSlots && ahead)
-            slot(s / 3, c + 1, nba, sta);
-        });
-    wait_dma_barrier(0);  // chunk c + 1 is in LDS; no wave reads stage st any more
-    st = sta;
-  }
+  size_t c = 0;
+  const size_t nfull = nb / kEKB;
   const int nbc = static_cast<int>(nb - nfull * kEKB);
-  if (nbc > 0)
-    fold_tail_q8_2x4<kEBlock, 32 * 16, kEHRow>(acc, qa + st * kEStage, qb + st * kEStage,
-                                               hx + st * kHStage, hy + st * kHStage, nbc);
-
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const size_t col = n0 + wn * 128 + j * 32 + li;
+  const size_t m0 = t.m0, n0 = t.n0;
+  if constexpr (kQ4) {
+    const uint16_t *qx = t.q4x();
+    const float *qy = t.q4y();
+    // The fast fold until a chunk holds a non-finite d_x among the wave's
+    // weight rows, then the exact one.  The exact loop issues its DMA as
+    // inline assembly: with a second copy of the DMA intrinsics in the kernel,
+    // the compiler makes every LDS read of the fast loop that follows a DMA
+    // issue wait for that DMA (4096^3 185 against 155 us).
+    for (; c < nfull; ++c) {
+      if (q4_chunk_nonfinite<kEHRow>(dsh + st * kHStage + wm * 64, kEKB, t.lane))
+        break;
+      st = chunk256(
+          t, c, st,
+          [&](auto after_step) {
+            fold_chunk_q4_2x4<false, kEKB, kEBlock, 32 * 16, kEHRow, kEBN>(
+                acc, qa + st * kEStage, qb + st * kEStage, qx + st * kHStage,
+                qy + st * kEFyStage, after_step);
+          },
+          publish);
+    }
+    for (; c < nfull; ++c)
+      st = chunk256<true>(
+          t, c, st,
+          [&](auto after_step) {
+            fold_chunk_q4_2x4<true, kEKB, kEBlock, 32 * 16, kEHRow, kEBN>(
+                acc, qa + st * kEStage, qb + st * kEStage, qx + st * kHStage,
+                qy + st * kEFyStage, after_step);
+          },
+          publish);
+    if (nbc > 0)
+      fold_tail_q4_2x4<true, kEBlock, 32 * 16, kEHRow, kEBN>(
+          acc, qa + st * kEStage, qb + st * kEStage, qx + st * kHStage, qy + st * kEFyStage, nbc);
+    // Lane (li, h) holds weight row li of tile (i, j) and its tokens 8g + 4h + e:
+    // each tile goes through a wave-private 32 x 33 fp32 buffer in the quant
+    // stage no wave reads any more (the last full chunk's if a tail follows,
+    // else the other) and is stored as 32 consecutive tokens of one row per
+    // half-wave.
+    float *tb =
+        reinterpret_cast<float *>(qs + (nbc > 0 ? 1 - st : st) * kEStage) + t.wave * 32 * 33;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const size_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (row < nr && col < nc)
-          s[row * bs + col] = acc[i][j][e];
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          tb[li * 33 + 8 * (e >> 2) + 4 * h + (e & 3)] = acc[i][j][e];
+        __builtin_amdgcn_wave_barrier();
+        const size_t col = n0 + wn * 128 + j * 32 + li;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const int r = 2 * k + h;  // this half-wave's weight row of the tile
+          const size_t row = m0 + wm * 64 + i * 32 + r;
+          const float v = tb[r * 33 + li];
+          if (row < nr && col < nc)
+            s[row * bs + col] = v;
+        }
+        __builtin_amdgcn_wave_barrier();
       }
+  } else {
+    const uint16_t *hx = t.hx(), *hy = t.hy();
+    for (; c < nfull; ++c)
+      st = chunk256(
+          t, c, st,
+          [&](auto after_step) {
+            fold_chunk_q8_2x4<kEKB, kEBlock, 32 * 16, kEHRow>(
+                acc, qa + st * kEStage, qb + st * kEStage, hx + st * kHStage, hy + st * kHStage,
+                after_step);
+          },
+          publish);
+    if (nbc > 0)
+      fold_tail_q8_2x4<kEBlock, 32 * 16, kEHRow>(acc, qa + st * kEStage, qb + st * kEStage,
+                                                 hx + st * kHStage, hy + st * kHStage, nbc);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const size_t col = n0 + wn * 128 + j * 32 + li;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const size_t row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (row < nr && col < nc)
+            s[row * bs + col] = acc[i][j][e];
+        }
+    }
   }
 }
 
@@ -822,7 +1017,17 @@ __global__ __launch_bounds__(kEThreads, 1) void gemm_tiles256_q8(size_t nb, floa
                                                                  size_t nc, size_t bs) {
   __shared__ __align__(16) int8_t qs[kEStages * kEStage];
   __shared__ __align__(16) uint16_t dsh[kEStages * kEKB * kEHRow];
-  gemm_tiles256_body(nb, s, tx, ty, nr, nc, bs, qs, dsh);
+  gemm_tiles256_body<false>(nb, s, tx, ty, nr, nc, bs, qs, dsh, nullptr);
+}
+
+__global__ __launch_bounds__(kEThreads, 1) void gemm_tiles256_q4(size_t nb, float *s,
+                                                                 const uint8_t *tx,
+                                                                 const uint8_t *ty, size_t nr,
+                                                                 size_t nc, size_t bs) {
+  __shared__ __align__(16) int8_t qs[kEStages * kEStage];
+  __shared__ __align__(16) uint16_t dsh[kEStages * kEKB * kEHRow];
+  __shared__ __align__(16) float fyd[kEStages * kEFyStage];
+  gemm_tiles256_body<true>(nb, s, tx, ty, nr, nc, bs, qs, dsh, fyd);
 }
 
 }  // namespace tcrv
@@ -943,7 +1148,10 @@ int gemm_tiles(size_t nb, float *s, const uint8_t *tx, const uint8_t *ty, size_t
     return TCRV_HIP_ERR_TOO_LARGE;
   const size_t tiles256 =
       ((nr + tcrv::kEBM - 1) / tcrv::kEBM) * ((nc + tcrv::kEBN - 1) / tcrv::kEBN);
-  if (q4)
+  if (q4 && tiles256_first(tiles, tiles256))
+    tcrv::gemm_tiles256_q4<<<dim3(static_cast<unsigned>(tiles256)), dim3(tcrv::kEThreads), 0,
+                             st>>>(nb, s, tx, ty, nr, nc, bs);
+  else if (q4)
     tcrv::gemm_tiles_q4<<<dim3(static_cast<unsigned>(tiles)), dim3(tcrv::kDThreads), 0, st>>>(
         nb, s, tx, ty, nr, nc, bs);
   else if (tiles256_first(tiles, tiles256))

@@ -421,4 +421,125 @@ __device__ __forceinline__ void fold_tail_q4(float (&acc)[2][16], const int8_t *
   }
 }
 
+// ---- the Q4_0 fold over 2 x 4 tiles per wave ------------------------------
+// The fold of one tile and block with d_y already in registers (dy[e]: the
+// token of accumulator element e); every fl(sumi * d_x) of the step is formed
+// before the first fma that takes one, so the d_y reads issued at the step's
+// start have landed by then.  The same operations per element as q4_fold.
+template <bool kExact>
+__device__ __forceinline__ void q4_fold_dy(float (&acc)[16], const v16f &F, uint32_t ux,
+                                           const float (&dy)[16]) {
+  float dx = f16_bits(ux);
+  asm volatile("" : "+v"(dx));
+  const float c = -kSeed * dx;
+  float t[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    t[e] = kExact ? (F[e] - kSeed) * dx : fmaf(F[e], dx, c);
+  asm volatile("" : "+v"(t[0]), "+v"(t[1]), "+v"(t[2]), "+v"(t[3]), "+v"(t[4]), "+v"(t[5]),
+               "+v"(t[6]), "+v"(t[7]), "+v"(t[8]), "+v"(t[9]), "+v"(t[10]), "+v"(t[11]),
+               "+v"(t[12]), "+v"(t[13]), "+v"(t[14]), "+v"(t[15]));
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    acc[e] = fmaf(t[e], dy[e], acc[e]);
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    asm volatile("" : "+v"(acc[e]));
+}
+
+// d_y of a lane's 16 tokens of one token tile and block (tokens 8g + 4h + j at
+// fy + 8g, four 128-bit LDS reads).
+__device__ __forceinline__ void q4_read_dy(float (&dy)[16], const float *fy) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float4 v = *reinterpret_cast<const float4 *>(fy + 8 * g);
+    dy[4 * g + 0] = v.x;
+    dy[4 * g + 1] = v.y;
+    dy[4 * g + 2] = v.z;
+    dy[4 * g + 3] = v.w;
+  }
+}
+
+// One chunk of kBlocks blocks for a wave's two weight tiles (B operand at
+// qw + i * kTile, d_x at hx + 32 i) and four token tiles (A operand at
+// qt + j * kTile, fp32 d_y at fy + 32 j, block b kFyRow floats on) on
+// transposed 32 x 32 tiles, steps s = 8b + 2j + i: every tile's blocks in
+// ascending order.  The seeded MFMA of step s+1 is issued in step s; the
+// operand reads follow fold_chunk_q8_2x4's schedule (token tile j+1 in step
+// (b, j, 0), the next block's weight operands in steps (b, 3, 0) and
+// (b, 3, 1)); a token tile's d_y is read once per block, in its step i = 0,
+// and serves both weight tiles.
+template <bool kExact, int kBlocks, int kBlockStride, int kTile, int kScaleRow, int kFyRow,
+          typename AfterStep>
+__device__ __forceinline__ void fold_chunk_q4_2x4(float (&acc)[2][4][16], const int8_t *qw,
+                                                  const int8_t *qt, const uint16_t *hx,
+                                                  const float *fy, AfterStep &&after_step) {
+  v4i w[2], t[2];
+  uint32_t ux[2];
+  float dy[16];
+  w[0] = q8_frag<kBlockStride>(qw, 0);
+  w[1] = q8_frag<kBlockStride>(qw + kTile, 0);
+  t[0] = q8_frag<kBlockStride>(qt, 0);
+  ux[0] = q8_scale<kScaleRow>(hx, 0);
+  ux[1] = q8_scale<kScaleRow>(hx + 32, 0);
+  // the seed, hidden from instruction selection: as a known constant it is
+  // rebuilt from scalar registers (24 instructions) each time register
+  // pressure evicts it
+  v16i seed;
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    seed[e] = kSeedBits;
+  asm volatile("" : "+v"(seed));
+  auto sums = [&](const v4i &tk, const v4i &wt) {
+    return __builtin_bit_cast(v16f, __builtin_amdgcn_mfma_i32_32x32x32_i8(tk, wt, seed, 0, 0, 0));
+  };
+  v16f cur = sums(t[0], w[0]);
+#pragma unroll
+  for (int s = 0; s < 8 * kBlocks; ++s) {
+    const int b = s >> 3, j = (s >> 1) & 3, i = s & 1;
+    if (i == 0) {
+      q4_read_dy(dy, fy + b * kFyRow + 32 * j);
+      if (j < 3) {
+        t[(j + 1) & 1] = q8_frag<kBlockStride>(qt + (j + 1) * kTile, b);
+      } else if (b + 1 < kBlocks) {
+        t[0] = q8_frag<kBlockStride>(qt, b + 1);
+        w[0] = q8_frag<kBlockStride>(qw, b + 1);
+      }
+    } else if (j == 3 && b + 1 < kBlocks) {
+      w[1] = q8_frag<kBlockStride>(qw + kTile, b + 1);
+    }
+    v16f nxt;
+    if (s + 1 < 8 * kBlocks)
+      nxt = sums(t[((s + 1) >> 1) & 1], w[(s + 1) & 1]);
+    q4_fold_dy<kExact>(acc[i][j], cur, ux[i], dy);
+    if (j == 3 && b + 1 < kBlocks)  // this block's last use of d_x of tile i
+      ux[i] = q8_scale<kScaleRow>(hx + 32 * i, b + 1);
+    if (s + 1 < 8 * kBlocks) {
+      asm volatile("" : "+v"(nxt));
+      cur = nxt;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    after_step(s);
+  }
+}
+
+// A trailing partial chunk of nbc blocks over the 2 x 4 transposed tiles.
+template <bool kExact, int kBlockStride, int kTile, int kScaleRow, int kFyRow>
+__device__ __forceinline__ void fold_tail_q4_2x4(float (&acc)[2][4][16], const int8_t *qw,
+                                                 const int8_t *qt, const uint16_t *hx,
+                                                 const float *fy, int nbc) {
+  for (int b = 0; b < nbc; ++b) {
+    const v4i w0 = q8_frag<kBlockStride>(qw, b), w1 = q8_frag<kBlockStride>(qw + kTile, b);
+    const uint32_t ux0 = q8_scale<kScaleRow>(hx, b), ux1 = q8_scale<kScaleRow>(hx + 32, b);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const v4i tq = q8_frag<kBlockStride>(qt + j * kTile, b);
+      float dy[16];
+      q4_read_dy(dy, fy + b * kFyRow + 32 * j);
+      q4_fold_dy<kExact>(acc[0][j], q4_seeded_sums(tq, w0), ux0, dy);
+      q4_fold_dy<kExact>(acc[1][j], q4_seeded_sums(tq, w1), ux1, dy);
+    }
+  }
+}
+
 }  // namespace tcrv
