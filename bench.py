@@ -1134,7 +1134,7 @@ def main():
                          "frac": round(k["tops"] / INT8_PEAK_TOPS, 4),
                          "traffic": traffic.get("q8_0_q8_0_gemm_tiles", {}).get("bytes"),
                          "traffic_source": traffic_src,
-                         "kernel": "tcrv::gemm_tiles_q8<true>", "ops_per_launch": GEMM_OPS,
+                         "kernel": "tcrv::gemm_tiles256_q8", "ops_per_launch": GEMM_OPS,
                          "us_per_launch": round(k["us"], 2)},
         }
         if "gemv" not in res:

@@ -1035,9 +1035,11 @@ __global__ __launch_bounds__(kEThreads, 1) void gemm_tiles256_q4(size_t nb, floa
 namespace {
 
 constexpr bool kTiledPipe = true;
-// The Q8_0 tiled kernel's buffer-form DMA takes a K chunk's offset within a
-// 64-row group's records as a 32-bit soffset: nb * kTRec must stay below 2^32
-// (the last 1 KB kept for the lane offsets), K below 63 million.
+// The buffer-form DMA of the Q8_0 tiled kernels and of the 256 x 256 Q4_0
+// kernel takes a K chunk's offset within a 64-row group's records as a 32-bit
+// soffset: nb * kTRec must stay below 2^32 (the last 1 KB kept for the lane
+// offsets), K below 63 million.  The Q8_0 entries refuse more blocks; the Q4_0
+// ones run the 256 x 128 Q4_0 kernel (64-bit global_load_lds) there.
 constexpr size_t kMaxTiledNb = ((static_cast<size_t>(1) << 32) - 1024) / tcrv::kTRec;
 
 size_t tile_bytes(size_t nrows, size_t nb) {
@@ -1148,7 +1150,7 @@ int gemm_tiles(size_t nb, float *s, const uint8_t *tx, const uint8_t *ty, size_t
     return TCRV_HIP_ERR_TOO_LARGE;
   const size_t tiles256 =
       ((nr + tcrv::kEBM - 1) / tcrv::kEBM) * ((nc + tcrv::kEBN - 1) / tcrv::kEBN);
-  if (q4 && tiles256_first(tiles, tiles256))
+  if (q4 && nb <= kMaxTiledNb && tiles256_first(tiles, tiles256))
     tcrv::gemm_tiles256_q4<<<dim3(static_cast<unsigned>(tiles256)), dim3(tcrv::kEThreads), 0,
                              st>>>(nb, s, tx, ty, nr, nc, bs);
   else if (q4)

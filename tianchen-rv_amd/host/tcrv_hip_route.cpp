@@ -231,8 +231,26 @@ const tcrv_hip_schedule kSchedules[] = {
     {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_DECODE, "gemv_q4_0_q8_0_direct", "rows_per_wave", 8,
      0, "tcrv_hip_gemv_q4_0_q8_0_shaped", -1.0,
      "512 waves for 4096 rows leave half the SIMDs idle during the read"},
-    // the tiled Q8_0 GEMM: blocks per K chunk (two LDS stages for 5-6 blocks,
-    // three for 3-4); a build-time constant
+    // the tiled GEMMs: tokens per work-group tile (256 weight rows each); the
+    // entries pick per shape, the larger tile when its rounds of 256
+    // work-groups x 15 are at most the smaller tile's rounds x 8 (one round of
+    // 256 x 256 tiles takes ~1.87 rounds of 256 x 128 ones)
+    {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles_q8", "work_group_tokens", 128, 0,
+     nullptr, -1.0,
+     "16 waves of two 32x32 tiles, 6-block K chunks; where it takes fewer rounds (4096 x 2048 "
+     "outputs: one round)"},
+    {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles256_q8", "work_group_tokens", 256,
+     1, nullptr, -1.0,
+     "8 waves of 2 x 4 32x32 tiles, 4-block K chunks: half the LDS operand reads and a third fewer "
+     "DMA instructions per tile and block; the 4096^3 reference shape is one round"},
+    {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles_q4", "work_group_tokens", 128, 0,
+     nullptr, -1.0, "16 waves of two transposed 32x32 tiles; where it takes fewer rounds"},
+    {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles256_q4", "work_group_tokens", 256,
+     1, nullptr, -1.0,
+     "8 waves of 2 x 4 transposed tiles, a token tile's d_y read once for both weight tiles"},
+    // the 256 x 128 tiled Q8_0 GEMM: blocks per K chunk (two LDS stages for
+    // 5-6 blocks, three for 3-4; the 256 x 256 kernel fits two stages of 4);
+    // a build-time constant
     {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles_q8", "k_chunk_blocks", 3, 0,
      nullptr, -1.0, "three stages; the most barriers per K"},
     {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles_q8", "k_chunk_blocks", 4, 0,

@@ -11,7 +11,8 @@
       matching kernel
   rocprof_summary.py traffic <pmc-root>
       HBM bytes per dispatch of the GEMV and GEMM kernels (plain and tiled
-      GEMM, and the GEMM-tile pack) from the two
+      GEMM, and the GEMM-tile pack; a workload whose passes are absent is
+      skipped) from the two
       counter passes (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled by
       what the same counter reads for the known-size calibration kernel
       (add_f32 over n = 2^24: 128 MiB read, 64 MiB written per launch).
@@ -30,7 +31,7 @@ import sys
 KERNELS = {
     "gemv_q4_0_q8_0": "gemv_q4_0_q8_0_direct",
     "q8_0_q8_0_gemm": "gemm_wide<false>",
-    "q8_0_q8_0_gemm_tiles": "gemm_tiles_q8<true>",
+    "q8_0_q8_0_gemm_tiles": "gemm_tiles256_q8",
     "pack_both_to_gemm_tiles": "pack_gemm_tiles_span2",
     "calib": "add_f32_vec4",
 }
@@ -119,6 +120,8 @@ def traffic(root):
                                "scale": scale[ctr]}
     for key, tag in (("gemv_q4_0_q8_0", "gemv"), ("q8_0_q8_0_gemm", "gemm"),
                      ("q8_0_q8_0_gemm_tiles", "gemm"), ("pack_both_to_gemm_tiles", "gemm")):
+        if not all(os.path.isdir(os.path.join(root, f"pmc_{ctr}_{tag}")) for ctr in CALIB_BYTES):
+            continue  # that workload's counter passes were not run
         total = 0.0
         entry = {"kernel": KERNELS[key]}
         for ctr in CALIB_BYTES:
