@@ -1153,6 +1153,46 @@ def test_q8_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("quant", ["q8_0", "q4_0"])
+def test_gemm_ws_random_shapes(hip, oracle, dev, quant):
+    """24 seeded random shapes through the workspace entry (both tiled kernels, by the rounds
+    rule, and every chunk and tail split) against the plain entry, whole outputs bit for bit,
+    with padded row strides and output strides; one sampled row of each against the oracle."""
+    rng = np.random.default_rng(2026 if quant == "q8_0" else 2027)
+    make = synth.q8_0_matrix if quant == "q8_0" else synth.q4_0_matrix
+    seen = set()
+    for case in range(24):
+        nr = int(rng.integers(256, 4700))
+        nc = int(rng.choice([int(rng.integers(2, 300)), int(rng.integers(300, 4700))]))
+        nb = int(rng.integers(1, 19))
+        n = nb * 32
+        xpad, ypad = 2 * int(rng.integers(0, 9)), 2 * int(rng.integers(0, 9))
+        bs = nc + int(rng.integers(0, 5))
+        seen.add(_rounds(nr, nc, 256, 256) * 15 <= _rounds(nr, nc, 256, 128) * 8)
+        w = np.pad(make(nr, n, 3000 + case, 0.02), ((0, 0), (0, xpad)))
+        a = np.pad(synth.q8_0_matrix(nc, n, 4000 + case, 1.0), ((0, 0), (0, ypad)))
+        dw, da = to_dev(w, dev), to_dev(a, dev)
+        plain = getattr(hip, f"{quant}_q8_0_gemm")
+        ws_fn = getattr(hip, f"{quant}_q8_0_gemm_ws")
+        wsb = getattr(hip, f"{quant}_q8_0_gemm_workspace_bytes")(n, nr, nc)
+        ref = empty_dev(nr * bs, torch.float32, dev)
+        plain(n, ref, dw, da, a.shape[1], nr, nc, w.shape[1], bs)
+        want = from_dev(ref).reshape(nr, bs)[:, :nc]
+        ws = empty_dev(wsb, torch.uint8, dev)
+        s = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+        ws_fn(n, s, dw, da, a.shape[1], nr, nc, w.shape[1], bs, ws, wsb)
+        got = from_dev(s).reshape(nr, bs)
+        what = f"{quant} case {case}: {nr}x{nc}x{n} pads {xpad},{ypad} bs {bs}"
+        assert np.array_equal(got[:, :nc].view(np.uint32), want.view(np.uint32)), what
+        assert np.all(got[:, nc:] == -7.0), what
+        r = int(rng.integers(0, nr))
+        ora = (oracle.gemm_q8_0 if quant == "q8_0" else oracle.gemm_q4_0)
+        row = ora(n, w[r].copy(), a, a.shape[1], 1, nc, w.shape[1], nc, 8)
+        assert_f32_parity(got[r, :nc], row, what=f"{what}, row {r}")
+        del dw, da, ref, ws, s
+    assert seen == {True, False}  # both work-group tiles ran
+
+
 def test_q8_0_gemm_ws_full_size_sampled(hip, oracle, dev):
     """4096 x 4096 x 4096 through the workspace entry; 64 rows and 64 columns
     checked against the oracle."""
