@@ -1,7 +1,10 @@
 // gemm_tiled.hip -- the a9 Q8_0 x Q8_0 and a7 Q4_0 x Q8_0 GEMMs over operands
-// in the GEMM-tile layout, staged into LDS by DMA (global_load_lds_dwordx4): no
-// staging registers and no staging VALU, so every VGPR and VALU cycle goes to
-// the fold.
+// in the GEMM-tile layout, staged into LDS by DMA (buffer_load_dwordx4 ... lds,
+// global_load_lds_dwordx4): no staging registers and no staging VALU, so every
+// VGPR and VALU cycle goes to the fold.  Two work-group tiles: 256 weight rows
+// x 128 tokens (16 waves of 2 tiles, gemm_tiles_q8 / gemm_tiles_q4) and 256 x
+// 256 (8 waves of 2 x 4 tiles, gemm_tiles256_q8 / gemm_tiles256_q4); the
+// entries pick per shape (tiles256_first), the results are the same bits.
 //
 // GEMM-tile layout of a Q8_0 matrix of nrows rows x nb blocks (the same bytes
 // as the plain rows, regrouped): rows in groups of 64; for group g and block b
@@ -26,9 +29,9 @@ namespace tcrv {
 
 constexpr int kTG = 64;                        // rows per tile group
 constexpr int kTRec = 2 * kTG * 16 + kTG * 2;  // 2176 bytes per (group, block) record
-// K chunk and LDS stages, 4096^3 on one box (us): 6 blocks x 2 stages 163.7-164.4,
-// 5 x 2 163.5, 4 x 3 169.7-170.5, 3 x 3 174.9: one chunk in flight covers the DMA
-// latency, and longer chunks meet at fewer barriers.
+// The 256 x 128 kernels' K chunk and LDS stages, 4096^3 on one box (us): 6 blocks
+// x 2 stages 163.7-164.4, 5 x 2 163.5, 4 x 3 169.7-170.5, 3 x 3 174.9: one chunk
+// in flight covers the DMA latency, and longer chunks meet at fewer barriers.
 constexpr int kDBM = 256, kDBN = 128, kDKB = 6;  // work-group tile, blocks per K chunk
 constexpr int kDRows = kDBM + kDBN;               // 384 staged rows
 constexpr int kDHalf = kDRows * 16;               // 6144: one half of one block, all rows
