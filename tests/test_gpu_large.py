@@ -202,11 +202,12 @@ def test_gemm_tiled_operands_over_2_gib(hip, oracle, dev):
 
 @pytest.mark.parametrize("nb", [1973789, 1973790])
 def test_q8_0_gemm_ws_at_the_tiled_block_bound(hip, oracle, dev, nb):
-    """K at the tiled Q8_0 GEMM's bound: n/32 = 1 973 789 blocks takes the tiled kernel, whose
-    last K chunk then sits 13 KB below 2^32 bytes into a group's records (the DMA's 32-bit
-    chunk offset); one block more runs the plain GEMM.  256 weight rows x 2 tokens; every row
-    repeats a 2048-block pattern along K (built on the device), so the sampled rows' bytes are
-    known on the host."""
+    """K at the workspace entry's bound (the 256-row tiled kernels' 32-bit DMA chunk offset):
+    n/32 = 1 973 789 blocks (odd: no multi-column GEMV) is packed and runs the tiled kernel of
+    this shape -- one 32 x 32 tile a wave, its last block's records 2 KB below 2^32 bytes into
+    a group; one block more runs the plain GEMM.  256 weight rows x 2 tokens; every row repeats
+    a 2048-block pattern along K (built on the device), so the sampled rows' bytes are known on
+    the host."""
     nr, nc, pat = 256, 2, 2048
     n = nb * 32
     rb = nb * 34

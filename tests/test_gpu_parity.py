@@ -1127,10 +1127,11 @@ def test_q4_0_gemm_tiles_256x256(hip, oracle, dev, nr, nc, nb, xpad, ypad):
 
 
 def test_q8_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
-    """Shapes the tiled kernel does not serve run the plain entry and leave the
-    workspace alone; a workspace that is too small or misaligned is refused."""
+    """Shapes the tiled kernels do not serve, and a few tokens with 4-byte aligned rows (the
+    plain entry's multi-column GEMVs), run the plain entry and leave the workspace alone; a
+    workspace that is too small or misaligned is refused."""
     n, nb = 256, 8
-    for nr, nc in ((100, 70), (300, 1), (1, 40)):
+    for nr, nc in ((100, 70), (300, 1), (1, 40), (256, 16), (512, 24)):
         w = synth.q8_0_matrix(nr, n, 81, 0.02)
         a = synth.q8_0_matrix(nc, n, 82, 1.0)
         ws = to_dev(np.full(64, 0x5A, np.uint8), dev)
@@ -1141,12 +1142,12 @@ def test_q8_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
                                                         nc, 8))
         assert np.all(from_dev(ws) == 0x5A)
     w = synth.q8_0_matrix(256, n, 83, 0.02)
-    a = synth.q8_0_matrix(16, n, 84, 1.0)
-    need = hip.q8_0_q8_0_gemm_workspace_bytes(n, 256, 16)
+    a = synth.q8_0_matrix(32, n, 84, 1.0)  # past the multi-column GEMVs' 24 tokens
+    need = hip.q8_0_q8_0_gemm_workspace_bytes(n, 256, 32)
     ws = empty_dev(need + 16, torch.uint8, dev)
-    s = empty_dev(256 * 16, torch.float32, dev)
+    s = empty_dev(256 * 32, torch.float32, dev)
     call = lambda *args: hip.call("tcrv_hip_q8_0_q8_0_gemm_ws", n, s, to_dev(w, dev),
-                                  to_dev(a, dev), a.shape[1], 256, 16, w.shape[1], 16, *args, 0,
+                                  to_dev(a, dev), a.shape[1], 256, 32, w.shape[1], 32, *args, 0,
                                   check=False)
     assert call(ws, need - 1) == hip.ERR_BAD_SIZE
     assert call(ws[8:], need) == hip.ERR_MISALIGNED
@@ -1154,21 +1155,82 @@ def test_q8_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
 
 
 @pytest.mark.parametrize("quant", ["q8_0", "q4_0"])
+@pytest.mark.parametrize("nr,nc,nb", [
+    (4096, 130, 13),  # 32 tiles of 256 x 128; tokens end 2 rows into a record group; 7 + 6 blocks
+    (300, 70, 7),     # exactly one round of the 7 blocks in flight; partial row and token groups
+    (1000, 600, 1),   # one block: only the clamped prologue loads
+    (4100, 960, 20),  # 136 tiles of 256 x 128, 975 work-groups; two rounds and a 6-block rest
+    (256, 2, 14),     # two tokens (pre-packed: no multi-column GEMV route)
+])
+def test_gemm_tiles_one_tile_a_wave(hip, oracle, dev, quant, nr, nc, nb):
+    """Pre-packed operands where the 256-row tiles would not fill one round of the CUs: the
+    kernel with one 32 x 32 tile a wave; whole outputs against the plain entry bit for bit and
+    sampled rows against the oracle, with -128 block sums and a padded output stride."""
+    n = nb * 32
+    q4 = quant == "q4_0"
+    w = (synth.q4_0_matrix if q4 else synth.q8_0_matrix)(nr, n, 1030 + nb, 0.02)
+    a = synth.q8_0_matrix(nc, n, 1031 + nb, 1.0)
+    a[0, 2:34] = 0x80  # -128 quants: -8 x -128 (Q4_0) or -128 x -128 (Q8_0) block sums
+    if q4:
+        w[nr - 1, 2:18] = 0x00
+    else:
+        w[nr - 1, 2:34] = 0x80
+    bs = nc + 5
+    dw, da = to_dev(w, dev), to_dev(a, dev)
+    ref = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+    getattr(hip, f"{quant}_q8_0_gemm")(n, ref, dw, da, a.shape[1], nr, nc, w.shape[1], bs)
+    want = from_dev(ref).reshape(nr, bs)
+    tx = empty_dev(hip.gemm_tiles_bytes(nr, nb), torch.uint8, dev)
+    ty = empty_dev(hip.gemm_tiles_bytes(nc, nb), torch.uint8, dev)
+    getattr(hip, f"pack_{quant}_to_gemm_tiles")(nr, nb, dw, w.shape[1], tx)
+    hip.pack_q8_0_to_gemm_tiles(nc, nb, da, a.shape[1], ty)
+    s = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+    getattr(hip, f"{quant}_q8_0_gemm_tiles")(n, s, tx, ty, nr, nc, bs)
+    got = from_dev(s).reshape(nr, bs)
+    what = f"{quant} tiles {nr}x{nc}x{n}"
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), what
+    ora = oracle.gemm_q4_0 if q4 else oracle.gemm_q8_0
+    for r in sorted({0, nr // 2, nr - 1}):
+        row = ora(n, w[r].copy(), a, a.shape[1], 1, nc, w.shape[1], nc, 8)
+        assert_f32_parity(got[r, :nc], row, what=f"{what}, row {r}")
+
+
+def _ws_route(nr, nc, nb, bx, by):
+    """Which kernel the workspace entries run (the host's rules, restated): the plain entry's
+    multi-column GEMVs for a few tokens, the one-tile-a-wave kernel below one round of 256 x 128
+    tiles (and at most 1024 of its 64 x 64 work-groups), else the 256 x 256 or 256 x 128 tiles
+    by the rounds rule."""
+    if nc <= 24 and nb % 2 == 0 and bx % 4 == 0 and by % 4 == 0:
+        return "cols"
+    if -(-nr // 256) * -(-nc // 128) < 256 and -(-nr // 64) * -(-nc // 64) <= 1024:
+        return "32x32"
+    return "256x256" if _rounds(nr, nc, 256, 256) * 15 <= _rounds(nr, nc, 256, 128) * 8 \
+        else "256x128"
+
+
+@pytest.mark.parametrize("quant", ["q8_0", "q4_0"])
 def test_gemm_ws_random_shapes(hip, oracle, dev, quant):
-    """24 seeded random shapes through the workspace entry (both tiled kernels, by the rounds
-    rule, and every chunk and tail split) against the plain entry, whole outputs bit for bit,
-    with padded row strides and output strides; one sampled row of each against the oracle."""
+    """28 seeded random shapes through the workspace entry -- a few tokens, a few hundred,
+    thousands, and large outputs, so every route runs (the multi-column GEMVs, the one-tile-a-wave
+    kernel, both work-group tiles by the rounds rule) with every chunk and tail split -- against
+    the plain entry, whole outputs bit for bit, with padded row strides and output strides; one
+    sampled row of each against the oracle."""
     rng = np.random.default_rng(2026 if quant == "q8_0" else 2027)
     make = synth.q8_0_matrix if quant == "q8_0" else synth.q4_0_matrix
+    wb = 34 if quant == "q8_0" else 18
     seen = set()
-    for case in range(24):
-        nr = int(rng.integers(256, 4700))
-        nc = int(rng.choice([int(rng.integers(2, 300)), int(rng.integers(300, 4700))]))
+    for case in range(28):
+        kind = case % 4
+        if kind == 3:
+            nr, nc = int(rng.integers(4096, 8500)), int(rng.integers(2000, 4700))
+        else:
+            nr = int(rng.integers(256, 4700))
+            nc = int(rng.integers(*((2, 40), (40, 600), (600, 4700))[kind]))
         nb = int(rng.integers(1, 19))
         n = nb * 32
         xpad, ypad = 2 * int(rng.integers(0, 9)), 2 * int(rng.integers(0, 9))
         bs = nc + int(rng.integers(0, 5))
-        seen.add(_rounds(nr, nc, 256, 256) * 15 <= _rounds(nr, nc, 256, 128) * 8)
+        seen.add(_ws_route(nr, nc, nb, nb * wb + xpad, nb * 34 + ypad))
         w = np.pad(make(nr, n, 3000 + case, 0.02), ((0, 0), (0, xpad)))
         a = np.pad(synth.q8_0_matrix(nc, n, 4000 + case, 1.0), ((0, 0), (0, ypad)))
         dw, da = to_dev(w, dev), to_dev(a, dev)
@@ -1190,7 +1252,7 @@ def test_gemm_ws_random_shapes(hip, oracle, dev, quant):
         row = ora(n, w[r].copy(), a, a.shape[1], 1, nc, w.shape[1], nc, 8)
         assert_f32_parity(got[r, :nc], row, what=f"{what}, row {r}")
         del dw, da, ref, ws, s
-    assert seen == {True, False}  # both work-group tiles ran
+    assert seen == {"cols", "32x32", "256x256", "256x128"}  # every route ran
 
 
 def test_q8_0_gemm_ws_full_size_sampled(hip, oracle, dev):
@@ -1300,10 +1362,11 @@ def test_q4_0_gemm_tiles_checks(hip, dev):
 
 
 def test_q4_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
-    """Shapes the tiled kernel does not serve run the plain entry and leave the
-    workspace alone; a workspace that is too small or misaligned is refused."""
+    """Shapes the tiled kernels do not serve, and a few tokens with 4-byte aligned rows (the
+    plain entry's multi-column GEMVs), run the plain entry and leave the workspace alone; a
+    workspace that is too small or misaligned is refused."""
     n, nb = 256, 8
-    for nr, nc in ((100, 70), (300, 1), (1, 40)):
+    for nr, nc in ((100, 70), (300, 1), (1, 40), (256, 16), (512, 24)):
         w = synth.q4_0_matrix(nr, n, 85, 0.02)
         a = synth.q8_0_matrix(nc, n, 86, 1.0)
         ws = to_dev(np.full(64, 0x5A, np.uint8), dev)
@@ -1314,13 +1377,13 @@ def test_q4_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
                                                         nc, 8))
         assert np.all(from_dev(ws) == 0x5A)
     w = synth.q4_0_matrix(256, n, 87, 0.02)
-    a = synth.q8_0_matrix(16, n, 88, 1.0)
-    need = hip.q4_0_q8_0_gemm_workspace_bytes(n, 256, 16)
-    assert need == hip.gemm_tiles_bytes(256, nb) + hip.gemm_tiles_bytes(16, nb)
+    a = synth.q8_0_matrix(32, n, 88, 1.0)  # past the multi-column GEMVs' 24 tokens
+    need = hip.q4_0_q8_0_gemm_workspace_bytes(n, 256, 32)
+    assert need == hip.gemm_tiles_bytes(256, nb) + hip.gemm_tiles_bytes(32, nb)
     ws = empty_dev(need + 16, torch.uint8, dev)
-    s = empty_dev(256 * 16, torch.float32, dev)
+    s = empty_dev(256 * 32, torch.float32, dev)
     call = lambda *args: hip.call("tcrv_hip_q4_0_q8_0_gemm_ws", n, s, to_dev(w, dev),
-                                  to_dev(a, dev), a.shape[1], 256, 16, w.shape[1], 16, *args, 0,
+                                  to_dev(a, dev), a.shape[1], 256, 32, w.shape[1], 32, *args, 0,
                                   check=False)
     assert call(ws, need - 1) == hip.ERR_BAD_SIZE
     assert call(ws[8:], need) == hip.ERR_MISALIGNED

@@ -77,7 +77,7 @@ def test_q8_0_gemm_special_scales(hip, oracle, dev, nr, nc, nb, pad):
 
 
 def test_q8_0_gemm_ws_special_scales(hip, oracle, dev):
-    """The DMA-staged tiled GEMM (through the workspace entry)."""
+    """The workspace entry at a shape of few tiles (its one-tile-a-wave kernel)."""
     nr, nc, nb = 300, 130, 9
     n = nb * 32
     w = q8(nr, nb, 31, 0.02, nonfinite_every=16)
@@ -104,7 +104,8 @@ def test_q4_0_gemm_special_scales(hip, oracle, dev, nr, nc, nb):
 
 
 def test_q4_0_gemm_tiles_special_scales(hip, oracle, dev):
-    """The DMA-staged tiled Q4_0 GEMM over the GEMM-tile layout."""
+    """The tiled Q4_0 GEMM over the GEMM-tile layout at a shape of few tiles (one 32 x 32 tile
+    a wave)."""
     nr, nc, nb = 300, 130, 9
     n = nb * 32
     w = q4(nr, nb, 33, nonfinite_every=16)
@@ -116,7 +117,8 @@ def test_q4_0_gemm_tiles_special_scales(hip, oracle, dev):
 
 def test_q4_0_gemm_ws_special_scales(hip, oracle, dev):
     """The workspace entry: both operands packed in one launch (16-byte aligned
-    rows, 8-block spans), then the tiled Q4_0 GEMM."""
+    rows, 8-block spans), then the tiled Q4_0 GEMM (one 32 x 32 tile a wave at
+    this shape)."""
     nr, nc, nb = 320, 96, 16
     n = nb * 32
     w = q4(nr, nb, 35, nonfinite_every=16)
@@ -131,11 +133,12 @@ def test_q4_0_gemm_ws_special_scales(hip, oracle, dev):
 
 
 def test_q4_0_gemm_tiles_nonfinite_dx_mid_k(hip, oracle, dev):
-    """The tiled Q4_0 GEMM folds each 6-block chunk in a fast form that is exact
-    only for finite d_x, switching a wave to the exact form from the first chunk
-    whose d_x holds a non-finite value: +-Inf planted at the first chunk, in
-    the middle of K, in the last full chunk and in the partial tail, NaN, and an
-    infinite d_x over a zero block sum (0 * Inf = NaN)."""
+    """The pre-packed Q4_0 GEMM at a shape of few tiles (one 32 x 32 tile a wave,
+    folding every block in the exact three-instruction form) with non-finite d_x
+    across K: +-Inf planted in the first blocks, in the middle of K and near its
+    end, NaN, and an infinite d_x over a zero block sum (0 * Inf = NaN).  The
+    256-row tiles' fast-to-exact switch is covered by
+    test_gemm_ws_tiles_special_scales."""
     nr, nc, nb = 512, 256, 40  # 6 full chunks + 4 tail blocks
     n = nb * 32
     w = q4(nr, nb, 41)
@@ -175,16 +178,19 @@ def test_q4_0_gemm_nonfinite_dx_mid_k(hip, oracle, dev, nb):
     assert np.isinf(g[70]).any() and np.isnan(g[400]).all()  # the planted cases took effect
 
 
+@pytest.mark.parametrize("nr,nc,kernel", [(4096, 4096, "256x256"), (4196, 4166, "256x128"),
+                                          (4096, 130, "32x32")])
 @pytest.mark.parametrize("quant,nonfinite_every", [("q8_0", 16), ("q4_0", 16), ("q4_0", 0)])
-def test_gemm_ws_256x256_special_scales(hip, oracle, dev, quant, nonfinite_every):
-    """The 256 x 256 work-group tiles of the tiled GEMMs (4096 x 4096 outputs, through the
-    workspace entries): special scales in both operands, non-finite d_x in every 16th weight
-    row (every Q4_0 wave folds exactly from chunk 0) or, with none there, +-Inf and NaN
-    planted at chunk 0, in the middle of K, in the last full chunk and in the 1-block tail,
-    and an infinite d_x over a zero block sum.  Sampled rows, the planted ones included,
-    against the oracle."""
-    nr = nc = 4096
-    nb = 13  # 3 chunks of 4 blocks + 1
+def test_gemm_ws_tiles_special_scales(hip, oracle, dev, quant, nonfinite_every, nr, nc, kernel):
+    """Each work-group tile of the tiled GEMMs, through the workspace entries (256 x 256: 4096 x
+    4096 outputs; 256 x 128: 4196 x 4166, three rounds of it against two of the larger tile; one
+    32 x 32 tile a wave: 4096 x 130): special scales in both operands, non-finite d_x in every
+    16th weight row (every Q4_0 wave of the 256-row tiles folds exactly from chunk 0) or, with
+    none there, +-Inf and NaN planted at chunk 0, in the middle of K, in the last full chunk and
+    in the 1-block tail (chunks of 4 and of 6 blocks), and an infinite d_x over a zero block
+    sum.  Sampled rows, the planted ones included, against the oracle."""
+    print(f"{quant} {kernel} tiles {nr} x {nc}, non-finite every {nonfinite_every}", flush=True)
+    nb = 13  # 3 chunks of 4 blocks + 1; 2 chunks of 6 + 1
     n = nb * 32
     if quant == "q8_0":
         w, blk = q8(nr, nb, 51, 0.02, nonfinite_every=nonfinite_every), 34
@@ -210,7 +216,7 @@ def test_gemm_ws_256x256_special_scales(hip, oracle, dev, quant, nonfinite_every
     sub = np.ascontiguousarray(w[rows])
     ref = oracle.gemm_q8_0 if quant == "q8_0" else oracle.gemm_q4_0
     want = ref(n, sub, a, a.shape[1], len(rows), nc, w.shape[1], nc, 8)
-    assert_f32_parity_nan(got[rows].reshape(-1), want, what=f"{quant} 256x256 tiles")
+    assert_f32_parity_nan(got[rows].reshape(-1), want, what=f"{quant} {kernel} tiles")
     if not nonfinite_every:
         assert np.isinf(got[70]).any() and np.isnan(got[400]).all()  # the planted cases
 

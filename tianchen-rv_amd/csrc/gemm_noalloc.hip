@@ -74,7 +74,7 @@ int tcrv_hip_q8_0_q8_0_gemm_noalloc(size_t n, float *s, const uint8_t *vx, const
   // the shapes tcrv_hip_q8_0_q8_0_gemm_ws runs without its workspace (the
   // plain GEMM) need no scratch, and do not look its address up (the lookup
   // is the call that must stay outside a graph capture)
-  if (!gemm_ws_uses_workspace(n, nr, nc))
+  if (!gemm_ws_uses_workspace(n, vx, bx, vy, by, nr, nc))
     return tcrv_hip_q8_0_q8_0_gemm_ws(n, s, vx, vy, by, nr, nc, bx, bs, nullptr, 0, stream);
   if (tcrv_hip_q8_0_q8_0_gemm_workspace_bytes(n, nr, nc) > kScratchBytes)
     return TCRV_HIP_ERR_SCRATCH_LIMIT;

@@ -1033,6 +1033,153 @@ __global__ __launch_bounds__(kEThreads, 1) void gemm_tiles256_q4(size_t nb, floa
   gemm_tiles256_body<true>(nb, s, tx, ty, nr, nc, bs, qs, dsh, fyd);
 }
 
+// ---- few work-group tiles: one 32 x 32 tile a wave, no LDS -----------------
+// Where the 256-row tiles leave most CUs idle (a few hundred tokens against a
+// few thousand weight rows: 4096 x 128 is 16 work-groups of 256 x 128), each
+// wave folds one 32 x 32 output tile and a work-group of 4 waves covers one
+// 64-row record group of each operand (64 weight rows x 64 tokens).  A record
+// half is exactly a v_mfma_i32_32x32x32_i8 operand of 32 rows (lane l: row
+// l % 32, quants 16 (l / 32) .. + 15), so every operand is one 16-byte load per
+// lane straight into registers, kSAhead blocks in flight, and the MFMAs of
+// block b + 1 are issued before block b is folded.
+//   Q8_0: acc = fma((float)sumi, d_x * d_y, acc), d_x * d_y from the f16 MFMA
+//         (scales in k-slot 0 of lanes 0-31, zero elsewhere: exact products);
+//   Q4_0: acc = fma(fl((float)sumi * d_x), d_y, acc), the weight rows' d_x
+//         spread over the tile by the same f16 MFMA against 1.0 (exact), the
+//         lane's token scale d_y widened once per block.
+// Rows and tokens past nr / nc are the zero rows of the last record group and
+// are not stored.  Every output keeps its ascending-block fold: the same bits
+// as the other tiled kernels.
+constexpr int kSBM = 64, kSBN = 64;  // work-group tile (one record group each)
+constexpr int kSAhead = 7;           // blocks in flight a wave (8: 12 bytes of spills)
+
+struct Ops32 {
+  v4i a, b;
+  uint32_t ux, uy;
+};
+
+// At most two waves a SIMD: every register is then a VGPR (a higher occupancy
+// target puts the MFMA results in AGPRs, and each block then pays their copies
+// out).  Two waves per tile, each folding half of the outputs after issuing
+// the same loads and MFMAs, measured slower (4096 x 128 x 4096: 24.4 against
+// 17.3 us).
+template <bool kQ4>
+__global__ __launch_bounds__(256, 2) void gemm_tiles32(unsigned nb, float *s, const uint8_t *tx,
+                                                       const uint8_t *ty, size_t nr, size_t nc,
+                                                       size_t bs) {
+  const int lane = threadIdx.x & 63;
+  const int tile = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int wm = tile & 1, wn = tile >> 1;  // the tile's 32-row halves of the two groups
+  const int li = lane & 31, h = lane >> 5;
+  const unsigned tiles_m = static_cast<unsigned>((nr + kSBM - 1) / kSBM);
+  const unsigned tiles_n = static_cast<unsigned>((nc + kSBN - 1) / kSBN);
+  unsigned tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const uint8_t *ra = tx + static_cast<size_t>(tm) * nb * kTRec;
+  const uint8_t *rb = ty + static_cast<size_t>(tn) * nb * kTRec;
+  // lane offsets within a record; the record base is wave-uniform (SGPRs)
+  const unsigned qa = h * 1024 + (32 * wm + li) * 16, qb = h * 1024 + (32 * wn + li) * 16;
+  const unsigned sa = 2 * kTG * 16 + (32 * wm + li) * 2, sb = 2 * kTG * 16 + (32 * wn + li) * 2;
+  const uint32_t kmask = h ? 0u : 0xffffu;  // k-slot 0 of lanes 0-31 only
+  const uint32_t one = h ? 0u : 0x3c00u;    // fp16 1.0
+  const unsigned last = nb - 1;
+
+  // Buffer loads: the record's address is the descriptor's base (SGPRs, one
+  // per block and operand), the lane's 32-bit offset the VGPR offset, so no
+  // load pays a 64-bit VALU address add (global loads from a 64-bit per-lane
+  // address paid four a block: 4096 x 128 x 4096 21.8 -> 17.3 us).  Every
+  // offset stays inside the 2176-byte record the descriptor spans.
+  auto load = [&](unsigned b, Ops32 &o) {
+    const __amdgpu_buffer_rsrc_t pa = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(ra + static_cast<size_t>(b) * kTRec), (short)0, kTRec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t pb = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(rb + static_cast<size_t>(b) * kTRec), (short)0, kTRec, 0x00020000);
+    o.a = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(pa, qa, 0, 0));
+    o.b = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(pb, qb, 0, 0));
+    o.ux = __builtin_amdgcn_raw_buffer_load_b16(pa, sa, 0, 0);
+    o.uy = __builtin_amdgcn_raw_buffer_load_b16(pb, sb, 0, 0);
+  };
+  struct Step {
+    v16i sumi;
+    v16f scl;
+    float dy;
+  };
+  auto issue = [&](const Ops32 &o) {
+    Step t;
+    t.sumi = q8_sumi(o.a, o.b);
+    if constexpr (kQ4) {
+      t.scl = q8_dxy(o.ux & kmask, one);
+      t.dy = fp16_bits_to_f32(o.uy);
+      asm volatile("" : "+v"(t.dy));  // widened once (not an fma_mix per output)
+    } else {
+      t.scl = q8_dxy(o.ux & kmask, o.uy & kmask);
+      t.dy = 0.0f;
+    }
+    return t;
+  };
+  float acc[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    acc[e] = 0.0f;
+  auto fold = [&](const Step &t) {
+    if constexpr (kQ4) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc[e] = fmaf(static_cast<float>(t.sumi[e]) * t.scl[e], t.dy, acc[e]);
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        asm volatile("" : "+v"(acc[e]));
+    } else {  // all 16 conversions before the fmas, as q8_fold<true> (without its pin)
+      float f[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        f[e] = static_cast<float>(t.sumi[e]);
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        acc[e] = fmaf(f[e], t.scl[e], acc[e]);
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        asm volatile("" : "+v"(acc[e]));
+    }
+  };
+
+  Ops32 ring[kSAhead];
+#pragma unroll
+  for (int j = 0; j < kSAhead; ++j)
+    load(min(static_cast<unsigned>(j), last), ring[j]);
+  Step cur = issue(ring[0]);
+  load(min(static_cast<unsigned>(kSAhead), last), ring[0]);
+  // block b + 1 sits in slot (b + 1) % kSAhead: its MFMAs go out before block
+  // b's fold, and the slot is refilled with block b + 1 + kSAhead (clamped to
+  // the last block, whose extra copies are never folded).  Whole rounds of
+  // kSAhead blocks first, with no branch between the loads and their use, so
+  // the waits count exactly the loads still in flight.
+  auto step = [&](unsigned b, int j) {
+    const int kn = (j + 1) % kSAhead;
+    const Step nxt = issue(ring[kn]);
+    load(min(b + 1 + kSAhead, last), ring[kn]);
+    fold(cur);
+    cur = nxt;
+  };
+  unsigned b0 = 0;
+  for (; b0 + kSAhead <= nb; b0 += kSAhead) {
+#pragma unroll
+    for (int j = 0; j < kSAhead; ++j)
+      step(b0 + j, j);
+  }
+#pragma unroll
+  for (int j = 0; j < kSAhead - 1; ++j)
+    if (b0 + j < nb)
+      step(b0 + j, j);
+  const size_t col = static_cast<size_t>(tn) * kSBN + 32 * wn + li;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const size_t row = static_cast<size_t>(tm) * kSBM + 32 * wm + 8 * (e >> 2) + 4 * h + (e & 3);
+    if (row < nr && col < nc)
+      s[row * bs + col] = acc[e];
+  }
+}
+
 }  // namespace tcrv
 
 namespace {
@@ -1145,6 +1292,17 @@ bool tiles256_first(size_t tiles, size_t tiles256) {
   return (tiles256 + kCUs - 1) / kCUs * 15 <= (tiles + kCUs - 1) / kCUs * 8;
 }
 
+// Few work-group tiles: the one-tile-a-wave kernel where the 256 x 128 tiles
+// would not fill one round of the CUs and its own waves fit two rounds of two
+// a SIMD (at most 1024 work-groups).  Pre-packed operands, K 4096 unless
+// named, us, 256 x 128 tiles against it: 4096 x 128 72 / 17, 4096 x 512 74 /
+// 28, 4096 x 1024 75 / 53, 14336 x 128 72 / 27, 4096 x 128 x 14336 234 / 51;
+// but 14336 x 512 (1792 of its work-groups) 82 / 88, and from 256 tiles (a
+// full round) the larger tiles win: 4096 x 2048 93-98 against ~100.
+bool tiles32_first(size_t tiles, size_t tiles64, size_t nb) {
+  return tiles < 256 && tiles64 <= 1024 && nb <= 0xffffffffu;
+}
+
 int gemm_tiles(size_t nb, float *s, const uint8_t *tx, const uint8_t *ty, size_t nr, size_t nc,
                size_t bs, hipStream_t st, bool q4 = false) {
   using namespace tcrv_host;
@@ -1153,7 +1311,17 @@ int gemm_tiles(size_t nb, float *s, const uint8_t *tx, const uint8_t *ty, size_t
     return TCRV_HIP_ERR_TOO_LARGE;
   const size_t tiles256 =
       ((nr + tcrv::kEBM - 1) / tcrv::kEBM) * ((nc + tcrv::kEBN - 1) / tcrv::kEBN);
-  if (q4 && nb <= kMaxTiledNb && tiles256_first(tiles, tiles256))
+  const size_t tiles64 =
+      ((nr + tcrv::kSBM - 1) / tcrv::kSBM) * ((nc + tcrv::kSBN - 1) / tcrv::kSBN);
+  if (tiles32_first(tiles, tiles64, nb)) {
+    const unsigned nbu = static_cast<unsigned>(nb);
+    if (q4)
+      tcrv::gemm_tiles32<true><<<dim3(static_cast<unsigned>(tiles64)), dim3(256), 0, st>>>(
+          nbu, s, tx, ty, nr, nc, bs);
+    else
+      tcrv::gemm_tiles32<false><<<dim3(static_cast<unsigned>(tiles64)), dim3(256), 0, st>>>(
+          nbu, s, tx, ty, nr, nc, bs);
+  } else if (q4 && nb <= kMaxTiledNb && tiles256_first(tiles, tiles256))
     tcrv::gemm_tiles256_q4<<<dim3(static_cast<unsigned>(tiles256)), dim3(tcrv::kEThreads), 0,
                              st>>>(nb, s, tx, ty, nr, nc, bs);
   else if (q4)
@@ -1213,10 +1381,23 @@ namespace tcrv_host {
 
 // Shapes the tiled kernel does not serve run as tcrv_hip_q8_0_q8_0_gemm,
 // without the workspace: fewer weight rows than one 256-row tile, a single
-// token (decode), no blocks, or more than kMaxTiledNb blocks.
-bool gemm_ws_uses_workspace(size_t n, size_t nr, size_t nc) {
+// token (decode), no blocks, or more than kMaxTiledNb blocks.  So do a few
+// tokens that the plain entry's multi-column GEMVs take (even block count,
+// 4-byte aligned rows and strides): up to kWsColsMax tokens they beat packing
+// both operands for the tiled kernels (us, 4096 weight rows, K 4096, Q8_0 /
+// Q4_0: 16 tokens 15.0 / 16.3 against ~25 / ~28; 32 tokens 30.8 / 32.3
+// against ~25 / ~28).
+constexpr size_t kWsColsMax = 24;
+bool ws_cols_first(size_t nb, const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by,
+                   size_t nc) {
+  return nc <= kWsColsMax && nc <= kGemvColsMax && nb % 2 == 0 && aligned4(vx) &&
+         aligned4(vy) && bx % 4 == 0 && by % 4 == 0;
+}
+bool gemm_ws_uses_workspace(size_t n, const uint8_t *vx, size_t bx, const uint8_t *vy,
+                            size_t by, size_t nr, size_t nc) {
   const size_t nb = n / tcrv::kQK;
-  return nr >= static_cast<size_t>(tcrv::kDBM) && nc >= 2 && nb > 0 && nb <= kMaxTiledNb;
+  return nr >= static_cast<size_t>(tcrv::kDBM) && nc >= 2 && nb > 0 && nb <= kMaxTiledNb &&
+         !ws_cols_first(nb, vx, bx, vy, by, nc);
 }
 
 }  // namespace tcrv_host
@@ -1233,7 +1414,7 @@ int tcrv_hip_q8_0_q8_0_gemm_ws(size_t n, float *s, const uint8_t *vx, const uint
                                void *workspace, size_t workspace_bytes, void *stream) {
   using namespace tcrv_host;
   const size_t nb = n / tcrv::kQK;
-  if (!gemm_ws_uses_workspace(n, nr, nc))
+  if (!gemm_ws_uses_workspace(n, vx, bx, vy, by, nr, nc))
     return tcrv_hip_q8_0_q8_0_gemm(n, s, vx, vy, by, nr, nc, bx, bs, stream);
   if (bs < nc)
     return TCRV_HIP_ERR_BAD_SIZE;
@@ -1297,7 +1478,7 @@ int tcrv_hip_q4_0_q8_0_gemm_ws(size_t n, float *s, const uint8_t *vx, const uint
                                void *workspace, size_t workspace_bytes, void *stream) {
   using namespace tcrv_host;
   const size_t nb = n / tcrv::kQK;
-  if (!gemm_ws_uses_workspace(n, nr, nc))
+  if (!gemm_ws_uses_workspace(n, vx, bx, vy, by, nr, nc))
     return tcrv_hip_q4_0_q8_0_gemm(n, s, vx, vy, by, nr, nc, bx, bs, stream);
   if (bs < nc)
     return TCRV_HIP_ERR_BAD_SIZE;

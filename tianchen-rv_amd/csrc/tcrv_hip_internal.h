@@ -202,8 +202,9 @@ int gemv_cols_q8_0_q8_0(size_t nb, float *s, size_t bs, const uint8_t *vx, size_
                         const uint8_t *vy, size_t by, size_t nr, size_t nc, void *stream);
 
 // tcrv_hip_q8_0_q8_0_gemm_ws packs into its workspace and runs the tiled
-// kernel for this shape (otherwise it runs the plain GEMM and reads no
+// kernels for this call (otherwise it runs the plain GEMM and reads no
 // workspace); gemm_tiled.hip.
-bool gemm_ws_uses_workspace(size_t n, size_t nr, size_t nc);
+bool gemm_ws_uses_workspace(size_t n, const uint8_t *vx, size_t bx, const uint8_t *vy,
+                            size_t by, size_t nr, size_t nc);
 
 }  // namespace tcrv_host
