@@ -1195,6 +1195,47 @@ def test_gemm_tiles_one_tile_a_wave(hip, oracle, dev, quant, nr, nc, nb):
         assert_f32_parity(got[r, :nc], row, what=f"{what}, row {r}")
 
 
+@pytest.mark.parametrize("quant", ["q8_0", "q4_0"])
+@pytest.mark.parametrize("nr,nc,nb", [
+    (4096, 130, 16),  # 192 work-groups; tokens end 2 rows into a record group; two chunks
+    (300, 70, 8),     # one 8-block chunk; partial row and token groups
+    (1000, 600, 40),  # five chunks
+    (2100, 333, 24),
+])
+def test_gemm_plain_rows_few_tiles(hip, oracle, dev, quant, nr, nc, nb):
+    """The plain entries at shapes of few output tiles with 16-byte aligned rows and whole
+    8-block chunks: each work-group packs its 64 weight rows and 64 tokens into LDS records
+    chunk by chunk and folds one 32 x 32 tile a wave.  Whole outputs against the workspace
+    entry (the packed one-tile-a-wave kernel) bit for bit, sampled rows against the oracle,
+    with -128 block sums and a padded output stride."""
+    n = nb * 32
+    q4 = quant == "q4_0"
+    w = (synth.q4_0_matrix if q4 else synth.q8_0_matrix)(nr, n, 1040 + nb, 0.02)
+    a = synth.q8_0_matrix(nc, n, 1041 + nb, 1.0)
+    a[nc - 1, 2:34] = 0x80
+    if q4:
+        w[0, 2:18] = 0x00
+    else:
+        w[0, 2:34] = 0x80
+    bs = nc + 5
+    dw, da = to_dev(w, dev), to_dev(a, dev)
+    s = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+    getattr(hip, f"{quant}_q8_0_gemm")(n, s, dw, da, a.shape[1], nr, nc, w.shape[1], bs)
+    got = from_dev(s).reshape(nr, bs)
+    wsb = getattr(hip, f"{quant}_q8_0_gemm_workspace_bytes")(n, nr, nc)
+    ws = empty_dev(wsb, torch.uint8, dev)
+    s2 = to_dev(np.full(nr * bs, -7.0, np.float32), dev)
+    getattr(hip, f"{quant}_q8_0_gemm_ws")(n, s2, dw, da, a.shape[1], nr, nc, w.shape[1], bs, ws,
+                                          wsb)
+    want = from_dev(s2).reshape(nr, bs)
+    what = f"{quant} plain {nr}x{nc}x{n}"
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), what
+    ora = oracle.gemm_q4_0 if q4 else oracle.gemm_q8_0
+    for r in sorted({0, 1, nr // 2, nr - 1}):
+        row = ora(n, w[r].copy(), a, a.shape[1], 1, nc, w.shape[1], nc, 8)
+        assert_f32_parity(got[r, :nc], row, what=f"{what}, row {r}")
+
+
 def _ws_route(nr, nc, nb, bx, by):
     """Which kernel the workspace entries run (the host's rules, restated): the plain entry's
     multi-column GEMVs for a few tokens, the one-tile-a-wave kernel below one round of 256 x 128

@@ -953,10 +953,17 @@ extern "C" int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx,
                            : q8_0_rows_direct(nb, s, 1, vx, 0, vy, by, nc, stream);
     if (st != TCRV_HIP_ERR_UNSUPPORTED)
       return st;
-  } else if (nc <= kGemvColsMax) {  // a few tokens: multi-column GEMVs
-    const int st = gemv_cols_q8_0_q8_0(nb, s, bs, vx, bx, vy, by, nr, nc, stream);
-    if (st != TCRV_HIP_ERR_UNSUPPORTED)
-      return st;
+  } else {
+    if (nc > kColsFirstMax) {  // few output tiles: one 32 x 32 tile a wave
+      const int st = gemm_rows_few(false, nb, s, vx, bx, vy, by, nr, nc, bs, stream);
+      if (st != TCRV_HIP_ERR_UNSUPPORTED)
+        return st;
+    }
+    if (nc <= kGemvColsMax) {  // a few tokens: multi-column GEMVs
+      const int st = gemv_cols_q8_0_q8_0(nb, s, bs, vx, bx, vy, by, nr, nc, stream);
+      if (st != TCRV_HIP_ERR_UNSUPPORTED)
+        return st;
+    }
   }
   if (aligned4(vx) && aligned4(vy) && (nr == 1 || bx % 4 == 0) && (nc == 1 || by % 4 == 0)) {
     const size_t tiles =

@@ -1058,6 +1058,63 @@ struct Ops32 {
   uint32_t ux, uy;
 };
 
+// One block of a wave's 32 x 32 tile: the block sums, the scale products (Q8_0)
+// or the weight rows' d_x spread over the tile (Q4_0), and the lane's token
+// scale (Q4_0).  kmask keeps the scale in k-slot 0 of lanes 0-31 only; one is
+// fp16 1.0 there and 0 elsewhere.
+struct Step32 {
+  v16i sumi;
+  v16f scl;
+  float dy;
+};
+
+template <bool kQ4>
+__device__ __forceinline__ Step32 issue32(const Ops32 &o, uint32_t kmask, uint32_t one) {
+  Step32 t;
+  t.sumi = q8_sumi(o.a, o.b);
+  if constexpr (kQ4) {
+    t.scl = q8_dxy(o.ux & kmask, one);
+    t.dy = fp16_bits_to_f32(o.uy);
+    asm volatile("" : "+v"(t.dy));  // widened once (not an fma_mix per output)
+  } else {
+    t.scl = q8_dxy(o.ux & kmask, o.uy & kmask);
+    t.dy = 0.0f;
+  }
+  return t;
+}
+
+template <bool kQ4>
+__device__ __forceinline__ void fold32(float (&acc)[16], const Step32 &t) {
+  if constexpr (kQ4) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      acc[e] = fmaf(static_cast<float>(t.sumi[e]) * t.scl[e], t.dy, acc[e]);
+  } else {  // all 16 conversions before the fmas, as q8_fold<true> (without its pin)
+    float f[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      f[e] = static_cast<float>(t.sumi[e]);
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      acc[e] = fmaf(f[e], t.scl[e], acc[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    asm volatile("" : "+v"(acc[e]));
+}
+
+// Lane (li, h) of a 32 x 32 tile at weight row row0, token column col holds
+// rows row0 + 8 (e / 4) + 4h + e % 4.
+__device__ __forceinline__ void store32(float *s, const float (&acc)[16], size_t row0, size_t col,
+                                        int h, size_t nr, size_t nc, size_t bs) {
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    const size_t row = row0 + 8 * (e >> 2) + 4 * h + (e & 3);
+    if (row < nr && col < nc)
+      s[row * bs + col] = acc[e];
+  }
+}
+
 // At most two waves a SIMD: every register is then a VGPR (a higher occupancy
 // target puts the MFMA results in AGPRs, and each block then pays their copies
 // out).  Two waves per tile, each folding half of the outputs after issuing
@@ -1099,55 +1156,18 @@ __global__ __launch_bounds__(256, 2) void gemm_tiles32(unsigned nb, float *s, co
     o.ux = __builtin_amdgcn_raw_buffer_load_b16(pa, sa, 0, 0);
     o.uy = __builtin_amdgcn_raw_buffer_load_b16(pb, sb, 0, 0);
   };
-  struct Step {
-    v16i sumi;
-    v16f scl;
-    float dy;
-  };
-  auto issue = [&](const Ops32 &o) {
-    Step t;
-    t.sumi = q8_sumi(o.a, o.b);
-    if constexpr (kQ4) {
-      t.scl = q8_dxy(o.ux & kmask, one);
-      t.dy = fp16_bits_to_f32(o.uy);
-      asm volatile("" : "+v"(t.dy));  // widened once (not an fma_mix per output)
-    } else {
-      t.scl = q8_dxy(o.ux & kmask, o.uy & kmask);
-      t.dy = 0.0f;
-    }
-    return t;
-  };
+  const auto issue = [&](const Ops32 &o) { return issue32<kQ4>(o, kmask, one); };
   float acc[16];
 #pragma unroll
   for (int e = 0; e < 16; ++e)
     acc[e] = 0.0f;
-  auto fold = [&](const Step &t) {
-    if constexpr (kQ4) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        acc[e] = fmaf(static_cast<float>(t.sumi[e]) * t.scl[e], t.dy, acc[e]);
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        asm volatile("" : "+v"(acc[e]));
-    } else {  // all 16 conversions before the fmas, as q8_fold<true> (without its pin)
-      float f[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        f[e] = static_cast<float>(t.sumi[e]);
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        acc[e] = fmaf(f[e], t.scl[e], acc[e]);
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        asm volatile("" : "+v"(acc[e]));
-    }
-  };
+  const auto fold = [&](const Step32 &t) { fold32<kQ4>(acc, t); };
 
   Ops32 ring[kSAhead];
 #pragma unroll
   for (int j = 0; j < kSAhead; ++j)
     load(min(static_cast<unsigned>(j), last), ring[j]);
-  Step cur = issue(ring[0]);
+  Step32 cur = issue(ring[0]);
   load(min(static_cast<unsigned>(kSAhead), last), ring[0]);
   // block b + 1 sits in slot (b + 1) % kSAhead: its MFMAs go out before block
   // b's fold, and the slot is refilled with block b + 1 + kSAhead (clamped to
@@ -1156,7 +1176,7 @@ __global__ __launch_bounds__(256, 2) void gemm_tiles32(unsigned nb, float *s, co
   // the waits count exactly the loads still in flight.
   auto step = [&](unsigned b, int j) {
     const int kn = (j + 1) % kSAhead;
-    const Step nxt = issue(ring[kn]);
+    const Step32 nxt = issue(ring[kn]);
     load(min(b + 1 + kSAhead, last), ring[kn]);
     fold(cur);
     cur = nxt;
@@ -1171,12 +1191,186 @@ __global__ __launch_bounds__(256, 2) void gemm_tiles32(unsigned nb, float *s, co
   for (int j = 0; j < kSAhead - 1; ++j)
     if (b0 + j < nb)
       step(b0 + j, j);
-  const size_t col = static_cast<size_t>(tn) * kSBN + 32 * wn + li;
+  store32(s, acc, static_cast<size_t>(tm) * kSBM + 32 * wm,
+          static_cast<size_t>(tn) * kSBN + 32 * wn + li, h, nr, nc, bs);
+}
+
+// ---- the same tiles straight from the plain rows ---------------------------
+// For the reference ABI without a workspace (tcrv_hip_q8_0_q8_0_gemm,
+// tcrv_hip_q4_0_q8_0_gemm) at shapes of few output tiles: each work-group packs
+// its 64 weight rows and 64 tokens into records in LDS, one 8-block chunk at a
+// time, as the span pack does (a lane per row, the row's chunk span read whole
+// with aligned 128-bit loads: Q8_0 in two halves of 9 loads on two waves, Q4_0
+// 9 loads on one), and the four waves fold their 32 x 32 tiles from there as
+// gemm_tiles32 does from HBM.  Chunk c + 1 is loaded into registers before
+// chunk c is folded and written to the other LDS stage after; rows 16-byte
+// aligned and a whole number of chunks (n a multiple of 256).
+constexpr int kFKB = kPackSpan;     // blocks per K chunk
+constexpr int kFOp = kFKB * kTRec;  // 17408: one operand's records of a chunk
+constexpr int kFStage = 2 * kFOp;   // weights then tokens
+
+// This lane's part of a chunk: Q8_0 blocks 4h .. 4h + 3 of its row's span
+// (pieces 8h .. 8h + 8, 16 bytes each), Q4_0 all 8 blocks (pieces 0 .. 8).
+struct Span9 {
+  uint32_t v[36];
+};
+
+__device__ __forceinline__ void load_span9(const uint8_t *p, bool live, Span9 &w) {
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    const size_t row = static_cast<size_t>(tm) * kSBM + 32 * wm + 8 * (e >> 2) + 4 * h + (e & 3);
-    if (row < nr && col < nc)
-      s[row * bs + col] = acc[e];
+  for (int k = 0; k < 9; ++k) {
+    uint4 x = make_uint4(0u, 0u, 0u, 0u);
+    if (live)
+      x = reinterpret_cast<const uint4 *>(p)[k];
+    w.v[4 * k] = x.x; w.v[4 * k + 1] = x.y; w.v[4 * k + 2] = x.z; w.v[4 * k + 3] = x.w;
+  }
+}
+
+__device__ __forceinline__ void put_record(uint8_t *rec, int r, const uint32_t (&q)[8], uint32_t d) {
+  reinterpret_cast<uint4 *>(rec)[r] = make_uint4(q[0], q[1], q[2], q[3]);
+  reinterpret_cast<uint4 *>(rec + 1024)[r] = make_uint4(q[4], q[5], q[6], q[7]);
+  reinterpret_cast<uint16_t *>(rec + 2048)[r] = static_cast<uint16_t>(d);
+}
+
+// Q8_0 half kH of a chunk span: block j of the half is chunk block 4kH + j at
+// window byte 8kH + 34j (even j: the scale is the low half of that dword and
+// the quants start 2 bytes in; odd j: the scale is the high half of the dword
+// before the quants, which are dword aligned).
+template <int kH>
+__device__ __forceinline__ void put_q8_half(uint8_t *op, int r, const Span9 &w) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t q[8], d;
+    if ((j & 1) == 0) {
+      const int w0 = (8 * kH + 34 * j) / 4;
+      d = w.v[w0] & 0xffffu;
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+        q[m] = funnel16(w.v[w0 + m], w.v[w0 + m + 1]);
+    } else {
+      const int w0 = (8 * kH + 34 * j - 2) / 4;
+      d = w.v[w0] >> 16;
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+        q[m] = w.v[w0 + 1 + m];
+    }
+    put_record(op + (4 * kH + j) * kTRec, r, q, d);
+  }
+}
+
+// Q4_0 chunk span (144 bytes): block k at byte 18k, its nibbles decoded to n - 8.
+__device__ __forceinline__ void put_q4_span(uint8_t *op, int r, const Span9 &w) {
+#pragma unroll
+  for (int k = 0; k < kFKB; ++k) {
+    uint32_t raw[4], q[8], d;
+    if ((k & 1) == 0) {
+      const int w0 = 9 * k / 2;
+      d = w.v[w0] & 0xffffu;
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        raw[m] = funnel16(w.v[w0 + m], w.v[w0 + m + 1]);
+    } else {
+      const int w0 = (18 * k - 2) / 4;
+      d = w.v[w0] >> 16;
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        raw[m] = w.v[w0 + 1 + m];
+    }
+    decode_q4_quants(raw, q);
+    put_record(op + k * kTRec, r, q, d);
+  }
+}
+
+// kWave: the wave's index, a template argument so that each wave's staging
+// code has constant offsets (with the staging half a run-time value the
+// compiler merged the two halves' code into one with the window in scratch).
+template <bool kQ4, int kWave>
+__device__ __forceinline__ void rows_few_body(unsigned nb, float *s, const uint8_t *vx,
+                                              size_t bx, const uint8_t *vy, size_t by,
+                                              size_t nr, size_t nc, size_t bs, uint8_t *lds) {
+  const int lane = threadIdx.x & 63;
+  constexpr int wave = kWave;
+  constexpr int wm = wave & 1, wn = wave >> 1;
+  const int li = lane & 31, h = lane >> 5;
+  const unsigned tiles_m = static_cast<unsigned>((nr + kSBM - 1) / kSBM);
+  const unsigned tiles_n = static_cast<unsigned>((nc + kSBN - 1) / kSBN);
+  unsigned tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const size_t m0 = static_cast<size_t>(tm) * kSBM, n0 = static_cast<size_t>(tn) * kSBN;
+  // staging role: waves 0, 1 the weight rows (Q8_0 halves 0, 1; Q4_0 wave 0
+  // the whole span, wave 1 nothing), waves 2, 3 the token halves 0, 1
+  constexpr bool tok = wave >= 2;
+  constexpr int half = wave & 1;
+  constexpr bool stager = tok || !kQ4 || half == 0;
+  const size_t srow = (tok ? n0 : m0) + lane;
+  const bool live = stager && srow < (tok ? nc : nr);
+  constexpr int kXSpan = kFKB * (kQ4 ? kQ4Bytes : kQ8Bytes);
+  const uint8_t *src = tok ? vy + min(srow, nc - 1) * by + 128 * half
+                           : vx + min(srow, nr - 1) * bx + (kQ4 ? 0 : 128 * half);
+  const size_t span = tok ? kFKB * kQ8Bytes : kXSpan;
+  auto put = [&](int st, const Span9 &w) {
+    uint8_t *op = lds + st * kFStage + (tok ? kFOp : 0);
+    if constexpr (kQ4 && !tok)
+      put_q4_span(op, lane, w);
+    else
+      put_q8_half<half>(op, lane, w);
+  };
+
+  const uint32_t kmask = h ? 0u : 0xffffu;
+  const uint32_t one = h ? 0u : 0x3c00u;
+  const unsigned qa = h * 1024 + (32 * wm + li) * 16, qb = h * 1024 + (32 * wn + li) * 16;
+  const unsigned sa = 2 * kTG * 16 + (32 * wm + li) * 2, sb = 2 * kTG * 16 + (32 * wn + li) * 2;
+  auto ops = [&](int st, int k) {
+    const uint8_t *ra = lds + st * kFStage + k * kTRec, *rb = ra + kFOp;
+    Ops32 o;
+    o.a = *reinterpret_cast<const v4i *>(ra + qa);
+    o.b = *reinterpret_cast<const v4i *>(rb + qb);
+    o.ux = *reinterpret_cast<const uint16_t *>(ra + sa);
+    o.uy = *reinterpret_cast<const uint16_t *>(rb + sb);
+    return o;
+  };
+  float acc[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    acc[e] = 0.0f;
+
+  const unsigned nchunks = nb / kFKB;
+  Span9 w;
+  if (stager) {
+    load_span9(src, live, w);
+    put(0, w);
+  }
+  __syncthreads();
+  for (unsigned c = 0; c < nchunks; ++c) {
+    const int st = c & 1;
+    const bool more = c + 1 < nchunks;
+    if (stager && more)
+      load_span9(src + (c + 1) * span, live, w);
+    Step32 cur = issue32<kQ4>(ops(st, 0), kmask, one);
+#pragma unroll
+    for (int k = 0; k < kFKB; ++k) {
+      Step32 nxt;
+      if (k + 1 < kFKB)
+        nxt = issue32<kQ4>(ops(st, k + 1), kmask, one);
+      fold32<kQ4>(acc, cur);
+      cur = nxt;
+    }
+    if (stager && more)
+      put(st ^ 1, w);
+    __syncthreads();
+  }
+  store32(s, acc, m0 + 32 * wm, n0 + 32 * wn + li, h, nr, nc, bs);
+}
+
+template <bool kQ4>
+__global__ __launch_bounds__(256, 2) void gemm_rows_few(unsigned nb, float *s, const uint8_t *vx,
+                                                        size_t bx, const uint8_t *vy, size_t by,
+                                                        size_t nr, size_t nc, size_t bs) {
+  __shared__ __align__(16) uint8_t lds[2 * kFStage];
+  switch (__builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6)) {
+  case 0: rows_few_body<kQ4, 0>(nb, s, vx, bx, vy, by, nr, nc, bs, lds); break;
+  case 1: rows_few_body<kQ4, 1>(nb, s, vx, bx, vy, by, nr, nc, bs, lds); break;
+  case 2: rows_few_body<kQ4, 2>(nb, s, vx, bx, vy, by, nr, nc, bs, lds); break;
+  default: rows_few_body<kQ4, 3>(nb, s, vx, bx, vy, by, nr, nc, bs, lds); break;
   }
 }
 
@@ -1303,6 +1497,13 @@ bool tiles32_first(size_t tiles, size_t tiles64, size_t nb) {
   return tiles < 256 && tiles64 <= 1024 && nb <= 0xffffffffu;
 }
 
+size_t tiles64_of(size_t nr, size_t nc) {
+  return ((nr + tcrv::kSBM - 1) / tcrv::kSBM) * ((nc + tcrv::kSBN - 1) / tcrv::kSBN);
+}
+size_t tiles128_of(size_t nr, size_t nc) {
+  return ((nr + tcrv::kDBM - 1) / tcrv::kDBM) * ((nc + tcrv::kDBN - 1) / tcrv::kDBN);
+}
+
 int gemm_tiles(size_t nb, float *s, const uint8_t *tx, const uint8_t *ty, size_t nr, size_t nc,
                size_t bs, hipStream_t st, bool q4 = false) {
   using namespace tcrv_host;
@@ -1379,19 +1580,42 @@ int tcrv_hip_q8_0_q8_0_gemm_tiles(size_t n, float *s, const uint8_t *tx, const u
 
 namespace tcrv_host {
 
+// The plain-row entries' kernel for shapes of few output tiles (gemm_rows_few):
+// rows 16-byte aligned, a whole number of 8-block chunks.  Its staging costs
+// more than the fold (4096 x 128 x 4096 Q8_0: 31.0 us, 18.6 without staging
+// past the first chunk, 25.9 without the fold: each staging load instruction
+// touches 64 rows' lines), so it serves fewer work-groups than gemm_tiles32
+// does: past 768 (Q8_0) or 1024 (Q4_0) the 256-row kernels are as fast (4096 x
+// 1024 x 4096 Q8_0: 97 against 91-93 us; Q4_0 91 against 98-101).
+int gemm_rows_few(bool q4, size_t nb, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy,
+                  size_t by, size_t nr, size_t nc, size_t bs, void *stream) {
+  if (nr < 2 || nc < 2 || nb == 0 || nb % tcrv::kFKB != 0 || !aligned16(vx) || !aligned16(vy) ||
+      bx % 16 != 0 || by % 16 != 0)
+    return TCRV_HIP_ERR_UNSUPPORTED;
+  const size_t tiles64 = tiles64_of(nr, nc);
+  if (!tiles32_first(tiles128_of(nr, nc), tiles64, nb) || tiles64 > (q4 ? 1024u : 768u))
+    return TCRV_HIP_ERR_UNSUPPORTED;
+  const dim3 g(static_cast<unsigned>(tiles64)), b(256);
+  const unsigned nbu = static_cast<unsigned>(nb);
+  if (q4)
+    tcrv::gemm_rows_few<true><<<g, b, 0, as_stream(stream)>>>(nbu, s, vx, bx, vy, by, nr, nc, bs);
+  else
+    tcrv::gemm_rows_few<false><<<g, b, 0, as_stream(stream)>>>(nbu, s, vx, bx, vy, by, nr, nc, bs);
+  return launch_status();
+}
+
 // Shapes the tiled kernel does not serve run as tcrv_hip_q8_0_q8_0_gemm,
 // without the workspace: fewer weight rows than one 256-row tile, a single
 // token (decode), no blocks, or more than kMaxTiledNb blocks.  So do a few
 // tokens that the plain entry's multi-column GEMVs take (even block count,
-// 4-byte aligned rows and strides): up to kWsColsMax tokens they beat packing
+// 4-byte aligned rows and strides): up to kColsFirstMax tokens they beat packing
 // both operands for the tiled kernels (us, 4096 weight rows, K 4096, Q8_0 /
 // Q4_0: 16 tokens 15.0 / 16.3 against ~25 / ~28; 32 tokens 30.8 / 32.3
 // against ~25 / ~28).
-constexpr size_t kWsColsMax = 24;
 bool ws_cols_first(size_t nb, const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by,
                    size_t nc) {
-  return nc <= kWsColsMax && nc <= kGemvColsMax && nb % 2 == 0 && aligned4(vx) &&
-         aligned4(vy) && bx % 4 == 0 && by % 4 == 0;
+  return nc <= kColsFirstMax && nb % 2 == 0 && aligned4(vx) && aligned4(vy) && bx % 4 == 0 &&
+         by % 4 == 0;
 }
 bool gemm_ws_uses_workspace(size_t n, const uint8_t *vx, size_t bx, const uint8_t *vy,
                             size_t by, size_t nr, size_t nc) {

@@ -961,12 +961,19 @@ int tcrv_hip_q4_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t
     const int st = tcrv_host::q4_0_rows_direct(nb, s, 1, vx, 0, vy, by, nc, stream);
     if (st != TCRV_HIP_ERR_UNSUPPORTED)
       return st;
-  } else if (nc <= tcrv_host::kGemvColsMax) {
-    // a few tokens: the weights are read once per group of up to four columns
-    // (the MFMA GEMM would run only nr / 256 work-groups)
-    const int st = tcrv_host::gemv_cols_q4_0_q8_0(nb, s, bs, vx, bx, vy, by, nr, nc, stream);
-    if (st != TCRV_HIP_ERR_UNSUPPORTED)
-      return st;
+  } else {
+    if (nc > tcrv_host::kColsFirstMax) {  // few output tiles: one 32 x 32 tile a wave
+      const int st = tcrv_host::gemm_rows_few(true, nb, s, vx, bx, vy, by, nr, nc, bs, stream);
+      if (st != TCRV_HIP_ERR_UNSUPPORTED)
+        return st;
+    }
+    if (nc <= tcrv_host::kGemvColsMax) {
+      // a few tokens: the weights are read once per group of up to eight
+      // columns (the MFMA GEMM would run only nr / 256 work-groups)
+      const int st = tcrv_host::gemv_cols_q4_0_q8_0(nb, s, bs, vx, bx, vy, by, nr, nc, stream);
+      if (st != TCRV_HIP_ERR_UNSUPPORTED)
+        return st;
+    }
   }
   const int st = tcrv_host::q4_0_gemm_mfma(nb, s, vx, bx, vy, by, nr, nc, bs, stream);
   if (st != TCRV_HIP_ERR_UNSUPPORTED)

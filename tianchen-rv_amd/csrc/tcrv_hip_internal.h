@@ -196,6 +196,14 @@ int q4_0_grid(size_t n, float *s, const uint8_t *vx, size_t bx, const uint8_t *v
 // TCRV_HIP_ERR_UNSUPPORTED for an odd block count or operands/strides that are
 // not 4-byte aligned.
 constexpr size_t kGemvColsMax = 64;
+// Up to this many tokens the multi-column GEMVs run first; past it the
+// one-tile-a-wave GEMMs (gemm_rows_few from plain rows, gemm_tiled.hip) where
+// they serve the shape, then the GEMVs up to kGemvColsMax.
+constexpr size_t kColsFirstMax = 24;
+// The GEMM of few output tiles straight from plain rows (16-byte aligned rows
+// and strides, n a multiple of 256); TCRV_HIP_ERR_UNSUPPORTED otherwise.
+int gemm_rows_few(bool q4, size_t nb, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy,
+                  size_t by, size_t nr, size_t nc, size_t bs, void *stream);
 int gemv_cols_q4_0_q8_0(size_t nb, float *s, size_t bs, const uint8_t *vx, size_t bx,
                         const uint8_t *vy, size_t by, size_t nr, size_t nc, void *stream);
 int gemv_cols_q8_0_q8_0(size_t nb, float *s, size_t bs, const uint8_t *vx, size_t bx,
