@@ -60,6 +60,8 @@ GEMM_OPS = 2.0 * N * N * N                                      # 137 438 953 47
 PACK_BYTES = 2 * N * (N // 32) * 18                             # 18 874 368
 REPACK8_BYTES = N * (N // 32) * 34 + (N // 32) * 34 + N * 4     # 17 846 528
 BATCH_TOKENS = 4  # the batched-decode GEMM entries of `configs`
+PREFILL_TOKENS = 128  # the short-prompt GEMM entries of `configs`
+PREFILL_OPS = 2.0 * N * PREFILL_TOKENS * N                      # 4 294 967 296
 QUANT_BYTES = N * N * 4 + (N * N // 32) * 34                    # 84 934 656
 
 
@@ -605,6 +607,45 @@ def bench_configs(torch, lib, stream, args):
                      "sets": sets}
         del Wc, Cb, reg
 
+    # a short prompt: the a7 and a9 GEMMs with PREFILL_TOKENS tokens through the
+    # plain entries (few output tiles: packed in LDS per work-group, one 32 x 32
+    # tile a wave) and the workspace entries (packed per call, the same tile per
+    # wave straight from the records), every launch over its own weight copy
+    act = inputs("gemm_a")[:PREFILL_TOKENS].copy()
+    actd = torch.from_numpy(act).to(dev)
+    for quant, wsrc in (("q4_0", inputs("gemv_w")), ("q8_0", inputs("gemm_b"))):
+        sets = copies_for(wsrc.size, 2)
+        Wc = torch.empty((sets, wsrc.size), dtype=torch.uint8, device=dev)
+        Wc[:] = torch.from_numpy(wsrc.reshape(-1)).to(dev)
+        Cb = torch.empty((sets, N * PREFILL_TOKENS), device=dev)
+        bx = wsrc.shape[1]
+        plain = checked(getattr(lib, f"tcrv_hip_{quant}_q8_0_gemm"), f"{quant} prefill")
+        ws_fn = checked(getattr(lib, f"tcrv_hip_{quant}_q8_0_gemm_ws"), f"{quant} prefill ws")
+        wsb = getattr(lib, f"tcrv_hip_{quant}_q8_0_gemm_workspace_bytes")(N, N, PREFILL_TOKENS)
+        wsp = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        ptrs = [(Cb[i].data_ptr(), Wc[i].data_ptr()) for i in range(sets)]
+        calls = {
+            f"{quant}_q8_0_gemm_128_tokens": lambda i: plain(
+                N, ptrs[i % sets][0], ptrs[i % sets][1], actd.data_ptr(), act.shape[1], N,
+                PREFILL_TOKENS, bx, PREFILL_TOKENS, sp),
+            f"{quant}_q8_0_gemm_ws_128_tokens": lambda i: ws_fn(
+                N, ptrs[i % sets][0], ptrs[i % sets][1], actd.data_ptr(), act.shape[1], N,
+                PREFILL_TOKENS, bx, PREFILL_TOKENS, wsp.data_ptr(), wsb, sp)}
+        for name, step in calls.items():
+            reg = Region(torch, stream, step, 100)
+            reg.run()
+            us = sorted(reg.run() * 1e3 / 100 for _ in range(3))[1]
+            same_as_eager(torch, stream, Cb[99 % sets],
+                          lambda o, k=99 % sets: plain(N, o, Wc[k].data_ptr(), actd.data_ptr(),
+                                                       act.shape[1], N, PREFILL_TOKENS, bx,
+                                                       PREFILL_TOKENS, sp), name)
+            out[name] = {"workload": f"{'a7 Q4_0' if quant == 'q4_0' else 'a9 Q8_0'} x Q8_0 GEMM "
+                                     f"4096 weight rows x {PREFILL_TOKENS} tokens x 4096 "
+                                     f"({'workspace entry' if '_ws_' in name else 'plain entry'})",
+                         "us": round(us, 2), "TOPS": round(PREFILL_OPS / us / 1e6, 1),
+                         "sets": sets}
+        del Wc, Cb, wsp
+
     # a10 quantize_row_q8_0: 4096 activation rows x 4096 f32 -> Q8_0 (the prefill
     # GEMM's activation operand; read 64 MiB, write 17.8 MB)
     xf = torch.from_numpy(inputs("gemm_a_f32")).to(dev)
@@ -974,6 +1015,19 @@ def cpu_baseline_configs(seconds: float):
                                                      nt, wsrc.shape[1], nt, 1),
             lambda wsrc=wsrc, gemm=gemm, nt=nt: gemm(N, wsrc, act[:nt].copy(), act.shape[1], N,
                                                      nt, wsrc.shape[1], nt, threads))
+    # a short prompt: slices of 64 weight rows x 128 tokens (1/64 of the GEMM),
+    # OpenMP over the 64 rows
+    act128 = a8[:PREFILL_TOKENS].copy()
+    for name, wsrc, gemm in (("q4_0_q8_0_gemm_128_tokens", w, ora.gemm_q4_0),
+                             ("q8_0_q8_0_gemm_128_tokens", w8, ora.gemm_q8_0)):
+        w64 = wsrc[:64].copy()
+        out[name] = entry(
+            2.0 * 64 * PREFILL_TOKENS * N, "TOPS", "slices of 64 weight rows x 128 tokens x "
+            "4096 (1/64 of the GEMM each), OpenMP over the 64 weight rows",
+            lambda w64=w64, gemm=gemm: gemm(N, w64, act128, act128.shape[1], 64, PREFILL_TOKENS,
+                                            w64.shape[1], PREFILL_TOKENS, 1),
+            lambda w64=w64, gemm=gemm: gemm(N, w64, act128, act128.shape[1], 64, PREFILL_TOKENS,
+                                            w64.shape[1], PREFILL_TOKENS, threads))
     wx16 = ora.pack_q4_0x16(src, nx16)
     ax4s = [ora.pack_q8_0x4(a8[16 * t:16 * t + 16].copy(), 16, nb, a8.shape[1])
             for t in range(threads)]
