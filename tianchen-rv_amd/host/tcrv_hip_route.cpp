@@ -231,10 +231,18 @@ const tcrv_hip_schedule kSchedules[] = {
     {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_DECODE, "gemv_q4_0_q8_0_direct", "rows_per_wave", 8,
      0, "tcrv_hip_gemv_q4_0_q8_0_shaped", -1.0,
      "512 waves for 4096 rows leave half the SIMDs idle during the read"},
-    // the tiled GEMMs: tokens per work-group tile (256 weight rows each); the
-    // entries pick per shape, the larger tile when its rounds of 256
-    // work-groups x 15 are at most the smaller tile's rounds x 8 (one round of
-    // 256 x 256 tiles takes ~1.87 rounds of 256 x 128 ones)
+    // the tiled GEMMs: tokens per work-group tile; the entries pick per shape:
+    // 64 x 64 tiles of one 32 x 32 tile a wave where 256 x 128 tiles would not
+    // fill one round of the CUs (at most 1024 work-groups), else 256 weight
+    // rows and the larger tile when its rounds of 256 work-groups x 15 are at
+    // most the smaller tile's rounds x 8 (one round of 256 x 256 tiles takes
+    // ~1.87 rounds of 256 x 128 ones)
+    {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles32", "work_group_tokens", 64, 0,
+     nullptr, -1.0,
+     "one 32x32 tile a wave, operands straight from the records; where few output tiles "
+     "(4096 x 128 x 4096: 72 -> 17 us pre-packed); from plain rows gemm_rows_few"},
+    {"tcrv_rvv.q4_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles32", "work_group_tokens", 64, 0,
+     nullptr, -1.0, "one 32x32 tile a wave; where few output tiles (4096 x 128: 86 -> 20 us)"},
     {"tcrv_rvv.q8_0_q8_0_gemm", TCRV_HIP_M_PREFILL, "gemm_tiles_q8", "work_group_tokens", 128, 0,
      nullptr, -1.0,
      "16 waves of two 32x32 tiles, 6-block K chunks; where it takes fewer rounds (4096 x 2048 "
