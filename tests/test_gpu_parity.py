@@ -1157,15 +1157,17 @@ def test_q8_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
 @pytest.mark.parametrize("quant", ["q8_0", "q4_0"])
 @pytest.mark.parametrize("nr,nc,nb", [
     (4096, 130, 13),  # 32 tiles of 256 x 128; tokens end 2 rows into a record group; 7 + 6 blocks
-    (300, 70, 7),     # exactly one round of the 7 blocks in flight; partial row and token groups
+    (300, 70, 7),     # 16 x 16 tiles: 7 blocks (less than one round of the 12 in flight)
     (1000, 600, 1),   # one block: only the clamped prologue loads
     (4100, 960, 20),  # 136 tiles of 256 x 128, 975 work-groups; two rounds and a 6-block rest
-    (256, 2, 14),     # two tokens (pre-packed: no multi-column GEMV route)
+    (256, 2, 14),     # two tokens, 16 x 16 tiles: one round of 12 blocks and a 2-block rest
+    (4096, 64, 29),   # 16 x 16 tiles, 256 work-groups (the bound): two rounds and a 5-block rest
 ])
 def test_gemm_tiles_one_tile_a_wave(hip, oracle, dev, quant, nr, nc, nb):
     """Pre-packed operands where the 256-row tiles would not fill one round of the CUs: the
-    kernel with one 32 x 32 tile a wave; whole outputs against the plain entry bit for bit and
-    sampled rows against the oracle, with -128 block sums and a padded output stride."""
+    kernels with one 32 x 32 or one 16 x 16 tile a wave; whole outputs against the plain entry
+    bit for bit and sampled rows against the oracle, with -128 block sums and a padded output
+    stride."""
     n = nb * 32
     q4 = quant == "q4_0"
     w = (synth.q4_0_matrix if q4 else synth.q8_0_matrix)(nr, n, 1030 + nb, 0.02)
@@ -1238,13 +1240,13 @@ def test_gemm_plain_rows_few_tiles(hip, oracle, dev, quant, nr, nc, nb):
 
 def _ws_route(nr, nc, nb, bx, by):
     """Which kernel the workspace entries run (the host's rules, restated): the plain entry's
-    multi-column GEMVs for a few tokens, the one-tile-a-wave kernel below one round of 256 x 128
-    tiles (and at most 1024 of its 64 x 64 work-groups), else the 256 x 256 or 256 x 128 tiles
-    by the rounds rule."""
+    multi-column GEMVs for a few tokens, one tile a wave below one round of 256 x 128 tiles (and
+    at most 1024 of its 64 x 64 work-groups) -- 16 x 16 while those waves fit one a SIMD, else
+    32 x 32 -- else the 256 x 256 or 256 x 128 tiles by the rounds rule."""
     if nc <= 24 and nb % 2 == 0 and bx % 4 == 0 and by % 4 == 0:
         return "cols"
     if -(-nr // 256) * -(-nc // 128) < 256 and -(-nr // 64) * -(-nc // 64) <= 1024:
-        return "32x32"
+        return "16x16" if -(-nr // 32) * -(-nc // 32) <= 256 else "32x32"
     return "256x256" if _rounds(nr, nc, 256, 256) * 15 <= _rounds(nr, nc, 256, 128) * 8 \
         else "256x128"
 
@@ -1293,7 +1295,7 @@ def test_gemm_ws_random_shapes(hip, oracle, dev, quant):
         row = ora(n, w[r].copy(), a, a.shape[1], 1, nc, w.shape[1], nc, 8)
         assert_f32_parity(got[r, :nc], row, what=f"{what}, row {r}")
         del dw, da, ref, ws, s
-    assert seen == {"cols", "32x32", "256x256", "256x128"}  # every route ran
+    assert seen == {"cols", "16x16", "32x32", "256x256", "256x128"}  # every route ran
 
 
 def test_q8_0_gemm_ws_full_size_sampled(hip, oracle, dev):

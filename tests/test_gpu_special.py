@@ -181,12 +181,13 @@ def test_q4_0_gemm_nonfinite_dx_mid_k(hip, oracle, dev, nb):
 
 
 @pytest.mark.parametrize("nr,nc,kernel", [(4096, 4096, "256x256"), (4196, 4166, "256x128"),
-                                          (4096, 130, "32x32")])
+                                          (4096, 130, "32x32"), (4096, 40, "16x16")])
 @pytest.mark.parametrize("quant,nonfinite_every", [("q8_0", 16), ("q4_0", 16), ("q4_0", 0)])
 def test_gemm_ws_tiles_special_scales(hip, oracle, dev, quant, nonfinite_every, nr, nc, kernel):
     """Each work-group tile of the tiled GEMMs, through the workspace entries (256 x 256: 4096 x
     4096 outputs; 256 x 128: 4196 x 4166, three rounds of it against two of the larger tile; one
-    32 x 32 tile a wave: 4096 x 130): special scales in both operands, non-finite d_x in every
+    32 x 32 tile a wave: 4096 x 130; one 16 x 16 tile a wave: 4096 x 40): special scales in both
+    operands, non-finite d_x in every
     16th weight row (every Q4_0 wave of the 256-row tiles folds exactly from chunk 0) or, with
     none there, +-Inf and NaN planted at chunk 0, in the middle of K, in the last full chunk and
     in the 1-block tail (chunks of 4 and of 6 blocks), and an infinite d_x over a zero block

@@ -1195,6 +1195,134 @@ __global__ __launch_bounds__(256, 2) void gemm_tiles32(unsigned nb, float *s, co
           static_cast<size_t>(tn) * kSBN + 32 * wn + li, h, nr, nc, bs);
 }
 
+// ---- fewer still: one 16 x 16 tile a wave ----------------------------------
+// Where even the 32 x 32 tiles leave most SIMDs without a wave (4096 weight
+// rows x 64 tokens: 256 waves for 1024 SIMDs, each at one wave a SIMD, where
+// the fold issues at ~6 cycles an instruction), a wave folds one 16 x 16 tile
+// and a work-group of 4 waves a 32 x 32 tile (half of a record group's rows).  A
+// v_mfma_i32_16x16x32_i8 lane holds 8 quants, lane l: row l % 16, quants
+// 8 (l / 16) .. + 7 -- 8 bytes of one record half, so again one load per lane
+// and operand; the f16 MFMA (16x16x16) gives d_x * d_y (Q8_0) or spreads d_x
+// (Q4_0) as in the 32 x 32 kernel, from k-slot 0 of lanes 0-15.  Each output
+// keeps its ascending-block fold: the same bits.
+constexpr int kTBM = 32, kTBN = 32;  // work-group tile
+constexpr int kTAhead = 12;          // blocks in flight a wave
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+struct Ops16 {
+  long a, b;
+  uint32_t ux, uy;
+};
+
+struct Step16 {
+  v4i sumi;
+  v4f scl;
+  float dy;
+};
+
+__device__ __forceinline__ v4h kslot0_16(uint32_t bits) {
+  const v2h z = {};
+  return __builtin_shufflevector(__builtin_bit_cast(v2h, bits), z, 0, 1, 2, 3);
+}
+
+template <bool kQ4>
+__device__ __forceinline__ Step16 issue16(const Ops16 &o, uint32_t kmask, uint32_t one) {
+  Step16 t;
+  t.sumi = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.a, o.b, v4i{}, 0, 0, 0);
+  if constexpr (kQ4) {
+    t.scl = __builtin_amdgcn_mfma_f32_16x16x16f16(kslot0_16(o.ux & kmask), kslot0_16(one),
+                                                 v4f{}, 0, 0, 0);
+    t.dy = fp16_bits_to_f32(o.uy);
+    asm volatile("" : "+v"(t.dy));
+  } else {
+    t.scl = __builtin_amdgcn_mfma_f32_16x16x16f16(kslot0_16(o.ux & kmask),
+                                                 kslot0_16(o.uy & kmask), v4f{}, 0, 0, 0);
+    t.dy = 0.0f;
+  }
+  return t;
+}
+
+template <bool kQ4>
+__device__ __forceinline__ void fold16(float (&acc)[4], const Step16 &t) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (kQ4)
+      acc[e] = fmaf(static_cast<float>(t.sumi[e]) * t.scl[e], t.dy, acc[e]);
+    else
+      acc[e] = fmaf(static_cast<float>(t.sumi[e]), t.scl[e], acc[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    asm volatile("" : "+v"(acc[e]));
+}
+
+template <bool kQ4>
+__global__ __launch_bounds__(256, 2) void gemm_tiles16(unsigned nb, float *s, const uint8_t *tx,
+                                                    const uint8_t *ty, size_t nr, size_t nc,
+                                                    size_t bs) {
+  const int lane = threadIdx.x & 63;
+  const int tile = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int wm = tile & 1, wn = tile >> 1;  // the wave's 16-row halves of the 32 x 32 tile
+  const int li = lane & 15, q = lane >> 4;  // MFMA row / token li, quant group q
+  const unsigned tiles_m = static_cast<unsigned>((nr + kTBM - 1) / kTBM);
+  const unsigned tiles_n = static_cast<unsigned>((nc + kTBN - 1) / kTBN);
+  unsigned tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  // weight rows 32 tm + 16 wm + li: record group tm / 2, row (tm % 2) * 32 + 16 wm + li
+  const uint8_t *ra = tx + static_cast<size_t>(tm >> 1) * nb * kTRec;
+  const uint8_t *rb = ty + static_cast<size_t>(tn >> 1) * nb * kTRec;
+  const unsigned xr = (tm & 1) * 32 + 16 * wm + li, yr = (tn & 1) * 32 + 16 * wn + li;
+  const unsigned qa = (q >> 1) * 1024 + xr * 16 + 8 * (q & 1);
+  const unsigned qb = (q >> 1) * 1024 + yr * 16 + 8 * (q & 1);
+  const unsigned sa = 2 * kTG * 16 + xr * 2, sb = 2 * kTG * 16 + yr * 2;
+  const uint32_t kmask = q ? 0u : 0xffffu;  // k-slot 0 lives in lanes 0-15
+  const uint32_t one = q ? 0u : 0x3c00u;
+  const unsigned last = nb - 1;
+
+  auto load = [&](unsigned b, Ops16 &o) {
+    const __amdgpu_buffer_rsrc_t pa = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(ra + static_cast<size_t>(b) * kTRec), (short)0, kTRec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t pb = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(rb + static_cast<size_t>(b) * kTRec), (short)0, kTRec, 0x00020000);
+    o.a = __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(pa, qa, 0, 0));
+    o.b = __builtin_bit_cast(long, __builtin_amdgcn_raw_buffer_load_b64(pb, qb, 0, 0));
+    o.ux = __builtin_amdgcn_raw_buffer_load_b16(pa, sa, 0, 0);
+    o.uy = __builtin_amdgcn_raw_buffer_load_b16(pb, sb, 0, 0);
+  };
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  Ops16 ring[kTAhead];
+#pragma unroll
+  for (int j = 0; j < kTAhead; ++j)
+    load(min(static_cast<unsigned>(j), last), ring[j]);
+  Step16 cur = issue16<kQ4>(ring[0], kmask, one);
+  load(min(static_cast<unsigned>(kTAhead), last), ring[0]);
+  auto step = [&](unsigned b, int j) {
+    const int kn = (j + 1) % kTAhead;
+    const Step16 nxt = issue16<kQ4>(ring[kn], kmask, one);
+    load(min(b + 1 + kTAhead, last), ring[kn]);
+    fold16<kQ4>(acc, cur);
+    cur = nxt;
+  };
+  unsigned b0 = 0;
+  for (; b0 + kTAhead <= nb; b0 += kTAhead) {
+#pragma unroll
+    for (int j = 0; j < kTAhead; ++j)
+      step(b0 + j, j);
+  }
+#pragma unroll
+  for (int j = 0; j < kTAhead - 1; ++j)
+    if (b0 + j < nb)
+      step(b0 + j, j);
+  const size_t col = static_cast<size_t>(tn) * kTBN + 16 * wn + li;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const size_t row = static_cast<size_t>(tm) * kTBM + 16 * wm + 4 * q + e;
+    if (row < nr && col < nc)
+      s[row * bs + col] = acc[e];
+  }
+}
+
 // ---- the same tiles straight from the plain rows ---------------------------
 // For the reference ABI without a workspace (tcrv_hip_q8_0_q8_0_gemm,
 // tcrv_hip_q4_0_q8_0_gemm) at shapes of few output tiles: each work-group packs
@@ -1497,6 +1625,14 @@ bool tiles32_first(size_t tiles, size_t tiles64, size_t nb) {
   return tiles < 256 && tiles64 <= 1024 && nb <= 0xffffffffu;
 }
 
+// Fewer still: one 16 x 16 tile a wave while its waves fit one a SIMD (at most
+// 256 work-groups of 32 x 32).  Pre-packed, K 4096, us, 32 x 32 tiles against
+// it: 4096 x 2 17.0 / 13.1, 4096 x 64 17.1 / 13.7 (Q4_0 19.8 / 14.9); past
+// that its loads and doubled VALU per output lose (4096 x 128: 17.5 / 24.2).
+bool tiles16_first(size_t nr, size_t nc) {
+  return ((nr + tcrv::kTBM - 1) / tcrv::kTBM) * ((nc + tcrv::kTBN - 1) / tcrv::kTBN) <= 256;
+}
+
 size_t tiles64_of(size_t nr, size_t nc) {
   return ((nr + tcrv::kSBM - 1) / tcrv::kSBM) * ((nc + tcrv::kSBN - 1) / tcrv::kSBN);
 }
@@ -1514,7 +1650,17 @@ int gemm_tiles(size_t nb, float *s, const uint8_t *tx, const uint8_t *ty, size_t
       ((nr + tcrv::kEBM - 1) / tcrv::kEBM) * ((nc + tcrv::kEBN - 1) / tcrv::kEBN);
   const size_t tiles64 =
       ((nr + tcrv::kSBM - 1) / tcrv::kSBM) * ((nc + tcrv::kSBN - 1) / tcrv::kSBN);
-  if (tiles32_first(tiles, tiles64, nb)) {
+  if (tiles32_first(tiles, tiles64, nb) && tiles16_first(nr, nc)) {
+    const size_t tiles32n =
+        ((nr + tcrv::kTBM - 1) / tcrv::kTBM) * ((nc + tcrv::kTBN - 1) / tcrv::kTBN);
+    const unsigned nbu = static_cast<unsigned>(nb);
+    if (q4)
+      tcrv::gemm_tiles16<true><<<dim3(static_cast<unsigned>(tiles32n)), dim3(256), 0, st>>>(
+          nbu, s, tx, ty, nr, nc, bs);
+    else
+      tcrv::gemm_tiles16<false><<<dim3(static_cast<unsigned>(tiles32n)), dim3(256), 0, st>>>(
+          nbu, s, tx, ty, nr, nc, bs);
+  } else if (tiles32_first(tiles, tiles64, nb)) {
     const unsigned nbu = static_cast<unsigned>(nb);
     if (q4)
       tcrv::gemm_tiles32<true><<<dim3(static_cast<unsigned>(tiles64)), dim3(256), 0, st>>>(
