@@ -1142,12 +1142,12 @@ def test_q8_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
                                                         nc, 8))
         assert np.all(from_dev(ws) == 0x5A)
     w = synth.q8_0_matrix(256, n, 83, 0.02)
-    a = synth.q8_0_matrix(32, n, 84, 1.0)  # past the multi-column GEMVs' 24 tokens
-    need = hip.q8_0_q8_0_gemm_workspace_bytes(n, 256, 32)
+    a = synth.q8_0_matrix(72, n, 84, 1.0)  # past the multi-column GEMVs' 24 tokens
+    need = hip.q8_0_q8_0_gemm_workspace_bytes(n, 256, 72)
     ws = empty_dev(need + 16, torch.uint8, dev)
-    s = empty_dev(256 * 32, torch.float32, dev)
+    s = empty_dev(256 * 72, torch.float32, dev)
     call = lambda *args: hip.call("tcrv_hip_q8_0_q8_0_gemm_ws", n, s, to_dev(w, dev),
-                                  to_dev(a, dev), a.shape[1], 256, 32, w.shape[1], 32, *args, 0,
+                                  to_dev(a, dev), a.shape[1], 256, 72, w.shape[1], 72, *args, 0,
                                   check=False)
     assert call(ws, need - 1) == hip.ERR_BAD_SIZE
     assert call(ws[8:], need) == hip.ERR_MISALIGNED
@@ -1420,13 +1420,13 @@ def test_q4_0_gemm_ws_fallbacks_and_checks(hip, oracle, dev):
                                                         nc, 8))
         assert np.all(from_dev(ws) == 0x5A)
     w = synth.q4_0_matrix(256, n, 87, 0.02)
-    a = synth.q8_0_matrix(32, n, 88, 1.0)  # past the multi-column GEMVs' 24 tokens
-    need = hip.q4_0_q8_0_gemm_workspace_bytes(n, 256, 32)
-    assert need == hip.gemm_tiles_bytes(256, nb) + hip.gemm_tiles_bytes(32, nb)
+    a = synth.q8_0_matrix(72, n, 88, 1.0)  # past the multi-column GEMVs' 24 tokens
+    need = hip.q4_0_q8_0_gemm_workspace_bytes(n, 256, 72)
+    assert need == hip.gemm_tiles_bytes(256, nb) + hip.gemm_tiles_bytes(72, nb)
     ws = empty_dev(need + 16, torch.uint8, dev)
-    s = empty_dev(256 * 32, torch.float32, dev)
+    s = empty_dev(256 * 72, torch.float32, dev)
     call = lambda *args: hip.call("tcrv_hip_q4_0_q8_0_gemm_ws", n, s, to_dev(w, dev),
-                                  to_dev(a, dev), a.shape[1], 256, 32, w.shape[1], 32, *args, 0,
+                                  to_dev(a, dev), a.shape[1], 256, 72, w.shape[1], 72, *args, 0,
                                   check=False)
     assert call(ws, need - 1) == hip.ERR_BAD_SIZE
     assert call(ws[8:], need) == hip.ERR_MISALIGNED

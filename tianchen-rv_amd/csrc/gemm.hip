@@ -954,7 +954,7 @@ extern "C" int tcrv_hip_q8_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx,
     if (st != TCRV_HIP_ERR_UNSUPPORTED)
       return st;
   } else {
-    if (nc > kColsFirstMax) {  // few output tiles: one 32 x 32 tile a wave
+    if (!cols_first(nr, nc)) {  // few output tiles: one 32 x 32 tile a wave
       const int st = gemm_rows_few(false, nb, s, vx, bx, vy, by, nr, nc, bs, stream);
       if (st != TCRV_HIP_ERR_UNSUPPORTED)
         return st;

@@ -1754,20 +1754,20 @@ int gemm_rows_few(bool q4, size_t nb, float *s, const uint8_t *vx, size_t bx, co
 // without the workspace: fewer weight rows than one 256-row tile, a single
 // token (decode), no blocks, or more than kMaxTiledNb blocks.  So do a few
 // tokens that the plain entry's multi-column GEMVs take (even block count,
-// 4-byte aligned rows and strides): up to kColsFirstMax tokens they beat packing
-// both operands for the tiled kernels (us, 4096 weight rows, K 4096, Q8_0 /
-// Q4_0: 16 tokens 15.0 / 16.3 against ~25 / ~28; 32 tokens 30.8 / 32.3
-// against ~25 / ~28).
+// 4-byte aligned rows and strides; cols_first): there they beat packing both
+// operands for the tiled kernels (us, 4096 weight rows, K 4096, Q8_0 / Q4_0:
+// 16 tokens 15.0 / 16.3 against ~25 / ~28; 32 tokens 30.8 / 32.3 against
+// 23.9 / 26.9).
 bool ws_cols_first(size_t nb, const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by,
-                   size_t nc) {
-  return nc <= kColsFirstMax && nb % 2 == 0 && aligned4(vx) && aligned4(vy) && bx % 4 == 0 &&
+                   size_t nr, size_t nc) {
+  return cols_first(nr, nc) && nb % 2 == 0 && aligned4(vx) && aligned4(vy) && bx % 4 == 0 &&
          by % 4 == 0;
 }
 bool gemm_ws_uses_workspace(size_t n, const uint8_t *vx, size_t bx, const uint8_t *vy,
                             size_t by, size_t nr, size_t nc) {
   const size_t nb = n / tcrv::kQK;
   return nr >= static_cast<size_t>(tcrv::kDBM) && nc >= 2 && nb > 0 && nb <= kMaxTiledNb &&
-         !ws_cols_first(nb, vx, bx, vy, by, nc);
+         !ws_cols_first(nb, vx, bx, vy, by, nr, nc);
 }
 
 }  // namespace tcrv_host

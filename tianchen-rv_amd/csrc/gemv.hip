@@ -962,7 +962,7 @@ int tcrv_hip_q4_0_q8_0_gemm(size_t n, float *s, const uint8_t *vx, const uint8_t
     if (st != TCRV_HIP_ERR_UNSUPPORTED)
       return st;
   } else {
-    if (nc > tcrv_host::kColsFirstMax) {  // few output tiles: one 32 x 32 tile a wave
+    if (!tcrv_host::cols_first(nr, nc)) {  // few output tiles: one 32 x 32 tile a wave
       const int st = tcrv_host::gemm_rows_few(true, nb, s, vx, bx, vy, by, nr, nc, bs, stream);
       if (st != TCRV_HIP_ERR_UNSUPPORTED)
         return st;

@@ -196,10 +196,17 @@ int q4_0_grid(size_t n, float *s, const uint8_t *vx, size_t bx, const uint8_t *v
 // TCRV_HIP_ERR_UNSUPPORTED for an odd block count or operands/strides that are
 // not 4-byte aligned.
 constexpr size_t kGemvColsMax = 64;
-// Up to this many tokens the multi-column GEMVs run first; past it the
+// The multi-column GEMVs run first up to kColsFirstMax tokens; past it the
 // one-tile-a-wave GEMMs (gemm_rows_few from plain rows, gemm_tiled.hip) where
-// they serve the shape, then the GEMVs up to kGemvColsMax.
+// they serve the shape, then the GEMVs up to kGemvColsMax.  A GEMV launch
+// serves 8 tokens at ~6 us for K 4096 whatever the weight rows (it is bound by
+// its K loop at few rows: 256 x 40 x 4096 Q8_0 32 us as five launches against
+// 18-27 us on the tiles), so the switch depends on the tokens only.
 constexpr size_t kColsFirstMax = 24;
+inline bool cols_first(size_t nr, size_t nc) {
+  (void)nr;
+  return nc <= kColsFirstMax;
+}
 // The GEMM of few output tiles straight from plain rows (16-byte aligned rows
 // and strides, n a multiple of 256); TCRV_HIP_ERR_UNSUPPORTED otherwise.
 int gemm_rows_few(bool q4, size_t nb, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy,
