@@ -1327,12 +1327,10 @@ __global__ __launch_bounds__(256, 2) void gemm_tiles16(unsigned nb, float *s, co
 // For the reference ABI without a workspace (tcrv_hip_q8_0_q8_0_gemm,
 // tcrv_hip_q4_0_q8_0_gemm) at shapes of few output tiles: each work-group packs
 // its 64 weight rows and 64 tokens into records in LDS, one 8-block chunk at a
-// time, as the span pack does (a lane per row, the row's chunk span read whole
-// with aligned 128-bit loads: Q8_0 in two halves of 9 loads on two waves, Q4_0
-// 9 loads on one), and the four waves fold their 32 x 32 tiles from there as
-// gemm_tiles32 does from HBM.  Chunk c + 1 is loaded into registers before
-// chunk c is folded and written to the other LDS stage after; rows 16-byte
-// aligned and a whole number of chunks (n a multiple of 256).
+// time (a lane per row, the row's chunk span realigned as the span pack does:
+// Q8_0 in two halves on two waves, Q4_0 weights whole on one), and the four
+// waves fold their 32 x 32 tiles from there as gemm_tiles32 does from HBM.
+// Rows 16-byte aligned and a whole number of chunks (n a multiple of 256).
 constexpr int kFKB = kPackSpan;     // blocks per K chunk
 constexpr int kFOp = kFKB * kTRec;  // 17408: one operand's records of a chunk
 constexpr int kFStage = 2 * kFOp;   // weights then tokens
@@ -1342,16 +1340,6 @@ constexpr int kFStage = 2 * kFOp;   // weights then tokens
 struct Span9 {
   uint32_t v[36];
 };
-
-__device__ __forceinline__ void load_span9(const uint8_t *p, bool live, Span9 &w) {
-#pragma unroll
-  for (int k = 0; k < 9; ++k) {
-    uint4 x = make_uint4(0u, 0u, 0u, 0u);
-    if (live)
-      x = reinterpret_cast<const uint4 *>(p)[k];
-    w.v[4 * k] = x.x; w.v[4 * k + 1] = x.y; w.v[4 * k + 2] = x.z; w.v[4 * k + 3] = x.w;
-  }
-}
 
 __device__ __forceinline__ void put_record(uint8_t *rec, int r, const uint32_t (&q)[8], uint32_t d) {
   reinterpret_cast<uint4 *>(rec)[r] = make_uint4(q[0], q[1], q[2], q[3]);
@@ -1408,9 +1396,21 @@ __device__ __forceinline__ void put_q4_span(uint8_t *op, int r, const Span9 &w) 
   }
 }
 
-// kWave: the wave's index, a template argument so that each wave's staging
-// code has constant offsets (with the staging half a run-time value the
-// compiler merged the two halves' code into one with the window in scratch).
+// The staging: a chunk's raw row spans (64 weight rows, 64 tokens, row after
+// row: 272 bytes a Q8_0 span, 144 a Q4_0 one) come in by LDS DMA
+// (global_load_lds_dwordx4, 64 consecutive 16-byte pieces per instruction: a
+// few rows' lines each), and the lanes then read their row's span from LDS
+// (b128 reads at a 272- or 144-byte stride: 16 lanes cover all 64 banks) and
+// write its records.  Loading the spans straight into registers, a lane per
+// row, put 64 rows' lines under every load instruction (4096 x 128 x 4096
+// Q8_0: 31.0 against 27.7 us; 14336 x 128: 54.7 against 39.7; Q4_0, bound by
+// its three-instruction fold, unchanged).  One raw buffer and one record
+// buffer: the DMA of chunk c + 1 runs under chunk c's fold, the repack between
+// two barriers.
+constexpr int kFRawX8 = kTG * kFKB * kQ8Bytes;  // 17408
+constexpr int kFRawX4 = kTG * kFKB * kQ4Bytes;  // 9216
+constexpr int kFRawY = kTG * kFKB * kQ8Bytes;   // 17408
+
 template <bool kQ4, int kWave>
 __device__ __forceinline__ void rows_few_body(unsigned nb, float *s, const uint8_t *vx,
                                               size_t bx, const uint8_t *vy, size_t by,
@@ -1424,31 +1424,72 @@ __device__ __forceinline__ void rows_few_body(unsigned nb, float *s, const uint8
   unsigned tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const size_t m0 = static_cast<size_t>(tm) * kSBM, n0 = static_cast<size_t>(tn) * kSBN;
-  // staging role: waves 0, 1 the weight rows (Q8_0 halves 0, 1; Q4_0 wave 0
-  // the whole span, wave 1 nothing), waves 2, 3 the token halves 0, 1
+
+  constexpr int kRawX = kQ4 ? kFRawX4 : kFRawX8;
+  constexpr int kXSpan = kFKB * (kQ4 ? kQ4Bytes : kQ8Bytes);  // bytes of a row's chunk
+  constexpr int kYSpan = kFKB * kQ8Bytes;
+  constexpr int kXPieces = kXSpan / 16, kYPieces = kYSpan / 16;  // 17 or 9; 17
+  constexpr int kInst = kXPieces + kYPieces;  // DMA instructions a chunk (64 rows each operand)
+  constexpr int kMine = (kInst - wave + 3) / 4;  // this wave's: instructions wave, wave + 4, ..
+  uint8_t *raw = lds;                     // weights' spans, then the tokens'
+  uint8_t *rec = lds + kRawX + kFRawY;    // the chunk's records: weights, then tokens
+
+  // this lane's source of each of the wave's DMA instructions (chunk 0):
+  // instruction i moves flat pieces 64m .. 64m + 63 of its operand (m = i, or
+  // i - kXPieces for the tokens), row f / pieces, piece f % pieces; rows past
+  // nr / nc repeat the last one (their outputs are not stored)
+  const uint8_t *src[kMine];
+#pragma unroll
+  for (int j = 0; j < kMine; ++j) {
+    const int i = wave + 4 * j;
+    const bool y = i >= kXPieces;
+    const int m = y ? i - kXPieces : i;
+    const int pieces = y ? kYPieces : kXPieces;
+    const int f = 64 * m + lane;
+    const size_t row = y ? min(n0 + f / pieces, nc - 1) : min(m0 + f / pieces, nr - 1);
+    src[j] = (y ? vy + row * by : vx + row * bx) + 16 * (f % pieces);
+  }
+  auto dma = [&](unsigned c) {
+#pragma unroll
+    for (int j = 0; j < kMine; ++j) {
+      const int i = wave + 4 * j;
+      const bool y = i >= kXPieces;
+      const int m = y ? i - kXPieces : i;
+      lds_void *to = (lds_void *)((char __attribute__((address_space(3))) *)raw +
+                                  (y ? kRawX : 0) + 1024 * m);
+      __builtin_amdgcn_global_load_lds(src[j] + static_cast<size_t>(c) * (y ? kYSpan : kXSpan),
+                                       to, 16, 0, 0);
+    }
+  };
+  // repack roles: waves 0, 1 the weight rows (Q8_0 halves 0, 1; Q4_0 wave 0 the
+  // whole span), waves 2, 3 the token halves; lane = row of the group
   constexpr bool tok = wave >= 2;
   constexpr int half = wave & 1;
-  constexpr bool stager = tok || !kQ4 || half == 0;
-  const size_t srow = (tok ? n0 : m0) + lane;
-  const bool live = stager && srow < (tok ? nc : nr);
-  constexpr int kXSpan = kFKB * (kQ4 ? kQ4Bytes : kQ8Bytes);
-  const uint8_t *src = tok ? vy + min(srow, nc - 1) * by + 128 * half
-                           : vx + min(srow, nr - 1) * bx + (kQ4 ? 0 : 128 * half);
-  const size_t span = tok ? kFKB * kQ8Bytes : kXSpan;
-  auto put = [&](int st, const Span9 &w) {
-    uint8_t *op = lds + st * kFStage + (tok ? kFOp : 0);
-    if constexpr (kQ4 && !tok)
-      put_q4_span(op, lane, w);
-    else
-      put_q8_half<half>(op, lane, w);
+  constexpr bool packer = tok || !kQ4 || half == 0;
+  auto repack = [&] {
+    if constexpr (packer) {
+      const uint8_t *rs = raw + (tok ? kRawX + lane * kYSpan : lane * kXSpan) +
+                          ((kQ4 && !tok) ? 0 : 128 * half);
+      Span9 w;
+#pragma unroll
+      for (int k = 0; k < 9; ++k) {
+        const uint4 x = reinterpret_cast<const uint4 *>(rs)[k];
+        w.v[4 * k] = x.x; w.v[4 * k + 1] = x.y; w.v[4 * k + 2] = x.z; w.v[4 * k + 3] = x.w;
+      }
+      uint8_t *op = rec + (tok ? kFOp : 0);
+      if constexpr (kQ4 && !tok)
+        put_q4_span(op, lane, w);
+      else
+        put_q8_half<half>(op, lane, w);
+    }
   };
 
   const uint32_t kmask = h ? 0u : 0xffffu;
   const uint32_t one = h ? 0u : 0x3c00u;
   const unsigned qa = h * 1024 + (32 * wm + li) * 16, qb = h * 1024 + (32 * wn + li) * 16;
   const unsigned sa = 2 * kTG * 16 + (32 * wm + li) * 2, sb = 2 * kTG * 16 + (32 * wn + li) * 2;
-  auto ops = [&](int st, int k) {
-    const uint8_t *ra = lds + st * kFStage + k * kTRec, *rb = ra + kFOp;
+  auto ops = [&](int k) {
+    const uint8_t *ra = rec + k * kTRec, *rb = ra + kFOp;
     Ops32 o;
     o.a = *reinterpret_cast<const v4i *>(ra + qa);
     o.b = *reinterpret_cast<const v4i *>(rb + qb);
@@ -1462,29 +1503,30 @@ __device__ __forceinline__ void rows_few_body(unsigned nb, float *s, const uint8
     acc[e] = 0.0f;
 
   const unsigned nchunks = nb / kFKB;
-  Span9 w;
-  if (stager) {
-    load_span9(src, live, w);
-    put(0, w);
-  }
+  dma(0);
+  __builtin_amdgcn_s_waitcnt(0x070);  // this wave's DMA has landed
+  __syncthreads();                     // and every wave's
+  repack();
   __syncthreads();
   for (unsigned c = 0; c < nchunks; ++c) {
-    const int st = c & 1;
     const bool more = c + 1 < nchunks;
-    if (stager && more)
-      load_span9(src + (c + 1) * span, live, w);
-    Step32 cur = issue32<kQ4>(ops(st, 0), kmask, one);
+    if (more)
+      dma(c + 1);  // the raw buffer: its last reader, the repack, is past a barrier
+    Step32 cur = issue32<kQ4>(ops(0), kmask, one);
 #pragma unroll
     for (int k = 0; k < kFKB; ++k) {
       Step32 nxt;
       if (k + 1 < kFKB)
-        nxt = issue32<kQ4>(ops(st, k + 1), kmask, one);
+        nxt = issue32<kQ4>(ops(k + 1), kmask, one);
       fold32<kQ4>(acc, cur);
       cur = nxt;
     }
-    if (stager && more)
-      put(st ^ 1, w);
-    __syncthreads();
+    if (more) {
+      __builtin_amdgcn_s_waitcnt(0x070);
+      __syncthreads();  // every DMA landed, every wave done with the records
+      repack();
+      __syncthreads();
+    }
   }
   store32(s, acc, m0 + 32 * wm, n0 + 32 * wn + li, h, nr, nc, bs);
 }
@@ -1493,7 +1535,10 @@ template <bool kQ4>
 __global__ __launch_bounds__(256, 2) void gemm_rows_few(unsigned nb, float *s, const uint8_t *vx,
                                                         size_t bx, const uint8_t *vy, size_t by,
                                                         size_t nr, size_t nc, size_t bs) {
-  __shared__ __align__(16) uint8_t lds[2 * kFStage];
+  __shared__ __align__(16) uint8_t lds[kFRawX8 + kFRawY + kFStage];  // raw spans, records
+  // the wave index as a template argument: each wave's staging offsets are
+  // constants (as a run-time value the compiler merged the two halves' repack
+  // code with the span window in scratch)
   switch (__builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6)) {
   case 0: rows_few_body<kQ4, 0>(nb, s, vx, bx, vy, by, nr, nc, bs, lds); break;
   case 1: rows_few_body<kQ4, 1>(nb, s, vx, bx, vy, by, nr, nc, bs, lds); break;
@@ -1727,19 +1772,16 @@ int tcrv_hip_q8_0_q8_0_gemm_tiles(size_t n, float *s, const uint8_t *tx, const u
 namespace tcrv_host {
 
 // The plain-row entries' kernel for shapes of few output tiles (gemm_rows_few):
-// rows 16-byte aligned, a whole number of 8-block chunks.  Its staging costs
-// more than the fold (4096 x 128 x 4096 Q8_0: 31.0 us, 18.6 without staging
-// past the first chunk, 25.9 without the fold: each staging load instruction
-// touches 64 rows' lines), so it serves fewer work-groups than gemm_tiles32
-// does: past 768 (Q8_0) or 1024 (Q4_0) the 256-row kernels are as fast (4096 x
-// 1024 x 4096 Q8_0: 97 against 91-93 us; Q4_0 91 against 98-101).
+// rows 16-byte aligned, a whole number of 8-block chunks, the shapes
+// gemm_tiles32 serves (at its 1024 work-groups the 256-row kernels are as fast:
+// 4096 x 1024 x 4096 Q8_0 91.6 against 91-93 us).
 int gemm_rows_few(bool q4, size_t nb, float *s, const uint8_t *vx, size_t bx, const uint8_t *vy,
                   size_t by, size_t nr, size_t nc, size_t bs, void *stream) {
   if (nr < 2 || nc < 2 || nb == 0 || nb % tcrv::kFKB != 0 || !aligned16(vx) || !aligned16(vy) ||
       bx % 16 != 0 || by % 16 != 0)
     return TCRV_HIP_ERR_UNSUPPORTED;
   const size_t tiles64 = tiles64_of(nr, nc);
-  if (!tiles32_first(tiles128_of(nr, nc), tiles64, nb) || tiles64 > (q4 ? 1024u : 768u))
+  if (!tiles32_first(tiles128_of(nr, nc), tiles64, nb))
     return TCRV_HIP_ERR_UNSUPPORTED;
   const dim3 g(static_cast<unsigned>(tiles64)), b(256);
   const unsigned nbu = static_cast<unsigned>(nb);
