@@ -1327,16 +1327,16 @@ __global__ __launch_bounds__(256, 2) void gemm_tiles16(unsigned nb, float *s, co
 // For the reference ABI without a workspace (tcrv_hip_q8_0_q8_0_gemm,
 // tcrv_hip_q4_0_q8_0_gemm) at shapes of few output tiles: each work-group packs
 // its 64 weight rows and 64 tokens into records in LDS, one 8-block chunk at a
-// time (a lane per row, the row's chunk span realigned as the span pack does:
-// Q8_0 in two halves on two waves, Q4_0 weights whole on one), and the four
+// time (a lane per row, the row's chunk span realigned as the span pack does,
+// in two halves on two waves per operand), and the four
 // waves fold their 32 x 32 tiles from there as gemm_tiles32 does from HBM.
 // Rows 16-byte aligned and a whole number of chunks (n a multiple of 256).
 constexpr int kFKB = kPackSpan;     // blocks per K chunk
 constexpr int kFOp = kFKB * kTRec;  // 17408: one operand's records of a chunk
 constexpr int kFStage = 2 * kFOp;   // weights then tokens
 
-// This lane's part of a chunk: Q8_0 blocks 4h .. 4h + 3 of its row's span
-// (pieces 8h .. 8h + 8, 16 bytes each), Q4_0 all 8 blocks (pieces 0 .. 8).
+// This lane's part of a chunk: blocks 4h .. 4h + 3 of its row's span, Q8_0
+// pieces 8h .. 8h + 8 (16 bytes each), Q4_0 pieces 4h .. 4h + 4.
 struct Span9 {
   uint32_t v[36];
 };
@@ -1373,26 +1373,30 @@ __device__ __forceinline__ void put_q8_half(uint8_t *op, int r, const Span9 &w) 
   }
 }
 
-// Q4_0 chunk span (144 bytes): block k at byte 18k, its nibbles decoded to n - 8.
-__device__ __forceinline__ void put_q4_span(uint8_t *op, int r, const Span9 &w) {
+// Q4_0 half kH of a chunk span (144 bytes, block k at byte 18k): blocks 4kH ..
+// 4kH + 3 from the window of pieces 4kH .. 4kH + 4 (bytes 64kH .. 64kH + 79),
+// block j at window byte 8kH + 18j, its nibbles decoded to n - 8.
+template <int kH>
+__device__ __forceinline__ void put_q4_half(uint8_t *op, int r, const Span9 &w) {
 #pragma unroll
-  for (int k = 0; k < kFKB; ++k) {
+  for (int j = 0; j < 4; ++j) {
     uint32_t raw[4], q[8], d;
-    if ((k & 1) == 0) {
-      const int w0 = 9 * k / 2;
+    const int o = 8 * kH + 18 * j;
+    if ((j & 1) == 0) {
+      const int w0 = o / 4;
       d = w.v[w0] & 0xffffu;
 #pragma unroll
       for (int m = 0; m < 4; ++m)
         raw[m] = funnel16(w.v[w0 + m], w.v[w0 + m + 1]);
     } else {
-      const int w0 = (18 * k - 2) / 4;
+      const int w0 = (o - 2) / 4;
       d = w.v[w0] >> 16;
 #pragma unroll
       for (int m = 0; m < 4; ++m)
         raw[m] = w.v[w0 + 1 + m];
     }
     decode_q4_quants(raw, q);
-    put_record(op + k * kTRec, r, q, d);
+    put_record(op + (4 * kH + j) * kTRec, r, q, d);
   }
 }
 
@@ -1461,27 +1465,27 @@ __device__ __forceinline__ void rows_few_body(unsigned nb, float *s, const uint8
                                        to, 16, 0, 0);
     }
   };
-  // repack roles: waves 0, 1 the weight rows (Q8_0 halves 0, 1; Q4_0 wave 0 the
-  // whole span), waves 2, 3 the token halves; lane = row of the group
+  // repack roles: waves 0, 1 the weight rows' halves (blocks 0-3, 4-7), waves
+  // 2, 3 the tokens' halves; lane = row of the group.  A Q8_0 half is pieces
+  // 8h .. 8h + 8 of the span, a Q4_0 half pieces 4h .. 4h + 4.
   constexpr bool tok = wave >= 2;
   constexpr int half = wave & 1;
-  constexpr bool packer = tok || !kQ4 || half == 0;
+  constexpr bool q4x = kQ4 && !tok;
+  constexpr int kWin = q4x ? 5 : 9;  // pieces a lane reads
   auto repack = [&] {
-    if constexpr (packer) {
-      const uint8_t *rs = raw + (tok ? kRawX + lane * kYSpan : lane * kXSpan) +
-                          ((kQ4 && !tok) ? 0 : 128 * half);
-      Span9 w;
+    const uint8_t *rs = raw + (tok ? kRawX + lane * kYSpan : lane * kXSpan) +
+                        (q4x ? 64 : 128) * half;
+    Span9 w;
 #pragma unroll
-      for (int k = 0; k < 9; ++k) {
-        const uint4 x = reinterpret_cast<const uint4 *>(rs)[k];
-        w.v[4 * k] = x.x; w.v[4 * k + 1] = x.y; w.v[4 * k + 2] = x.z; w.v[4 * k + 3] = x.w;
-      }
-      uint8_t *op = rec + (tok ? kFOp : 0);
-      if constexpr (kQ4 && !tok)
-        put_q4_span(op, lane, w);
-      else
-        put_q8_half<half>(op, lane, w);
+    for (int k = 0; k < kWin; ++k) {
+      const uint4 x = reinterpret_cast<const uint4 *>(rs)[k];
+      w.v[4 * k] = x.x; w.v[4 * k + 1] = x.y; w.v[4 * k + 2] = x.z; w.v[4 * k + 3] = x.w;
     }
+    uint8_t *op = rec + (tok ? kFOp : 0);
+    if constexpr (q4x)
+      put_q4_half<half>(op, lane, w);
+    else
+      put_q8_half<half>(op, lane, w);
   };
 
   const uint32_t kmask = h ? 0u : 0xffffu;
@@ -1805,11 +1809,24 @@ bool ws_cols_first(size_t nb, const uint8_t *vx, size_t bx, const uint8_t *vy, s
   return cols_first(nr, nc) && nb % 2 == 0 && aligned4(vx) && aligned4(vy) && bx % 4 == 0 &&
          by % 4 == 0;
 }
+// And where the plain entry's few-tile kernel, which packs in LDS, beats a
+// separate pack: up to 448 of its work-groups at K up to 4096, past the 16 x 16
+// tiles' shapes (us, plain against the workspace path: 4096 x 128 x 4096 28.0 /
+// 30.6 Q8_0, 31.5 / 32.2 Q4_0; 14336 x 128 40.7 / 48.7, 42.0 / 45.9; but 4096 x
+// 512 41.8 / 39.9, 4096 x 128 x 14336 84.1 / 72.5).
+bool ws_rows_few_first(size_t nb, const uint8_t *vx, size_t bx, const uint8_t *vy, size_t by,
+                       size_t nr, size_t nc) {
+  return nb % tcrv::kFKB == 0 && nb <= 128 && aligned16(vx) && aligned16(vy) && bx % 16 == 0 &&
+         by % 16 == 0 && tiles32_first(tiles128_of(nr, nc), tiles64_of(nr, nc), nb) &&
+         !tiles16_first(nr, nc) && tiles64_of(nr, nc) <= 448;
+}
+
 bool gemm_ws_uses_workspace(size_t n, const uint8_t *vx, size_t bx, const uint8_t *vy,
                             size_t by, size_t nr, size_t nc) {
   const size_t nb = n / tcrv::kQK;
   return nr >= static_cast<size_t>(tcrv::kDBM) && nc >= 2 && nb > 0 && nb <= kMaxTiledNb &&
-         !ws_cols_first(nb, vx, bx, vy, by, nr, nc);
+         !ws_cols_first(nb, vx, bx, vy, by, nr, nc) &&
+         !ws_rows_few_first(nb, vx, bx, vy, by, nr, nc);
 }
 
 }  // namespace tcrv_host
