@@ -135,7 +135,7 @@ def test_q4_0_gemm_ws_special_scales(hip, oracle, dev):
 
 
 def test_q4_0_gemm_tiles_nonfinite_dx_mid_k(hip, oracle, dev):
-    """The pre-packed Q4_0 GEMM at a shape of few tiles (one 32 x 32 tile a wave,
+    """The pre-packed Q4_0 GEMM at a shape of few tiles (one 16 x 16 tile a wave,
     folding every block in the exact three-instruction form) with non-finite d_x
     across K: +-Inf planted in the first blocks, in the middle of K and near its
     end, NaN, and an infinite d_x over a zero block sum (0 * Inf = NaN).  The
@@ -159,8 +159,9 @@ def test_q4_0_gemm_tiles_nonfinite_dx_mid_k(hip, oracle, dev):
 
 @pytest.mark.parametrize("nb", [40, 42])
 def test_q4_0_gemm_nonfinite_dx_mid_k(hip, oracle, dev, nb):
-    """The plain Q4_0 entry's 256 x 128 wide kernel with non-finite d_x planted
-    across K: +-Inf in the first chunk of one wave's rows, in the middle of K,
+    """The plain Q4_0 entry with non-finite d_x planted across K (nb = 40: the
+    plain-row few-tile kernel, fast form then the exact pass on its NaN outputs;
+    nb = 42: the 256 x 128 wide kernel): +-Inf in the first chunk of one wave's rows, in the middle of K,
     in the last block and (nb = 42) in the partial tail, NaN, and an infinite
     d_x over a zero block sum (0 * Inf = NaN)."""
     nr, nc = 512, 256
