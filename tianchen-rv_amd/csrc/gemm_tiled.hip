@@ -1058,62 +1058,37 @@ struct Ops32 {
   uint32_t ux, uy;
 };
 
-// One block of a wave's 32 x 32 tile.  Q8_0: the block sums and the scale
-// products d_x * d_y.  Q4_0, on the transposed tile (tokens as the MFMA's A
-// operand, weights as B: lane (li, h) holds weight row li and tokens
-// 8(e / 4) + 4h + e % 4): the seeded sums F = M + sumi (q4_seeded_sums), d_y of
-// the tokens spread over the tile by the f16 MFMA against 1.0, and the lane's
-// d_x.  kmask keeps a scale in k-slot 0 of lanes 0-31 only; one is fp16 1.0
-// there and 0 elsewhere.
+// One block of a wave's 32 x 32 tile: the block sums, the scale products (Q8_0)
+// or the weight rows' d_x spread over the tile (Q4_0), and the lane's token
+// scale (Q4_0).  kmask keeps the scale in k-slot 0 of lanes 0-31 only; one is
+// fp16 1.0 there and 0 elsewhere.
 struct Step32 {
-  v16i sumi;  // Q4_0: the bits of F
-  v16f scl;   // Q8_0: d_x * d_y; Q4_0: d_y
-  float dx;   // Q4_0
+  v16i sumi;
+  v16f scl;
+  float dy;
 };
 
-// The Q4_0 MFMA's accumulator input M in every element, made once and hidden
-// from instruction selection, which would otherwise rebuild it (16 moves) for
-// every block.
-__device__ __forceinline__ v16i seed32() {
-  v16i seed;
-#pragma unroll
-  for (int e = 0; e < 16; ++e)
-    seed[e] = kSeedBits;
-  asm volatile("" : "+v"(seed));
-  return seed;
-}
-
 template <bool kQ4>
-__device__ __forceinline__ Step32 issue32(const Ops32 &o, uint32_t kmask, uint32_t one,
-                                          const v16i &seed) {
+__device__ __forceinline__ Step32 issue32(const Ops32 &o, uint32_t kmask, uint32_t one) {
   Step32 t;
+  t.sumi = q8_sumi(o.a, o.b);
   if constexpr (kQ4) {
-    t.sumi = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.b, o.a, seed, 0, 0, 0);
-    t.scl = q8_dxy(o.uy & kmask, one);
-    t.dx = fp16_bits_to_f32(o.ux);
-    asm volatile("" : "+v"(t.dx));  // widened once (not an fma_mix per output)
+    t.scl = q8_dxy(o.ux & kmask, one);
+    t.dy = fp16_bits_to_f32(o.uy);
+    asm volatile("" : "+v"(t.dy));  // widened once (not an fma_mix per output)
   } else {
-    t.sumi = q8_sumi(o.a, o.b);
     t.scl = q8_dxy(o.ux & kmask, o.uy & kmask);
-    t.dx = 0.0f;
+    t.dy = 0.0f;
   }
   return t;
 }
 
-// Q4_0 folds fl(sumi * d_x) as fma(F, d_x, -M * d_x) (kExact false: one
-// instruction, exact while d_x is finite) or as (F - M) * d_x (kExact), then
-// fma with d_y.  A non-finite d_x turns the fast form into NaN in all 16 of
-// the lane's outputs (F * inf - inf, or NaN), and NaN stays: a tile with no
-// NaN output had only finite d_x and holds the exact form's bits; one with a
-// NaN output is folded again in the exact form (tile32_has_nan).
-template <bool kQ4, bool kExact = false>
+template <bool kQ4>
 __device__ __forceinline__ void fold32(float (&acc)[16], const Step32 &t) {
   if constexpr (kQ4) {
-    const v16f F = __builtin_bit_cast(v16f, t.sumi);
-    const float c = -kSeed * t.dx;  // -M * d_x, exact (unused by the exact form)
 #pragma unroll
     for (int e = 0; e < 16; ++e)
-      acc[e] = fmaf(kExact ? (F[e] - kSeed) * t.dx : fmaf(F[e], t.dx, c), t.scl[e], acc[e]);
+      acc[e] = fmaf(static_cast<float>(t.sumi[e]) * t.scl[e], t.dy, acc[e]);
   } else {  // all 16 conversions before the fmas, as q8_fold<true> (without its pin)
     float f[16];
 #pragma unroll
@@ -1128,31 +1103,13 @@ __device__ __forceinline__ void fold32(float (&acc)[16], const Step32 &t) {
     asm volatile("" : "+v"(acc[e]));
 }
 
-// Whether any output of the wave's tile is NaN (wave-uniform).
-__device__ __forceinline__ bool tile32_has_nan(const float (&acc)[16]) {
-  bool nan = false;
-#pragma unroll
-  for (int e = 0; e < 16; ++e)
-    nan = nan || __builtin_isnan(acc[e]);
-  return __builtin_amdgcn_ballot_w64(nan) != 0;
-}
-
-template <bool B>
-struct ExactTag {
-  static constexpr bool value = B;
-};
-
-// Lane (li, h) of a 32 x 32 tile at weight row row0, token col0: Q8_0 holds
-// token col0 + li of rows row0 + 8 (e / 4) + 4h + e % 4; Q4_0 (transposed) row
-// row0 + li of those tokens.
-template <bool kQ4>
-__device__ __forceinline__ void store32(float *s, const float (&acc)[16], size_t row0,
-                                        size_t col0, int li, int h, size_t nr, size_t nc,
-                                        size_t bs) {
+// Lane (li, h) of a 32 x 32 tile at weight row row0, token column col holds
+// rows row0 + 8 (e / 4) + 4h + e % 4.
+__device__ __forceinline__ void store32(float *s, const float (&acc)[16], size_t row0, size_t col,
+                                        int h, size_t nr, size_t nc, size_t bs) {
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
-    const size_t j = 8 * (e >> 2) + 4 * h + (e & 3);
-    const size_t row = kQ4 ? row0 + li : row0 + j, col = kQ4 ? col0 + j : col0 + li;
+    const size_t row = row0 + 8 * (e >> 2) + 4 * h + (e & 3);
     if (row < nr && col < nc)
       s[row * bs + col] = acc[e];
   }
@@ -1199,50 +1156,43 @@ __global__ __launch_bounds__(256, 2) void gemm_tiles32(unsigned nb, float *s, co
     o.ux = __builtin_amdgcn_raw_buffer_load_b16(pa, sa, 0, 0);
     o.uy = __builtin_amdgcn_raw_buffer_load_b16(pb, sb, 0, 0);
   };
-  const v16i seed = seed32();
-  const auto issue = [&](const Ops32 &o) { return issue32<kQ4>(o, kmask, one, seed); };
+  const auto issue = [&](const Ops32 &o) { return issue32<kQ4>(o, kmask, one); };
   float acc[16];
-  // the whole K loop, in the fast or (Q4_0, a tile with a NaN output) the exact form
-  auto run = [&](auto exact) {
-    constexpr bool kExact = decltype(exact)::value;
 #pragma unroll
-    for (int e = 0; e < 16; ++e)
-      acc[e] = 0.0f;
-    Ops32 ring[kSAhead];
+  for (int e = 0; e < 16; ++e)
+    acc[e] = 0.0f;
+  const auto fold = [&](const Step32 &t) { fold32<kQ4>(acc, t); };
+
+  Ops32 ring[kSAhead];
+#pragma unroll
+  for (int j = 0; j < kSAhead; ++j)
+    load(min(static_cast<unsigned>(j), last), ring[j]);
+  Step32 cur = issue(ring[0]);
+  load(min(static_cast<unsigned>(kSAhead), last), ring[0]);
+  // block b + 1 sits in slot (b + 1) % kSAhead: its MFMAs go out before block
+  // b's fold, and the slot is refilled with block b + 1 + kSAhead (clamped to
+  // the last block, whose extra copies are never folded).  Whole rounds of
+  // kSAhead blocks first, with no branch between the loads and their use, so
+  // the waits count exactly the loads still in flight.
+  auto step = [&](unsigned b, int j) {
+    const int kn = (j + 1) % kSAhead;
+    const Step32 nxt = issue(ring[kn]);
+    load(min(b + 1 + kSAhead, last), ring[kn]);
+    fold(cur);
+    cur = nxt;
+  };
+  unsigned b0 = 0;
+  for (; b0 + kSAhead <= nb; b0 += kSAhead) {
 #pragma unroll
     for (int j = 0; j < kSAhead; ++j)
-      load(min(static_cast<unsigned>(j), last), ring[j]);
-    Step32 cur = issue(ring[0]);
-    load(min(static_cast<unsigned>(kSAhead), last), ring[0]);
-    // block b + 1 sits in slot (b + 1) % kSAhead: its MFMAs go out before block
-    // b's fold, and the slot is refilled with block b + 1 + kSAhead (clamped to
-    // the last block, whose extra copies are never folded).  Whole rounds of
-    // kSAhead blocks first, with no branch between the loads and their use, so
-    // the waits count exactly the loads still in flight.
-    auto step = [&](unsigned b, int j) {
-      const int kn = (j + 1) % kSAhead;
-      const Step32 nxt = issue(ring[kn]);
-      load(min(b + 1 + kSAhead, last), ring[kn]);
-      fold32<kQ4, kExact>(acc, cur);
-      cur = nxt;
-    };
-    unsigned b0 = 0;
-    for (; b0 + kSAhead <= nb; b0 += kSAhead) {
+      step(b0 + j, j);
+  }
 #pragma unroll
-      for (int j = 0; j < kSAhead; ++j)
-        step(b0 + j, j);
-    }
-#pragma unroll
-    for (int j = 0; j < kSAhead - 1; ++j)
-      if (b0 + j < nb)
-        step(b0 + j, j);
-  };
-  run(ExactTag<false>{});
-  if constexpr (kQ4)
-    if (tile32_has_nan(acc))
-      run(ExactTag<true>{});
-  store32<kQ4>(s, acc, static_cast<size_t>(tm) * kSBM + 32 * wm,
-               static_cast<size_t>(tn) * kSBN + 32 * wn, li, h, nr, nc, bs);
+  for (int j = 0; j < kSAhead - 1; ++j)
+    if (b0 + j < nb)
+      step(b0 + j, j);
+  store32(s, acc, static_cast<size_t>(tm) * kSBM + 32 * wm,
+          static_cast<size_t>(tn) * kSBN + 32 * wn + li, h, nr, nc, bs);
 }
 
 // ---- fewer still: one 16 x 16 tile a wave ----------------------------------
@@ -1468,8 +1418,7 @@ constexpr int kFRawY = kTG * kFKB * kQ8Bytes;   // 17408
 template <bool kQ4, int kWave>
 __device__ __forceinline__ void rows_few_body(unsigned nb, float *s, const uint8_t *vx,
                                               size_t bx, const uint8_t *vy, size_t by,
-                                              size_t nr, size_t nc, size_t bs, uint8_t *lds,
-                                              int *redo) {
+                                              size_t nr, size_t nc, size_t bs, uint8_t *lds) {
   const int lane = threadIdx.x & 63;
   constexpr int wave = kWave;
   constexpr int wm = wave & 1, wn = wave >> 1;
@@ -1552,59 +1501,38 @@ __device__ __forceinline__ void rows_few_body(unsigned nb, float *s, const uint8
     o.uy = *reinterpret_cast<const uint16_t *>(rb + sb);
     return o;
   };
-  const v16i seed = seed32();
   float acc[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e)
+    acc[e] = 0.0f;
+
   const unsigned nchunks = nb / kFKB;
-  // the whole K loop, in the fast or (Q4_0, a tile with a NaN output) the exact
-  // form; it starts with no DMA in flight and ends with every wave past its
-  // last record read only after the next barrier
-  auto run = [&](auto exact) {
-    constexpr bool kExact = decltype(exact)::value;
+  dma(0);
+  __builtin_amdgcn_s_waitcnt(0x070);  // this wave's DMA has landed
+  __syncthreads();                     // and every wave's
+  repack();
+  __syncthreads();
+  for (unsigned c = 0; c < nchunks; ++c) {
+    const bool more = c + 1 < nchunks;
+    if (more)
+      dma(c + 1);  // the raw buffer: its last reader, the repack, is past a barrier
+    Step32 cur = issue32<kQ4>(ops(0), kmask, one);
 #pragma unroll
-    for (int e = 0; e < 16; ++e)
-      acc[e] = 0.0f;
-    dma(0);
-    __builtin_amdgcn_s_waitcnt(0x070);  // this wave's DMA has landed
-    __syncthreads();                     // and every wave's
-    repack();
-    __syncthreads();
-    for (unsigned c = 0; c < nchunks; ++c) {
-      const bool more = c + 1 < nchunks;
-      if (more)
-        dma(c + 1);  // the raw buffer: its last reader, the repack, is past a barrier
-      Step32 cur = issue32<kQ4>(ops(0), kmask, one, seed);
-#pragma unroll
-      for (int k = 0; k < kFKB; ++k) {
-        Step32 nxt;
-        if (k + 1 < kFKB)
-          nxt = issue32<kQ4>(ops(k + 1), kmask, one, seed);
-        fold32<kQ4, kExact>(acc, cur);
-        cur = nxt;
-      }
-      if (more) {
-        __builtin_amdgcn_s_waitcnt(0x070);
-        __syncthreads();  // every DMA landed, every wave done with the records
-        repack();
-        __syncthreads();
-      }
+    for (int k = 0; k < kFKB; ++k) {
+      Step32 nxt;
+      if (k + 1 < kFKB)
+        nxt = issue32<kQ4>(ops(k + 1), kmask, one);
+      fold32<kQ4>(acc, cur);
+      cur = nxt;
     }
-  };
-  if constexpr (kQ4) {
-    if (threadIdx.x == 0)
-      *redo = 0;  // read after the barriers of the loop below
+    if (more) {
+      __builtin_amdgcn_s_waitcnt(0x070);
+      __syncthreads();  // every DMA landed, every wave done with the records
+      repack();
+      __syncthreads();
+    }
   }
-  run(ExactTag<false>{});
-  if constexpr (kQ4) {
-    // the staging is shared, so the work-group folds again if any wave's tile
-    // has a NaN output; the barrier also orders every wave's last record read
-    // before the second pass's repack
-    if (tile32_has_nan(acc) && lane == 0)
-      *redo = 1;
-    __syncthreads();
-    if (*redo)
-      run(ExactTag<true>{});
-  }
-  store32<kQ4>(s, acc, m0 + 32 * wm, n0 + 32 * wn, li, h, nr, nc, bs);
+  store32(s, acc, m0 + 32 * wm, n0 + 32 * wn + li, h, nr, nc, bs);
 }
 
 template <bool kQ4>
@@ -1612,15 +1540,14 @@ __global__ __launch_bounds__(256, 2) void gemm_rows_few(unsigned nb, float *s, c
                                                         size_t bx, const uint8_t *vy, size_t by,
                                                         size_t nr, size_t nc, size_t bs) {
   __shared__ __align__(16) uint8_t lds[kFRawX8 + kFRawY + kFStage];  // raw spans, records
-  __shared__ int redo;  // Q4_0: fold again in the exact form
   // the wave index as a template argument: each wave's staging offsets are
   // constants (as a run-time value the compiler merged the two halves' repack
   // code with the span window in scratch)
   switch (__builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6)) {
-  case 0: rows_few_body<kQ4, 0>(nb, s, vx, bx, vy, by, nr, nc, bs, lds, &redo); break;
-  case 1: rows_few_body<kQ4, 1>(nb, s, vx, bx, vy, by, nr, nc, bs, lds, &redo); break;
-  case 2: rows_few_body<kQ4, 2>(nb, s, vx, bx, vy, by, nr, nc, bs, lds, &redo); break;
-  default: rows_few_body<kQ4, 3>(nb, s, vx, bx, vy, by, nr, nc, bs, lds, &redo); break;
+  case 0: rows_few_body<kQ4, 0>(nb, s, vx, bx, vy, by, nr, nc, bs, lds); break;
+  case 1: rows_few_body<kQ4, 1>(nb, s, vx, bx, vy, by, nr, nc, bs, lds); break;
+  case 2: rows_few_body<kQ4, 2>(nb, s, vx, bx, vy, by, nr, nc, bs, lds); break;
+  default: rows_few_body<kQ4, 3>(nb, s, vx, bx, vy, by, nr, nc, bs, lds); break;
   }
 }
 
