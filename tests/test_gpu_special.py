@@ -160,8 +160,8 @@ def test_q4_0_gemm_tiles_nonfinite_dx_mid_k(hip, oracle, dev):
 @pytest.mark.parametrize("nb", [40, 42])
 def test_q4_0_gemm_nonfinite_dx_mid_k(hip, oracle, dev, nb):
     """The plain Q4_0 entry with non-finite d_x planted across K (nb = 40: the
-    plain-row few-tile kernel, fast form then the exact pass on its NaN outputs;
-    nb = 42: the 256 x 128 wide kernel): +-Inf in the first chunk of one wave's rows, in the middle of K,
+    plain-row few-tile kernel, one 32 x 32 tile a wave; nb = 42: the 256 x 128
+    wide kernel): +-Inf in the first chunk of one wave's rows, in the middle of K,
     in the last block and (nb = 42) in the partial tail, NaN, and an infinite
     d_x over a zero block sum (0 * Inf = NaN)."""
     nr, nc = 512, 256
