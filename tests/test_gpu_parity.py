@@ -1203,6 +1203,9 @@ def test_gemm_tiles_one_tile_a_wave(hip, oracle, dev, quant, nr, nc, nb):
     (300, 70, 8),     # one 8-block chunk; partial row and token groups
     (1000, 600, 40),  # five chunks
     (2100, 333, 24),
+    (1000, 600, 48),  # six chunks
+    (4096, 128, 128),  # the bench shape: sixteen chunks
+    (4100, 300, 32),  # 325 work-groups
 ])
 def test_gemm_plain_rows_few_tiles(hip, oracle, dev, quant, nr, nc, nb):
     """The plain entries at shapes of few output tiles with 16-byte aligned rows and whole

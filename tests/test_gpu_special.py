@@ -60,6 +60,7 @@ def q4(rows, nb, seed, nonfinite_every=0):
     (300, 130, 9, 0),    # wide 256 x 128 tiles: 2 full chunks + 1 block
     (256, 128, 8, 0),    # few tiles, 16-byte rows: packed in LDS, one 32 x 32 tile a wave
     (600, 200, 24, 0),   # the same over three 8-block chunks
+    (600, 200, 48, 0),   # the same over six chunks
     (100, 70, 9, 16),    # 128 x 128 tiles (fewer than 256 weight rows)
     (33, 20, 5, 2),      # rows 2-byte aligned only: the raw-block kernel
     (64, 1, 8, 0),       # decode shape: register-direct block dots
@@ -94,6 +95,7 @@ def test_q8_0_gemm_ws_special_scales(hip, oracle, dev):
 
 @pytest.mark.parametrize("nr,nc,nb", [(300, 130, 9), (100, 70, 9), (64, 1, 8), (1, 40, 8),
                                       (600, 200, 24),  # packed in LDS, a 32 x 32 tile a wave
+                                      (600, 200, 48),  # the same, six chunks
                                       (200, 4, 8), (64, 3, 10)])  # the last two: multi-column GEMVs
 def test_q4_0_gemm_special_scales(hip, oracle, dev, nr, nc, nb):
     n = nb * 32
